@@ -1,0 +1,239 @@
+#!/usr/bin/env python3
+"""FT fwd+bwd throughput on one MI355X.
+
+One step = forward and backward of both perspectives through
+SparseLinearFunction (two applies sharing W and b, autograd summing the two
+dense weight grads), on inputs already resident in HBM.  Prints one JSON line:
+positions/s, the roofline of the dominant kernel (algorithmic bytes per launch
+over its average HIP-event duration), and a CPU baseline (the PyTorch-CPU
+restatement timed on a bounded sample of the same workload).
+
+  python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--workload 1]
+                  [--bwd sorted|atomic] [--cpu-seconds 12] [--no-cpu]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "stockfish-trainer_amd")
+for _p in (PKG, ROOT):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "FT fwd+bwd positions/sec @B=65536,L1=1040; achieved GB/s vs HBM peak"
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def kernel_bytes(kind: str, w, idx_pair) -> float | None:
+    from sft_amd import workloads as wl
+
+    if kind == "fwd_f32_gather":
+        return sum(wl.fwd_kernel_bytes(i, w.N, w.L) for i in idx_pair) / 2
+    if kind == "bwd_feature_gather":
+        return sum(wl.bwd_gather_kernel_bytes(i, w.N, w.L) for i in idx_pair) / 2
+    if kind == "bwd_atomic_scatter":
+        return sum(wl.fwd_kernel_bytes(i, w.N, w.L) for i in idx_pair) / 2
+    if kind == "bwd_bias_partial":
+        return 4.0 * w.B * w.L
+    return None
+
+
+def load_traffic(workload_name: str, kind: str):
+    """HBM bytes per launch from the committed rocprofv3 PMC summary, if any."""
+    path = os.path.join(ROOT, "profiles", f"traffic_{kind}_{workload_name}.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        d = json.load(f)
+    return d.get("traffic_bytes_per_launch")
+
+
+def cpu_baseline(w, d, seconds: float) -> dict:
+    import numpy as np
+    import torch
+
+    from oracle.torch_cpu_ft import CpuFtStep
+
+    threads = len(os.sched_getaffinity(0))
+    env_threads = os.environ.get("OMP_NUM_THREADS")
+    if env_threads and env_threads.isdigit():
+        threads = min(threads, int(env_threads))
+    torch.set_num_threads(threads)
+    Bs = min(w.B, 4096)
+    step = CpuFtStep(d["idx_w"][:Bs], d["idx_b"][:Bs], d["W"], d["bias"], d["g_w"][:Bs], d["g_b"][:Bs])
+    step()  # warm-up
+    n, t0 = 0, time.perf_counter()
+    while True:
+        step()
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or n >= 200:
+            break
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    del np
+    return {
+        "value": Bs * n / el,
+        "unit": "positions/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{n} fwd+bwd steps of both perspectives on the first {Bs} positions of {w.name} "
+                  f"(N={w.N}, L={w.L}), torch {torch.__version__} embedding_bag on {threads} threads, "
+                  f"{el:.1f} s; cpu: {model}",
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", type=int, default=1)
+    ap.add_argument("--bwd", choices=["sorted", "atomic"], default="sorted")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
+              "(this build runs the FT on a single MI355X).", file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+
+    from sft_amd import _native, workloads
+    from src.model.modules.feature_transformer import SparseLinearFunction
+    from src.model.modules.feature_transformer import kernel as ftk
+
+    w = workloads.WORKLOADS[args.workload]
+    if w.quantized:
+        print("the int16 workload is forward-only; use tests or --workload 0..3", file=sys.stderr)
+        return 2
+    dev = torch.device("cuda:0")
+    _native.lib()  # fail loudly if the library is missing
+    log(f"[bench] generating {w.name}: B={w.B} N={w.N} K={w.K} active U[{w.lo},{w.hi}] L={w.L}")
+    d = workloads.make_fp32_inputs(w)
+    iw = torch.from_numpy(d["idx_w"]).to(dev)
+    ib = torch.from_numpy(d["idx_b"]).to(dev)
+    W = torch.from_numpy(d["W"]).to(dev).requires_grad_(True)
+    b = torch.from_numpy(d["bias"]).to(dev).requires_grad_(True)
+    gw = torch.from_numpy(d["g_w"]).to(dev)
+    gb = torch.from_numpy(d["g_b"]).to(dev)
+
+    if args.bwd == "atomic":
+        orig = ftk._BackwardKernel.__call__
+
+        def atomic_call(self, *a, **k):
+            k["atomic"] = True
+            return orig(self, *a, **k)
+
+        ftk._BackwardKernel.__call__ = atomic_call
+
+    def step():
+        W.grad = None
+        b.grad = None
+        ow = SparseLinearFunction.apply(iw, W, b)
+        ob = SparseLinearFunction.apply(ib, W, b)
+        torch.autograd.backward([ow, ob], [gw, gb])
+
+    log(f"[bench] warmup {args.warmup} steps")
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    _native.prof_enable(True)
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record()
+    for _ in range(args.steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = e0.elapsed_time(e1) / args.steps
+    prof = _native.prof_collect()
+    _native.prof_enable(False)
+    log(f"[bench] timed {args.steps} steps: {ms:.3f} ms/step (wall {wall * 1e3 / args.steps:.3f} ms/step)")
+
+    step_bytes = workloads.step_bytes(d["idx_w"], d["idx_b"], w.N, w.L)
+    kern = {}
+    for kind, (tot, cnt) in prof.items():
+        avg = tot / cnt
+        kb = kernel_bytes(kind, w, (d["idx_w"], d["idx_b"]))
+        kern[kind] = {"avg_ms": avg, "launches_per_step": cnt / args.steps,
+                      "gbs": (kb / (avg * 1e-3) / 1e9) if kb else None}
+        log(f"[bench]   {kind:22s} {avg:8.4f} ms x {cnt / args.steps:.0f}/step"
+            + (f"  {kern[kind]['gbs']:8.1f} GB/s algorithmic" if kb else ""))
+    dom = max(prof, key=lambda k: prof[k][0])
+    dom_avg = prof[dom][0] / prof[dom][1]
+    dom_bytes = kernel_bytes(dom, w, (d["idx_w"], d["idx_b"]))
+    achieved = dom_bytes / (dom_avg * 1e-3) / 1e9
+    traffic = load_traffic(w.name, dom)
+
+    result = {
+        "metric": METRIC,
+        "value": w.B / (ms * 1e-3),
+        "unit": "positions/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic",
+        "config": {
+            "workload": w.name, "feature_set": w.feature_set, "batch": w.B, "num_inputs": w.N,
+            "max_active": w.K, "active": [w.lo, w.hi], "output_size": w.L, "bwd": args.bwd,
+            "parallelism": "single-gpu",
+            "input_sha256": {k: workloads.sha256(v) for k, v in d.items()},
+        },
+        "step_bytes": step_bytes,
+        "step_gbs": step_bytes / (ms * 1e-3) / 1e9,
+        "step_frac_of_hbm_peak": step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+        "roofline": {
+            "kernel": dom,
+            "bound": "hbm",
+            "achieved": achieved,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": achieved / HBM_PEAK_GBS,
+            "traffic": traffic,
+            "algorithmic_bytes_per_launch": dom_bytes,
+            "avg_launch_ms": dom_avg,
+        },
+        "kernels": kern,
+    }
+    if not args.no_cpu:
+        log(f"[bench] cpu baseline ({args.cpu_seconds:.0f} s budget)")
+        result["cpu_baseline"] = cpu_baseline(w, d, args.cpu_seconds)
+        result["gpu_over_cpu"] = result["value"] / result["cpu_baseline"]["value"]
+    else:
+        result["cpu_baseline"] = None
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,136 @@
+/*
+ * sft_ft.h -- C ABI of the MI355X (gfx950) sparse feature-transformer library
+ * (libsft_ft.so).
+ *
+ * The library replaces the two TileLang kernels and their loader behind the
+ * reference's SparseLinearFunction (rgodha24/stockfish-trainer,
+ * src/model/modules/feature_transformer/, abbreviated FT/ below) and adds the
+ * int16 quantized inference forward.
+ *
+ * Conventions shared by every entry point:
+ *   - All tensor pointers are device pointers (hipMalloc / torch CUDA tensors),
+ *     dense row-major.  Scalars are passed by value.  `stream` is a hipStream_t
+ *     passed as void* (NULL = the null stream); all work is enqueued on it, in
+ *     stream order, with no host synchronisation and no device allocation.
+ *   - idx is int32 [batch, max_active]; -1 marks an inactive slot anywhere in a
+ *     row (FT/kernel.py:97-98).  Values outside [0, num_inputs) other than -1
+ *     (undefined behaviour in the reference) are treated as inactive, so a bad
+ *     index can never address memory outside the tables.
+ *   - Return value: SFT_OK (0) or a negative SFT_E* code.  Arguments are
+ *     validated on the host before anything is launched; on error nothing is
+ *     enqueued and sft_last_error() returns a message (thread-local).
+ *   - Entry points are reentrant and may be called from any host thread.
+ */
+#ifndef SFT_FT_H
+#define SFT_FT_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SFT_ABI_VERSION 1
+
+#define SFT_OK 0
+#define SFT_EINVAL (-1)     /* null pointer, size or range out of bounds        */
+#define SFT_EWORKSPACE (-2) /* workspace missing or smaller than required       */
+#define SFT_EHIP (-3)       /* HIP runtime error while enqueueing               */
+#define SFT_EUNSUPPORTED (-4)
+
+/* sft_ft_bwd_f32 flags */
+#define SFT_BWD_ACCUMULATE 0x0u /* dW[f] += ..., db += ...  (reference semantics)  */
+#define SFT_BWD_OVERWRITE 0x1u  /* every row of dW and all of db are written      */
+#define SFT_BWD_SORTED 0x00u    /* stable sort by feature + per-feature row sum;
+                                   deterministic, reference summation order     */
+#define SFT_BWD_ATOMIC 0x10u    /* position-major scatter with fp32 atomics;
+                                   order of the adds is not deterministic       */
+
+/* sft_ft_fwd_i16 flags */
+#define SFT_Q16_ACC32 0x0u  /* exact int32 accumulation, then clamp            */
+#define SFT_Q16_WRAP16 0x1u /* int16 accumulator with wrapping adds, then clamp */
+
+/* Version of this ABI (SFT_ABI_VERSION of the header the library was built with). */
+int sft_abi_version(void);
+
+/* Message for the last non-zero return on the calling thread ("" if none). */
+const char *sft_last_error(void);
+
+/*
+ * fp32 forward: out[b, c] = bias[c] + sum_{k active} weight[idx[b, k], c],
+ * added bias first then k ascending in binary32 (the reference order).
+ * Overwrites out [batch, output_size].
+ * Replaces make_sparse_input_linear_forward_kernel(K, L)(idx, W, b, out)
+ * (FT/kernel.py:301-312) and the TileLang kernel it runs (FT/kernel.py:66-105).
+ */
+int sft_ft_fwd_f32(const int32_t *idx, int64_t batch, int32_t max_active, const float *weight,
+                   int64_t num_inputs, int32_t output_size, const float *bias, float *out,
+                   void *stream);
+
+/*
+ * Bytes of device workspace sft_ft_bwd_f32 needs for these sizes and flags.
+ * May query the current device (sort tuning is per architecture).
+ * No reference counterpart: the reference takes its temporaries from torch
+ * inside the call (FT/kernel.py:108-138).
+ */
+int sft_ft_bwd_f32_workspace_size(int64_t batch, int32_t max_active, int64_t num_inputs,
+                                  int32_t output_size, uint32_t flags, size_t *bytes);
+
+/*
+ * fp32 backward:
+ *   weight_grad[f, :] (+)= sum over slots (b, k) with idx[b, k] == f of grad_out[b, :]
+ *   bias_grad[:]      (+)= sum_b grad_out[b, :]
+ * With SFT_BWD_ACCUMULATE (reference semantics, FT/kernel.py:183-186,269) rows of
+ * features that do not occur are left untouched; with SFT_BWD_OVERWRITE they are
+ * zeroed, so the caller needs no zero-fill.
+ * workspace must hold sft_ft_bwd_f32_workspace_size(...) bytes (256-byte aligned).
+ * Replaces make_sparse_input_linear_backward_kernel(K, L)(idx, dW, db, grad_out)
+ * (FT/kernel.py:315-319, 255-283) with its prep (FT/kernel.py:108-138) and
+ * TileLang kernel (FT/kernel.py:141-188).
+ */
+int sft_ft_bwd_f32(const int32_t *idx, int64_t batch, int32_t max_active, const float *grad_out,
+                   int64_t num_inputs, int32_t output_size, float *weight_grad, float *bias_grad,
+                   void *workspace, size_t workspace_bytes, uint32_t flags, void *stream);
+
+/*
+ * int16 quantized inference forward (no reference counterpart: the reference's
+ * int16 inference lives in its empty `stockfish` submodule; the weights come
+ * from the export scaling of src/model/quantize.py:76-93):
+ *   acc[b, c]      = bias[c] + sum_{k active} weight[idx[b, k], c]     (int32, exact)
+ *   out[b, c]      = clamp(flags & SFT_Q16_WRAP16 ? (int16)acc : acc, clip_lo, clip_hi)
+ *   psqt_out[b, p] = sum_{k active} psqt_weight[idx[b, k], p]         (int32)
+ * psqt_weight/psqt_out may both be NULL (psqt_size ignored).
+ * Requires max_active < 65536 so the int32 sum cannot overflow.
+ */
+int sft_ft_fwd_i16(const int32_t *idx, int64_t batch, int32_t max_active, const int16_t *weight,
+                   int64_t num_inputs, int32_t output_size, const int16_t *bias,
+                   const int32_t *psqt_weight, int32_t psqt_size, int16_t *out,
+                   int32_t *psqt_out, int32_t clip_lo, int32_t clip_hi, uint32_t flags,
+                   void *stream);
+
+/*
+ * Export quantization on the device (src/model/quantize.py:83-84):
+ * out[i] = round_half_even(float32(x[i] * scale)) saturated to int16.
+ * No reference counterpart as a kernel (the reference runs it as torch ops).
+ */
+int sft_quantize_i16(const float *x, int64_t n, float scale, int16_t *out, void *stream);
+
+/*
+ * Kernel timing over a measured region (no reference counterpart).  While
+ * enabled, every launch made by the entry points above is bracketed by a pair
+ * of HIP events on its stream.  sft_prof_collect() waits for the recorded
+ * events, adds each launch's duration into total_ms[kind] / launches[kind]
+ * (arrays of n_kinds entries, kinds numbered as sft_prof_kind_name) and forgets
+ * them.  Enabling or disabling also forgets pending events.
+ */
+int sft_prof_enable(int on);
+int sft_prof_num_kinds(void);
+const char *sft_prof_kind_name(int kind);
+int sft_prof_collect(double *total_ms, int64_t *launches, int n_kinds);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SFT_FT_H */

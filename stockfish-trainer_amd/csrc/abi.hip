@@ -1,0 +1,249 @@
+// C ABI entry points of libsft_ft.so: host-side validation, dispatch, error
+// reporting and the optional per-launch event timing.
+#include <atomic>
+#include <climits>
+#include <mutex>
+#include <vector>
+
+#include "common.h"
+
+namespace sft {
+
+int fwd_f32(const int32_t *idx, int64_t B, int K, const float *W, int64_t N, int L, const float *bias, float *out,
+            hipStream_t s);
+int fwd_i16(const int32_t *idx, int64_t B, int K, const int16_t *W, int64_t N, int L, const int16_t *bias,
+            const int32_t *psqt, int P, int16_t *out, int32_t *psqt_out, int lo, int hi, int wrap16, hipStream_t s);
+int quantize_i16(const float *x, int64_t n, float scale, int16_t *out, hipStream_t s);
+int bwd_workspace(int64_t B, int K, int64_t N, int L, uint32_t flags, size_t *bytes);
+int bwd_f32(const int32_t *idx, int64_t B, int K, const float *grad, int64_t N, int L, float *dW, float *db,
+            void *ws, size_t ws_bytes, uint32_t flags, hipStream_t s);
+
+namespace {
+thread_local std::string t_error;
+}
+
+const char *error_cstr() { return t_error.c_str(); }
+void set_error(const std::string &msg) { t_error = msg; }
+void clear_error() { t_error.clear(); }
+int fail(int code, const std::string &msg) {
+  t_error = msg;
+  return code;
+}
+int check_launch(const char *what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(SFT_EHIP, std::string(what) + ": " + hipGetErrorString(e));
+  return SFT_OK;
+}
+
+Mapping choose_mapping(int64_t chunks, int min_group) {
+  // Largest lane group whose single-slab lane use is >= 75%; otherwise the
+  // single-slab mapping with the best lane use; rows too wide for one slab
+  // use G = 64 and as few slabs as possible.
+  static const int groups[4] = {64, 32, 16, 8};
+  Mapping best{64, kMaxCpl, (int)ceil_div(chunks, (int64_t)kWave * kMaxCpl)};
+  if (chunks > (int64_t)kWave * kMaxCpl) {
+    best.cpl = (int)ceil_div(chunks, (int64_t)kWave * best.slabs);
+    return best;
+  }
+  double best_eff = -1.0;
+  for (int G : groups) {
+    if (G < min_group) continue;
+    const int64_t cpl = ceil_div(chunks, G);
+    if (cpl > kMaxCpl) continue;
+    const double eff = (double)chunks / (double)(G * cpl);
+    if (eff >= 0.75) return Mapping{G, (int)cpl, 1};
+    if (eff > best_eff) {
+      best_eff = eff;
+      best = Mapping{G, (int)cpl, 1};
+    }
+  }
+  return best;
+}
+
+// ------------------------------------------------------------ profiling ----
+namespace {
+struct PendingLaunch {
+  hipEvent_t start, stop;
+  int kind;
+};
+std::atomic<bool> g_prof_on{false};
+std::mutex g_prof_mu;
+std::vector<PendingLaunch> g_pending;
+std::vector<hipEvent_t> g_event_pool;
+
+hipEvent_t take_event() {
+  if (!g_event_pool.empty()) {
+    hipEvent_t e = g_event_pool.back();
+    g_event_pool.pop_back();
+    return e;
+  }
+  hipEvent_t e = nullptr;
+  if (hipEventCreate(&e) != hipSuccess) return nullptr;
+  return e;
+}
+
+void drop_pending_locked() {
+  for (auto &p : g_pending) {
+    g_event_pool.push_back(p.start);
+    g_event_pool.push_back(p.stop);
+  }
+  g_pending.clear();
+}
+
+struct ActiveScope {
+  hipEvent_t start, stop;
+  int kind;
+  hipStream_t stream;
+};
+
+const char *const kKindNames[kProfNumKinds] = {
+    "fwd_f32_gather",   "bwd_feature_sort",  "bwd_segment_offsets", "bwd_feature_gather", "bwd_bias_partial",
+    "bwd_bias_final",   "bwd_atomic_scatter", "bwd_zero_fill",      "fwd_i16_gather",     "quantize_i16",
+};
+}  // namespace
+
+ProfScope::ProfScope(int kind, hipStream_t stream) : slot_(nullptr) {
+  if (!g_prof_on.load(std::memory_order_relaxed)) return;
+  std::lock_guard<std::mutex> lock(g_prof_mu);
+  hipEvent_t a = take_event(), b = take_event();
+  if (!a || !b) return;
+  if (hipEventRecord(a, stream) != hipSuccess) return;
+  slot_ = new ActiveScope{a, b, kind, stream};
+}
+
+ProfScope::~ProfScope() {
+  if (!slot_) return;
+  ActiveScope *sc = static_cast<ActiveScope *>(slot_);
+  std::lock_guard<std::mutex> lock(g_prof_mu);
+  if (hipEventRecord(sc->stop, sc->stream) == hipSuccess) g_pending.push_back(PendingLaunch{sc->start, sc->stop, sc->kind});
+  delete sc;
+}
+
+}  // namespace sft
+
+using namespace sft;
+
+namespace {
+
+bool bad_sizes(int64_t B, int32_t K, int64_t N, int32_t L, std::string &why) {
+  if (B < 0) why = "batch must be >= 0";
+  else if (K <= 0) why = "max_active must be > 0";
+  else if (N <= 0 || N >= INT32_MAX) why = "num_inputs must be in [1, 2^31-1)";
+  else if (L <= 0) why = "output_size must be > 0";
+  else if (B * (int64_t)K >= INT32_MAX) why = "batch * max_active must be < 2^31-1";
+  else if ((int64_t)N * L >= ((int64_t)1 << 40) || B * (int64_t)L >= ((int64_t)1 << 40)) why = "tensor too large";
+  else return false;
+  return true;
+}
+
+}  // namespace
+
+extern "C" {
+
+int sft_abi_version(void) { return SFT_ABI_VERSION; }
+
+const char *sft_last_error(void) { return error_cstr(); }
+
+int sft_ft_fwd_f32(const int32_t *idx, int64_t batch, int32_t max_active, const float *weight, int64_t num_inputs,
+                   int32_t output_size, const float *bias, float *out, void *stream) {
+  clear_error();
+  std::string why;
+  if (bad_sizes(batch, max_active, num_inputs, output_size, why)) return fail(SFT_EINVAL, "sft_ft_fwd_f32: " + why);
+  if (!weight || !bias || (batch > 0 && (!idx || !out))) return fail(SFT_EINVAL, "sft_ft_fwd_f32: null pointer");
+  if (batch == 0) return SFT_OK;
+  return fwd_f32(idx, batch, max_active, weight, num_inputs, output_size, bias, out, (hipStream_t)stream);
+}
+
+int sft_ft_bwd_f32_workspace_size(int64_t batch, int32_t max_active, int64_t num_inputs, int32_t output_size,
+                                  uint32_t flags, size_t *bytes) {
+  clear_error();
+  std::string why;
+  if (!bytes) return fail(SFT_EINVAL, "sft_ft_bwd_f32_workspace_size: null pointer");
+  if (bad_sizes(batch, max_active, num_inputs, output_size, why))
+    return fail(SFT_EINVAL, "sft_ft_bwd_f32_workspace_size: " + why);
+  if (flags & ~(SFT_BWD_OVERWRITE | SFT_BWD_ATOMIC))
+    return fail(SFT_EINVAL, "sft_ft_bwd_f32_workspace_size: unknown flags");
+  return bwd_workspace(batch, max_active, num_inputs, output_size, flags, bytes);
+}
+
+int sft_ft_bwd_f32(const int32_t *idx, int64_t batch, int32_t max_active, const float *grad_out, int64_t num_inputs,
+                   int32_t output_size, float *weight_grad, float *bias_grad, void *workspace, size_t workspace_bytes,
+                   uint32_t flags, void *stream) {
+  clear_error();
+  std::string why;
+  if (bad_sizes(batch, max_active, num_inputs, output_size, why)) return fail(SFT_EINVAL, "sft_ft_bwd_f32: " + why);
+  if (!weight_grad || !bias_grad || (batch > 0 && (!idx || !grad_out)))
+    return fail(SFT_EINVAL, "sft_ft_bwd_f32: null pointer");
+  if (flags & ~(SFT_BWD_OVERWRITE | SFT_BWD_ATOMIC)) return fail(SFT_EINVAL, "sft_ft_bwd_f32: unknown flags");
+  return bwd_f32(idx, batch, max_active, grad_out, num_inputs, output_size, weight_grad, bias_grad, workspace,
+                 workspace_bytes, flags, (hipStream_t)stream);
+}
+
+int sft_ft_fwd_i16(const int32_t *idx, int64_t batch, int32_t max_active, const int16_t *weight, int64_t num_inputs,
+                   int32_t output_size, const int16_t *bias, const int32_t *psqt_weight, int32_t psqt_size,
+                   int16_t *out, int32_t *psqt_out, int32_t clip_lo, int32_t clip_hi, uint32_t flags, void *stream) {
+  clear_error();
+  std::string why;
+  if (bad_sizes(batch, max_active, num_inputs, output_size, why)) return fail(SFT_EINVAL, "sft_ft_fwd_i16: " + why);
+  if (max_active >= 65536) return fail(SFT_EINVAL, "sft_ft_fwd_i16: max_active must be < 65536");
+  if (!weight || !bias || (batch > 0 && (!idx || !out))) return fail(SFT_EINVAL, "sft_ft_fwd_i16: null pointer");
+  if ((psqt_weight == nullptr) != (psqt_out == nullptr))
+    return fail(SFT_EINVAL, "sft_ft_fwd_i16: psqt_weight and psqt_out must both be set or both be NULL");
+  if (psqt_weight && (psqt_size <= 0 || psqt_size > kWave))
+    return fail(SFT_EINVAL, "sft_ft_fwd_i16: psqt_size must be in [1, 64]");
+  if (clip_lo > clip_hi || clip_lo < -32768 || clip_hi > 32767)
+    return fail(SFT_EINVAL, "sft_ft_fwd_i16: need -32768 <= clip_lo <= clip_hi <= 32767");
+  if (flags & ~SFT_Q16_WRAP16) return fail(SFT_EINVAL, "sft_ft_fwd_i16: unknown flags");
+  if (batch == 0) return SFT_OK;
+  return fwd_i16(idx, batch, max_active, weight, num_inputs, output_size, bias, psqt_weight,
+                 psqt_weight ? psqt_size : 0, out, psqt_out, clip_lo, clip_hi, (flags & SFT_Q16_WRAP16) ? 1 : 0,
+                 (hipStream_t)stream);
+}
+
+int sft_quantize_i16(const float *x, int64_t n, float scale, int16_t *out, void *stream) {
+  clear_error();
+  if (n < 0) return fail(SFT_EINVAL, "sft_quantize_i16: n must be >= 0");
+  if (n > 0 && (!x || !out)) return fail(SFT_EINVAL, "sft_quantize_i16: null pointer");
+  return quantize_i16(x, n, scale, out, (hipStream_t)stream);
+}
+
+int sft_prof_enable(int on) {
+  clear_error();
+  std::lock_guard<std::mutex> lock(g_prof_mu);
+  drop_pending_locked();
+  g_prof_on.store(on != 0);
+  return SFT_OK;
+}
+
+int sft_prof_num_kinds(void) { return kProfNumKinds; }
+
+const char *sft_prof_kind_name(int kind) {
+  if (kind < 0 || kind >= kProfNumKinds) return "";
+  return kKindNames[kind];
+}
+
+int sft_prof_collect(double *total_ms, int64_t *launches, int n_kinds) {
+  clear_error();
+  if (!total_ms || !launches || n_kinds < 0) return fail(SFT_EINVAL, "sft_prof_collect: bad arguments");
+  std::lock_guard<std::mutex> lock(g_prof_mu);
+  int rc = SFT_OK;
+  for (auto &p : g_pending) {
+    if (hipEventSynchronize(p.stop) != hipSuccess) {
+      rc = fail(SFT_EHIP, "sft_prof_collect: event wait failed");
+      continue;
+    }
+    float ms = 0.0f;
+    if (hipEventElapsedTime(&ms, p.start, p.stop) != hipSuccess) {
+      rc = fail(SFT_EHIP, "sft_prof_collect: elapsed time failed");
+      continue;
+    }
+    if (p.kind < n_kinds) {
+      total_ms[p.kind] += ms;
+      launches[p.kind] += 1;
+    }
+  }
+  drop_pending_locked();
+  return rc;
+}
+
+}  // extern "C"

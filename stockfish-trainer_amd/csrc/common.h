@@ -1,0 +1,104 @@
+// Shared definitions of the gfx950 FT kernels and their host launchers.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <string>
+
+#include "sft_ft.h"
+
+namespace sft {
+
+// Native clang vectors: elementwise +, 16-byte loads/stores (global_load_dwordx4).
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef short i16x8 __attribute__((ext_vector_type(8)));
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+
+constexpr int kWave = 64;          // CDNA wavefront width
+constexpr int kWavesPerBlock = 4;  // 256-thread workgroups
+constexpr int kBlock = kWave * kWavesPerBlock;
+constexpr int kMaxCpl = 8;         // max vector chunks per lane per pass
+constexpr size_t kMaxIndexLds = 64 * 1024;  // LDS budget of the per-block index lists
+
+// ---- host-side error plumbing (thread-local, read by sft_last_error) ----
+void set_error(const std::string &msg);
+void clear_error();
+int fail(int code, const std::string &msg);
+int check_launch(const char *what);
+
+// ---- kernel timing hooks (active only between sft_prof_enable(1) and (0)) ----
+enum ProfKind : int {
+  kProfFwdF32 = 0,
+  kProfBwdSort,
+  kProfBwdOffsets,
+  kProfBwdGather,
+  kProfBwdBiasPartial,
+  kProfBwdBiasFinal,
+  kProfBwdAtomic,
+  kProfBwdZero,
+  kProfFwdI16,
+  kProfQuantize,
+  kProfNumKinds
+};
+struct ProfScope {
+  ProfScope(int kind, hipStream_t stream);
+  ~ProfScope();
+  void *slot_;
+};
+
+// ---- lane/position mapping shared by the row-gather kernels ----
+// A lane group of G lanes (G in {8,16,32,64}) owns one row (a position in the
+// forward, a feature in the backward).  Lane t of the group handles vector
+// chunks c = slab*G*CPL + t + G*j, j < CPL, so consecutive lanes read
+// consecutive 16-byte chunks.  Rows wider than G*CPL chunks use several
+// column slabs (grid.y).
+struct Mapping {
+  int G;
+  int cpl;
+  int slabs;
+};
+Mapping choose_mapping(int64_t chunks, int min_group = 8);
+
+// ---- device helpers ----
+__device__ __forceinline__ int lane_id() { return __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0)); }
+
+// Number of set bits of `mask` in lanes below the calling lane.
+__device__ __forceinline__ int popc_below(uint64_t mask) {
+  return __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0));
+}
+
+__device__ __forceinline__ uint64_t ballot(bool p) { return __builtin_amdgcn_ballot_w64(p); }
+
+__device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+// Compacts the active slots of `npos` consecutive index rows (row p at
+// idx + (pos0 + p) * K) into list[p * kpad + 0 .. count[p]), keeping slot order.
+// Called by one whole wave; rows at or past B get count 0.  A slot is active
+// when 0 <= v < N.  The wave owns list/count; callers barrier before reading.
+__device__ __forceinline__ void compact_rows(const int32_t *__restrict__ idx, int64_t B, int K, int N,
+                                             int64_t pos0, int npos, int *list, int kpad, int *count) {
+  const int lane = lane_id();
+  for (int p = 0; p < npos; ++p) {
+    const int64_t pos = pos0 + p;
+    int base = 0;
+    if (pos < B) {
+      const int32_t *row = idx + pos * (int64_t)K;
+      for (int k0 = 0; k0 < K; k0 += kWave) {
+        const int k = k0 + lane;
+        int v = -1;
+        if (k < K) v = row[k];
+        const bool ok = (unsigned)v < (unsigned)N;
+        const uint64_t m = ballot(ok);
+        if (ok) list[p * kpad + base + popc_below(m)] = v;
+        base += __popcll(m);
+      }
+    }
+    if (lane == 0) count[p] = base;
+  }
+}
+
+__host__ __device__ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+__host__ __device__ inline int round_up4(int v) { return (v + 3) & ~3; }
+
+}  // namespace sft

@@ -1,0 +1,337 @@
+// Sparse FT forward kernels for gfx950: fp32 gather-sum and int16 quantized
+// gather-sum.
+//
+// Mapping (see Mapping in common.h): a 256-thread workgroup is 4 waves; each
+// wave serves 64/G positions, one lane group of G lanes per position.  The wave
+// first compacts its positions' index rows into LDS (active slots only, slot
+// order kept), then every lane accumulates its 16-byte column chunks over the
+// compacted list, U rows at a time: the U*CPL row loads of a step are issued
+// before any add, then the adds run in slot order.  For G == 64 the index is
+// wave-uniform and is moved to an SGPR, so the row base address is scalar.
+//
+// fp32: acc = bias, then acc += W[idx[k]] for active k ascending; every add is
+// a binary32 add in the reference order (FT/kernel.py:93-100), so the result
+// is bit-identical to that order.
+// int16: exact int32 accumulation (order-free), optional wrap to int16, clamp.
+#include <algorithm>
+
+#include "common.h"
+
+namespace sft {
+
+namespace {
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+template <typename T>
+__device__ __forceinline__ T zero_of() {
+  return T(0);
+}
+
+// Reads compacted slots k..k+3 of a list (kpad is a multiple of 4 and k % 4 == 0).
+__device__ __forceinline__ i32x4 read4(const int *list, int k) { return *reinterpret_cast<const i32x4 *>(list + k); }
+
+// Wave-wide min and max of a value that is constant within each lane group.
+template <int G>
+__device__ __forceinline__ void group_minmax(int v, int &vmin, int &vmax) {
+  vmin = v;
+  vmax = v;
+#pragma unroll
+  for (int off = G; off < kWave; off <<= 1) {
+    vmin = min(vmin, __shfl_xor(vmin, off));
+    vmax = max(vmax, __shfl_xor(vmax, off));
+  }
+  vmin = uniform(vmin);
+  vmax = uniform(vmax);
+}
+
+// ------------------------------------------------------------------ fp32 ----
+template <typename T, int G, int CPL, int U>
+__global__ __launch_bounds__(kBlock) void fwd_f32_kernel(const int32_t *__restrict__ idx, int64_t B, int K, int N,
+                                                         const T *__restrict__ W, int64_t cols,
+                                                         const T *__restrict__ bias, T *__restrict__ out, int kpad) {
+  static_assert(U == 4, "index reads are 4-wide");
+  constexpr int PPW = kWave / G;
+  extern __shared__ int smem[];
+  const int wave = uniform(threadIdx.x / kWave);
+  const int lane = threadIdx.x % kWave;
+  int *list = smem + wave * PPW * kpad;
+  int *count = smem + kWavesPerBlock * PPW * kpad + wave * PPW;
+  const int64_t pos0 = ((int64_t)blockIdx.x * kWavesPerBlock + wave) * PPW;
+  compact_rows(idx, B, K, N, pos0, PPW, list, kpad, count);
+  __syncthreads();
+
+  const int g = lane / G, t = lane % G;
+  const int64_t pos = pos0 + g;
+  const int n = count[g];
+  int nmin, nmax;
+  group_minmax<G>(n, nmin, nmax);
+  const int *mylist = list + g * kpad;
+
+  const int64_t c0 = (int64_t)blockIdx.y * (G * CPL) + t;
+  bool colok[CPL];
+  T acc[CPL];
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) {
+    colok[j] = (c0 + G * j) < cols;
+    acc[j] = colok[j] ? bias[c0 + G * j] : zero_of<T>();
+  }
+
+  int k = 0;
+  for (; k + U <= nmin; k += U) {
+    i32x4 f4 = read4(mylist, k);
+    T w[U][CPL];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      int f = f4[u];
+      if (G == kWave) f = uniform(f);
+      const T *row = W + (int64_t)f * cols + c0;
+#pragma unroll
+      for (int j = 0; j < CPL; ++j)
+        if (colok[j]) w[u][j] = row[G * j];
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int j = 0; j < CPL; ++j)
+        if (colok[j]) acc[j] += w[u][j];
+  }
+  for (; k < nmax; k += U) {
+    i32x4 f4 = read4(mylist, k);
+    T w[U][CPL];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const bool v = k + u < n;
+      int f = v ? f4[u] : 0;
+      if (G == kWave) f = uniform(f);
+      const T *row = W + (int64_t)f * cols + c0;
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) {
+        w[u][j] = zero_of<T>();
+        if (v && colok[j]) w[u][j] = row[G * j];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const bool v = k + u < n;
+#pragma unroll
+      for (int j = 0; j < CPL; ++j)
+        if (v && colok[j]) acc[j] += w[u][j];
+    }
+  }
+
+  if (pos < B) {
+    T *o = out + pos * cols + c0;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j)
+      if (colok[j]) __builtin_nontemporal_store(acc[j], o + G * j);
+  }
+}
+
+// ----------------------------------------------------------------- int16 ----
+template <typename T>
+struct Q16;
+template <>
+struct Q16<i16x8> {
+  typedef i32x8 Acc;
+  static __device__ __forceinline__ Acc widen(i16x8 v) { return __builtin_convertvector(v, i32x8); }
+  static __device__ __forceinline__ i16x8 finish(Acc a, int lo, int hi, int wrap16) {
+    if (wrap16) a = __builtin_convertvector(__builtin_convertvector(a, i16x8), i32x8);  // low 16 bits, sign-extended
+    a = a < lo ? (Acc)lo : a;
+    a = a > hi ? (Acc)hi : a;
+    return __builtin_convertvector(a, i16x8);
+  }
+};
+template <>
+struct Q16<short> {
+  typedef int Acc;
+  static __device__ __forceinline__ Acc widen(short v) { return (int)v; }
+  static __device__ __forceinline__ short finish(Acc a, int lo, int hi, int wrap16) {
+    if (wrap16) a = (int)(short)(unsigned short)(unsigned)a;
+    a = a < lo ? lo : a;
+    a = a > hi ? hi : a;
+    return (short)a;
+  }
+};
+
+template <typename T, int G, int CPL, int U>
+__global__ __launch_bounds__(kBlock) void fwd_i16_kernel(const int32_t *__restrict__ idx, int64_t B, int K, int N,
+                                                         const T *__restrict__ W, int64_t cols,
+                                                         const T *__restrict__ bias,
+                                                         const int32_t *__restrict__ psqt, int P,
+                                                         T *__restrict__ out, int32_t *__restrict__ psqt_out,
+                                                         int clip_lo, int clip_hi, int wrap16, int kpad) {
+  static_assert(U == 4, "index reads are 4-wide");
+  typedef typename Q16<T>::Acc Acc;
+  constexpr int PPW = kWave / G;
+  extern __shared__ int smem[];
+  const int wave = uniform(threadIdx.x / kWave);
+  const int lane = threadIdx.x % kWave;
+  int *list = smem + wave * PPW * kpad;
+  int *count = smem + kWavesPerBlock * PPW * kpad + wave * PPW;
+  const int64_t pos0 = ((int64_t)blockIdx.x * kWavesPerBlock + wave) * PPW;
+  compact_rows(idx, B, K, N, pos0, PPW, list, kpad, count);
+  __syncthreads();
+
+  const int g = lane / G, t = lane % G;
+  const int64_t pos = pos0 + g;
+  const int n = count[g];
+  int nmin, nmax;
+  group_minmax<G>(n, nmin, nmax);
+  const int *mylist = list + g * kpad;
+  // PSQT columns: lane t < P of the group, slab 0 only (host guarantees P <= G).
+  const bool do_psqt = psqt != nullptr && blockIdx.y == 0 && t < P;
+  int pacc = 0;
+
+  const int64_t c0 = (int64_t)blockIdx.y * (G * CPL) + t;
+  bool colok[CPL];
+  Acc acc[CPL];
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) {
+    colok[j] = (c0 + G * j) < cols;
+    acc[j] = colok[j] ? Q16<T>::widen(bias[c0 + G * j]) : (Acc)0;
+  }
+
+  for (int k = 0; k < nmax; k += U) {
+    i32x4 f4 = read4(mylist, k);
+    T w[U][CPL];
+    int pw[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const bool v = k + u < n;
+      int f = v ? f4[u] : 0;
+      if (G == kWave) f = uniform(f);
+      const T *row = W + (int64_t)f * cols + c0;
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) {
+        w[u][j] = T(0);
+        if (v && colok[j]) w[u][j] = row[G * j];
+      }
+      pw[u] = 0;
+      if (v && do_psqt) pw[u] = psqt[(int64_t)f * P + t];
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) acc[j] += Q16<T>::widen(w[u][j]);
+      pacc += pw[u];
+    }
+  }
+  (void)nmin;
+
+  if (pos < B) {
+    T *o = out + pos * cols + c0;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j)
+      if (colok[j]) __builtin_nontemporal_store(Q16<T>::finish(acc[j], clip_lo, clip_hi, wrap16), o + G * j);
+    if (do_psqt) psqt_out[pos * P + t] = pacc;
+  }
+}
+
+// --------------------------------------------------------------- quantize ----
+__global__ __launch_bounds__(kBlock) void quantize_i16_kernel(const float *__restrict__ x, int64_t n, float scale,
+                                                              int16_t *__restrict__ out) {
+  for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += (int64_t)gridDim.x * kBlock) {
+    float r = __builtin_rintf(x[i] * scale);  // binary32 product, round half to even
+    r = fminf(fmaxf(r, -32768.0f), 32767.0f);
+    out[i] = (int16_t)r;
+  }
+}
+
+// ------------------------------------------------------------- dispatch ----
+template <typename T, int G, int CPL>
+void launch_fwd_f32(dim3 grid, size_t lds, hipStream_t s, const int32_t *idx, int64_t B, int K, int N, const void *W,
+                    int64_t cols, const void *bias, void *out, int kpad) {
+  hipLaunchKernelGGL((fwd_f32_kernel<T, G, CPL, 4>), grid, dim3(kBlock), lds, s, idx, B, K, N,
+                     static_cast<const T *>(W), cols, static_cast<const T *>(bias), static_cast<T *>(out), kpad);
+}
+
+template <typename T, int G, int CPL>
+void launch_fwd_i16(dim3 grid, size_t lds, hipStream_t s, const int32_t *idx, int64_t B, int K, int N, const void *W,
+                    int64_t cols, const void *bias, const int32_t *psqt, int P, void *out, int32_t *psqt_out, int lo,
+                    int hi, int wrap16, int kpad) {
+  hipLaunchKernelGGL((fwd_i16_kernel<T, G, CPL, 4>), grid, dim3(kBlock), lds, s, idx, B, K, N,
+                     static_cast<const T *>(W), cols, static_cast<const T *>(bias), psqt, P, static_cast<T *>(out),
+                     psqt_out, lo, hi, wrap16, kpad);
+}
+
+#define SFT_CPL_CASES(FN, T, G, ...) \
+  switch (m.cpl) {                   \
+    case 1: FN<T, G, 1>(__VA_ARGS__); break; \
+    case 2: FN<T, G, 2>(__VA_ARGS__); break; \
+    case 3: FN<T, G, 3>(__VA_ARGS__); break; \
+    case 4: FN<T, G, 4>(__VA_ARGS__); break; \
+    case 5: FN<T, G, 5>(__VA_ARGS__); break; \
+    case 6: FN<T, G, 6>(__VA_ARGS__); break; \
+    case 7: FN<T, G, 7>(__VA_ARGS__); break; \
+    default: FN<T, G, 8>(__VA_ARGS__); break; \
+  }
+
+#define SFT_G_CASES(FN, T, ...)                          \
+  switch (m.G) {                                         \
+    case 64: SFT_CPL_CASES(FN, T, 64, __VA_ARGS__) break; \
+    case 32: SFT_CPL_CASES(FN, T, 32, __VA_ARGS__) break; \
+    case 16: SFT_CPL_CASES(FN, T, 16, __VA_ARGS__) break; \
+    default: SFT_CPL_CASES(FN, T, 8, __VA_ARGS__) break;  \
+  }
+
+}  // namespace
+
+size_t index_lds_bytes(int G, int K) {
+  const int ppw = kWave / G;
+  return (size_t)(kWavesPerBlock * ppw * round_up4(K) + kWavesPerBlock * ppw) * sizeof(int);
+}
+
+int fwd_f32(const int32_t *idx, int64_t B, int K, const float *W, int64_t N, int L, const float *bias, float *out,
+            hipStream_t s) {
+  const bool vec = (L % 4 == 0) && ((uintptr_t)W % 16 == 0) && ((uintptr_t)bias % 16 == 0) &&
+                   ((uintptr_t)out % 16 == 0);
+  const int64_t cols = vec ? L / 4 : L;
+  const Mapping m = choose_mapping(cols);
+  const int ppb = kWavesPerBlock * (kWave / m.G);
+  const dim3 grid((unsigned)ceil_div(B, ppb), (unsigned)m.slabs);
+  const size_t lds = index_lds_bytes(m.G, K);
+  if (lds > kMaxIndexLds) return fail(SFT_EUNSUPPORTED, "sft_ft_fwd_f32: max_active too large for the LDS index lists");
+  const int kpad = round_up4(K);
+  ProfScope prof(kProfFwdF32, s);
+  if (vec) {
+    SFT_G_CASES(launch_fwd_f32, f32x4, grid, lds, s, idx, B, K, (int)N, W, cols, bias, out, kpad)
+  } else {
+    SFT_G_CASES(launch_fwd_f32, float, grid, lds, s, idx, B, K, (int)N, W, cols, bias, out, kpad)
+  }
+  return check_launch("sft_ft_fwd_f32");
+}
+
+int fwd_i16(const int32_t *idx, int64_t B, int K, const int16_t *W, int64_t N, int L, const int16_t *bias,
+            const int32_t *psqt, int P, int16_t *out, int32_t *psqt_out, int lo, int hi, int wrap16, hipStream_t s) {
+  const bool vec = (L % 8 == 0) && ((uintptr_t)W % 16 == 0) && ((uintptr_t)bias % 16 == 0) &&
+                   ((uintptr_t)out % 16 == 0);
+  const int64_t cols = vec ? L / 8 : L;
+  int min_group = 8;
+  while (min_group < P) min_group <<= 1;
+  const Mapping m = choose_mapping(cols, min_group);
+  const int ppb = kWavesPerBlock * (kWave / m.G);
+  const dim3 grid((unsigned)ceil_div(B, ppb), (unsigned)m.slabs);
+  const size_t lds = index_lds_bytes(m.G, K);
+  if (lds > kMaxIndexLds) return fail(SFT_EUNSUPPORTED, "sft_ft_fwd_i16: max_active too large for the LDS index lists");
+  const int kpad = round_up4(K);
+  ProfScope prof(kProfFwdI16, s);
+  if (vec) {
+    SFT_G_CASES(launch_fwd_i16, i16x8, grid, lds, s, idx, B, K, (int)N, W, cols, bias, psqt, P, out, psqt_out, lo,
+                hi, wrap16, kpad)
+  } else {
+    SFT_G_CASES(launch_fwd_i16, short, grid, lds, s, idx, B, K, (int)N, W, cols, bias, psqt, P, out, psqt_out, lo,
+                hi, wrap16, kpad)
+  }
+  return check_launch("sft_ft_fwd_i16");
+}
+
+int quantize_i16(const float *x, int64_t n, float scale, int16_t *out, hipStream_t s) {
+  if (n == 0) return SFT_OK;
+  const int64_t blocks = std::min<int64_t>(ceil_div(n, kBlock), 1 << 16);
+  ProfScope prof(kProfQuantize, s);
+  hipLaunchKernelGGL(quantize_i16_kernel, dim3((unsigned)blocks), dim3(kBlock), 0, s, x, n, scale, out);
+  return check_launch("sft_quantize_i16");
+}
+
+}  // namespace sft

@@ -1,0 +1,213 @@
+"""ctypes binding of libsft_ft.so, the C-ABI FT library (include/sft_ft.h).
+
+The functions here take torch CUDA tensors, check dtype/shape/device on the
+host, and pass raw device pointers plus the caller's current HIP stream to the
+library.  There is no CPU or torch fallback: when the library is missing, or a
+tensor is not on a GPU, they raise.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch
+
+PKG_ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_PATH = os.path.join(PKG_ROOT, "lib", "libsft_ft.so")
+
+SFT_OK = 0
+SFT_BWD_ACCUMULATE = 0x0
+SFT_BWD_OVERWRITE = 0x1
+SFT_BWD_SORTED = 0x00
+SFT_BWD_ATOMIC = 0x10
+SFT_Q16_ACC32 = 0x0
+SFT_Q16_WRAP16 = 0x1
+
+_vp = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_i32 = ctypes.c_int32
+_u32 = ctypes.c_uint32
+
+# name -> (restype, argtypes); mirrors include/sft_ft.h
+SIGNATURES = {
+    "sft_abi_version": (ctypes.c_int, []),
+    "sft_last_error": (ctypes.c_char_p, []),
+    "sft_ft_fwd_f32": (ctypes.c_int, [_vp, _i64, _i32, _vp, _i64, _i32, _vp, _vp, _vp]),
+    "sft_ft_bwd_f32_workspace_size": (
+        ctypes.c_int, [_i64, _i32, _i64, _i32, _u32, ctypes.POINTER(ctypes.c_size_t)]),
+    "sft_ft_bwd_f32": (
+        ctypes.c_int, [_vp, _i64, _i32, _vp, _i64, _i32, _vp, _vp, _vp, ctypes.c_size_t, _u32, _vp]),
+    "sft_ft_fwd_i16": (
+        ctypes.c_int,
+        [_vp, _i64, _i32, _vp, _i64, _i32, _vp, _vp, _i32, _vp, _vp, _i32, _i32, _u32, _vp]),
+    "sft_quantize_i16": (ctypes.c_int, [_vp, _i64, ctypes.c_float, _vp, _vp]),
+    "sft_prof_enable": (ctypes.c_int, [ctypes.c_int]),
+    "sft_prof_num_kinds": (ctypes.c_int, []),
+    "sft_prof_kind_name": (ctypes.c_char_p, [ctypes.c_int]),
+    "sft_prof_collect": (
+        ctypes.c_int, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int64), ctypes.c_int]),
+}
+
+_lib = None
+_lock = threading.Lock()
+
+
+class NativeLibraryMissing(RuntimeError):
+    pass
+
+
+def lib() -> ctypes.CDLL:
+    """Load libsft_ft.so once; raise if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not os.path.exists(LIB_PATH):
+                raise NativeLibraryMissing(
+                    f"{LIB_PATH} not found: build it with `python -c 'import __graft_entry__ as g; g.build()'` "
+                    "or `make -C stockfish-trainer_amd/csrc`")
+            handle = ctypes.CDLL(LIB_PATH)
+            for name, (res, args) in SIGNATURES.items():
+                fn = getattr(handle, name)
+                fn.restype = res
+                fn.argtypes = args
+            _lib = handle
+    return _lib
+
+
+def last_error() -> str:
+    msg = lib().sft_last_error()
+    return msg.decode() if msg else ""
+
+
+def _check(rc: int, what: str) -> None:
+    if rc != SFT_OK:
+        raise RuntimeError(f"{what} failed (code {rc}): {last_error()}")
+
+
+def _ptr(t: torch.Tensor | None):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(device: torch.device) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _require(cond: bool, msg: str) -> None:
+    if not cond:
+        raise ValueError(msg)
+
+
+def _on_gpu(device: torch.device, *tensors: torch.Tensor) -> None:
+    _require(device.type == "cuda", "sft: tensors must be on a GPU (no CPU path exists)")
+    for t in tensors:
+        _require(t.device == device, "sft: all tensors must be on the same device")
+        _require(t.is_contiguous(), "sft: tensors must be contiguous")
+
+
+def ft_fwd_f32(idx: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor, out: torch.Tensor) -> None:
+    """out[b] = bias + sum of weight rows selected by idx[b] (reference order)."""
+    _require(idx.dim() == 2 and idx.dtype == torch.int32, "idx must be int32 [B, K]")
+    _require(weight.dim() == 2 and weight.dtype == torch.float32, "weight must be float32 [N, L]")
+    B, K = idx.shape
+    N, L = weight.shape
+    _require(bias.shape == (L,) and bias.dtype == torch.float32, "bias must be float32 [L]")
+    _require(out.shape == (B, L) and out.dtype == torch.float32, "out must be float32 [B, L]")
+    _on_gpu(idx.device, idx, weight, bias, out)
+    with torch.cuda.device(idx.device):
+        _check(lib().sft_ft_fwd_f32(_ptr(idx), B, K, _ptr(weight), N, L, _ptr(bias), _ptr(out),
+                                    _stream(idx.device)), "sft_ft_fwd_f32")
+
+
+_ws_cache: dict = {}
+
+
+def bwd_workspace_bytes(B: int, K: int, N: int, L: int, flags: int, device: torch.device) -> int:
+    key = (device.index, B, K, N, L, flags)
+    got = _ws_cache.get(key)
+    if got is None:
+        n = ctypes.c_size_t(0)
+        with torch.cuda.device(device):
+            _check(lib().sft_ft_bwd_f32_workspace_size(B, K, N, L, flags, ctypes.byref(n)),
+                   "sft_ft_bwd_f32_workspace_size")
+        got = _ws_cache[key] = int(n.value)
+    return got
+
+
+def ft_bwd_f32(idx: torch.Tensor, weight_grad: torch.Tensor, bias_grad: torch.Tensor,
+               grad_out: torch.Tensor, flags: int = SFT_BWD_ACCUMULATE) -> None:
+    """weight_grad[f] (+)= sum of grad_out rows whose idx row holds f; bias_grad (+)= column sums."""
+    _require(idx.dim() == 2 and idx.dtype == torch.int32, "idx must be int32 [B, K]")
+    _require(weight_grad.dim() == 2 and weight_grad.dtype == torch.float32, "weight_grad must be float32 [N, L]")
+    B, K = idx.shape
+    N, L = weight_grad.shape
+    _require(bias_grad.shape == (L,) and bias_grad.dtype == torch.float32, "bias_grad must be float32 [L]")
+    _require(grad_out.shape == (B, L) and grad_out.dtype == torch.float32, "grad_out must be float32 [B, L]")
+    _on_gpu(idx.device, idx, weight_grad, bias_grad, grad_out)
+    nbytes = bwd_workspace_bytes(B, K, N, L, flags, idx.device)
+    ws = torch.empty(max(nbytes, 1) + 256, dtype=torch.uint8, device=idx.device)
+    off = (-ws.data_ptr()) % 256
+    with torch.cuda.device(idx.device):
+        _check(lib().sft_ft_bwd_f32(_ptr(idx), B, K, _ptr(grad_out), N, L, _ptr(weight_grad), _ptr(bias_grad),
+                                    ctypes.c_void_p(ws.data_ptr() + off), nbytes, flags, _stream(idx.device)),
+               "sft_ft_bwd_f32")
+
+
+def ft_fwd_i16(idx: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor, out: torch.Tensor,
+               psqt_weight: torch.Tensor | None = None, psqt_out: torch.Tensor | None = None,
+               clip_lo: int = 0, clip_hi: int = 127, wrap16: bool = False) -> None:
+    _require(idx.dim() == 2 and idx.dtype == torch.int32, "idx must be int32 [B, K]")
+    _require(weight.dim() == 2 and weight.dtype == torch.int16, "weight must be int16 [N, L]")
+    B, K = idx.shape
+    N, L = weight.shape
+    _require(bias.shape == (L,) and bias.dtype == torch.int16, "bias must be int16 [L]")
+    _require(out.shape == (B, L) and out.dtype == torch.int16, "out must be int16 [B, L]")
+    tensors = [idx, weight, bias, out]
+    P = 0
+    if psqt_weight is not None or psqt_out is not None:
+        _require(psqt_weight is not None and psqt_out is not None, "psqt_weight and psqt_out go together")
+        _require(psqt_weight.dim() == 2 and psqt_weight.shape[0] == N and psqt_weight.dtype == torch.int32,
+                 "psqt_weight must be int32 [N, P]")
+        P = psqt_weight.shape[1]
+        _require(psqt_out.shape == (B, P) and psqt_out.dtype == torch.int32, "psqt_out must be int32 [B, P]")
+        tensors += [psqt_weight, psqt_out]
+    _on_gpu(idx.device, *tensors)
+    flags = SFT_Q16_WRAP16 if wrap16 else SFT_Q16_ACC32
+    with torch.cuda.device(idx.device):
+        _check(lib().sft_ft_fwd_i16(_ptr(idx), B, K, _ptr(weight), N, L, _ptr(bias), _ptr(psqt_weight), P,
+                                    _ptr(out), _ptr(psqt_out), clip_lo, clip_hi, flags, _stream(idx.device)),
+               "sft_ft_fwd_i16")
+
+
+def quantize_i16(x: torch.Tensor, scale: float) -> torch.Tensor:
+    """round_half_even(x * scale) saturated to int16, computed by the library on the GPU."""
+    _require(x.dtype == torch.float32, "x must be float32")
+    _on_gpu(x.device, x)
+    out = torch.empty(x.shape, dtype=torch.int16, device=x.device)
+    with torch.cuda.device(x.device):
+        _check(lib().sft_quantize_i16(_ptr(x), x.numel(), float(scale), _ptr(out), _stream(x.device)),
+               "sft_quantize_i16")
+    return out
+
+
+# ---- per-launch kernel timing ----
+def prof_enable(on: bool) -> None:
+    _check(lib().sft_prof_enable(1 if on else 0), "sft_prof_enable")
+
+
+def prof_kind_names() -> list[str]:
+    n = lib().sft_prof_num_kinds()
+    return [lib().sft_prof_kind_name(i).decode() for i in range(n)]
+
+
+def prof_collect() -> dict:
+    """{kind_name: (total_ms, launches)} for launches since the last collect."""
+    names = prof_kind_names()
+    n = len(names)
+    ms = (ctypes.c_double * n)()
+    cnt = (ctypes.c_int64 * n)()
+    _check(lib().sft_prof_collect(ms, cnt, n), "sft_prof_collect")
+    return {names[i]: (ms[i], cnt[i]) for i in range(n) if cnt[i] > 0}

@@ -1,0 +1,122 @@
+"""The C-ABI library loads, exports what include/sft_ft.h declares, and rejects
+bad arguments on the host before any GPU work (no compute calls here)."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from conftest import ROOT
+from sft_amd import _native
+
+HEADER = os.path.join(ROOT, "include", "sft_ft.h")
+
+
+def header_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(sft_\w+)\s*\(", text)))
+
+
+def test_header_declares_the_binding_table():
+    assert header_functions() == sorted(_native.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _native.lib()
+    for name in header_functions():
+        assert hasattr(lib, name), name
+
+
+def test_abi_version_matches_header():
+    m = re.search(r"#define SFT_ABI_VERSION (\d+)", open(HEADER).read())
+    assert _native.lib().sft_abi_version() == int(m.group(1))
+
+
+def test_flag_values_match_header():
+    text = open(HEADER).read()
+    for name in ("SFT_BWD_OVERWRITE", "SFT_BWD_ATOMIC", "SFT_Q16_WRAP16"):
+        m = re.search(rf"#define {name} (0x[0-9a-fA-F]+)u", text)
+        assert int(m.group(1), 16) == getattr(_native, name)
+
+
+P = ctypes.c_void_p(0x1000)  # never dereferenced: every call below fails validation first
+
+
+@pytest.mark.parametrize("args,needle", [
+    ((None, 4, 2, P, 10, 8, P, P, None), "null pointer"),
+    ((P, -1, 2, P, 10, 8, P, P, None), "batch"),
+    ((P, 4, 0, P, 10, 8, P, P, None), "max_active"),
+    ((P, 4, 2, P, 0, 8, P, P, None), "num_inputs"),
+    ((P, 4, 2, P, 10, 0, P, P, None), "output_size"),
+    ((P, 4, 2, None, 10, 8, P, P, None), "null pointer"),
+    ((P, 2**30, 4, P, 10, 8, P, P, None), "batch * max_active"),
+])
+def test_fwd_f32_rejects(args, needle):
+    lib = _native.lib()
+    rc = lib.sft_ft_fwd_f32(*args)
+    assert rc == -1
+    assert needle in _native.last_error()
+
+
+def test_fwd_f32_empty_batch_is_a_noop():
+    assert _native.lib().sft_ft_fwd_f32(None, 0, 4, P, 10, 8, P, None, None) == 0
+    assert _native.last_error() == ""
+
+
+def test_bwd_rejects_flags_and_pointers():
+    lib = _native.lib()
+    assert lib.sft_ft_bwd_f32(P, 4, 2, P, 10, 8, P, P, P, 0, 0x100, None) == -1
+    assert "flags" in _native.last_error()
+    assert lib.sft_ft_bwd_f32(P, 4, 2, P, 10, 8, None, P, P, 0, 0, None) == -1
+    assert "null" in _native.last_error()
+    n = ctypes.c_size_t(0)
+    assert lib.sft_ft_bwd_f32_workspace_size(4, 2, 10, 8, 0x8, ctypes.byref(n)) == -1
+    assert lib.sft_ft_bwd_f32_workspace_size(4, 2, 10, 8, 0, None) == -1
+
+
+def test_i16_rejects():
+    lib = _native.lib()
+    base = [P, 4, 2, P, 10, 8, P, None, 0, P, None, 0, 127, 0, None]
+    a = list(base); a[7] = P  # psqt weight without output
+    assert lib.sft_ft_fwd_i16(*a) == -1 and "psqt" in _native.last_error()
+    a = list(base); a[7] = P; a[10] = P; a[8] = 65
+    assert lib.sft_ft_fwd_i16(*a) == -1 and "psqt_size" in _native.last_error()
+    a = list(base); a[11], a[12] = 5, 4
+    assert lib.sft_ft_fwd_i16(*a) == -1 and "clip" in _native.last_error()
+    a = list(base); a[2] = 70000
+    assert lib.sft_ft_fwd_i16(*a) == -1 and "65536" in _native.last_error()
+    a = list(base); a[13] = 2
+    assert lib.sft_ft_fwd_i16(*a) == -1 and "flags" in _native.last_error()
+
+
+def test_quantize_rejects():
+    lib = _native.lib()
+    assert lib.sft_quantize_i16(P, -1, 1.0, P, None) == -1
+    assert lib.sft_quantize_i16(None, 5, 1.0, P, None) == -1
+    assert lib.sft_quantize_i16(None, 0, 1.0, None, None) == 0
+
+
+def test_error_is_thread_local_and_cleared():
+    import threading
+
+    lib = _native.lib()
+    assert lib.sft_ft_fwd_f32(None, 4, 2, P, 10, 8, P, P, None) == -1
+    seen = []
+    t = threading.Thread(target=lambda: seen.append(_native.last_error()))
+    t.start()
+    t.join()
+    assert seen == [""]
+    assert "null" in _native.last_error()
+    assert lib.sft_abi_version() > 0
+    assert lib.sft_ft_fwd_f32(None, 0, 4, P, 10, 8, P, None, None) == 0
+    assert _native.last_error() == ""
+
+
+def test_profiling_kinds_and_empty_collect():
+    names = _native.prof_kind_names()
+    assert "fwd_f32_gather" in names and "bwd_feature_gather" in names
+    _native.prof_enable(True)
+    assert _native.prof_collect() == {}
+    _native.prof_enable(False)

@@ -1,0 +1,129 @@
+"""fp32 backward on the GPU.  Sorted mode: weight grad bit-exact with the
+reference-order oracle; bias grad within 1e-5 of binary64.  Atomic mode: both
+within 1e-4 row-normwise of binary64 (atomic-order rounding only)."""
+
+import numpy as np
+import pytest
+import torch
+
+from gpu_helpers import DEV, announce, case, dev, dw_rel_err, host, rel_err
+from oracle import ft_oracle
+from sft_amd import _native, workloads
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [
+    (1, 1, 10, 4, 8, 0, 4, False),
+    (2, 37, 517, 32, 136, 0, 32, False),
+    (3, 300, 2000, 32, 1048, 16, 32, True),
+    (4, 129, 100, 160, 1048, 32, 160, False),
+    (5, 65, 77, 7, 13, 0, 7, False),
+    (7, 64, 50, 5, 2100, 0, 5, False),
+    (8, 3000, 23232, 32, 136, 16, 32, True),
+    (9, 333, 4000, 48, 520, 0, 48, False),
+]
+
+
+def run_bwd(idx, G, N, flags, dW0=None, db0=None):
+    L = G.shape[1]
+    dW = torch.zeros(N, L, device=DEV) if dW0 is None else dev(dW0)
+    db = torch.zeros(L, device=DEV) if db0 is None else dev(db0)
+    if flags & _native.SFT_BWD_OVERWRITE:
+        dW.fill_(float("nan"))
+        db.fill_(float("nan"))
+    _native.ft_bwd_f32(dev(idx), dW, db, dev(G), flags)
+    return host(dW), host(db)
+
+
+@pytest.mark.parametrize("seed,B,N,K,L,lo,hi,sort", SHAPES)
+@pytest.mark.parametrize("overwrite", [False, True])
+def test_sorted_bwd_matches_reference_order(seed, B, N, K, L, lo, hi, sort, overwrite):
+    announce(f"bwd sorted seed={seed} B={B} N={N} K={K} L={L} overwrite={overwrite}")
+    idx, _, _, G = case(seed, B, N, K, L, lo, hi, sort)
+    g = np.random.default_rng(seed + 100)
+    dW0 = None if overwrite else g.standard_normal((N, L)).astype(np.float32)
+    db0 = None if overwrite else g.standard_normal(L).astype(np.float32)
+    flags = _native.SFT_BWD_OVERWRITE if overwrite else _native.SFT_BWD_ACCUMULATE
+    dW, db = run_bwd(idx, G, N, flags, dW0, db0)
+    rW, _ = ft_oracle.bwd_f32(idx, G, N, dW0, db0)
+    assert np.array_equal(dW, rW)
+    db_ref = (0 if db0 is None else db0.astype(np.float64)) + G.astype(np.float64).sum(0)
+    assert rel_err(db, db_ref) <= 1e-5
+
+
+@pytest.mark.parametrize("seed,B,N,K,L,lo,hi,sort", SHAPES)
+@pytest.mark.parametrize("overwrite", [False, True])
+def test_atomic_bwd_within_tolerance(seed, B, N, K, L, lo, hi, sort, overwrite):
+    announce(f"bwd atomic seed={seed} B={B} N={N} K={K} L={L} overwrite={overwrite}")
+    idx, _, _, G = case(seed, B, N, K, L, lo, hi, sort)
+    flags = _native.SFT_BWD_ATOMIC | (_native.SFT_BWD_OVERWRITE if overwrite else 0)
+    dW, db = run_bwd(idx, G, N, flags)
+    r64, rb64 = ft_oracle.bwd_f64(idx, G, N)
+    assert dw_rel_err(dW, r64) <= 1e-4
+    assert rel_err(db, rb64) <= 1e-4
+
+
+def test_bwd_duplicates_and_out_of_range():
+    announce("bwd repeated features and out-of-range indices")
+    N, L = 12, 20
+    idx = np.array([[3, 3, 40, -1], [11, -5, 3, 0], [-1, -1, -1, -1]], np.int32)
+    g = np.random.default_rng(5)
+    G = g.standard_normal((3, L)).astype(np.float32)
+    clean = np.where((idx >= 0) & (idx < N), idx, -1).astype(np.int32)
+    for flags in (0, _native.SFT_BWD_OVERWRITE, _native.SFT_BWD_ATOMIC):
+        dW, _ = run_bwd(idx, G, N, flags)
+        rW, _ = ft_oracle.bwd_f32(clean, G, N)
+        if flags & _native.SFT_BWD_ATOMIC:
+            assert dw_rel_err(dW, ft_oracle.bwd_f64(clean, G, N)[0]) <= 1e-6
+        else:
+            assert np.array_equal(dW, rW)
+
+
+def test_bwd_all_inactive_and_empty_batch():
+    announce("bwd all inactive / empty batch")
+    N, L = 9, 8
+    idx = np.full((4, 3), -1, np.int32)
+    G = np.ones((4, L), np.float32)
+    dW0 = np.full((N, L), 7.0, np.float32)
+    dW, db = run_bwd(idx, G, N, 0, dW0, np.zeros(L, np.float32))
+    assert np.array_equal(dW, dW0) and np.array_equal(db, np.full(L, 4.0, np.float32))
+    dW, db = run_bwd(idx, G, N, _native.SFT_BWD_OVERWRITE)
+    assert not dW.any() and np.array_equal(db, np.full(L, 4.0, np.float32))
+    e = np.zeros((0, 3), np.int32)
+    dW, db = run_bwd(e, np.zeros((0, L), np.float32), N, _native.SFT_BWD_OVERWRITE)
+    assert not dW.any() and not db.any()
+
+
+@pytest.mark.parametrize("wid", [0, 1, 2, 3])
+def test_bwd_full_workload(wid):
+    w = workloads.WORKLOADS[wid]
+    announce(f"bwd workload {w.name} B={w.B} N={w.N} K={w.K} L={w.L}")
+    d = workloads.make_fp32_inputs(w)
+    idx, G = d["idx_w"], d["g_w"]
+    dW = torch.empty(w.N, w.L, device=DEV)
+    db = torch.empty(w.L, device=DEV)
+    _native.ft_bwd_f32(dev(idx), dW, db, dev(G), _native.SFT_BWD_OVERWRITE)
+    rW, _ = ft_oracle.bwd_f32(idx, G, w.N)
+    assert np.array_equal(host(dW), rW)
+    assert rel_err(host(db), G.astype(np.float64).sum(0)) <= 1e-5
+    # adjoint identity at full size: <fwd(W) - b, G> == <W, dW>
+    Wt = dev(d["W"])
+    out = torch.empty(w.B, w.L, device=DEV)
+    _native.ft_fwd_f32(dev(idx), Wt, torch.zeros(w.L, device=DEV), out)
+    prod = out.double() * dev(G).double()
+    lhs = float(prod.sum())
+    rhs = float((Wt.double() * dW.double()).sum())
+    assert abs(lhs - rhs) <= 1e-6 * float(prod.abs().sum())
+
+
+@pytest.mark.parametrize("wid", [1, 3])
+def test_atomic_bwd_full_workload(wid):
+    w = workloads.WORKLOADS[wid]
+    announce(f"bwd atomic workload {w.name}")
+    d = workloads.make_fp32_inputs(w)
+    idx, G = d["idx_b"], d["g_b"]
+    dW = torch.empty(w.N, w.L, device=DEV)
+    db = torch.empty(w.L, device=DEV)
+    _native.ft_bwd_f32(dev(idx), dW, db, dev(G), _native.SFT_BWD_OVERWRITE | _native.SFT_BWD_ATOMIC)
+    r64, _ = ft_oracle.bwd_f64(idx, G, w.N)
+    assert dw_rel_err(host(dW), r64) <= 1e-4

@@ -1,0 +1,87 @@
+"""fp32 forward on the GPU vs the ordered oracle: bit-exact, and within 1e-5
+row-normwise of binary64."""
+
+import numpy as np
+import pytest
+import torch
+
+from gpu_helpers import DEV, announce, case, dev, host, rel_err
+from oracle import ft_oracle
+from sft_amd import _native, workloads
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [
+    # seed, B, N, K, L, lo, hi, sort
+    (1, 1, 10, 4, 8, 0, 4, False),
+    (2, 37, 517, 32, 136, 0, 32, False),      # narrow rows: 8-lane groups
+    (3, 300, 2000, 32, 1048, 16, 32, True),   # 64-lane groups, 5 chunks per lane
+    (4, 129, 100, 160, 1048, 32, 160, False),  # K = 160
+    (5, 65, 77, 7, 13, 0, 7, False),          # L % 4 != 0: scalar path
+    (6, 200, 300, 32, 1040, 16, 32, True),
+    (7, 64, 50, 5, 2100, 0, 5, False),        # L > 2048: several column slabs
+    (8, 1000, 23232, 32, 136, 16, 32, True),
+    (9, 333, 4000, 48, 520, 0, 48, False),    # 32-lane groups
+    (10, 5, 3, 70, 12, 0, 3, False),          # K > 64: two compaction rounds
+]
+
+
+@pytest.mark.parametrize("seed,B,N,K,L,lo,hi,sort", SHAPES)
+def test_fwd_matches_oracle(seed, B, N, K, L, lo, hi, sort):
+    announce(f"fwd seed={seed} B={B} N={N} K={K} L={L}")
+    idx, W, b, _ = case(seed, B, N, K, L, lo, hi, sort)
+    out = torch.empty(B, L, device=DEV)
+    _native.ft_fwd_f32(dev(idx), dev(W), dev(b), out)
+    y = host(out)
+    assert np.array_equal(y, ft_oracle.fwd_f32(idx, W, b))
+    assert rel_err(y, ft_oracle.fwd_f64(idx, W, b)) <= 1e-5
+
+
+def test_fwd_repeated_feature_and_last_row():
+    announce("fwd repeated features, index N-1")
+    N, L = 40, 64
+    idx = np.array([[3, 3, 3, -1], [N - 1, 0, N - 1, 5], [-1, -1, -1, -1]], np.int32)
+    g = np.random.default_rng(0)
+    W = g.standard_normal((N, L)).astype(np.float32)
+    b = g.standard_normal(L).astype(np.float32)
+    out = torch.empty(3, L, device=DEV)
+    _native.ft_fwd_f32(dev(idx), dev(W), dev(b), out)
+    assert np.array_equal(host(out), ft_oracle.fwd_f32(idx, W, b))
+
+
+def test_fwd_out_of_range_indices_are_inactive():
+    announce("fwd out-of-range indices")
+    N, L = 30, 16
+    idx = np.array([[0, 30, 5, -7], [2**31 - 1, 1, -2**31, 29]], np.int32)
+    g = np.random.default_rng(1)
+    W = g.standard_normal((N, L)).astype(np.float32)
+    b = g.standard_normal(L).astype(np.float32)
+    out = torch.empty(2, L, device=DEV)
+    _native.ft_fwd_f32(dev(idx), dev(W), dev(b), out)
+    clean = np.where((idx >= 0) & (idx < N), idx, -1).astype(np.int32)
+    assert np.array_equal(host(out), ft_oracle.fwd_f32(clean, W, b))
+
+
+def test_fwd_unaligned_views_use_the_scalar_path():
+    announce("fwd unaligned weight view")
+    g = np.random.default_rng(2)
+    N, L, B, K = 50, 12, 20, 6
+    big = torch.from_numpy(g.standard_normal(N * L + 1).astype(np.float32)).to(DEV)
+    W = big[1:].view(N, L)  # 4-byte offset: not 16-byte aligned
+    idx = workloads.make_indices(g, B, N, K, 0, K)
+    b = g.standard_normal(L).astype(np.float32)
+    out = torch.empty(B, L, device=DEV)
+    _native.ft_fwd_f32(dev(idx), W, dev(b), out)
+    assert np.array_equal(host(out), ft_oracle.fwd_f32(idx, host(W), b))
+
+
+@pytest.mark.parametrize("wid", [0, 1, 2, 3])
+def test_fwd_full_workload(wid):
+    w = workloads.WORKLOADS[wid]
+    announce(f"fwd workload {w.name} B={w.B} N={w.N} K={w.K} L={w.L}")
+    d = workloads.make_fp32_inputs(w, with_grads=False)
+    Wt, bt = dev(d["W"]), dev(d["bias"])
+    for key in ("idx_w", "idx_b"):
+        out = torch.empty(w.B, w.L, device=DEV)
+        _native.ft_fwd_f32(dev(d[key]), Wt, bt, out)
+        assert np.array_equal(host(out), ft_oracle.fwd_f32(d[key], d["W"], d["bias"])), key

@@ -1,0 +1,65 @@
+"""int16 quantized forward and the device quantizer: bit-exact with the oracle."""
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import golden
+from gpu_helpers import DEV, announce, dev, host
+from oracle import ft_oracle
+from sft_amd import _native, workloads
+from sft_amd.quantized import QuantizedFeatureTransformer, quantize_weight_i16, quantized_ft_forward
+
+pytestmark = pytest.mark.gpu
+
+
+def test_q16_fixture():
+    announce("q16 fixture")
+    d = golden("q16_tiny")
+    out, pout = quantized_ft_forward(dev(d["idx"]), dev(d["Wq"]), dev(d["bq"]), dev(d["psqt"]), 0, 127, False)
+    assert np.array_equal(host(out), d["out_acc32"]) and np.array_equal(host(pout), d["psqt_out"])
+    out, _ = quantized_ft_forward(dev(d["idx"]), dev(d["Wq"]), dev(d["bq"]), None, 0, 127, True)
+    assert np.array_equal(host(out), d["out_wrap16"])
+    out, _ = quantized_ft_forward(dev(d["idx"]), dev(d["Wq"]), dev(d["bq"]), None, -32768, 32767, True)
+    assert np.array_equal(host(out), d["raw_wrap16"])
+
+
+@pytest.mark.parametrize("seed,B,N,K,L,P", [
+    (1, 50, 300, 32, 1040, 8), (2, 77, 64, 7, 13, 3), (3, 129, 1000, 160, 256, 0),
+    (4, 1000, 22528, 32, 128, 8), (5, 3, 10, 4, 2104, 8), (6, 40, 100, 32, 520, 64)])
+@pytest.mark.parametrize("wrap16", [False, True])
+def test_q16_matches_oracle(seed, B, N, K, L, P, wrap16):
+    announce(f"q16 seed={seed} B={B} N={N} K={K} L={L} P={P} wrap16={wrap16}")
+    g = np.random.default_rng(seed)
+    idx = workloads.make_indices(g, B, N, K, 0, K, sort=False)
+    Wq = g.integers(-3000, 3000, size=(N, L)).astype(np.int16)
+    bq = g.integers(-3000, 3000, size=L).astype(np.int16)
+    ps = g.integers(-10**6, 10**6, size=(N, P)).astype(np.int32) if P else None
+    for lo, hi in ((0, 127), (-32768, 32767), (-100, 255)):
+        out, pout = quantized_ft_forward(dev(idx), dev(Wq), dev(bq), None if ps is None else dev(ps), lo, hi, wrap16)
+        ro, rp = ft_oracle.fwd_i16(idx, Wq, bq, ps, lo, hi, wrap16)
+        assert np.array_equal(host(out), ro)
+        if P:
+            assert np.array_equal(host(pout), rp)
+
+
+@pytest.mark.parametrize("scale", [127.0, 255.0])
+def test_full_workload_q16(scale):
+    w = workloads.WORKLOADS[4]
+    announce(f"q16 workload {w.name} scale={scale}")
+    d = workloads.make_q16_inputs(w, scale=scale)
+    qft = QuantizedFeatureTransformer(dev(d["Wq"]), dev(d["bq"]), dev(d["psqt"]), 0, 127)
+    (ow, pw), (ob, pb) = qft(dev(d["idx_w"]), dev(d["idx_w"][::-1].copy()))
+    ro, rp = ft_oracle.fwd_i16(d["idx_w"], d["Wq"], d["bq"], d["psqt"], 0, 127, False)
+    assert np.array_equal(host(ow), ro) and np.array_equal(host(pw), rp)
+    assert np.array_equal(host(ob), ro[::-1]) and np.array_equal(host(pb), rp[::-1])
+
+
+def test_device_quantizer_matches_oracle():
+    announce("quantize kernel")
+    d = golden("quant_tiny")
+    assert np.array_equal(host(quantize_weight_i16(dev(d["x"]), float(d["scale"]))), d["q"])
+    g = np.random.default_rng(3)
+    x = (g.standard_normal((1000, 1040)) * 0.02).astype(np.float32)
+    for scale in (127.0, 255.0):
+        assert np.array_equal(host(quantize_weight_i16(dev(x), scale)), ft_oracle.quantize_i16(x, scale))

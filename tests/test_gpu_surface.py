@@ -1,0 +1,83 @@
+"""The reference-shaped surface end to end on the GPU: SparseLinearFunction
+through autograd, the kernel factories, and ComposedFeatureTransformer."""
+
+import numpy as np
+import pytest
+import torch
+
+from gpu_helpers import DEV, announce, case, dev, host, rel_err
+from oracle import ft_oracle
+from sft_amd import workloads
+from src.model.modules.feature_transformer import SparseLinearFunction
+from src.model.modules.feature_transformer.kernel import (
+    make_sparse_input_linear_backward_kernel,
+    make_sparse_input_linear_forward_kernel,
+)
+from src.model.modules.features import get_feature_cls
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("B,N,K,L", [(300, 2000, 32, 1048), (513, 777, 32, 136), (64, 90, 160, 264)])
+def test_two_perspectives_through_autograd(B, N, K, L):
+    announce(f"autograd two perspectives B={B} N={N} K={K} L={L}")
+    iw, W, b, Gw = case(11, B, N, K, L)
+    ib, _, _, Gb = case(12, B, N, K, L, sort=True)
+    Wt = dev(W).requires_grad_(True)
+    bt = dev(b).requires_grad_(True)
+    ow = SparseLinearFunction.apply(dev(iw), Wt, bt)
+    ob = SparseLinearFunction.apply(dev(ib), Wt, bt)
+    assert np.array_equal(host(ow), ft_oracle.fwd_f32(iw, W, b))
+    assert np.array_equal(host(ob), ft_oracle.fwd_f32(ib, W, b))
+    torch.autograd.backward([ow, ob], [dev(Gw), dev(Gb)])
+    rw, _ = ft_oracle.bwd_f32(iw, Gw, N)
+    rb, _ = ft_oracle.bwd_f32(ib, Gb, N)
+    assert np.array_equal(host(Wt.grad), rw + rb)  # autograd adds the two dense grads in fp32
+    db64 = Gw.astype(np.float64).sum(0) + Gb.astype(np.float64).sum(0)
+    assert rel_err(host(bt.grad), db64) <= 1e-5
+
+
+def test_factories_accumulate_like_the_reference():
+    announce("factory accumulate semantics")
+    B, N, K, L = 100, 300, 32, 136
+    idx, W, b, G = case(21, B, N, K, L)
+    fwd = make_sparse_input_linear_forward_kernel(K, L)
+    bwd = make_sparse_input_linear_backward_kernel(K, L)
+    out = torch.empty(B, L, device=DEV)
+    fwd(dev(idx), dev(W), dev(b), out)
+    assert np.array_equal(host(out), ft_oracle.fwd_f32(idx, W, b))
+    dW0 = np.random.default_rng(1).standard_normal((N, L)).astype(np.float32)
+    db0 = np.ones(L, np.float32)
+    dW, db = dev(dW0), dev(db0)
+    bwd(dev(idx), dW, db, dev(G))
+    rW, _ = ft_oracle.bwd_f32(idx, G, N, dW0, db0)
+    assert np.array_equal(host(dW), rW)
+    assert rel_err(host(db), db0 + G.astype(np.float64).sum(0)) <= 1e-5
+
+
+def test_composed_halfka_with_virtual_rows():
+    announce("ComposedFeatureTransformer HalfKAv2_hm^ L=40")
+    torch.manual_seed(0)
+    L = 40
+    ft = get_feature_cls("HalfKAv2_hm^")(L).to(DEV)
+    f = ft.features[0]
+    with torch.no_grad():
+        f.virtual_weight.normal_(0, 0.01)
+    B = 700
+    g = np.random.default_rng(2)
+    iw = workloads.make_indices(g, B, 24576, 32, 16, 32)
+    ib = workloads.make_indices(g, B, 24576, 32, 16, 32, sort=False)
+    Gw = g.standard_normal((B, L)).astype(np.float32)
+    Gb = g.standard_normal((B, L)).astype(np.float32)
+    ow, ob = ft(dev(iw), dev(ib))
+    merged = host(ft.merged_weight())
+    bias = host(ft.bias)
+    assert np.array_equal(host(ow), ft_oracle.fwd_f32(iw, merged, bias))
+    assert np.array_equal(host(ob), ft_oracle.fwd_f32(ib, merged, bias))
+    torch.autograd.backward([ow, ob], [dev(Gw), dev(Gb)])
+    rw, _ = ft_oracle.bwd_f32(iw, Gw, 24576)
+    rb, _ = ft_oracle.bwd_f32(ib, Gb, 24576)
+    dmerged = rw + rb
+    assert np.array_equal(host(f.weight.grad), dmerged)
+    v64 = dmerged.astype(np.float64).reshape(32, 768, L).sum(0)
+    assert rel_err(host(f.virtual_weight.grad), v64) <= 1e-5
