@@ -37,9 +37,9 @@ def log(msg: str) -> None:
 def kernel_bytes(kind: str, w, idx_pair) -> float | None:
     from sft_amd import workloads as wl
 
-    if kind == "fwd_f32_gather":
+    if kind in ("fwd_f32_gather", "fwd_f32_tiled_gather"):
         return sum(wl.fwd_kernel_bytes(i, w.N, w.L) for i in idx_pair) / 2
-    if kind == "bwd_feature_gather":
+    if kind in ("bwd_feature_gather", "bwd_tiled_gather"):
         return sum(wl.bwd_gather_kernel_bytes(i, w.N, w.L) for i in idx_pair) / 2
     if kind == "bwd_atomic_scatter":
         return sum(wl.fwd_kernel_bytes(i, w.N, w.L) for i in idx_pair) / 2

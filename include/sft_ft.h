@@ -39,6 +39,11 @@ extern "C" {
 #define SFT_EHIP (-3)       /* HIP runtime error while enqueueing               */
 #define SFT_EUNSUPPORTED (-4)
 
+/* sft_ft_fwd_f32_ex flags */
+#define SFT_FWD_AUTO 0x0u /* tiled gather when the shape allows it and the workspace
+                             suffices, otherwise the row gather               */
+#define SFT_FWD_ROWS 0x1u /* always the row gather (workspace unused)        */
+
 /* sft_ft_bwd_f32 flags */
 #define SFT_BWD_ACCUMULATE 0x0u /* dW[f] += ..., db += ...  (reference semantics)  */
 #define SFT_BWD_OVERWRITE 0x1u  /* every row of dW and all of db are written      */
@@ -46,6 +51,8 @@ extern "C" {
                                    deterministic, reference summation order     */
 #define SFT_BWD_ATOMIC 0x10u    /* position-major scatter with fp32 atomics;
                                    order of the adds is not deterministic       */
+#define SFT_BWD_ROWS 0x2u       /* sorted algorithm with whole-row gathers only
+                                   (no column tiling); same results            */
 
 /* sft_ft_fwd_i16 flags */
 #define SFT_Q16_ACC32 0x0u  /* exact int32 accumulation, then clamp            */
@@ -67,6 +74,26 @@ const char *sft_last_error(void);
 int sft_ft_fwd_f32(const int32_t *idx, int64_t batch, int32_t max_active, const float *weight,
                    int64_t num_inputs, int32_t output_size, const float *bias, float *out,
                    void *stream);
+
+/*
+ * Bytes of device workspace sft_ft_fwd_f32_ex uses for these sizes and flags
+ * (0 when the shape runs the row gather).  Host-only computation.
+ * No reference counterpart (the reference kernel takes no workspace).
+ */
+int sft_ft_fwd_f32_workspace_size(int64_t batch, int32_t max_active, int64_t num_inputs,
+                                  int32_t output_size, uint32_t flags, size_t *bytes);
+
+/*
+ * fp32 forward with a workspace: same result, bit for bit, as sft_ft_fwd_f32.
+ * With SFT_FWD_AUTO and a workspace of sft_ft_fwd_f32_workspace_size() bytes
+ * (256-byte aligned), the table is first copied into 32-column tiles in the
+ * workspace and gathered tile by tile, each tile from one XCD's L2.
+ * Replaces the same reference call as sft_ft_fwd_f32
+ * (FT/kernel.py:301-312, 66-105).
+ */
+int sft_ft_fwd_f32_ex(const int32_t *idx, int64_t batch, int32_t max_active, const float *weight,
+                      int64_t num_inputs, int32_t output_size, const float *bias, float *out,
+                      void *workspace, size_t workspace_bytes, uint32_t flags, void *stream);
 
 /*
  * Bytes of device workspace sft_ft_bwd_f32 needs for these sizes and flags.

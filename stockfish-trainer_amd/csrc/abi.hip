@@ -14,6 +14,10 @@ int fwd_f32(const int32_t *idx, int64_t B, int K, const float *W, int64_t N, int
 int fwd_i16(const int32_t *idx, int64_t B, int K, const int16_t *W, int64_t N, int L, const int16_t *bias,
             const int32_t *psqt, int P, int16_t *out, int32_t *psqt_out, int lo, int hi, int wrap16, hipStream_t s);
 int quantize_i16(const float *x, int64_t n, float scale, int16_t *out, hipStream_t s);
+size_t fwd_tiled_workspace(int64_t N, int L);
+bool fwd_tiled_supported(int64_t N, int L, const void *W, const void *bias, const void *out);
+int fwd_f32_tiled(const int32_t *idx, int64_t B, int K, const float *W, int64_t N, int L, const float *bias, float *out,
+                  void *ws, size_t ws_bytes, hipStream_t s);
 int bwd_workspace(int64_t B, int K, int64_t N, int L, uint32_t flags, size_t *bytes);
 int bwd_f32(const int32_t *idx, int64_t B, int K, const float *grad, int64_t N, int L, float *dW, float *db,
             void *ws, size_t ws_bytes, uint32_t flags, hipStream_t s);
@@ -99,6 +103,7 @@ struct ActiveScope {
 const char *const kKindNames[kProfNumKinds] = {
     "fwd_f32_gather",   "bwd_feature_sort",  "bwd_segment_offsets", "bwd_feature_gather", "bwd_bias_partial",
     "bwd_bias_final",   "bwd_atomic_scatter", "bwd_zero_fill",      "fwd_i16_gather",     "quantize_i16",
+    "fwd_tile_relayout", "fwd_f32_tiled_gather", "bwd_tiled_gather", "bwd_grad_relayout",
 };
 }  // namespace
 
@@ -154,6 +159,36 @@ int sft_ft_fwd_f32(const int32_t *idx, int64_t batch, int32_t max_active, const 
   return fwd_f32(idx, batch, max_active, weight, num_inputs, output_size, bias, out, (hipStream_t)stream);
 }
 
+int sft_ft_fwd_f32_workspace_size(int64_t batch, int32_t max_active, int64_t num_inputs, int32_t output_size,
+                                  uint32_t flags, size_t *bytes) {
+  clear_error();
+  std::string why;
+  if (!bytes) return fail(SFT_EINVAL, "sft_ft_fwd_f32_workspace_size: null pointer");
+  if (bad_sizes(batch, max_active, num_inputs, output_size, why))
+    return fail(SFT_EINVAL, "sft_ft_fwd_f32_workspace_size: " + why);
+  if (flags & ~SFT_FWD_ROWS) return fail(SFT_EINVAL, "sft_ft_fwd_f32_workspace_size: unknown flags");
+  const bool tiled = !(flags & SFT_FWD_ROWS) && fwd_tiled_supported(num_inputs, output_size, nullptr, nullptr, nullptr);
+  *bytes = tiled ? fwd_tiled_workspace(num_inputs, output_size) : 0;
+  return SFT_OK;
+}
+
+int sft_ft_fwd_f32_ex(const int32_t *idx, int64_t batch, int32_t max_active, const float *weight, int64_t num_inputs,
+                      int32_t output_size, const float *bias, float *out, void *workspace, size_t workspace_bytes,
+                      uint32_t flags, void *stream) {
+  clear_error();
+  std::string why;
+  if (bad_sizes(batch, max_active, num_inputs, output_size, why)) return fail(SFT_EINVAL, "sft_ft_fwd_f32_ex: " + why);
+  if (!weight || !bias || (batch > 0 && (!idx || !out))) return fail(SFT_EINVAL, "sft_ft_fwd_f32_ex: null pointer");
+  if (flags & ~SFT_FWD_ROWS) return fail(SFT_EINVAL, "sft_ft_fwd_f32_ex: unknown flags");
+  if (batch == 0) return SFT_OK;
+  const bool tiled = !(flags & SFT_FWD_ROWS) && fwd_tiled_supported(num_inputs, output_size, weight, bias, out) &&
+                     workspace != nullptr && workspace_bytes >= fwd_tiled_workspace(num_inputs, output_size);
+  if (tiled)
+    return fwd_f32_tiled(idx, batch, max_active, weight, num_inputs, output_size, bias, out, workspace,
+                         workspace_bytes, (hipStream_t)stream);
+  return fwd_f32(idx, batch, max_active, weight, num_inputs, output_size, bias, out, (hipStream_t)stream);
+}
+
 int sft_ft_bwd_f32_workspace_size(int64_t batch, int32_t max_active, int64_t num_inputs, int32_t output_size,
                                   uint32_t flags, size_t *bytes) {
   clear_error();
@@ -161,7 +196,7 @@ int sft_ft_bwd_f32_workspace_size(int64_t batch, int32_t max_active, int64_t num
   if (!bytes) return fail(SFT_EINVAL, "sft_ft_bwd_f32_workspace_size: null pointer");
   if (bad_sizes(batch, max_active, num_inputs, output_size, why))
     return fail(SFT_EINVAL, "sft_ft_bwd_f32_workspace_size: " + why);
-  if (flags & ~(SFT_BWD_OVERWRITE | SFT_BWD_ATOMIC))
+  if (flags & ~(SFT_BWD_OVERWRITE | SFT_BWD_ATOMIC | SFT_BWD_ROWS))
     return fail(SFT_EINVAL, "sft_ft_bwd_f32_workspace_size: unknown flags");
   return bwd_workspace(batch, max_active, num_inputs, output_size, flags, bytes);
 }
@@ -174,7 +209,7 @@ int sft_ft_bwd_f32(const int32_t *idx, int64_t batch, int32_t max_active, const 
   if (bad_sizes(batch, max_active, num_inputs, output_size, why)) return fail(SFT_EINVAL, "sft_ft_bwd_f32: " + why);
   if (!weight_grad || !bias_grad || (batch > 0 && (!idx || !grad_out)))
     return fail(SFT_EINVAL, "sft_ft_bwd_f32: null pointer");
-  if (flags & ~(SFT_BWD_OVERWRITE | SFT_BWD_ATOMIC)) return fail(SFT_EINVAL, "sft_ft_bwd_f32: unknown flags");
+  if (flags & ~(SFT_BWD_OVERWRITE | SFT_BWD_ATOMIC | SFT_BWD_ROWS)) return fail(SFT_EINVAL, "sft_ft_bwd_f32: unknown flags");
   return bwd_f32(idx, batch, max_active, grad_out, num_inputs, output_size, weight_grad, bias_grad, workspace,
                  workspace_bytes, flags, (hipStream_t)stream);
 }

@@ -39,6 +39,10 @@ enum ProfKind : int {
   kProfBwdZero,
   kProfFwdI16,
   kProfQuantize,
+  kProfFwdRelayout,
+  kProfFwdTiled,
+  kProfBwdTiled,
+  kProfBwdRelayout,
   kProfNumKinds
 };
 struct ProfScope {
@@ -75,10 +79,31 @@ __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirs
 // Compacts the active slots of `npos` consecutive index rows (row p at
 // idx + (pos0 + p) * K) into list[p * kpad + 0 .. count[p]), keeping slot order.
 // Called by one whole wave; rows at or past B get count 0.  A slot is active
-// when 0 <= v < N.  The wave owns list/count; callers barrier before reading.
+// when 0 <= v < N.  For K <= 64 one ballot covers 64 / Kp rows (Kp = K rounded
+// up to a power of two): lane l reads slot l % Kp of row l / Kp and ranks
+// itself among the active lanes of its own Kp-lane segment.  The wave owns
+// list/count; callers barrier before reading.
 __device__ __forceinline__ void compact_rows(const int32_t *__restrict__ idx, int64_t B, int K, int N,
                                              int64_t pos0, int npos, int *list, int kpad, int *count) {
   const int lane = lane_id();
+  if (K <= kWave) {
+    int kp = 1;
+    while (kp < K) kp <<= 1;
+    const int rows_per_ballot = kWave / kp;
+    const int seg = lane / kp, slot = lane % kp;
+    const uint64_t segmask = (kp == kWave) ? ~0ull : (((1ull << kp) - 1) << (seg * kp));
+    for (int p0 = 0; p0 < npos; p0 += rows_per_ballot) {
+      const int p = p0 + seg;
+      const int64_t pos = pos0 + p;
+      int v = -1;
+      if (p < npos && pos < B && slot < K) v = idx[pos * (int64_t)K + slot];
+      const bool ok = (unsigned)v < (unsigned)N;
+      const uint64_t m = ballot(ok) & segmask;
+      if (ok) list[p * kpad + popc_below(m)] = v;
+      if (slot == 0 && p < npos) count[p] = __popcll(m);
+    }
+    return;
+  }
   for (int p = 0; p < npos; ++p) {
     const int64_t pos = pos0 + p;
     int base = 0;
@@ -96,6 +121,31 @@ __device__ __forceinline__ void compact_rows(const int32_t *__restrict__ idx, in
     }
     if (lane == 0) count[p] = base;
   }
+}
+
+// ---- XCD-aware tile schedule ----
+// MI355X runs a dispatch's workgroups round-robin over its 8 XCDs (workgroup i
+// on XCD i % 8), and each XCD has its own 4 MB L2.  Tiled kernels give every
+// XCD whole column tiles: workgroup i serves the (i / 8)-th item of XCD i % 8,
+// where XCD x owns tiles x, x + 8, ... (all chunks of one tile, then the next)
+// and the tiles left over after the last full round of 8 are split by chunks
+// across all XCDs.  Any other placement only costs locality, never results.
+constexpr int kXcds = 8;
+struct TileItem {
+  int tile, chunk;
+};
+__host__ __device__ inline int64_t tile_sched_items_per_xcd(int ntiles, int nchunks) {
+  const int full = ntiles / kXcds, rem = ntiles % kXcds;
+  return (int64_t)full * nchunks + ((int64_t)rem * nchunks + kXcds - 1) / kXcds;
+}
+__device__ __forceinline__ TileItem tile_sched_item(int64_t bid, int ntiles, int nchunks) {
+  const int xcd = (int)(bid % kXcds);
+  const int64_t j = bid / kXcds;
+  const int full = ntiles / kXcds;
+  const int64_t fj = (int64_t)full * nchunks;
+  if (j < fj) return TileItem{xcd + kXcds * (int)(j / nchunks), (int)(j % nchunks)};
+  const int64_t g = (j - fj) * kXcds + xcd;
+  return TileItem{kXcds * full + (int)(g / nchunks), (int)(g % nchunks)};  // tile >= ntiles: no work
 }
 
 __host__ __device__ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }

@@ -23,18 +23,24 @@
 namespace sft {
 
 size_t index_lds_bytes(int G, int K);
+void launch_tile_relayout(const f32x4 *src, int64_t rows, int64_t cols4, f32x4 *dst, hipStream_t s);
 
 namespace {
 
 constexpr int kBiasRowsPerBlock = 128;
 constexpr int kBiasMaxParts = 512;
 
+// Sort key of flat slot s = b * K + k: chunk(b) * N + f for an active slot,
+// nchunks * N for an inactive one.  With one chunk this is the feature itself.
 struct SortKey {
   const int32_t *idx;
   unsigned N;
+  int K;
+  int chunk_rows;
+  unsigned sentinel;
   __host__ __device__ unsigned operator()(int s) const {
     const unsigned v = (unsigned)idx[s];
-    return v < N ? v : N;
+    return v < N ? (unsigned)((s / K) / chunk_rows) * N + v : sentinel;
   }
 };
 struct SlotPosition {
@@ -45,21 +51,22 @@ struct SlotPosition {
 typedef rocprim::transform_iterator<rocprim::counting_iterator<int>, SortKey, unsigned> KeyIter;
 typedef rocprim::transform_iterator<rocprim::counting_iterator<int>, SlotPosition, int> PosIter;
 
-unsigned key_bits(int64_t N) {
+unsigned key_bits(int64_t maxkey) {
   unsigned bits = 1;
-  while (((int64_t)1 << bits) <= N) ++bits;  // keys lie in [0, N]
+  while (((int64_t)1 << bits) <= maxkey) ++bits;  // keys lie in [0, maxkey]
   return bits;
 }
 
-hipError_t run_sort(void *temp, size_t &temp_bytes, const int32_t *idx, int64_t M, int K, int64_t N,
-                    unsigned *keys_out, int *pos_out, hipStream_t s) {
-  KeyIter keys_in(rocprim::counting_iterator<int>(0), SortKey{idx, (unsigned)N});
+hipError_t run_sort(void *temp, size_t &temp_bytes, const int32_t *idx, int64_t M, int K, int64_t N, int chunk_rows,
+                    int nchunks, unsigned *keys_out, int *pos_out, hipStream_t s) {
+  const int64_t nk = (int64_t)nchunks * N;
+  KeyIter keys_in(rocprim::counting_iterator<int>(0), SortKey{idx, (unsigned)N, K, chunk_rows, (unsigned)nk});
   PosIter pos_in(rocprim::counting_iterator<int>(0), SlotPosition{K});
   return rocprim::radix_sort_pairs(temp, temp_bytes, keys_in, keys_out, pos_in, pos_out, (unsigned)M, 0u,
-                                   key_bits(N), s);
+                                   key_bits(nk), s);
 }
 
-// seg_start[f] for f in [0, N]: index of the first sorted key >= f.
+// seg_start[k] for k in [0, N]: index of the first sorted key >= k (N = key count).
 __global__ __launch_bounds__(kBlock) void seg_offsets_kernel(const unsigned *__restrict__ keys, int64_t M, int64_t N,
                                                              int32_t *__restrict__ seg_start) {
   const int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
@@ -171,6 +178,82 @@ __global__ __launch_bounds__(kBlock) void gather_rows_kernel(const int32_t *__re
   }
 }
 
+// ---------------------------------------------------- tiled feature gather ----
+// dW[f, tile] for one 32-column tile, from the grad re-laid out as column
+// tiles (Gt: tile t holds columns [32t, 32t + 32) of every position, 128 B per
+// position).  The slots are sorted by (position half, feature), and the batch
+// is done in two launches: half 0 stores dW[f, tile] = its sum, half 1 loads
+// that value and keeps adding.  Either way a feature's sum is acc = 0,
+// acc += grad[b] over its positions ascending: the reference order
+// (FT/kernel.py:122, 178-181), bit for bit.  A lane group of 8 lanes x 16 B
+// owns one feature's tile row; tiles go to XCDs whole (tile_sched_item), so an
+// XCD reads one tile-half of Gt at a time: 32768 x 128 B = 4 MB, its L2.
+#ifndef SFT_BWD_TILED_U
+#define SFT_BWD_TILED_U 8
+#endif
+constexpr int kBwdTileCh = 8;  // float4 chunks per 32-column tile row
+constexpr int kBwdFeatPerBlock = kWavesPerBlock * (kWave / kBwdTileCh);  // 32
+
+__global__ __launch_bounds__(kBlock) void bwd_tiled_gather_kernel(const int32_t *__restrict__ seg,
+                                                                  const int32_t *__restrict__ sorted_pos, int64_t N,
+                                                                  const f32x4 *__restrict__ gt, int64_t B,
+                                                                  int64_t cols4, f32x4 *__restrict__ dW, int first,
+                                                                  int ntiles, int ngroups) {
+  constexpr int U = SFT_BWD_TILED_U;
+  const TileItem it = tile_sched_item(blockIdx.x, ntiles, ngroups);
+  if (it.tile >= ntiles) return;
+  const int wave = uniform(threadIdx.x / kWave);
+  const int lane = threadIdx.x % kWave;
+  const int g = lane / kBwdTileCh, t = lane % kBwdTileCh;
+  const int64_t col4 = (int64_t)it.tile * kBwdTileCh + t;
+  const bool colok = col4 < cols4;
+  const int64_t f = (int64_t)it.chunk * kBwdFeatPerBlock + wave * (kWave / kBwdTileCh) + g;
+  int s0 = 0, s1 = 0;
+  if (f < N) {
+    s0 = seg[f];
+    s1 = seg[f + 1];
+  }
+  const int n = s1 - s0;
+  const bool wave_has_work = ballot(n > 0) != 0;  // wave-uniform
+  if (!first && !wave_has_work) return;             // nothing to add anywhere in the wave
+  int nmin, nmax;
+  group_minmax<kBwdTileCh>(n, nmin, nmax);
+  const int32_t *plist = sorted_pos + s0;
+  const f32x4 *gcol = gt + (int64_t)it.tile * B * kBwdTileCh + t;
+  f32x4 *d = dW + f * cols4 + col4;
+  f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+  if (!first && n > 0 && f < N && colok) acc = *d;
+  int k = 0;
+  if (colok) {
+    for (; k + U <= nmin; k += U) {
+      int b[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) b[u] = plist[k + u];
+      f32x4 w[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) w[u] = gcol[(int64_t)b[u] * kBwdTileCh];
+#pragma unroll
+      for (int u = 0; u < U; ++u) acc += w[u];
+    }
+  }
+  for (; k < nmax; k += U) {
+    f32x4 w[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      w[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+      if (k + u < n && colok) w[u] = gcol[(int64_t)plist[k + u] * kBwdTileCh];
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (k + u < n) acc += w[u];
+  }
+  if (f >= N || !colok) return;
+  if (first)
+    *d = acc;
+  else if (n > 0)
+    *d = acc;
+}
+
 // Position-major fp32 atomic scatter.  One wave per position (lanes over
 // consecutive floats, so each atomic instruction covers 256 contiguous bytes);
 // FPL floats per lane per slab.
@@ -206,45 +289,77 @@ __global__ __launch_bounds__(kBlock) void zero_kernel(float *__restrict__ p, int
   for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += (int64_t)gridDim.x * kBlock) p[i] = 0.0f;
 }
 
-// partial[blk, c] = sum of grad[r, c] over the block's rows, 4 interleaved
-// accumulators combined as (s0 + s1) + (s2 + s3): a fixed order.
-template <typename T>
+// partial[blk, c] = sum of grad[r, c] over the block's rows.  Wave w of the
+// block takes rows r0 + w, r0 + w + 4, ... (U rows per step, loads first),
+// lane l owns chunks c0 + l + 64 j like the row gathers; the four wave sums
+// are combined in a fixed order.  Deterministic.
+template <typename T, int CPL>
 __global__ __launch_bounds__(kBlock) void bias_partial_kernel(const T *__restrict__ grad, int64_t B, int64_t cols,
                                                               int64_t rows_per_block, T *__restrict__ partial) {
+  constexpr int U = 4;
+  __shared__ T red[kWavesPerBlock][kWave * CPL];
+  const int wave = uniform(threadIdx.x / kWave);
+  const int lane = threadIdx.x % kWave;
+  const int64_t c0 = (int64_t)blockIdx.y * (kWave * CPL) + lane;
   const int64_t r0 = (int64_t)blockIdx.x * rows_per_block;
   const int64_t r1 = std::min<int64_t>(B, r0 + rows_per_block);
-  for (int64_t c = threadIdx.x; c < cols; c += kBlock) {
-    T s0 = T(0), s1 = T(0), s2 = T(0), s3 = T(0);
-    int64_t r = r0;
-    for (; r + 4 <= r1; r += 4) {
-      const T *p = grad + r * cols + c;
-      s0 += p[0];
-      s1 += p[cols];
-      s2 += p[2 * cols];
-      s3 += p[3 * cols];
+  bool colok[CPL];
+  T acc[CPL];
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) {
+    colok[j] = c0 + kWave * j < cols;
+    acc[j] = T(0);
+  }
+  for (int64_t r = r0 + wave; r < r1; r += kWavesPerBlock * U) {
+    T v[U][CPL];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t rr = r + (int64_t)kWavesPerBlock * u;
+      const T *row = grad + rr * cols + c0;
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) {
+        v[u][j] = T(0);
+        if (rr < r1 && colok[j]) v[u][j] = row[kWave * j];
+      }
     }
-    for (; r < r1; ++r) s0 += grad[r * cols + c];
-    partial[(int64_t)blockIdx.x * cols + c] = (s0 + s1) + (s2 + s3);
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) acc[j] += v[u][j];
+  }
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) red[wave][lane + kWave * j] = acc[j];
+  __syncthreads();
+  for (int i = threadIdx.x; i < kWave * CPL; i += kBlock) {
+    const int64_t c = (int64_t)blockIdx.y * (kWave * CPL) + i;
+    if (c < cols) partial[(int64_t)blockIdx.x * cols + c] = (red[0][i] + red[1][i]) + (red[2][i] + red[3][i]);
   }
 }
 
-// db[c] (+)= sum over parts of partial[p, c]; wave w takes parts w, w+4, ...,
-// and the four wave sums are combined in a fixed order.
+template <typename T>
+__device__ __forceinline__ T shfl_xor_t(T v, int m);
+template <>
+__device__ __forceinline__ float shfl_xor_t<float>(float v, int m) {
+  return __shfl_xor(v, m);
+}
+template <>
+__device__ __forceinline__ f32x4 shfl_xor_t<f32x4>(f32x4 v, int m) {
+  return f32x4{__shfl_xor(v.x, m), __shfl_xor(v.y, m), __shfl_xor(v.z, m), __shfl_xor(v.w, m)};
+}
+
+// db[c] (+)= sum over parts of partial[p, c].  One wave per column chunk: lane
+// l sums parts l, l+64, ..., then a fixed xor-shuffle tree.  Deterministic.
 template <typename T>
 __global__ __launch_bounds__(kBlock) void bias_final_kernel(const T *__restrict__ partial, int nparts, int64_t cols,
                                                             T *__restrict__ db, int overwrite) {
-  __shared__ T red[kWavesPerBlock][kWave];
-  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-  const int64_t c = (int64_t)blockIdx.x * kWave + lane;
+  const int wave = uniform(threadIdx.x / kWave), lane = threadIdx.x % kWave;
+  const int64_t c = (int64_t)blockIdx.x * kWavesPerBlock + wave;
+  if (c >= cols) return;
   T s = T(0);
-  if (c < cols)
-    for (int p = wave; p < nparts; p += kWavesPerBlock) s += partial[(int64_t)p * cols + c];
-  red[wave][lane] = s;
-  __syncthreads();
-  if (wave == 0 && c < cols) {
-    const T tot = (red[0][lane] + red[1][lane]) + (red[2][lane] + red[3][lane]);
-    db[c] = overwrite ? tot : db[c] + tot;
-  }
+  for (int p = lane; p < nparts; p += kWave) s += partial[(int64_t)p * cols + c];
+#pragma unroll
+  for (int m = 1; m < kWave; m <<= 1) s += shfl_xor_t(s, m);
+  if (lane == 0) db[c] = overwrite ? s : db[c] + s;
 }
 
 template <typename T, int G, int CPL>
@@ -277,7 +392,7 @@ void launch_gather(dim3 grid, hipStream_t s, const int32_t *seg_start, const int
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 struct BwdLayout {
-  size_t keys, pos, seg, partial, temp, temp_bytes, total;
+  size_t keys, pos, seg, partial, temp, temp_bytes, gt, total;
   int nparts;
 };
 
@@ -285,6 +400,21 @@ int bias_parts(int64_t B) {
   return (int)std::max<int64_t>(1, std::min<int64_t>(kBiasMaxParts, ceil_div(B, kBiasRowsPerBlock)));
 }
 
+bool tiled_shape(int L, uint32_t flags) {
+  return !(flags & (SFT_BWD_ATOMIC | SFT_BWD_ROWS)) && (flags & SFT_BWD_OVERWRITE) && L % 4 == 0 &&
+         L >= 32 * kXcds;
+}
+
+// Position halves of the tiled gather (one launch each).
+constexpr int kBwdHalves = 2;
+int sort_chunks(int64_t B, int L, uint32_t flags) {
+  return tiled_shape(L, flags) && B >= kBwdHalves ? kBwdHalves : 1;
+}
+int64_t half_rows(int64_t B) { return ceil_div(B, kBwdHalves); }
+
+// The sort and offsets buffers are sized for the tiled (chunked) key space,
+// which also covers the one-chunk key space of the row gather, so the choice
+// between the two can wait for the pointers' alignment at call time.
 int make_layout(int64_t B, int K, int64_t N, int L, uint32_t flags, BwdLayout &lay) {
   const int64_t M = B * K;
   lay.nparts = bias_parts(B);
@@ -294,18 +424,27 @@ int make_layout(int64_t B, int K, int64_t N, int L, uint32_t flags, BwdLayout &l
   lay.keys = lay.pos = lay.seg = lay.temp = off;
   lay.temp_bytes = 0;
   if (!(flags & SFT_BWD_ATOMIC) && M > 0) {
+    const int nc = sort_chunks(B, L, flags);
     lay.keys = off;
     off = align256(off + (size_t)M * sizeof(unsigned));
     lay.pos = off;
     off = align256(off + (size_t)M * sizeof(int));
     lay.seg = off;
-    off = align256(off + (size_t)(N + 1) * sizeof(int32_t));
-    size_t tb = 0;
-    hipError_t e = run_sort(nullptr, tb, nullptr, M, K, N, nullptr, nullptr, nullptr);
+    off = align256(off + (size_t)(nc * N + 1) * sizeof(int32_t));
+    size_t tb = 0, tb1 = 0;
+    hipError_t e = run_sort(nullptr, tb, nullptr, M, K, N, (int)(nc > 1 ? half_rows(B) : std::max<int64_t>(B, 1)), nc,
+                            nullptr, nullptr, nullptr);
+    if (e == hipSuccess) e = run_sort(nullptr, tb1, nullptr, M, K, N, (int)std::max<int64_t>(B, 1), 1, nullptr,
+                                      nullptr, nullptr);
     if (e != hipSuccess) return fail(SFT_EHIP, std::string("sort workspace query: ") + hipGetErrorString(e));
     lay.temp = off;
-    lay.temp_bytes = tb;
-    off = align256(off + tb);
+    lay.temp_bytes = std::max(tb, tb1);
+    off = align256(off + lay.temp_bytes);
+  }
+  lay.gt = off;
+  if (!(flags & SFT_BWD_ATOMIC) && M > 0 && sort_chunks(B, L, flags) > 1) {
+    const int64_t ntiles = ceil_div(L, 32);
+    off = align256(off + (size_t)(ntiles * B * 32) * sizeof(float));
   }
   lay.total = off;
   return SFT_OK;
@@ -338,20 +477,36 @@ int bwd_f32(const int32_t *idx, int64_t B, int K, const float *grad, int64_t N, 
     const bool vec = (L % 4 == 0) && ((uintptr_t)grad % 16 == 0) && ((uintptr_t)db % 16 == 0);
     const int64_t cols = vec ? L / 4 : L;
     const int64_t rows = ceil_div(std::max<int64_t>(B, 1), lay.nparts);
+    const int cpl = (int)std::min<int64_t>(ceil_div(cols, kWave), kMaxCpl);
+    const dim3 pgrid((unsigned)lay.nparts, (unsigned)ceil_div(cols, (int64_t)kWave * cpl));
     {
       ProfScope prof(kProfBwdBiasPartial, s);
-      if (vec)
-        hipLaunchKernelGGL(bias_partial_kernel<f32x4>, dim3(lay.nparts), dim3(kBlock), 0, s,
-                           reinterpret_cast<const f32x4 *>(grad), B, cols, rows,
-                           reinterpret_cast<f32x4 *>(w + lay.partial));
-      else
-        hipLaunchKernelGGL(bias_partial_kernel<float>, dim3(lay.nparts), dim3(kBlock), 0, s, grad, B, cols, rows,
-                           reinterpret_cast<float *>(w + lay.partial));
+#define SFT_BIAS_CASE(T, C)                                                                                  \
+  hipLaunchKernelGGL((bias_partial_kernel<T, C>), pgrid, dim3(kBlock), 0, s, reinterpret_cast<const T *>(grad), \
+                     B, cols, rows, reinterpret_cast<T *>(w + lay.partial))
+#define SFT_BIAS_SWITCH(T)               \
+  switch (cpl) {                         \
+    case 1: SFT_BIAS_CASE(T, 1); break;  \
+    case 2: SFT_BIAS_CASE(T, 2); break;  \
+    case 3: SFT_BIAS_CASE(T, 3); break;  \
+    case 4: SFT_BIAS_CASE(T, 4); break;  \
+    case 5: SFT_BIAS_CASE(T, 5); break;  \
+    case 6: SFT_BIAS_CASE(T, 6); break;  \
+    case 7: SFT_BIAS_CASE(T, 7); break;  \
+    default: SFT_BIAS_CASE(T, 8); break; \
+  }
+      if (vec) {
+        SFT_BIAS_SWITCH(f32x4)
+      } else {
+        SFT_BIAS_SWITCH(float)
+      }
+#undef SFT_BIAS_SWITCH
+#undef SFT_BIAS_CASE
     }
     if ((rc = check_launch("bias partial sums")) != SFT_OK) return rc;
     {
       ProfScope prof(kProfBwdBiasFinal, s);
-      const dim3 grid((unsigned)ceil_div(cols, kWave));
+      const dim3 grid((unsigned)ceil_div(cols, kWavesPerBlock));
       if (vec)
         hipLaunchKernelGGL(bias_final_kernel<f32x4>, grid, dim3(kBlock), 0, s,
                            reinterpret_cast<const f32x4 *>(w + lay.partial), lay.nparts, cols,
@@ -397,27 +552,48 @@ int bwd_f32(const int32_t *idx, int64_t B, int K, const float *grad, int64_t N, 
   unsigned *keys = reinterpret_cast<unsigned *>(w + lay.keys);
   int32_t *pos = reinterpret_cast<int32_t *>(w + lay.pos);
   int32_t *seg = reinterpret_cast<int32_t *>(w + lay.seg);
-  if (M > 0) {
-    ProfScope prof(kProfBwdSort, s);
-    size_t tb = lay.temp_bytes;
-    hipError_t e = run_sort(w + lay.temp, tb, idx, M, K, N, keys, pos, s);
-    if (e != hipSuccess) return fail(SFT_EHIP, std::string("feature sort: ") + hipGetErrorString(e));
-  }
-  if (M > 0) {
-    ProfScope prof(kProfBwdOffsets, s);
-    hipLaunchKernelGGL(seg_offsets_kernel, dim3((unsigned)ceil_div(M + 1, kBlock)), dim3(kBlock), 0, s, keys, M, N,
-                       seg);
-    if ((rc = check_launch("segment offsets")) != SFT_OK) return rc;
-  } else if (!overwrite) {
-    return SFT_OK;  // nothing active: dW untouched
-  }
   if (M == 0) {
-    // overwrite with no slots at all: every row is zero
-    const int64_t n = N * (int64_t)L;
+    if (!overwrite) return SFT_OK;  // nothing active: dW untouched
+    const int64_t n = N * (int64_t)L;  // overwrite with no slots at all: every row is zero
     ProfScope prof(kProfBwdZero, s);
     hipLaunchKernelGGL(zero_kernel, dim3((unsigned)std::min<int64_t>(ceil_div(n, kBlock), 1 << 16)), dim3(kBlock), 0,
                        s, dW, n);
     return check_launch("weight grad zero fill");
+  }
+  const bool tiled = tiled_shape(L, flags) && (uintptr_t)grad % 16 == 0 && (uintptr_t)dW % 16 == 0;
+  const int nc = tiled ? sort_chunks(B, L, flags) : 1;
+  const int chunk_rows = (int)(nc > 1 ? half_rows(B) : B);
+  const int64_t nkeys = (int64_t)nc * N;
+  {
+    ProfScope prof(kProfBwdSort, s);
+    size_t tb = lay.temp_bytes;
+    hipError_t e = run_sort(w + lay.temp, tb, idx, M, K, N, chunk_rows, nc, keys, pos, s);
+    if (e != hipSuccess) return fail(SFT_EHIP, std::string("feature sort: ") + hipGetErrorString(e));
+  }
+  {
+    ProfScope prof(kProfBwdOffsets, s);
+    hipLaunchKernelGGL(seg_offsets_kernel, dim3((unsigned)ceil_div(M + 1, kBlock)), dim3(kBlock), 0, s, keys, M, nkeys,
+                       seg);
+    if ((rc = check_launch("segment offsets")) != SFT_OK) return rc;
+  }
+  if (tiled) {
+    const int64_t cols4 = L / 4;
+    const int ntiles = (int)ceil_div(cols4, kBwdTileCh);
+    const int ngroups = (int)ceil_div(N, kBwdFeatPerBlock);
+    const int64_t blocks = tile_sched_items_per_xcd(ntiles, ngroups) * kXcds;
+    f32x4 *gt = reinterpret_cast<f32x4 *>(w + lay.gt);
+    {
+      ProfScope prof(kProfBwdRelayout, s);
+      launch_tile_relayout(reinterpret_cast<const f32x4 *>(grad), B, cols4, gt, s);
+      if ((rc = check_launch("grad relayout")) != SFT_OK) return rc;
+    }
+    for (int h = 0; h < nc; ++h) {
+      ProfScope prof(kProfBwdTiled, s);
+      hipLaunchKernelGGL(bwd_tiled_gather_kernel, dim3((unsigned)blocks), dim3(kBlock), 0, s, seg + (int64_t)h * N,
+                         pos, N, gt, B, cols4, reinterpret_cast<f32x4 *>(dW), h == 0 ? 1 : 0, ntiles, ngroups);
+      if ((rc = check_launch("tiled feature gather")) != SFT_OK) return rc;
+    }
+    return SFT_OK;
   }
   {
     const bool vec = (L % 4 == 0) && ((uintptr_t)grad % 16 == 0) && ((uintptr_t)dW % 16 == 0);

@@ -228,6 +228,78 @@ __global__ __launch_bounds__(kBlock) void fwd_i16_kernel(const int32_t *__restri
   }
 }
 
+// ------------------------------------------------------ tiled fp32 gather ----
+// The table is first re-laid out as column tiles: tile t holds columns
+// [32t, 32t + 32) of every row, 128 bytes per row, rows contiguous, so one
+// tile is N * 128 B (2.97 MB for N = 23 232) and fits one XCD's 4 MB L2.
+// The gather then runs tile by tile on each XCD (tile_sched_item), lane
+// groups of 8 lanes x 16 B covering one tile row per position, so every
+// table read after the first touch of a tile is an L2 hit.
+constexpr int kTileF = 32;                 // floats per tile row
+constexpr int kTileCh = kTileF / 4;        // float4 chunks per tile row (= lane group size)
+#ifndef SFT_TILED_ROUNDS
+#define SFT_TILED_ROUNDS 2
+#endif
+constexpr int kTiledRounds = SFT_TILED_ROUNDS;                        // position rounds per block
+constexpr int kTiledPosPerRound = kWavesPerBlock * (kWave / kTileCh);  // 32
+constexpr int kTiledPosPerBlock = kTiledPosPerRound * kTiledRounds;
+
+__global__ __launch_bounds__(kBlock) void fwd_tiled_kernel(const int32_t *__restrict__ idx, int64_t B, int K, int N,
+                                                           const f32x4 *__restrict__ Wt, int64_t cols4,
+                                                           const f32x4 *__restrict__ bias, f32x4 *__restrict__ out,
+                                                           int kpad, int ntiles, int nchunks) {
+  constexpr int U = 4;
+  constexpr int PPW = kWave / kTileCh;  // 8 positions per wave per round
+  extern __shared__ int smem[];
+  const TileItem it = tile_sched_item(blockIdx.x, ntiles, nchunks);
+  if (it.tile >= ntiles) return;  // whole block: uniform
+  const int wave = uniform(threadIdx.x / kWave);
+  const int lane = threadIdx.x % kWave;
+  int *list = smem + wave * PPW * kpad;
+  int *count = smem + kWavesPerBlock * PPW * kpad + wave * PPW;
+  const int g = lane / kTileCh, t = lane % kTileCh;
+  const int64_t col4 = (int64_t)it.tile * kTileCh + t;
+  const bool colok = col4 < cols4;
+  const f32x4 b4 = colok ? bias[col4] : f32x4{0.f, 0.f, 0.f, 0.f};
+  const f32x4 *wtile = Wt + (int64_t)it.tile * N * kTileCh + t;
+
+  for (int round = 0; round < kTiledRounds; ++round) {
+    const int64_t pos0 = (int64_t)it.chunk * kTiledPosPerBlock + round * kTiledPosPerRound + wave * PPW;
+    compact_rows(idx, B, K, N, pos0, PPW, list, kpad, count);
+    __syncthreads();
+    const int64_t pos = pos0 + g;
+    const int n = count[g];
+    int nmin, nmax;
+    group_minmax<kTileCh>(n, nmin, nmax);
+    const int *mylist = list + g * kpad;
+    f32x4 acc = b4;
+    int k = 0;
+    for (; k + U <= nmin; k += U) {
+      const i32x4 f4 = read4(mylist, k);
+      f32x4 w[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) w[u] = colok ? wtile[(int64_t)f4[u] * kTileCh] : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int u = 0; u < U; ++u) acc += w[u];
+    }
+    for (; k < nmax; k += U) {
+      const i32x4 f4 = read4(mylist, k);
+      f32x4 w[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const bool v = k + u < n;
+        w[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+        if (v && colok) w[u] = wtile[(int64_t)f4[u] * kTileCh];
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        if (k + u < n) acc += w[u];
+    }
+    if (pos < B && colok) __builtin_nontemporal_store(acc, out + pos * cols4 + col4);
+    __syncthreads();
+  }
+}
+
 // --------------------------------------------------------------- quantize ----
 __global__ __launch_bounds__(kBlock) void quantize_i16_kernel(const float *__restrict__ x, int64_t n, float scale,
                                                               int16_t *__restrict__ out) {
@@ -277,6 +349,23 @@ void launch_fwd_i16(dim3 grid, size_t lds, hipStream_t s, const int32_t *idx, in
 
 }  // namespace
 
+// Wt[(t * N + r) * 8 + q] = W[r, 4 * (8 t + q) .. +3]; padding chunks of the last tile are not written.
+static __global__ __launch_bounds__(kBlock) void tile_relayout_kernel(const f32x4 *__restrict__ W, int64_t N, int64_t cols4,
+                                                               f32x4 *__restrict__ Wt) {
+  const int64_t total = N * cols4;
+  for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < total; i += (int64_t)gridDim.x * kBlock) {
+    const int64_t r = i / cols4, c = i % cols4;
+    const int64_t t = c / 8, q = c % 8;
+    Wt[(t * N + r) * 8 + q] = W[i];
+  }
+}
+
+void launch_tile_relayout(const f32x4 *src, int64_t rows, int64_t cols4, f32x4 *dst, hipStream_t s) {
+  const int64_t total = rows * cols4;
+  hipLaunchKernelGGL(tile_relayout_kernel, dim3((unsigned)std::min<int64_t>(ceil_div(total, kBlock), 1 << 16)),
+                     dim3(kBlock), 0, s, src, rows, cols4, dst);
+}
+
 size_t index_lds_bytes(int G, int K) {
   const int ppw = kWave / G;
   return (size_t)(kWavesPerBlock * ppw * round_up4(K) + kWavesPerBlock * ppw) * sizeof(int);
@@ -300,6 +389,44 @@ int fwd_f32(const int32_t *idx, int64_t B, int K, const float *W, int64_t N, int
     SFT_G_CASES(launch_fwd_f32, float, grid, lds, s, idx, B, K, (int)N, W, cols, bias, out, kpad)
   }
   return check_launch("sft_ft_fwd_f32");
+}
+
+size_t fwd_tiled_workspace(int64_t N, int L) {
+  if (L % 4 != 0) return 0;
+  const int64_t ntiles = ceil_div(L, kTileF);
+  return (size_t)(ntiles * N * kTileF) * sizeof(float);
+}
+
+bool fwd_tiled_supported(int64_t N, int L, const void *W, const void *bias, const void *out) {
+  return L % 4 == 0 && L >= kTileF * kXcds && N * kTileF * 4 <= (int64_t)(3u << 20) &&
+         (uintptr_t)W % 16 == 0 && (uintptr_t)bias % 16 == 0 && (uintptr_t)out % 16 == 0;
+}
+
+int fwd_f32_tiled(const int32_t *idx, int64_t B, int K, const float *W, int64_t N, int L, const float *bias, float *out,
+                  void *ws, size_t ws_bytes, hipStream_t s) {
+  if (ws_bytes < fwd_tiled_workspace(N, L) || ws == nullptr || (uintptr_t)ws % 256 != 0)
+    return fail(SFT_EWORKSPACE, "sft_ft_fwd_f32_ex: workspace smaller than sft_ft_fwd_f32_workspace_size() "
+                                "or not 256-byte aligned");
+  const int64_t cols4 = L / 4;
+  const int ntiles = (int)ceil_div(L, kTileF);
+  const int kpad = round_up4(K);
+  const size_t lds = index_lds_bytes(kTileCh, K);
+  if (lds > kMaxIndexLds) return fail(SFT_EUNSUPPORTED, "sft_ft_fwd_f32_ex: max_active too large for the LDS index lists");
+  f32x4 *wt = static_cast<f32x4 *>(ws);
+  {
+    ProfScope prof(kProfFwdRelayout, s);
+    launch_tile_relayout(reinterpret_cast<const f32x4 *>(W), N, cols4, wt, s);
+  }
+  int rc = check_launch("sft_ft_fwd_f32_ex (relayout)");
+  if (rc != SFT_OK) return rc;
+  const int nchunks = (int)ceil_div(B, kTiledPosPerBlock);
+  const int64_t blocks = tile_sched_items_per_xcd(ntiles, nchunks) * kXcds;
+  {
+    ProfScope prof(kProfFwdTiled, s);
+    hipLaunchKernelGGL(fwd_tiled_kernel, dim3((unsigned)blocks), dim3(kBlock), lds, s, idx, B, K, (int)N, wt, cols4,
+                       reinterpret_cast<const f32x4 *>(bias), reinterpret_cast<f32x4 *>(out), kpad, ntiles, nchunks);
+  }
+  return check_launch("sft_ft_fwd_f32_ex (tiled gather)");
 }
 
 int fwd_i16(const int32_t *idx, int64_t B, int K, const int16_t *W, int64_t N, int L, const int16_t *bias,

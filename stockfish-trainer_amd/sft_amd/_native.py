@@ -18,10 +18,13 @@ PKG_ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 LIB_PATH = os.path.join(PKG_ROOT, "lib", "libsft_ft.so")
 
 SFT_OK = 0
+SFT_FWD_AUTO = 0x0
+SFT_FWD_ROWS = 0x1
 SFT_BWD_ACCUMULATE = 0x0
 SFT_BWD_OVERWRITE = 0x1
 SFT_BWD_SORTED = 0x00
 SFT_BWD_ATOMIC = 0x10
+SFT_BWD_ROWS = 0x2
 SFT_Q16_ACC32 = 0x0
 SFT_Q16_WRAP16 = 0x1
 
@@ -35,6 +38,10 @@ SIGNATURES = {
     "sft_abi_version": (ctypes.c_int, []),
     "sft_last_error": (ctypes.c_char_p, []),
     "sft_ft_fwd_f32": (ctypes.c_int, [_vp, _i64, _i32, _vp, _i64, _i32, _vp, _vp, _vp]),
+    "sft_ft_fwd_f32_workspace_size": (
+        ctypes.c_int, [_i64, _i32, _i64, _i32, _u32, ctypes.POINTER(ctypes.c_size_t)]),
+    "sft_ft_fwd_f32_ex": (
+        ctypes.c_int, [_vp, _i64, _i32, _vp, _i64, _i32, _vp, _vp, _vp, ctypes.c_size_t, _u32, _vp]),
     "sft_ft_bwd_f32_workspace_size": (
         ctypes.c_int, [_i64, _i32, _i64, _i32, _u32, ctypes.POINTER(ctypes.c_size_t)]),
     "sft_ft_bwd_f32": (
@@ -108,8 +115,13 @@ def _on_gpu(device: torch.device, *tensors: torch.Tensor) -> None:
         _require(t.is_contiguous(), "sft: tensors must be contiguous")
 
 
-def ft_fwd_f32(idx: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor, out: torch.Tensor) -> None:
-    """out[b] = bias + sum of weight rows selected by idx[b] (reference order)."""
+def ft_fwd_f32(idx: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor, out: torch.Tensor,
+               rows: bool = False) -> None:
+    """out[b] = bias + sum of weight rows selected by idx[b] (reference order, bit-exact).
+
+    By default the library's tiled gather runs when the shape allows it, with a
+    workspace taken from torch's allocator; rows=True forces the row gather.
+    """
     _require(idx.dim() == 2 and idx.dtype == torch.int32, "idx must be int32 [B, K]")
     _require(weight.dim() == 2 and weight.dtype == torch.float32, "weight must be float32 [N, L]")
     B, K = idx.shape
@@ -117,24 +129,41 @@ def ft_fwd_f32(idx: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor, out:
     _require(bias.shape == (L,) and bias.dtype == torch.float32, "bias must be float32 [L]")
     _require(out.shape == (B, L) and out.dtype == torch.float32, "out must be float32 [B, L]")
     _on_gpu(idx.device, idx, weight, bias, out)
+    flags = SFT_FWD_ROWS if rows else SFT_FWD_AUTO
+    nbytes = _workspace_bytes("fwd", B, K, N, L, flags, idx.device)
+    ws, ptr = _workspace(nbytes, idx.device)
     with torch.cuda.device(idx.device):
-        _check(lib().sft_ft_fwd_f32(_ptr(idx), B, K, _ptr(weight), N, L, _ptr(bias), _ptr(out),
-                                    _stream(idx.device)), "sft_ft_fwd_f32")
+        _check(lib().sft_ft_fwd_f32_ex(_ptr(idx), B, K, _ptr(weight), N, L, _ptr(bias), _ptr(out), ptr, nbytes,
+                                       flags, _stream(idx.device)), "sft_ft_fwd_f32_ex")
+    del ws
 
 
 _ws_cache: dict = {}
 
 
-def bwd_workspace_bytes(B: int, K: int, N: int, L: int, flags: int, device: torch.device) -> int:
-    key = (device.index, B, K, N, L, flags)
+def _workspace_bytes(which: str, B: int, K: int, N: int, L: int, flags: int, device: torch.device) -> int:
+    key = (which, device.index, B, K, N, L, flags)
     got = _ws_cache.get(key)
     if got is None:
         n = ctypes.c_size_t(0)
+        fn = lib().sft_ft_fwd_f32_workspace_size if which == "fwd" else lib().sft_ft_bwd_f32_workspace_size
         with torch.cuda.device(device):
-            _check(lib().sft_ft_bwd_f32_workspace_size(B, K, N, L, flags, ctypes.byref(n)),
-                   "sft_ft_bwd_f32_workspace_size")
+            _check(fn(B, K, N, L, flags, ctypes.byref(n)), f"sft_ft_{which}_f32_workspace_size")
         got = _ws_cache[key] = int(n.value)
     return got
+
+
+def bwd_workspace_bytes(B: int, K: int, N: int, L: int, flags: int, device: torch.device) -> int:
+    return _workspace_bytes("bwd", B, K, N, L, flags, device)
+
+
+def _workspace(nbytes: int, device: torch.device):
+    """A 256-byte aligned device buffer of nbytes from torch's caching allocator."""
+    if nbytes == 0:
+        return None, None
+    ws = torch.empty(nbytes + 256, dtype=torch.uint8, device=device)
+    off = (-ws.data_ptr()) % 256
+    return ws, ctypes.c_void_p(ws.data_ptr() + off)
 
 
 def ft_bwd_f32(idx: torch.Tensor, weight_grad: torch.Tensor, bias_grad: torch.Tensor,
@@ -148,12 +177,11 @@ def ft_bwd_f32(idx: torch.Tensor, weight_grad: torch.Tensor, bias_grad: torch.Te
     _require(grad_out.shape == (B, L) and grad_out.dtype == torch.float32, "grad_out must be float32 [B, L]")
     _on_gpu(idx.device, idx, weight_grad, bias_grad, grad_out)
     nbytes = bwd_workspace_bytes(B, K, N, L, flags, idx.device)
-    ws = torch.empty(max(nbytes, 1) + 256, dtype=torch.uint8, device=idx.device)
-    off = (-ws.data_ptr()) % 256
+    ws, ptr = _workspace(nbytes, idx.device)
     with torch.cuda.device(idx.device):
         _check(lib().sft_ft_bwd_f32(_ptr(idx), B, K, _ptr(grad_out), N, L, _ptr(weight_grad), _ptr(bias_grad),
-                                    ctypes.c_void_p(ws.data_ptr() + off), nbytes, flags, _stream(idx.device)),
-               "sft_ft_bwd_f32")
+                                    ptr, nbytes, flags, _stream(idx.device)), "sft_ft_bwd_f32")
+    del ws
 
 
 def ft_fwd_i16(idx: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor, out: torch.Tensor,

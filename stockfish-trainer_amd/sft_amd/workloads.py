@@ -70,13 +70,19 @@ def make_indices(g: np.random.Generator, B: int, N: int, K: int, lo: int, hi: in
     """
     if not (0 <= lo <= hi <= K and hi <= N):
         raise ValueError("need 0 <= lo <= hi <= K and hi <= N")
-    vals = g.integers(0, N, size=(B, hi), dtype=np.int64)
-    while hi > 1:
-        s = np.sort(vals, axis=1)
-        bad = np.nonzero((s[:, 1:] == s[:, :-1]).any(axis=1))[0]
-        if bad.size == 0:
-            break
-        vals[bad] = g.integers(0, N, size=(bad.size, hi), dtype=np.int64)
+    if hi * hi <= 2 * N:
+        # sparse rows: a whole-row redraw is rarely needed (P(repeat) <~ hi^2 / 2N)
+        vals = g.integers(0, N, size=(B, hi), dtype=np.int64)
+        while hi > 1:
+            s = np.sort(vals, axis=1)
+            bad = np.nonzero((s[:, 1:] == s[:, :-1]).any(axis=1))[0]
+            if bad.size == 0:
+                break
+            vals[bad] = g.integers(0, N, size=(bad.size, hi), dtype=np.int64)
+    else:
+        # dense rows: exact draws without replacement, row by row
+        vals = np.stack([g.choice(N, size=hi, replace=False) for _ in range(B)]) if B else \
+            np.zeros((0, hi), np.int64)
     counts = g.integers(lo, hi + 1, size=B)
     keep = np.arange(hi)[None, :] < counts[:, None]
     big = np.int64(N) + 1

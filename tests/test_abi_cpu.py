@@ -36,7 +36,7 @@ def test_abi_version_matches_header():
 
 def test_flag_values_match_header():
     text = open(HEADER).read()
-    for name in ("SFT_BWD_OVERWRITE", "SFT_BWD_ATOMIC", "SFT_Q16_WRAP16"):
+    for name in ("SFT_BWD_OVERWRITE", "SFT_BWD_ATOMIC", "SFT_BWD_ROWS", "SFT_FWD_ROWS", "SFT_Q16_WRAP16"):
         m = re.search(rf"#define {name} (0x[0-9a-fA-F]+)u", text)
         assert int(m.group(1), 16) == getattr(_native, name)
 

@@ -16,11 +16,13 @@ SHAPES = [
     (1, 1, 10, 4, 8, 0, 4, False),
     (2, 37, 517, 32, 136, 0, 32, False),
     (3, 300, 2000, 32, 1048, 16, 32, True),
-    (4, 129, 100, 160, 1048, 32, 160, False),
+    (4, 129, 300, 160, 1048, 32, 160, False),
     (5, 65, 77, 7, 13, 0, 7, False),
     (7, 64, 50, 5, 2100, 0, 5, False),
     (8, 3000, 23232, 32, 136, 16, 32, True),
     (9, 333, 4000, 48, 520, 0, 48, False),
+    (10, 20000, 700, 32, 256, 0, 32, True),  # several position chunks, long segments
+    (11, 17000, 5, 3, 1040, 0, 3, False),    # three features: every segment spans all chunks
 ]
 
 
@@ -37,13 +39,16 @@ def run_bwd(idx, G, N, flags, dW0=None, db0=None):
 
 @pytest.mark.parametrize("seed,B,N,K,L,lo,hi,sort", SHAPES)
 @pytest.mark.parametrize("overwrite", [False, True])
-def test_sorted_bwd_matches_reference_order(seed, B, N, K, L, lo, hi, sort, overwrite):
-    announce(f"bwd sorted seed={seed} B={B} N={N} K={K} L={L} overwrite={overwrite}")
+@pytest.mark.parametrize("rows", [False, True])
+def test_sorted_bwd_matches_reference_order(seed, B, N, K, L, lo, hi, sort, overwrite, rows):
+    announce(f"bwd sorted seed={seed} B={B} N={N} K={K} L={L} overwrite={overwrite} rows={rows}")
     idx, _, _, G = case(seed, B, N, K, L, lo, hi, sort)
     g = np.random.default_rng(seed + 100)
     dW0 = None if overwrite else g.standard_normal((N, L)).astype(np.float32)
     db0 = None if overwrite else g.standard_normal(L).astype(np.float32)
     flags = _native.SFT_BWD_OVERWRITE if overwrite else _native.SFT_BWD_ACCUMULATE
+    if rows:
+        flags |= _native.SFT_BWD_ROWS
     dW, db = run_bwd(idx, G, N, flags, dW0, db0)
     rW, _ = ft_oracle.bwd_f32(idx, G, N, dW0, db0)
     assert np.array_equal(dW, rW)
@@ -100,11 +105,12 @@ def test_bwd_full_workload(wid):
     announce(f"bwd workload {w.name} B={w.B} N={w.N} K={w.K} L={w.L}")
     d = workloads.make_fp32_inputs(w)
     idx, G = d["idx_w"], d["g_w"]
-    dW = torch.empty(w.N, w.L, device=DEV)
-    db = torch.empty(w.L, device=DEV)
-    _native.ft_bwd_f32(dev(idx), dW, db, dev(G), _native.SFT_BWD_OVERWRITE)
     rW, _ = ft_oracle.bwd_f32(idx, G, w.N)
-    assert np.array_equal(host(dW), rW)
+    for flags in (_native.SFT_BWD_OVERWRITE | _native.SFT_BWD_ROWS, _native.SFT_BWD_OVERWRITE):
+        dW = torch.empty(w.N, w.L, device=DEV)
+        db = torch.empty(w.L, device=DEV)
+        _native.ft_bwd_f32(dev(idx), dW, db, dev(G), flags)
+        assert np.array_equal(host(dW), rW), flags
     assert rel_err(host(db), G.astype(np.float64).sum(0)) <= 1e-5
     # adjoint identity at full size: <fwd(W) - b, G> == <W, dW>
     Wt = dev(d["W"])

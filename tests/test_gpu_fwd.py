@@ -16,22 +16,25 @@ SHAPES = [
     (1, 1, 10, 4, 8, 0, 4, False),
     (2, 37, 517, 32, 136, 0, 32, False),      # narrow rows: 8-lane groups
     (3, 300, 2000, 32, 1048, 16, 32, True),   # 64-lane groups, 5 chunks per lane
-    (4, 129, 100, 160, 1048, 32, 160, False),  # K = 160
+    (4, 129, 300, 160, 1048, 32, 160, False),  # K = 160
     (5, 65, 77, 7, 13, 0, 7, False),          # L % 4 != 0: scalar path
     (6, 200, 300, 32, 1040, 16, 32, True),
     (7, 64, 50, 5, 2100, 0, 5, False),        # L > 2048: several column slabs
     (8, 1000, 23232, 32, 136, 16, 32, True),
     (9, 333, 4000, 48, 520, 0, 48, False),    # 32-lane groups
     (10, 5, 3, 70, 12, 0, 3, False),          # K > 64: two compaction rounds
+    (11, 1000, 24576, 32, 256, 0, 32, False),  # largest table the tiled gather takes; 8 tiles
+    (12, 77, 900, 13, 1040, 0, 13, False),    # K = 13: four rows per ballot
 ]
 
 
 @pytest.mark.parametrize("seed,B,N,K,L,lo,hi,sort", SHAPES)
-def test_fwd_matches_oracle(seed, B, N, K, L, lo, hi, sort):
-    announce(f"fwd seed={seed} B={B} N={N} K={K} L={L}")
+@pytest.mark.parametrize("rows", [False, True])
+def test_fwd_matches_oracle(seed, B, N, K, L, lo, hi, sort, rows):
+    announce(f"fwd seed={seed} B={B} N={N} K={K} L={L} rows={rows}")
     idx, W, b, _ = case(seed, B, N, K, L, lo, hi, sort)
     out = torch.empty(B, L, device=DEV)
-    _native.ft_fwd_f32(dev(idx), dev(W), dev(b), out)
+    _native.ft_fwd_f32(dev(idx), dev(W), dev(b), out, rows=rows)
     y = host(out)
     assert np.array_equal(y, ft_oracle.fwd_f32(idx, W, b))
     assert rel_err(y, ft_oracle.fwd_f64(idx, W, b)) <= 1e-5
@@ -75,6 +78,14 @@ def test_fwd_unaligned_views_use_the_scalar_path():
     assert np.array_equal(host(out), ft_oracle.fwd_f32(idx, host(W), b))
 
 
+def test_tiled_workspace_query():
+    n = _native._workspace_bytes("fwd", 65536, 32, 23232, 1048, _native.SFT_FWD_AUTO, DEV)
+    assert n == 33 * 23232 * 32 * 4
+    assert _native._workspace_bytes("fwd", 65536, 32, 23232, 136, _native.SFT_FWD_AUTO, DEV) == 0
+    assert _native._workspace_bytes("fwd", 65536, 32, 85296, 1048, _native.SFT_FWD_AUTO, DEV) == 0
+    assert _native._workspace_bytes("fwd", 65536, 32, 23232, 1048, _native.SFT_FWD_ROWS, DEV) == 0
+
+
 @pytest.mark.parametrize("wid", [0, 1, 2, 3])
 def test_fwd_full_workload(wid):
     w = workloads.WORKLOADS[wid]
@@ -82,6 +93,8 @@ def test_fwd_full_workload(wid):
     d = workloads.make_fp32_inputs(w, with_grads=False)
     Wt, bt = dev(d["W"]), dev(d["bias"])
     for key in ("idx_w", "idx_b"):
-        out = torch.empty(w.B, w.L, device=DEV)
-        _native.ft_fwd_f32(dev(d[key]), Wt, bt, out)
-        assert np.array_equal(host(out), ft_oracle.fwd_f32(d[key], d["W"], d["bias"])), key
+        ref = ft_oracle.fwd_f32(d[key], d["W"], d["bias"])
+        for rows in (False, True):
+            out = torch.empty(w.B, w.L, device=DEV)
+            _native.ft_fwd_f32(dev(d[key]), Wt, bt, out, rows=rows)
+            assert np.array_equal(host(out), ref), (key, rows)

@@ -18,7 +18,7 @@ from src.model.modules.features import get_feature_cls
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("B,N,K,L", [(300, 2000, 32, 1048), (513, 777, 32, 136), (64, 90, 160, 264)])
+@pytest.mark.parametrize("B,N,K,L", [(300, 2000, 32, 1048), (513, 777, 32, 136), (64, 400, 160, 264)])
 def test_two_perspectives_through_autograd(B, N, K, L):
     announce(f"autograd two perspectives B={B} N={N} K={K} L={L}")
     iw, W, b, Gw = case(11, B, N, K, L)

@@ -133,3 +133,11 @@ def test_step_bytes_formula():
     assert (w.B, w.N, w.K, w.L) == (65536, 23232, 32, 1048)
     # mean active 24: 2 * 2 * (4*32 + 4*1048*25) = 419 712 bytes per position
     assert 2 * 2 * (4 * 32 + 4 * 1048 * 25) == 419712
+
+
+def test_workload_indices_dense_rows_terminate():
+    """Rows holding most of the table (160 of 300) use exact draws without replacement."""
+    idx = workloads.make_indices(np.random.default_rng(4), 129, 300, 160, 32, 160, sort=False)
+    for r in idx:
+        a = r[r >= 0]
+        assert 32 <= len(a) <= 160 and len(np.unique(a)) == len(a) and a.max() < 300
