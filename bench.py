@@ -34,17 +34,28 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
-def kernel_bytes(kind: str, w, idx_pair) -> float | None:
+def kernel_step_bytes(kind: str, w, idx_pair) -> float | None:
+    """Algorithmic bytes one step moves through the kernels of `kind` (both perspectives).
+
+    Gathers: 4 B per index slot, 4*L per gathered or scattered row, 4*L per
+    output row (forward) or written weight-grad row (backward); re-layouts:
+    the table or grad read once and written once; bias partials: the grad
+    read once.  Bytes per launch = this / launches per step.
+    """
     from sft_amd import workloads as wl
 
     if kind in ("fwd_f32_gather", "fwd_f32_tiled_gather"):
-        return sum(wl.fwd_kernel_bytes(i, w.N, w.L) for i in idx_pair) / 2
+        return float(sum(wl.fwd_kernel_bytes(i, w.N, w.L) for i in idx_pair))
     if kind in ("bwd_feature_gather", "bwd_tiled_gather"):
-        return sum(wl.bwd_gather_kernel_bytes(i, w.N, w.L) for i in idx_pair) / 2
+        return float(sum(wl.bwd_gather_kernel_bytes(i, w.N, w.L) for i in idx_pair))
     if kind == "bwd_atomic_scatter":
-        return sum(wl.fwd_kernel_bytes(i, w.N, w.L) for i in idx_pair) / 2
+        return float(sum(wl.fwd_kernel_bytes(i, w.N, w.L) for i in idx_pair))
+    if kind == "fwd_tile_relayout":
+        return 2 * 2 * 4.0 * w.N * w.L
+    if kind == "bwd_grad_relayout":
+        return 2 * 2 * 4.0 * w.B * w.L
     if kind == "bwd_bias_partial":
-        return 4.0 * w.B * w.L
+        return 2 * 4.0 * w.B * w.L
     return None
 
 
@@ -179,14 +190,16 @@ def main() -> int:
     kern = {}
     for kind, (tot, cnt) in prof.items():
         avg = tot / cnt
-        kb = kernel_bytes(kind, w, (d["idx_w"], d["idx_b"]))
+        sb = kernel_step_bytes(kind, w, (d["idx_w"], d["idx_b"]))
+        per_launch = sb / (cnt / args.steps) if sb else None
         kern[kind] = {"avg_ms": avg, "launches_per_step": cnt / args.steps,
-                      "gbs": (kb / (avg * 1e-3) / 1e9) if kb else None}
+                      "bytes_per_launch": per_launch,
+                      "gbs": (per_launch / (avg * 1e-3) / 1e9) if per_launch else None}
         log(f"[bench]   {kind:22s} {avg:8.4f} ms x {cnt / args.steps:.0f}/step"
-            + (f"  {kern[kind]['gbs']:8.1f} GB/s algorithmic" if kb else ""))
+            + (f"  {kern[kind]['gbs']:8.1f} GB/s algorithmic" if per_launch else ""))
     dom = max(prof, key=lambda k: prof[k][0])
     dom_avg = prof[dom][0] / prof[dom][1]
-    dom_bytes = kernel_bytes(dom, w, (d["idx_w"], d["idx_b"]))
+    dom_bytes = kern[dom]["bytes_per_launch"]
     achieved = dom_bytes / (dom_avg * 1e-3) / 1e9
     traffic = load_traffic(w.name, dom)
 

@@ -64,6 +64,17 @@ struct Mapping {
 };
 Mapping choose_mapping(int64_t chunks, int min_group = 8);
 
+// Loads of arrays streamed once per tile pass (index rows, sorted position
+// lists): marked non-temporal so they do not displace the tile held in L2.
+#ifndef SFT_STREAM_NT
+#define SFT_STREAM_NT 0
+#endif
+#if SFT_STREAM_NT
+#define SFT_STREAM_LOAD(p) __builtin_nontemporal_load(p)
+#else
+#define SFT_STREAM_LOAD(p) (*(p))
+#endif
+
 // ---- device helpers ----
 __device__ __forceinline__ int lane_id() { return __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0)); }
 
@@ -96,7 +107,7 @@ __device__ __forceinline__ void compact_rows(const int32_t *__restrict__ idx, in
       const int p = p0 + seg;
       const int64_t pos = pos0 + p;
       int v = -1;
-      if (p < npos && pos < B && slot < K) v = idx[pos * (int64_t)K + slot];
+      if (p < npos && pos < B && slot < K) v = SFT_STREAM_LOAD(idx + pos * (int64_t)K + slot);
       const bool ok = (unsigned)v < (unsigned)N;
       const uint64_t m = ballot(ok) & segmask;
       if (ok) list[p * kpad + popc_below(m)] = v;

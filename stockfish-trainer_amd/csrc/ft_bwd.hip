@@ -23,7 +23,6 @@
 namespace sft {
 
 size_t index_lds_bytes(int G, int K);
-void launch_tile_relayout(const f32x4 *src, int64_t rows, int64_t cols4, f32x4 *dst, hipStream_t s);
 
 namespace {
 
@@ -228,7 +227,7 @@ __global__ __launch_bounds__(kBlock) void bwd_tiled_gather_kernel(const int32_t 
     for (; k + U <= nmin; k += U) {
       int b[U];
 #pragma unroll
-      for (int u = 0; u < U; ++u) b[u] = plist[k + u];
+      for (int u = 0; u < U; ++u) b[u] = SFT_STREAM_LOAD(plist + k + u);
       f32x4 w[U];
 #pragma unroll
       for (int u = 0; u < U; ++u) w[u] = gcol[(int64_t)b[u] * kBwdTileCh];
@@ -241,7 +240,7 @@ __global__ __launch_bounds__(kBlock) void bwd_tiled_gather_kernel(const int32_t 
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       w[u] = f32x4{0.f, 0.f, 0.f, 0.f};
-      if (k + u < n && colok) w[u] = gcol[(int64_t)plist[k + u] * kBwdTileCh];
+      if (k + u < n && colok) w[u] = gcol[(int64_t)SFT_STREAM_LOAD(plist + k + u) * kBwdTileCh];
     }
 #pragma unroll
     for (int u = 0; u < U; ++u)
@@ -293,9 +292,14 @@ __global__ __launch_bounds__(kBlock) void zero_kernel(float *__restrict__ p, int
 // block takes rows r0 + w, r0 + w + 4, ... (U rows per step, loads first),
 // lane l owns chunks c0 + l + 64 j like the row gathers; the four wave sums
 // are combined in a fixed order.  Deterministic.
+//
+// When gt is not null (T = f32x4 only), each grad chunk read is also stored to
+// the column-tile layout of the tiled gather: gt[(c / 8) * B + r][c % 8], so the
+// grad crosses HBM once for both the bias sum and the re-layout.
 template <typename T, int CPL>
 __global__ __launch_bounds__(kBlock) void bias_partial_kernel(const T *__restrict__ grad, int64_t B, int64_t cols,
-                                                              int64_t rows_per_block, T *__restrict__ partial) {
+                                                              int64_t rows_per_block, T *__restrict__ partial,
+                                                              T *__restrict__ gt) {
   constexpr int U = 4;
   __shared__ T red[kWavesPerBlock][kWave * CPL];
   const int wave = uniform(threadIdx.x / kWave);
@@ -320,6 +324,17 @@ __global__ __launch_bounds__(kBlock) void bias_partial_kernel(const T *__restric
       for (int j = 0; j < CPL; ++j) {
         v[u][j] = T(0);
         if (rr < r1 && colok[j]) v[u][j] = row[kWave * j];
+      }
+    }
+    if (gt != nullptr) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int64_t rr = r + (int64_t)kWavesPerBlock * u;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+          const int64_t c = c0 + kWave * j;
+          if (rr < r1 && colok[j]) gt[((c >> 3) * B + rr) * 8 + (c & 7)] = v[u][j];
+        }
       }
     }
 #pragma unroll
@@ -405,8 +420,11 @@ bool tiled_shape(int L, uint32_t flags) {
          L >= 32 * kXcds;
 }
 
-// Position halves of the tiled gather (one launch each).
-constexpr int kBwdHalves = 2;
+// Position chunks of the tiled gather (one launch each).
+#ifndef SFT_BWD_CHUNKS
+#define SFT_BWD_CHUNKS 2
+#endif
+constexpr int kBwdHalves = SFT_BWD_CHUNKS;
 int sort_chunks(int64_t B, int L, uint32_t flags) {
   return tiled_shape(L, flags) && B >= kBwdHalves ? kBwdHalves : 1;
 }
@@ -472,6 +490,12 @@ int bwd_f32(const int32_t *idx, int64_t B, int K, const float *grad, int64_t N, 
   const int overwrite = (flags & SFT_BWD_OVERWRITE) ? 1 : 0;
   const int64_t M = B * K;
 
+  // The tiled weight-grad gather reads the grad in column tiles; the bias pass
+  // writes that layout while it streams the grad.
+  const bool tiled = !(flags & SFT_BWD_ATOMIC) && M > 0 && tiled_shape(L, flags) && (uintptr_t)grad % 16 == 0 &&
+                     (uintptr_t)dW % 16 == 0 && (uintptr_t)db % 16 == 0;
+  f32x4 *gt = tiled ? reinterpret_cast<f32x4 *>(w + lay.gt) : nullptr;
+
   // ---- bias grad ----
   {
     const bool vec = (L % 4 == 0) && ((uintptr_t)grad % 16 == 0) && ((uintptr_t)db % 16 == 0);
@@ -483,7 +507,7 @@ int bwd_f32(const int32_t *idx, int64_t B, int K, const float *grad, int64_t N, 
       ProfScope prof(kProfBwdBiasPartial, s);
 #define SFT_BIAS_CASE(T, C)                                                                                  \
   hipLaunchKernelGGL((bias_partial_kernel<T, C>), pgrid, dim3(kBlock), 0, s, reinterpret_cast<const T *>(grad), \
-                     B, cols, rows, reinterpret_cast<T *>(w + lay.partial))
+                     B, cols, rows, reinterpret_cast<T *>(w + lay.partial), reinterpret_cast<T *>(gt))
 #define SFT_BIAS_SWITCH(T)               \
   switch (cpl) {                         \
     case 1: SFT_BIAS_CASE(T, 1); break;  \
@@ -560,7 +584,6 @@ int bwd_f32(const int32_t *idx, int64_t B, int K, const float *grad, int64_t N, 
                        s, dW, n);
     return check_launch("weight grad zero fill");
   }
-  const bool tiled = tiled_shape(L, flags) && (uintptr_t)grad % 16 == 0 && (uintptr_t)dW % 16 == 0;
   const int nc = tiled ? sort_chunks(B, L, flags) : 1;
   const int chunk_rows = (int)(nc > 1 ? half_rows(B) : B);
   const int64_t nkeys = (int64_t)nc * N;
@@ -581,12 +604,6 @@ int bwd_f32(const int32_t *idx, int64_t B, int K, const float *grad, int64_t N, 
     const int ntiles = (int)ceil_div(cols4, kBwdTileCh);
     const int ngroups = (int)ceil_div(N, kBwdFeatPerBlock);
     const int64_t blocks = tile_sched_items_per_xcd(ntiles, ngroups) * kXcds;
-    f32x4 *gt = reinterpret_cast<f32x4 *>(w + lay.gt);
-    {
-      ProfScope prof(kProfBwdRelayout, s);
-      launch_tile_relayout(reinterpret_cast<const f32x4 *>(grad), B, cols4, gt, s);
-      if ((rc = check_launch("grad relayout")) != SFT_OK) return rc;
-    }
     for (int h = 0; h < nc; ++h) {
       ProfScope prof(kProfBwdTiled, s);
       hipLaunchKernelGGL(bwd_tiled_gather_kernel, dim3((unsigned)blocks), dim3(kBlock), 0, s, seg + (int64_t)h * N,

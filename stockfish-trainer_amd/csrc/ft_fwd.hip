@@ -238,7 +238,7 @@ __global__ __launch_bounds__(kBlock) void fwd_i16_kernel(const int32_t *__restri
 constexpr int kTileF = 32;                 // floats per tile row
 constexpr int kTileCh = kTileF / 4;        // float4 chunks per tile row (= lane group size)
 #ifndef SFT_TILED_ROUNDS
-#define SFT_TILED_ROUNDS 2
+#define SFT_TILED_ROUNDS 1
 #endif
 constexpr int kTiledRounds = SFT_TILED_ROUNDS;                        // position rounds per block
 constexpr int kTiledPosPerRound = kWavesPerBlock * (kWave / kTileCh);  // 32
