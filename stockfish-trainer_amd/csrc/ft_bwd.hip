@@ -187,6 +187,9 @@ __global__ __launch_bounds__(kBlock) void gather_rows_kernel(const int32_t *__re
 // (FT/kernel.py:122, 178-181), bit for bit.  A lane group of 8 lanes x 16 B
 // owns one feature's tile row; tiles go to XCDs whole (tile_sched_item), so an
 // XCD reads one tile-half of Gt at a time: 32768 x 128 B = 4 MB, its L2.
+#ifndef SFT_BWD_NT_STORE
+#define SFT_BWD_NT_STORE 0
+#endif
 #ifndef SFT_BWD_TILED_U
 #define SFT_BWD_TILED_U 8
 #endif
@@ -222,35 +225,40 @@ __global__ __launch_bounds__(kBlock) void bwd_tiled_gather_kernel(const int32_t 
   f32x4 *d = dW + f * cols4 + col4;
   f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
   if (!first && n > 0 && f < N && colok) acc = *d;
+  // Positions are fetched 8 at a time, one per lane of the group, and
+  // broadcast inside the group, so a step costs one index load for 8 rows.
+  static_assert(U == kBwdTileCh, "one position per lane of the group");
   int k = 0;
-  if (colok) {
-    for (; k + U <= nmin; k += U) {
-      int b[U];
-#pragma unroll
-      for (int u = 0; u < U; ++u) b[u] = SFT_STREAM_LOAD(plist + k + u);
-      f32x4 w[U];
-#pragma unroll
-      for (int u = 0; u < U; ++u) w[u] = gcol[(int64_t)b[u] * kBwdTileCh];
-#pragma unroll
-      for (int u = 0; u < U; ++u) acc += w[u];
-    }
-  }
-  for (; k < nmax; k += U) {
+  for (; k + U <= nmin; k += U) {
+    const int mine = plist[k + t];
     f32x4 w[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
+      const int b = __shfl(mine, u, kBwdTileCh);
+      w[u] = colok ? gcol[(int64_t)b * kBwdTileCh] : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) acc += w[u];
+  }
+  for (; k < nmax; k += U) {
+    const int mine = (k + t < n) ? plist[k + t] : 0;
+    f32x4 w[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int b = __shfl(mine, u, kBwdTileCh);
       w[u] = f32x4{0.f, 0.f, 0.f, 0.f};
-      if (k + u < n && colok) w[u] = gcol[(int64_t)SFT_STREAM_LOAD(plist + k + u) * kBwdTileCh];
+      if (k + u < n && colok) w[u] = gcol[(int64_t)b * kBwdTileCh];
     }
 #pragma unroll
     for (int u = 0; u < U; ++u)
       if (k + u < n) acc += w[u];
   }
   if (f >= N || !colok) return;
-  if (first)
-    *d = acc;
-  else if (n > 0)
-    *d = acc;
+#if SFT_BWD_NT_STORE
+  if (first || n > 0) __builtin_nontemporal_store(acc, d);
+#else
+  if (first || n > 0) *d = acc;
+#endif
 }
 
 // Position-major fp32 atomic scatter.  One wave per position (lanes over

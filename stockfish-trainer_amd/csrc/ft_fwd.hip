@@ -237,6 +237,9 @@ __global__ __launch_bounds__(kBlock) void fwd_i16_kernel(const int32_t *__restri
 // table read after the first touch of a tile is an L2 hit.
 constexpr int kTileF = 32;                 // floats per tile row
 constexpr int kTileCh = kTileF / 4;        // float4 chunks per tile row (= lane group size)
+#ifndef SFT_FWD_TILED_U
+#define SFT_FWD_TILED_U 4
+#endif
 #ifndef SFT_TILED_ROUNDS
 #define SFT_TILED_ROUNDS 1
 #endif
@@ -248,7 +251,7 @@ __global__ __launch_bounds__(kBlock) void fwd_tiled_kernel(const int32_t *__rest
                                                            const f32x4 *__restrict__ Wt, int64_t cols4,
                                                            const f32x4 *__restrict__ bias, f32x4 *__restrict__ out,
                                                            int kpad, int ntiles, int nchunks) {
-  constexpr int U = 4;
+  constexpr int U = SFT_FWD_TILED_U;
   constexpr int PPW = kWave / kTileCh;  // 8 positions per wave per round
   extern __shared__ int smem[];
   const TileItem it = tile_sched_item(blockIdx.x, ntiles, nchunks);
@@ -275,24 +278,30 @@ __global__ __launch_bounds__(kBlock) void fwd_tiled_kernel(const int32_t *__rest
     f32x4 acc = b4;
     int k = 0;
     for (; k + U <= nmin; k += U) {
-      const i32x4 f4 = read4(mylist, k);
+      int fi[U];
+#pragma unroll
+      for (int u = 0; u < U; u += 4) {
+        const i32x4 f4 = read4(mylist, k + u);
+        fi[u] = f4[0], fi[u + 1] = f4[1], fi[u + 2] = f4[2], fi[u + 3] = f4[3];
+      }
       f32x4 w[U];
 #pragma unroll
-      for (int u = 0; u < U; ++u) w[u] = colok ? wtile[(int64_t)f4[u] * kTileCh] : f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int u = 0; u < U; ++u) w[u] = colok ? wtile[(int64_t)fi[u] * kTileCh] : f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int u = 0; u < U; ++u) acc += w[u];
     }
-    for (; k < nmax; k += U) {
+    for (; k < nmax; k += 4) {
+      constexpr int UT = 4;
       const i32x4 f4 = read4(mylist, k);
-      f32x4 w[U];
+      f32x4 w[UT];
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
+      for (int u = 0; u < UT; ++u) {
         const bool v = k + u < n;
         w[u] = f32x4{0.f, 0.f, 0.f, 0.f};
         if (v && colok) w[u] = wtile[(int64_t)f4[u] * kTileCh];
       }
 #pragma unroll
-      for (int u = 0; u < U; ++u)
+      for (int u = 0; u < UT; ++u)
         if (k + u < n) acc += w[u];
     }
     if (pos < B && colok) __builtin_nontemporal_store(acc, out + pos * cols4 + col4);
