@@ -97,7 +97,7 @@ int sft_ft_fwd_f32_ex(const int32_t *idx, int64_t batch, int32_t max_active, con
 
 /*
  * Bytes of device workspace sft_ft_bwd_f32 needs for these sizes and flags.
- * May query the current device (sort tuning is per architecture).
+ * Host-only computation.
  * No reference counterpart: the reference takes its temporaries from torch
  * inside the call (FT/kernel.py:108-138).
  */

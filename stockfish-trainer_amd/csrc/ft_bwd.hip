@@ -2,8 +2,9 @@
 //
 // Default algorithm (SFT_BWD_SORTED), deterministic and in the reference's
 // summation order (FT/kernel.py:108-138, 167-186):
-//   1. stable radix sort of the flat slots s = b*K + k by feature key
-//      (inactive slots get key N and sort to the end); values are positions b.
+//   1. stable radix sort (ft_sort.hip) of the flat slots s = b*K + k by key
+//      (position chunk, feature); inactive slots sort to the end; values are
+//      positions b.
 //   2. seg_start[f] = first sorted slot with key >= f, for f = 0..N.
 //   3. one lane group per feature row: acc = 0, acc += grad[b] over the
 //      feature's positions in ascending order, then one store of the row
@@ -12,10 +13,6 @@
 // the position's grad row into dW[f] with fp32 atomics.
 // Bias grad (FT/kernel.py:269): per-block column partial sums, then a fixed-
 // order reduction of the partials; deterministic.
-#include <rocprim/device/device_radix_sort.hpp>
-#include <rocprim/iterator/counting_iterator.hpp>
-#include <rocprim/iterator/transform_iterator.hpp>
-
 #include <algorithm>
 
 #include "common.h"
@@ -23,47 +20,14 @@
 namespace sft {
 
 size_t index_lds_bytes(int G, int K);
+size_t slot_sort_workspace(int64_t M);
+int slot_sort(const int32_t *idx, int64_t M, int K, int64_t N, int chunk_rows, int nchunks, void *ws,
+              unsigned **keys_sorted, int **pos_sorted, hipStream_t s);
 
 namespace {
 
 constexpr int kBiasRowsPerBlock = 128;
 constexpr int kBiasMaxParts = 512;
-
-// Sort key of flat slot s = b * K + k: chunk(b) * N + f for an active slot,
-// nchunks * N for an inactive one.  With one chunk this is the feature itself.
-struct SortKey {
-  const int32_t *idx;
-  unsigned N;
-  int K;
-  int chunk_rows;
-  unsigned sentinel;
-  __host__ __device__ unsigned operator()(int s) const {
-    const unsigned v = (unsigned)idx[s];
-    return v < N ? (unsigned)((s / K) / chunk_rows) * N + v : sentinel;
-  }
-};
-struct SlotPosition {
-  int K;
-  __host__ __device__ int operator()(int s) const { return s / K; }
-};
-
-typedef rocprim::transform_iterator<rocprim::counting_iterator<int>, SortKey, unsigned> KeyIter;
-typedef rocprim::transform_iterator<rocprim::counting_iterator<int>, SlotPosition, int> PosIter;
-
-unsigned key_bits(int64_t maxkey) {
-  unsigned bits = 1;
-  while (((int64_t)1 << bits) <= maxkey) ++bits;  // keys lie in [0, maxkey]
-  return bits;
-}
-
-hipError_t run_sort(void *temp, size_t &temp_bytes, const int32_t *idx, int64_t M, int K, int64_t N, int chunk_rows,
-                    int nchunks, unsigned *keys_out, int *pos_out, hipStream_t s) {
-  const int64_t nk = (int64_t)nchunks * N;
-  KeyIter keys_in(rocprim::counting_iterator<int>(0), SortKey{idx, (unsigned)N, K, chunk_rows, (unsigned)nk});
-  PosIter pos_in(rocprim::counting_iterator<int>(0), SlotPosition{K});
-  return rocprim::radix_sort_pairs(temp, temp_bytes, keys_in, keys_out, pos_in, pos_out, (unsigned)M, 0u,
-                                   key_bits(nk), s);
-}
 
 // seg_start[k] for k in [0, N]: index of the first sorted key >= k (N = key count).
 __global__ __launch_bounds__(kBlock) void seg_offsets_kernel(const unsigned *__restrict__ keys, int64_t M, int64_t N,
@@ -196,20 +160,83 @@ __global__ __launch_bounds__(kBlock) void gather_rows_kernel(const int32_t *__re
 constexpr int kBwdTileCh = 8;  // float4 chunks per 32-column tile row
 constexpr int kBwdFeatPerBlock = kWavesPerBlock * (kWave / kBwdTileCh);  // 32
 
+#ifndef SFT_BWD_POS_LDS
+#define SFT_BWD_POS_LDS 4096
+#endif
+constexpr int kBwdPosLds = SFT_BWD_POS_LDS;  // staged positions per workgroup
+
+// Sums one lane group's positions from `list` (LDS or global) into acc.
+template <bool FROM_LDS>
+__device__ __forceinline__ void bwd_tile_sum(const int32_t *list, int n, int nmin, int nmax, int t, bool colok,
+                                             const f32x4 *__restrict__ gcol, f32x4 &acc) {
+  constexpr int U = SFT_BWD_TILED_U;
+  static_assert(U == kBwdTileCh, "one position per lane of the group");
+  int k = 0;
+  for (; k + U <= nmin; k += U) {
+    int b[U];
+    if (FROM_LDS) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) b[u] = list[k + u];
+    } else {
+      const int mine = list[k + t];
+#pragma unroll
+      for (int u = 0; u < U; ++u) b[u] = __shfl(mine, u, kBwdTileCh);
+    }
+    f32x4 w[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) w[u] = colok ? gcol[(int64_t)b[u] * kBwdTileCh] : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < U; ++u) acc += w[u];
+  }
+  for (; k < nmax; k += U) {
+    int b[U];
+    if (FROM_LDS) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) b[u] = (k + u < n) ? list[k + u] : 0;
+    } else {
+      const int mine = (k + t < n) ? list[k + t] : 0;
+#pragma unroll
+      for (int u = 0; u < U; ++u) b[u] = __shfl(mine, u, kBwdTileCh);
+    }
+    f32x4 w[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      w[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+      if (k + u < n && colok) w[u] = gcol[(int64_t)b[u] * kBwdTileCh];
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (k + u < n) acc += w[u];
+  }
+}
+
+// The 32 features of a workgroup are consecutive, so their position lists
+// form one contiguous range of the sorted array; it is copied to LDS with
+// coalesced loads and read from there, which keeps the position reads off the
+// in-order vector-memory counter the row loads wait on.  Ranges longer than
+// kBwdPosLds entries read their positions from global memory instead.
 __global__ __launch_bounds__(kBlock) void bwd_tiled_gather_kernel(const int32_t *__restrict__ seg,
                                                                   const int32_t *__restrict__ sorted_pos, int64_t N,
                                                                   const f32x4 *__restrict__ gt, int64_t B,
                                                                   int64_t cols4, f32x4 *__restrict__ dW, int first,
                                                                   int ntiles, int ngroups) {
-  constexpr int U = SFT_BWD_TILED_U;
+  __shared__ int spos[kBwdPosLds];
   const TileItem it = tile_sched_item(blockIdx.x, ntiles, ngroups);
-  if (it.tile >= ntiles) return;
+  if (it.tile >= ntiles) return;  // whole block: uniform
+  const int64_t fb = (int64_t)it.chunk * kBwdFeatPerBlock;
+  const int64_t fe = fb + kBwdFeatPerBlock < N ? fb + kBwdFeatPerBlock : N;
+  const int r0 = seg[fb], r1 = seg[fe];
+  const bool staged = (r1 - r0) <= kBwdPosLds;  // block-uniform
+  if (staged) {
+    for (int i = threadIdx.x; i < r1 - r0; i += kBlock) spos[i] = sorted_pos[r0 + i];
+    __syncthreads();
+  }
   const int wave = uniform(threadIdx.x / kWave);
   const int lane = threadIdx.x % kWave;
   const int g = lane / kBwdTileCh, t = lane % kBwdTileCh;
   const int64_t col4 = (int64_t)it.tile * kBwdTileCh + t;
   const bool colok = col4 < cols4;
-  const int64_t f = (int64_t)it.chunk * kBwdFeatPerBlock + wave * (kWave / kBwdTileCh) + g;
+  const int64_t f = fb + wave * (kWave / kBwdTileCh) + g;
   int s0 = 0, s1 = 0;
   if (f < N) {
     s0 = seg[f];
@@ -220,39 +247,14 @@ __global__ __launch_bounds__(kBlock) void bwd_tiled_gather_kernel(const int32_t 
   if (!first && !wave_has_work) return;             // nothing to add anywhere in the wave
   int nmin, nmax;
   group_minmax<kBwdTileCh>(n, nmin, nmax);
-  const int32_t *plist = sorted_pos + s0;
   const f32x4 *gcol = gt + (int64_t)it.tile * B * kBwdTileCh + t;
   f32x4 *d = dW + f * cols4 + col4;
   f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
   if (!first && n > 0 && f < N && colok) acc = *d;
-  // Positions are fetched 8 at a time, one per lane of the group, and
-  // broadcast inside the group, so a step costs one index load for 8 rows.
-  static_assert(U == kBwdTileCh, "one position per lane of the group");
-  int k = 0;
-  for (; k + U <= nmin; k += U) {
-    const int mine = plist[k + t];
-    f32x4 w[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int b = __shfl(mine, u, kBwdTileCh);
-      w[u] = colok ? gcol[(int64_t)b * kBwdTileCh] : f32x4{0.f, 0.f, 0.f, 0.f};
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) acc += w[u];
-  }
-  for (; k < nmax; k += U) {
-    const int mine = (k + t < n) ? plist[k + t] : 0;
-    f32x4 w[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int b = __shfl(mine, u, kBwdTileCh);
-      w[u] = f32x4{0.f, 0.f, 0.f, 0.f};
-      if (k + u < n && colok) w[u] = gcol[(int64_t)b * kBwdTileCh];
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u)
-      if (k + u < n) acc += w[u];
-  }
+  if (staged)
+    bwd_tile_sum<true>(spos + (s0 - r0), n, nmin, nmax, t, colok, gcol, acc);
+  else
+    bwd_tile_sum<false>(sorted_pos + s0, n, nmin, nmax, t, colok, gcol, acc);
   if (f >= N || !colok) return;
 #if SFT_BWD_NT_STORE
   if (first || n > 0) __builtin_nontemporal_store(acc, d);
@@ -415,7 +417,7 @@ void launch_gather(dim3 grid, hipStream_t s, const int32_t *seg_start, const int
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 struct BwdLayout {
-  size_t keys, pos, seg, partial, temp, temp_bytes, gt, total;
+  size_t sort, seg, partial, gt, total;
   int nparts;
 };
 
@@ -447,30 +449,18 @@ int make_layout(int64_t B, int K, int64_t N, int L, uint32_t flags, BwdLayout &l
   size_t off = 0;
   lay.partial = off;
   off = align256(off + (size_t)lay.nparts * (size_t)L * sizeof(float));
-  lay.keys = lay.pos = lay.seg = lay.temp = off;
-  lay.temp_bytes = 0;
+  lay.sort = lay.seg = lay.gt = off;
   if (!(flags & SFT_BWD_ATOMIC) && M > 0) {
     const int nc = sort_chunks(B, L, flags);
-    lay.keys = off;
-    off = align256(off + (size_t)M * sizeof(unsigned));
-    lay.pos = off;
-    off = align256(off + (size_t)M * sizeof(int));
+    lay.sort = off;
+    off = align256(off + slot_sort_workspace(M));
     lay.seg = off;
     off = align256(off + (size_t)(nc * N + 1) * sizeof(int32_t));
-    size_t tb = 0, tb1 = 0;
-    hipError_t e = run_sort(nullptr, tb, nullptr, M, K, N, (int)(nc > 1 ? half_rows(B) : std::max<int64_t>(B, 1)), nc,
-                            nullptr, nullptr, nullptr);
-    if (e == hipSuccess) e = run_sort(nullptr, tb1, nullptr, M, K, N, (int)std::max<int64_t>(B, 1), 1, nullptr,
-                                      nullptr, nullptr);
-    if (e != hipSuccess) return fail(SFT_EHIP, std::string("sort workspace query: ") + hipGetErrorString(e));
-    lay.temp = off;
-    lay.temp_bytes = std::max(tb, tb1);
-    off = align256(off + lay.temp_bytes);
-  }
-  lay.gt = off;
-  if (!(flags & SFT_BWD_ATOMIC) && M > 0 && sort_chunks(B, L, flags) > 1) {
-    const int64_t ntiles = ceil_div(L, 32);
-    off = align256(off + (size_t)(ntiles * B * 32) * sizeof(float));
+    lay.gt = off;
+    if (nc > 1) {
+      const int64_t ntiles = ceil_div(L, 32);
+      off = align256(off + (size_t)(ntiles * B * 32) * sizeof(float));
+    }
   }
   lay.total = off;
   return SFT_OK;
@@ -581,8 +571,6 @@ int bwd_f32(const int32_t *idx, int64_t B, int K, const float *grad, int64_t N, 
   }
 
   // ---- sorted (deterministic) weight grad ----
-  unsigned *keys = reinterpret_cast<unsigned *>(w + lay.keys);
-  int32_t *pos = reinterpret_cast<int32_t *>(w + lay.pos);
   int32_t *seg = reinterpret_cast<int32_t *>(w + lay.seg);
   if (M == 0) {
     if (!overwrite) return SFT_OK;  // nothing active: dW untouched
@@ -595,11 +583,11 @@ int bwd_f32(const int32_t *idx, int64_t B, int K, const float *grad, int64_t N, 
   const int nc = tiled ? sort_chunks(B, L, flags) : 1;
   const int chunk_rows = (int)(nc > 1 ? half_rows(B) : B);
   const int64_t nkeys = (int64_t)nc * N;
+  unsigned *keys = nullptr;
+  int32_t *pos = nullptr;
   {
     ProfScope prof(kProfBwdSort, s);
-    size_t tb = lay.temp_bytes;
-    hipError_t e = run_sort(w + lay.temp, tb, idx, M, K, N, chunk_rows, nc, keys, pos, s);
-    if (e != hipSuccess) return fail(SFT_EHIP, std::string("feature sort: ") + hipGetErrorString(e));
+    if ((rc = slot_sort(idx, M, K, N, chunk_rows, nc, w + lay.sort, &keys, &pos, s)) != SFT_OK) return rc;
   }
   {
     ProfScope prof(kProfBwdOffsets, s);
