@@ -57,6 +57,7 @@ extern "C" {
 /* sft_ft_fwd_i16 flags */
 #define SFT_Q16_ACC32 0x0u  /* exact int32 accumulation, then clamp            */
 #define SFT_Q16_WRAP16 0x1u /* int16 accumulator with wrapping adds, then clamp */
+#define SFT_Q16_ROWS 0x2u   /* sft_ft_fwd_i16_ex: always the row gather          */
 
 /* Version of this ABI (SFT_ABI_VERSION of the header the library was built with). */
 int sft_abi_version(void);
@@ -135,6 +136,26 @@ int sft_ft_fwd_i16(const int32_t *idx, int64_t batch, int32_t max_active, const 
                    const int32_t *psqt_weight, int32_t psqt_size, int16_t *out,
                    int32_t *psqt_out, int32_t clip_lo, int32_t clip_hi, uint32_t flags,
                    void *stream);
+
+/*
+ * Bytes of device workspace sft_ft_fwd_i16_ex uses (0 when the shape runs the
+ * row gather).  Host-only computation.  No reference counterpart.
+ */
+int sft_ft_fwd_i16_workspace_size(int64_t batch, int32_t max_active, int64_t num_inputs,
+                                  int32_t output_size, int32_t psqt_size, uint32_t flags,
+                                  size_t *bytes);
+
+/*
+ * int16 forward with a workspace: same results, bit for bit, as sft_ft_fwd_i16.
+ * Unless SFT_Q16_ROWS is set, shapes with output_size % 8 == 0, at least 8
+ * column tiles of 64 and psqt_size <= 8 copy the table into 64-column tiles in
+ * the workspace and gather them XCD by XCD from L2.
+ */
+int sft_ft_fwd_i16_ex(const int32_t *idx, int64_t batch, int32_t max_active,
+                      const int16_t *weight, int64_t num_inputs, int32_t output_size,
+                      const int16_t *bias, const int32_t *psqt_weight, int32_t psqt_size,
+                      int16_t *out, int32_t *psqt_out, int32_t clip_lo, int32_t clip_hi,
+                      void *workspace, size_t workspace_bytes, uint32_t flags, void *stream);
 
 /*
  * Export quantization on the device (src/model/quantize.py:83-84):

@@ -19,6 +19,11 @@ bool fwd_tiled_supported(int64_t N, int L, const void *W, const void *bias, cons
 int fwd_f32_tiled(const int32_t *idx, int64_t B, int K, const float *W, int64_t N, int L, const float *bias, float *out,
                   void *ws, size_t ws_bytes, hipStream_t s);
 int bwd_workspace(int64_t B, int K, int64_t N, int L, uint32_t flags, size_t *bytes);
+size_t fwd_i16_tiled_workspace(int64_t N, int L);
+bool fwd_i16_tiled_supported(int64_t N, int L, int P, const void *W, const void *bias, const void *out);
+int fwd_i16_tiled(const int32_t *idx, int64_t B, int K, const int16_t *W, int64_t N, int L, const int16_t *bias,
+                  const int32_t *psqt, int P, int16_t *out, int32_t *psqt_out, int lo, int hi, int wrap16, void *ws,
+                  size_t ws_bytes, hipStream_t s);
 int bwd_f32(const int32_t *idx, int64_t B, int K, const float *grad, int64_t N, int L, float *dW, float *db,
             void *ws, size_t ws_bytes, uint32_t flags, hipStream_t s);
 
@@ -103,7 +108,7 @@ struct ActiveScope {
 const char *const kKindNames[kProfNumKinds] = {
     "fwd_f32_gather",   "bwd_feature_sort",  "bwd_segment_offsets", "bwd_feature_gather", "bwd_bias_partial",
     "bwd_bias_final",   "bwd_atomic_scatter", "bwd_zero_fill",      "fwd_i16_gather",     "quantize_i16",
-    "fwd_tile_relayout", "fwd_f32_tiled_gather", "bwd_tiled_gather", "bwd_grad_relayout",
+    "fwd_tile_relayout", "fwd_f32_tiled_gather", "bwd_tiled_gather", "bwd_grad_relayout", "fwd_i16_tiled_gather",
 };
 }  // namespace
 
@@ -214,25 +219,69 @@ int sft_ft_bwd_f32(const int32_t *idx, int64_t batch, int32_t max_active, const 
                  workspace_bytes, flags, (hipStream_t)stream);
 }
 
+static int check_i16_args(const char *who, const int32_t *idx, int64_t batch, int32_t max_active,
+                          const int16_t *weight, int64_t num_inputs, int32_t output_size, const int16_t *bias,
+                          const int32_t *psqt_weight, int32_t psqt_size, int16_t *out, int32_t *psqt_out,
+                          int32_t clip_lo, int32_t clip_hi, uint32_t flags) {
+  std::string why;
+  const std::string w(who);
+  if (bad_sizes(batch, max_active, num_inputs, output_size, why)) return fail(SFT_EINVAL, w + ": " + why);
+  if (max_active >= 65536) return fail(SFT_EINVAL, w + ": max_active must be < 65536");
+  if (!weight || !bias || (batch > 0 && (!idx || !out))) return fail(SFT_EINVAL, w + ": null pointer");
+  if ((psqt_weight == nullptr) != (psqt_out == nullptr))
+    return fail(SFT_EINVAL, w + ": psqt_weight and psqt_out must both be set or both be NULL");
+  if (psqt_weight && (psqt_size <= 0 || psqt_size > kWave)) return fail(SFT_EINVAL, w + ": psqt_size must be in [1, 64]");
+  if (clip_lo > clip_hi || clip_lo < -32768 || clip_hi > 32767)
+    return fail(SFT_EINVAL, w + ": need -32768 <= clip_lo <= clip_hi <= 32767");
+  if (flags & ~(SFT_Q16_WRAP16 | SFT_Q16_ROWS)) return fail(SFT_EINVAL, w + ": unknown flags");
+  return SFT_OK;
+}
+
 int sft_ft_fwd_i16(const int32_t *idx, int64_t batch, int32_t max_active, const int16_t *weight, int64_t num_inputs,
                    int32_t output_size, const int16_t *bias, const int32_t *psqt_weight, int32_t psqt_size,
                    int16_t *out, int32_t *psqt_out, int32_t clip_lo, int32_t clip_hi, uint32_t flags, void *stream) {
   clear_error();
-  std::string why;
-  if (bad_sizes(batch, max_active, num_inputs, output_size, why)) return fail(SFT_EINVAL, "sft_ft_fwd_i16: " + why);
-  if (max_active >= 65536) return fail(SFT_EINVAL, "sft_ft_fwd_i16: max_active must be < 65536");
-  if (!weight || !bias || (batch > 0 && (!idx || !out))) return fail(SFT_EINVAL, "sft_ft_fwd_i16: null pointer");
-  if ((psqt_weight == nullptr) != (psqt_out == nullptr))
-    return fail(SFT_EINVAL, "sft_ft_fwd_i16: psqt_weight and psqt_out must both be set or both be NULL");
-  if (psqt_weight && (psqt_size <= 0 || psqt_size > kWave))
-    return fail(SFT_EINVAL, "sft_ft_fwd_i16: psqt_size must be in [1, 64]");
-  if (clip_lo > clip_hi || clip_lo < -32768 || clip_hi > 32767)
-    return fail(SFT_EINVAL, "sft_ft_fwd_i16: need -32768 <= clip_lo <= clip_hi <= 32767");
-  if (flags & ~SFT_Q16_WRAP16) return fail(SFT_EINVAL, "sft_ft_fwd_i16: unknown flags");
+  int rc = check_i16_args("sft_ft_fwd_i16", idx, batch, max_active, weight, num_inputs, output_size, bias, psqt_weight,
+                          psqt_size, out, psqt_out, clip_lo, clip_hi, flags);
+  if (rc != SFT_OK) return rc;
   if (batch == 0) return SFT_OK;
   return fwd_i16(idx, batch, max_active, weight, num_inputs, output_size, bias, psqt_weight,
                  psqt_weight ? psqt_size : 0, out, psqt_out, clip_lo, clip_hi, (flags & SFT_Q16_WRAP16) ? 1 : 0,
                  (hipStream_t)stream);
+}
+
+int sft_ft_fwd_i16_workspace_size(int64_t batch, int32_t max_active, int64_t num_inputs, int32_t output_size,
+                                  int32_t psqt_size, uint32_t flags, size_t *bytes) {
+  clear_error();
+  std::string why;
+  if (!bytes) return fail(SFT_EINVAL, "sft_ft_fwd_i16_workspace_size: null pointer");
+  if (bad_sizes(batch, max_active, num_inputs, output_size, why))
+    return fail(SFT_EINVAL, "sft_ft_fwd_i16_workspace_size: " + why);
+  if (flags & ~(SFT_Q16_WRAP16 | SFT_Q16_ROWS)) return fail(SFT_EINVAL, "sft_ft_fwd_i16_workspace_size: unknown flags");
+  const bool tiled = !(flags & SFT_Q16_ROWS) &&
+                     fwd_i16_tiled_supported(num_inputs, output_size, psqt_size, nullptr, nullptr, nullptr);
+  *bytes = tiled ? fwd_i16_tiled_workspace(num_inputs, output_size) : 0;
+  return SFT_OK;
+}
+
+int sft_ft_fwd_i16_ex(const int32_t *idx, int64_t batch, int32_t max_active, const int16_t *weight,
+                      int64_t num_inputs, int32_t output_size, const int16_t *bias, const int32_t *psqt_weight,
+                      int32_t psqt_size, int16_t *out, int32_t *psqt_out, int32_t clip_lo, int32_t clip_hi,
+                      void *workspace, size_t workspace_bytes, uint32_t flags, void *stream) {
+  clear_error();
+  int rc = check_i16_args("sft_ft_fwd_i16_ex", idx, batch, max_active, weight, num_inputs, output_size, bias,
+                          psqt_weight, psqt_size, out, psqt_out, clip_lo, clip_hi, flags);
+  if (rc != SFT_OK) return rc;
+  if (batch == 0) return SFT_OK;
+  const int P = psqt_weight ? psqt_size : 0;
+  const int wrap = (flags & SFT_Q16_WRAP16) ? 1 : 0;
+  const bool tiled = !(flags & SFT_Q16_ROWS) && fwd_i16_tiled_supported(num_inputs, output_size, P, weight, bias, out) &&
+                     workspace != nullptr && workspace_bytes >= fwd_i16_tiled_workspace(num_inputs, output_size);
+  if (tiled)
+    return fwd_i16_tiled(idx, batch, max_active, weight, num_inputs, output_size, bias, psqt_weight, P, out, psqt_out,
+                         clip_lo, clip_hi, wrap, workspace, workspace_bytes, (hipStream_t)stream);
+  return fwd_i16(idx, batch, max_active, weight, num_inputs, output_size, bias, psqt_weight, P, out, psqt_out, clip_lo,
+                 clip_hi, wrap, (hipStream_t)stream);
 }
 
 int sft_quantize_i16(const float *x, int64_t n, float scale, int16_t *out, void *stream) {

@@ -43,6 +43,7 @@ enum ProfKind : int {
   kProfFwdTiled,
   kProfBwdTiled,
   kProfBwdRelayout,
+  kProfFwdI16Tiled,
   kProfNumKinds
 };
 struct ProfScope {

@@ -309,6 +309,72 @@ __global__ __launch_bounds__(kBlock) void fwd_tiled_kernel(const int32_t *__rest
   }
 }
 
+// ----------------------------------------------------- tiled int16 gather ----
+// Same schedule as the fp32 tiled gather over an int16 table re-laid out in
+// 64-column tiles (128 B per row; 2.9 MB per tile at N = 22 528).  Lane t of
+// an 8-lane group owns 8 int16 columns, widened to int32 before adding (exact);
+// PSQT columns (P <= 8 int32 per row) are gathered by the tile-0 workgroups.
+__global__ __launch_bounds__(kBlock) void fwd_i16_tiled_kernel(const int32_t *__restrict__ idx, int64_t B, int K,
+                                                               int N, const i16x8 *__restrict__ Wt, int64_t cols8,
+                                                               const i16x8 *__restrict__ bias,
+                                                               const int32_t *__restrict__ psqt, int P,
+                                                               i16x8 *__restrict__ out, int32_t *__restrict__ psqt_out,
+                                                               int clip_lo, int clip_hi, int wrap16, int kpad,
+                                                               int ntiles, int nchunks) {
+  constexpr int U = 4;
+  constexpr int PPW = kWave / kTileCh;
+  extern __shared__ int smem[];
+  const TileItem it = tile_sched_item(blockIdx.x, ntiles, nchunks);
+  if (it.tile >= ntiles) return;
+  const int wave = uniform(threadIdx.x / kWave);
+  const int lane = threadIdx.x % kWave;
+  int *list = smem + wave * PPW * kpad;
+  int *count = smem + kWavesPerBlock * PPW * kpad + wave * PPW;
+  const int g = lane / kTileCh, t = lane % kTileCh;
+  const int64_t col = (int64_t)it.tile * kTileCh + t;
+  const bool colok = col < cols8;
+  const bool do_psqt = psqt != nullptr && it.tile == 0 && t < P;
+  const i16x8 *wtile = Wt + (int64_t)it.tile * N * kTileCh + t;
+  const i32x8 b8 = colok ? Q16<i16x8>::widen(bias[col]) : (i32x8)0;
+
+  for (int round = 0; round < kTiledRounds; ++round) {
+    const int64_t pos0 = (int64_t)it.chunk * kTiledPosPerBlock + round * kTiledPosPerRound + wave * PPW;
+    compact_rows(idx, B, K, N, pos0, PPW, list, kpad, count);
+    __syncthreads();
+    const int64_t pos = pos0 + g;
+    const int n = count[g];
+    int nmin, nmax;
+    group_minmax<kTileCh>(n, nmin, nmax);
+    (void)nmin;
+    const int *mylist = list + g * kpad;
+    i32x8 acc = b8;
+    int pacc = 0;
+    for (int k = 0; k < nmax; k += U) {
+      const i32x4 f4 = read4(mylist, k);
+      i16x8 w[U];
+      int pw[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const bool v = k + u < n;
+        w[u] = (i16x8)0;
+        if (v && colok) w[u] = wtile[(int64_t)f4[u] * kTileCh];
+        pw[u] = 0;
+        if (v && do_psqt) pw[u] = psqt[(int64_t)f4[u] * P + t];
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        acc += Q16<i16x8>::widen(w[u]);
+        pacc += pw[u];
+      }
+    }
+    if (pos < B) {
+      if (colok) __builtin_nontemporal_store(Q16<i16x8>::finish(acc, clip_lo, clip_hi, wrap16), out + pos * cols8 + col);
+      if (do_psqt) psqt_out[pos * P + t] = pacc;
+    }
+    __syncthreads();
+  }
+}
+
 // --------------------------------------------------------------- quantize ----
 __global__ __launch_bounds__(kBlock) void quantize_i16_kernel(const float *__restrict__ x, int64_t n, float scale,
                                                               int16_t *__restrict__ out) {
@@ -406,8 +472,11 @@ size_t fwd_tiled_workspace(int64_t N, int L) {
   return (size_t)(ntiles * N * kTileF) * sizeof(float);
 }
 
+#ifndef SFT_FWD_TILE_MAX_BYTES
+#define SFT_FWD_TILE_MAX_BYTES (64ll << 20)
+#endif
 bool fwd_tiled_supported(int64_t N, int L, const void *W, const void *bias, const void *out) {
-  return L % 4 == 0 && L >= kTileF * kXcds && N * kTileF * 4 <= (int64_t)(3u << 20) &&
+  return L % 4 == 0 && L >= kTileF * kXcds && N * kTileF * 4 <= (int64_t)(SFT_FWD_TILE_MAX_BYTES) &&
          (uintptr_t)W % 16 == 0 && (uintptr_t)bias % 16 == 0 && (uintptr_t)out % 16 == 0;
 }
 
@@ -436,6 +505,46 @@ int fwd_f32_tiled(const int32_t *idx, int64_t B, int K, const float *W, int64_t 
                        reinterpret_cast<const f32x4 *>(bias), reinterpret_cast<f32x4 *>(out), kpad, ntiles, nchunks);
   }
   return check_launch("sft_ft_fwd_f32_ex (tiled gather)");
+}
+
+size_t fwd_i16_tiled_workspace(int64_t N, int L) {
+  if (L % 8 != 0) return 0;
+  const int64_t ntiles = ceil_div(L / 8, kTileCh);
+  return (size_t)(ntiles * N * kTileCh) * 16;
+}
+
+bool fwd_i16_tiled_supported(int64_t N, int L, int P, const void *W, const void *bias, const void *out) {
+  return L % 8 == 0 && ceil_div(L / 8, kTileCh) >= kXcds && N * 128 <= (int64_t)(SFT_FWD_TILE_MAX_BYTES) && P <= 8 &&
+         (uintptr_t)W % 16 == 0 && (uintptr_t)bias % 16 == 0 && (uintptr_t)out % 16 == 0;
+}
+
+int fwd_i16_tiled(const int32_t *idx, int64_t B, int K, const int16_t *W, int64_t N, int L, const int16_t *bias,
+                  const int32_t *psqt, int P, int16_t *out, int32_t *psqt_out, int lo, int hi, int wrap16, void *ws,
+                  size_t ws_bytes, hipStream_t s) {
+  if (ws_bytes < fwd_i16_tiled_workspace(N, L) || ws == nullptr || (uintptr_t)ws % 256 != 0)
+    return fail(SFT_EWORKSPACE, "sft_ft_fwd_i16_ex: workspace smaller than sft_ft_fwd_i16_workspace_size() "
+                                "or not 256-byte aligned");
+  const int64_t cols8 = L / 8;
+  const int ntiles = (int)ceil_div(cols8, kTileCh);
+  const int kpad = round_up4(K);
+  const size_t lds = index_lds_bytes(kTileCh, K);
+  if (lds > kMaxIndexLds) return fail(SFT_EUNSUPPORTED, "sft_ft_fwd_i16_ex: max_active too large for the LDS index lists");
+  i16x8 *wt = static_cast<i16x8 *>(ws);
+  {
+    ProfScope prof(kProfFwdRelayout, s);
+    launch_tile_relayout(reinterpret_cast<const f32x4 *>(W), N, cols8, reinterpret_cast<f32x4 *>(wt), s);
+  }
+  int rc = check_launch("sft_ft_fwd_i16_ex (relayout)");
+  if (rc != SFT_OK) return rc;
+  const int nchunks = (int)ceil_div(B, kTiledPosPerBlock);
+  const int64_t blocks = tile_sched_items_per_xcd(ntiles, nchunks) * kXcds;
+  {
+    ProfScope prof(kProfFwdI16Tiled, s);
+    hipLaunchKernelGGL(fwd_i16_tiled_kernel, dim3((unsigned)blocks), dim3(kBlock), lds, s, idx, B, K, (int)N, wt,
+                       cols8, reinterpret_cast<const i16x8 *>(bias), psqt, P, reinterpret_cast<i16x8 *>(out),
+                       psqt_out, lo, hi, wrap16, kpad, ntiles, nchunks);
+  }
+  return check_launch("sft_ft_fwd_i16_ex (tiled gather)");
 }
 
 int fwd_i16(const int32_t *idx, int64_t B, int K, const int16_t *W, int64_t N, int L, const int16_t *bias,

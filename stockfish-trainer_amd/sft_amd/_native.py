@@ -27,6 +27,7 @@ SFT_BWD_ATOMIC = 0x10
 SFT_BWD_ROWS = 0x2
 SFT_Q16_ACC32 = 0x0
 SFT_Q16_WRAP16 = 0x1
+SFT_Q16_ROWS = 0x2
 
 _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -49,6 +50,11 @@ SIGNATURES = {
     "sft_ft_fwd_i16": (
         ctypes.c_int,
         [_vp, _i64, _i32, _vp, _i64, _i32, _vp, _vp, _i32, _vp, _vp, _i32, _i32, _u32, _vp]),
+    "sft_ft_fwd_i16_workspace_size": (
+        ctypes.c_int, [_i64, _i32, _i64, _i32, _i32, _u32, ctypes.POINTER(ctypes.c_size_t)]),
+    "sft_ft_fwd_i16_ex": (
+        ctypes.c_int,
+        [_vp, _i64, _i32, _vp, _i64, _i32, _vp, _vp, _i32, _vp, _vp, _i32, _i32, _vp, ctypes.c_size_t, _u32, _vp]),
     "sft_quantize_i16": (ctypes.c_int, [_vp, _i64, ctypes.c_float, _vp, _vp]),
     "sft_prof_enable": (ctypes.c_int, [ctypes.c_int]),
     "sft_prof_num_kinds": (ctypes.c_int, []),
@@ -186,7 +192,12 @@ def ft_bwd_f32(idx: torch.Tensor, weight_grad: torch.Tensor, bias_grad: torch.Te
 
 def ft_fwd_i16(idx: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor, out: torch.Tensor,
                psqt_weight: torch.Tensor | None = None, psqt_out: torch.Tensor | None = None,
-               clip_lo: int = 0, clip_hi: int = 127, wrap16: bool = False) -> None:
+               clip_lo: int = 0, clip_hi: int = 127, wrap16: bool = False, rows: bool = False) -> None:
+    """int16 forward (exact): out = clamp(bias + sum of rows), psqt_out = sum of PSQT rows.
+
+    The tiled gather runs when the shape allows it (workspace from torch);
+    rows=True forces the row gather.
+    """
     _require(idx.dim() == 2 and idx.dtype == torch.int32, "idx must be int32 [B, K]")
     _require(weight.dim() == 2 and weight.dtype == torch.int16, "weight must be int16 [N, L]")
     B, K = idx.shape
@@ -203,11 +214,20 @@ def ft_fwd_i16(idx: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor, out:
         _require(psqt_out.shape == (B, P) and psqt_out.dtype == torch.int32, "psqt_out must be int32 [B, P]")
         tensors += [psqt_weight, psqt_out]
     _on_gpu(idx.device, *tensors)
-    flags = SFT_Q16_WRAP16 if wrap16 else SFT_Q16_ACC32
+    flags = (SFT_Q16_WRAP16 if wrap16 else SFT_Q16_ACC32) | (SFT_Q16_ROWS if rows else 0)
+    key = ("i16", idx.device.index, B, K, N, L, P, flags)
+    nbytes = _ws_cache.get(key)
+    if nbytes is None:
+        n = ctypes.c_size_t(0)
+        _check(lib().sft_ft_fwd_i16_workspace_size(B, K, N, L, P, flags, ctypes.byref(n)),
+               "sft_ft_fwd_i16_workspace_size")
+        nbytes = _ws_cache[key] = int(n.value)
+    ws, ptr = _workspace(nbytes, idx.device)
     with torch.cuda.device(idx.device):
-        _check(lib().sft_ft_fwd_i16(_ptr(idx), B, K, _ptr(weight), N, L, _ptr(bias), _ptr(psqt_weight), P,
-                                    _ptr(out), _ptr(psqt_out), clip_lo, clip_hi, flags, _stream(idx.device)),
-               "sft_ft_fwd_i16")
+        _check(lib().sft_ft_fwd_i16_ex(_ptr(idx), B, K, _ptr(weight), N, L, _ptr(bias), _ptr(psqt_weight), P,
+                                       _ptr(out), _ptr(psqt_out), clip_lo, clip_hi, ptr, nbytes, flags,
+                                       _stream(idx.device)), "sft_ft_fwd_i16_ex")
+    del ws
 
 
 def quantize_i16(x: torch.Tensor, scale: float) -> torch.Tensor:

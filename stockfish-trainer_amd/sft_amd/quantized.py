@@ -18,14 +18,14 @@ from . import _native
 
 def quantized_ft_forward(idx: torch.Tensor, weight_q: torch.Tensor, bias_q: torch.Tensor,
                          psqt_q: torch.Tensor | None = None, clip_lo: int = 0, clip_hi: int = 127,
-                         wrap16: bool = False):
+                         wrap16: bool = False, rows: bool = False):
     """One perspective: (out int16 [B, L], psqt_out int32 [B, P] or None)."""
     B = idx.shape[0]
     out = torch.empty(B, weight_q.shape[1], dtype=torch.int16, device=idx.device)
     psqt_out = None
     if psqt_q is not None:
         psqt_out = torch.empty(B, psqt_q.shape[1], dtype=torch.int32, device=idx.device)
-    _native.ft_fwd_i16(idx, weight_q, bias_q, out, psqt_q, psqt_out, clip_lo, clip_hi, wrap16)
+    _native.ft_fwd_i16(idx, weight_q, bias_q, out, psqt_q, psqt_out, clip_lo, clip_hi, wrap16, rows)
     return out, psqt_out
 
 

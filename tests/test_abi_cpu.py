@@ -36,12 +36,12 @@ def test_abi_version_matches_header():
 
 def test_flag_values_match_header():
     text = open(HEADER).read()
-    for name in ("SFT_BWD_OVERWRITE", "SFT_BWD_ATOMIC", "SFT_BWD_ROWS", "SFT_FWD_ROWS", "SFT_Q16_WRAP16"):
+    for name in ("SFT_BWD_OVERWRITE", "SFT_BWD_ATOMIC", "SFT_BWD_ROWS", "SFT_FWD_ROWS", "SFT_Q16_WRAP16", "SFT_Q16_ROWS"):
         m = re.search(rf"#define {name} (0x[0-9a-fA-F]+)u", text)
         assert int(m.group(1), 16) == getattr(_native, name)
 
 
-P = ctypes.c_void_p(0x1000)  # never dereferenced: every call below fails validation first
+P = ctypes.c_void_p(0x1000)  # never dereferenced: every call below must fail validation before any launch
 
 
 @pytest.mark.parametrize("args,needle", [
@@ -87,7 +87,7 @@ def test_i16_rejects():
     assert lib.sft_ft_fwd_i16(*a) == -1 and "clip" in _native.last_error()
     a = list(base); a[2] = 70000
     assert lib.sft_ft_fwd_i16(*a) == -1 and "65536" in _native.last_error()
-    a = list(base); a[13] = 2
+    a = list(base); a[13] = 4  # not a defined flag bit
     assert lib.sft_ft_fwd_i16(*a) == -1 and "flags" in _native.last_error()
 
 

@@ -26,17 +26,20 @@ def test_q16_fixture():
 
 @pytest.mark.parametrize("seed,B,N,K,L,P", [
     (1, 50, 300, 32, 1040, 8), (2, 77, 64, 7, 13, 3), (3, 129, 1000, 160, 256, 0),
-    (4, 1000, 22528, 32, 128, 8), (5, 3, 10, 4, 2104, 8), (6, 40, 100, 32, 520, 64)])
+    (4, 1000, 22528, 32, 128, 8), (5, 3, 10, 4, 2104, 8), (6, 40, 100, 32, 520, 64),
+    (7, 500, 2000, 32, 512, 8), (8, 300, 700, 13, 1040, 3)])
 @pytest.mark.parametrize("wrap16", [False, True])
-def test_q16_matches_oracle(seed, B, N, K, L, P, wrap16):
-    announce(f"q16 seed={seed} B={B} N={N} K={K} L={L} P={P} wrap16={wrap16}")
+@pytest.mark.parametrize("rows", [False, True])
+def test_q16_matches_oracle(seed, B, N, K, L, P, wrap16, rows):
+    announce(f"q16 seed={seed} B={B} N={N} K={K} L={L} P={P} wrap16={wrap16} rows={rows}")
     g = np.random.default_rng(seed)
     idx = workloads.make_indices(g, B, N, K, 0, K, sort=False)
     Wq = g.integers(-3000, 3000, size=(N, L)).astype(np.int16)
     bq = g.integers(-3000, 3000, size=L).astype(np.int16)
     ps = g.integers(-10**6, 10**6, size=(N, P)).astype(np.int32) if P else None
     for lo, hi in ((0, 127), (-32768, 32767), (-100, 255)):
-        out, pout = quantized_ft_forward(dev(idx), dev(Wq), dev(bq), None if ps is None else dev(ps), lo, hi, wrap16)
+        out, pout = quantized_ft_forward(dev(idx), dev(Wq), dev(bq), None if ps is None else dev(ps), lo, hi, wrap16,
+                                         rows)
         ro, rp = ft_oracle.fwd_i16(idx, Wq, bq, ps, lo, hi, wrap16)
         assert np.array_equal(host(out), ro)
         if P:
@@ -53,6 +56,8 @@ def test_full_workload_q16(scale):
     ro, rp = ft_oracle.fwd_i16(d["idx_w"], d["Wq"], d["bq"], d["psqt"], 0, 127, False)
     assert np.array_equal(host(ow), ro) and np.array_equal(host(pw), rp)
     assert np.array_equal(host(ob), ro[::-1]) and np.array_equal(host(pb), rp[::-1])
+    o2, p2 = quantized_ft_forward(dev(d["idx_w"]), dev(d["Wq"]), dev(d["bq"]), dev(d["psqt"]), 0, 127, rows=True)
+    assert np.array_equal(host(o2), ro) and np.array_equal(host(p2), rp)
 
 
 def test_device_quantizer_matches_oracle():
