@@ -111,6 +111,61 @@ def cpu_baseline(w, d, seconds: float) -> dict:
     }
 
 
+def bench_q16(args, w, dev) -> int:
+    """int16 inference forward of both perspectives (the quantized workload): one
+    step = two tiled int16 gathers (with their table re-layouts) + PSQT columns."""
+    import torch
+
+    from sft_amd import _native, workloads
+    from sft_amd.quantized import QuantizedFeatureTransformer
+
+    log(f"[bench] generating {w.name}: B={w.B} N={w.N} K={w.K} active U[{w.lo},{w.hi}] L={w.L} int16")
+    d = workloads.make_q16_inputs(w)
+    d["idx_b"] = workloads.make_indices(workloads.rng(w.wid, workloads.S_BLACK), w.B, w.N, w.K, w.lo, w.hi)
+    qft = QuantizedFeatureTransformer(*(torch.from_numpy(d[k]).to(dev) for k in ("Wq", "bq", "psqt")), 0, 127)
+    iw = torch.from_numpy(d["idx_w"]).to(dev)
+    ib = torch.from_numpy(d["idx_b"]).to(dev)
+    for _ in range(args.warmup):
+        qft(iw, ib)
+    torch.cuda.synchronize()
+    _native.prof_enable(True)
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(args.steps):
+        qft(iw, ib)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / args.steps
+    prof = _native.prof_collect()
+    _native.prof_enable(False)
+    step_bytes = sum(workloads.q16_fwd_bytes(i, w.N, w.L, w.psqt) for i in (d["idx_w"], d["idx_b"]))
+    kern = {k: {"avg_ms": t / c, "launches_per_step": c / args.steps} for k, (t, c) in prof.items()}
+    for k, v in kern.items():
+        log(f"[bench]   {k:22s} {v['avg_ms']:8.4f} ms x {v['launches_per_step']:.0f}/step")
+    gather = [k for k in prof if "i16" in k][0]
+    g_avg = prof[gather][0] / prof[gather][1]
+    per_launch = step_bytes / 2
+    achieved = per_launch / (g_avg * 1e-3) / 1e9
+    result = {
+        "metric": "int16 FT forward positions/sec (both perspectives) @B=65536,L1=1040",
+        "value": w.B / (ms * 1e-3), "unit": "positions/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "int16", "data": "synthetic",
+        "config": {"workload": w.name, "feature_set": w.feature_set, "batch": w.B, "num_inputs": w.N,
+                   "max_active": w.K, "active": [w.lo, w.hi], "output_size": w.L, "psqt": w.psqt,
+                   "quant_scale": 127, "clip": [0, 127], "parallelism": "single-gpu"},
+        "step_bytes": step_bytes,
+        "roofline": {"kernel": gather, "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS, "traffic": load_traffic(w.name, gather),
+                     "algorithmic_bytes_per_launch": per_launch, "avg_launch_ms": g_avg},
+        "kernels": kern,
+        "cpu_baseline": None,
+    }
+    print(json.dumps(result), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -135,11 +190,10 @@ def main() -> int:
     from src.model.modules.feature_transformer import kernel as ftk
 
     w = workloads.WORKLOADS[args.workload]
-    if w.quantized:
-        print("the int16 workload is forward-only; use tests or --workload 0..3", file=sys.stderr)
-        return 2
     dev = torch.device("cuda:0")
     _native.lib()  # fail loudly if the library is missing
+    if w.quantized:
+        return bench_q16(args, w, dev)
     log(f"[bench] generating {w.name}: B={w.B} N={w.N} K={w.K} active U[{w.lo},{w.hi}] L={w.L}")
     d = workloads.make_fp32_inputs(w)
     iw = torch.from_numpy(d["idx_w"]).to(dev)
