@@ -22,16 +22,30 @@ namespace sft {
 size_t index_lds_bytes(int G, int K);
 size_t slot_sort_workspace(int64_t M);
 int slot_sort(const int32_t *idx, int64_t M, int K, int64_t N, int chunk_rows, int nchunks, void *ws,
-              unsigned **keys_sorted, int **pos_sorted, hipStream_t s);
+              unsigned **keys_sorted, int **pos_sorted, unsigned **digit_totals, int *digit_count,
+              hipStream_t s);
 
 namespace {
 
 constexpr int kBiasRowsPerBlock = 128;
 constexpr int kBiasMaxParts = 512;
 
-// seg_start[k] for k in [0, N]: index of the first sorted key >= k (N = key count).
-__global__ __launch_bounds__(kBlock) void seg_offsets_kernel(const unsigned *__restrict__ keys, int64_t M, int64_t N,
+// seg_start[k] for k in [0, N]: index of the first sorted key >= k, N = key
+// count.  The sorted array holds the active slots only; their number is the
+// sum of the sort's last digit totals (read here, on the device).
+__global__ __launch_bounds__(kBlock) void seg_offsets_kernel(const unsigned *__restrict__ keys, int64_t N,
+                                                             const unsigned *__restrict__ totals, int ntot,
                                                              int32_t *__restrict__ seg_start) {
+  __shared__ unsigned red[kBlock];
+  unsigned v = 0;
+  for (int d = threadIdx.x; d < ntot; d += kBlock) v += totals[d];
+  red[threadIdx.x] = v;
+  __syncthreads();
+  for (int off = kBlock / 2; off > 0; off >>= 1) {
+    if ((int)threadIdx.x < off) red[threadIdx.x] += red[threadIdx.x + off];
+    __syncthreads();
+  }
+  const int64_t M = red[0];
   const int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
   if (i > M) return;
   const int64_t cur = i < M ? (int64_t)keys[i] : N + 1;
@@ -583,16 +597,18 @@ int bwd_f32(const int32_t *idx, int64_t B, int K, const float *grad, int64_t N, 
   const int nc = tiled ? sort_chunks(B, L, flags) : 1;
   const int chunk_rows = (int)(nc > 1 ? half_rows(B) : B);
   const int64_t nkeys = (int64_t)nc * N;
-  unsigned *keys = nullptr;
+  unsigned *keys = nullptr, *totals = nullptr;
   int32_t *pos = nullptr;
+  int ntot = 0;
   {
     ProfScope prof(kProfBwdSort, s);
-    if ((rc = slot_sort(idx, M, K, N, chunk_rows, nc, w + lay.sort, &keys, &pos, s)) != SFT_OK) return rc;
+    if ((rc = slot_sort(idx, M, K, N, chunk_rows, nc, w + lay.sort, &keys, &pos, &totals, &ntot, s)) != SFT_OK)
+      return rc;
   }
   {
     ProfScope prof(kProfBwdOffsets, s);
-    hipLaunchKernelGGL(seg_offsets_kernel, dim3((unsigned)ceil_div(M + 1, kBlock)), dim3(kBlock), 0, s, keys, M, nkeys,
-                       seg);
+    hipLaunchKernelGGL(seg_offsets_kernel, dim3((unsigned)ceil_div(M + 1, kBlock)), dim3(kBlock), 0, s, keys, nkeys,
+                       totals, ntot, seg);
     if ((rc = check_launch("segment offsets")) != SFT_OK) return rc;
   }
   if (tiled) {

@@ -1,17 +1,20 @@
 // Stable LSD radix sort of the backward's flat index slots, for gfx950.
 //
-// Sorts the B*K slots s = b*K + k by key (SlotKey: chunk(b) * N + feature for
-// an active slot, a sentinel past every real key otherwise) carrying the slot's
-// position b, stably, so each key's positions come out in ascending order.
-// 8-bit digits, least significant first; each pass is
-//   upsweep:   per 2048-slot tile, a 256-bin digit histogram;
+// Sorts the active slots s = b*K + k (0 <= idx[s] < N) by key
+// chunk(b) * N + feature, carrying the slot's position b, stably, so each
+// key's positions come out in ascending order; inactive slots are dropped by
+// the first pass.  RB-bit digits (8, or 9 when two 9-bit passes cover a key
+// that 8-bit digits would need three for), least significant first; each pass:
+//   upsweep:   per 2048-slot tile, a 2^RB-bin digit histogram;
 //   scan:      per digit, an exclusive scan of its tile counts and the digit
 //              total; a digit's base is the scan of the totals (done in the
 //              downsweep), so (digit, tile) starts at base + its tile prefix;
 //   downsweep: per tile, stable ranks (digit-major, then slot order) from
-//              wave-wide match masks (8 ballots) and per-wave digit counts,
+//              wave-wide match masks (RB ballots) and per-wave digit counts,
 //              the tile reordered in LDS, then written out as contiguous runs.
-// The first pass reads the keys straight from the index matrix.
+// The first pass reads the keys straight from the index matrix.  Passes after
+// the first, and the segment-offset kernel, take the number of active slots
+// from the previous scan's digit totals, on the device.
 #include <algorithm>
 
 #include "common.h"
@@ -20,10 +23,9 @@ namespace sft {
 
 namespace {
 
-constexpr int kRadixBits = 8;
-constexpr int kRadix = 1 << kRadixBits;
 constexpr int kSortItems = 8;
 constexpr int kSortTile = kBlock * kSortItems;  // 2048 slots per tile
+constexpr int kMaxRadix = 512;
 
 // n / d for 32-bit n by a divisor fixed at launch: multiply-high by a magic
 // number (Granlund & Montgomery 1994, round-up variant): with l = ceil(log2 d)
@@ -46,7 +48,7 @@ struct FastDiv {
 };
 
 // Key of slot s (s < 2^31): chunk(b) * N + feature for an active slot, the
-// sentinel for an inactive one; the carried value is the position b = s / K.
+// sentinel (>= every real key) for an inactive one; the value is b = s / K.
 struct SlotKey {
   const int32_t *idx;
   unsigned N;
@@ -59,11 +61,32 @@ struct SlotKey {
   __device__ __forceinline__ int pos(int64_t s) const { return (int)divK((uint32_t)s); }
 };
 
+// Number of elements a pass reads: all slots for the first pass, else the
+// active count = sum of the previous scan's digit totals (block-wide sum).
+template <int R>
+__device__ __forceinline__ int64_t pass_count(bool first, int64_t M, const unsigned *__restrict__ totals,
+                                              unsigned *red) {
+  if (first) return M;
+  const int tid = threadIdx.x;
+  unsigned v = 0;
+  for (int d = tid; d < R; d += kBlock) v += totals[d];
+  red[tid] = v;
+  __syncthreads();
+  for (int off = kBlock / 2; off > 0; off >>= 1) {
+    if (tid < off) red[tid] += red[tid + off];
+    __syncthreads();
+  }
+  const int64_t n = red[0];
+  __syncthreads();
+  return n;
+}
+
 // Lanes of the wave holding the same digit as this lane (among `valid` lanes).
+template <int RB>
 __device__ __forceinline__ uint64_t match_digit(unsigned d, bool valid) {
   uint64_t peers = ballot(valid);
 #pragma unroll
-  for (int b = 0; b < kRadixBits; ++b) {
+  for (int b = 0; b < RB; ++b) {
     const bool bit = (d >> b) & 1u;
     const uint64_t m = ballot(bit);
     peers &= bit ? m : ~m;
@@ -71,22 +94,31 @@ __device__ __forceinline__ uint64_t match_digit(unsigned d, bool valid) {
   return peers;
 }
 
-template <bool FIRST>
+template <int RB, bool FIRST>
 __global__ __launch_bounds__(kBlock) void radix_upsweep(SlotKey sk, const unsigned *__restrict__ kin, int64_t M,
-                                                        int ntiles, int shift, unsigned *__restrict__ hist) {
-  __shared__ unsigned hw[kWavesPerBlock][kRadix];
+                                                        const unsigned *__restrict__ prev_totals, int ntiles,
+                                                        int shift, unsigned *__restrict__ hist) {
+  constexpr int R = 1 << RB;
+  __shared__ unsigned hw[kWavesPerBlock][R];
+  __shared__ unsigned red[kBlock];
   const int tid = threadIdx.x, wave = tid / kWave;
+  for (int d = tid; d < R; d += kBlock)
 #pragma unroll
-  for (int w = 0; w < kWavesPerBlock; ++w) hw[w][tid] = 0;
+    for (int w = 0; w < kWavesPerBlock; ++w) hw[w][d] = 0;
+  const int64_t count = pass_count<R>(FIRST, M, prev_totals, red);
   __syncthreads();
   const int64_t base = (int64_t)blockIdx.x * kSortTile;
 #pragma unroll
   for (int i = 0; i < kSortItems; ++i) {
     const int64_t e = base + (int64_t)i * kBlock + tid;
-    if (e < M) atomicAdd(&hw[wave][((FIRST ? sk.key(e) : kin[e]) >> shift) & (kRadix - 1)], 1u);
+    if (e < count) {
+      const unsigned k = FIRST ? sk.key(e) : kin[e];
+      if (!FIRST || k < sk.sentinel) atomicAdd(&hw[wave][(k >> shift) & (R - 1)], 1u);
+    }
   }
   __syncthreads();
-  hist[(int64_t)tid * ntiles + blockIdx.x] = hw[0][tid] + hw[1][tid] + hw[2][tid] + hw[3][tid];
+  for (int d = tid; d < R; d += kBlock)
+    hist[(int64_t)d * ntiles + blockIdx.x] = hw[0][d] + hw[1][d] + hw[2][d] + hw[3][d];
 }
 
 // Per digit d (one block each): exclusive scan of hist[d][0 .. ntiles) in
@@ -117,13 +149,15 @@ __global__ __launch_bounds__(kBlock) void radix_scan_digits(unsigned *__restrict
   if (tid == kBlock - 1) totals[blockIdx.x] = part[tid];
 }
 
-// Exclusive scan of 256 per-digit values by one wave (4 digits per lane).
-__device__ __forceinline__ void wave_scan_256(const unsigned *in, unsigned *out, int lane) {
-  unsigned c[kRadix / kWave];
+// Exclusive scan of R per-digit values by one wave (R / 64 digits per lane).
+template <int R>
+__device__ __forceinline__ void wave_scan_digits(const unsigned *in, unsigned *out, int lane) {
+  constexpr int PER = R / kWave;
+  unsigned c[PER];
   unsigned s = 0;
 #pragma unroll
-  for (int j = 0; j < kRadix / kWave; ++j) {
-    c[j] = in[lane * (kRadix / kWave) + j];
+  for (int j = 0; j < PER; ++j) {
+    c[j] = in[lane * PER + j];
     s += c[j];
   }
   unsigned incl = s;
@@ -134,92 +168,101 @@ __device__ __forceinline__ void wave_scan_256(const unsigned *in, unsigned *out,
   }
   unsigned run = incl - s;
 #pragma unroll
-  for (int j = 0; j < kRadix / kWave; ++j) {
-    out[lane * (kRadix / kWave) + j] = run;
+  for (int j = 0; j < PER; ++j) {
+    out[lane * PER + j] = run;
     run += c[j];
   }
 }
 
-template <bool FIRST>
+// Tile layout: wave w owns the contiguous quarter [w * 512, (w + 1) * 512) of
+// the tile and walks it in 64-slot rounds, so (wave, round, lane) is slot
+// order.  Each wave ranks its elements with its own digit counters (no block
+// barrier inside the loop); afterwards a digit's rank base for wave w is the
+// count of that digit in waves 0 .. w-1.
+template <int RB, bool FIRST>
 __global__ __launch_bounds__(kBlock) void radix_downsweep(SlotKey sk, const unsigned *__restrict__ kin,
                                                           const int *__restrict__ vin, unsigned *__restrict__ kout,
                                                           int *__restrict__ vout, const unsigned *__restrict__ offs,
                                                           const unsigned *__restrict__ totals, int64_t M, int ntiles,
                                                           int shift) {
+  constexpr int R = 1 << RB;
+  constexpr int PER_WAVE = kSortTile / kWavesPerBlock;  // 512
   __shared__ unsigned s_keys[kSortTile];
   __shared__ int s_vals[kSortTile];
-  __shared__ unsigned running[kRadix];
-  __shared__ unsigned wcnt[kWavesPerBlock][kRadix];
-  __shared__ unsigned dstart[kRadix];
-  __shared__ unsigned dtot[kRadix];
-  __shared__ unsigned dbase[kRadix];
+  __shared__ unsigned wrun[kWavesPerBlock][R];
+  __shared__ unsigned dstart[R];
+  __shared__ unsigned dtot[R];
+  __shared__ unsigned dbase[R];
   const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
-  const int64_t base = (int64_t)blockIdx.x * kSortTile;
-  const int count = (int)std::min<int64_t>(kSortTile, M - base);
-
-  running[tid] = 0;
-  dtot[tid] = totals[tid];
+  for (int d = tid; d < R; d += kBlock) {
+    dtot[d] = totals[d];
 #pragma unroll
-  for (int w = 0; w < kWavesPerBlock; ++w) wcnt[w][tid] = 0;
+    for (int w = 0; w < kWavesPerBlock; ++w) wrun[w][d] = 0;
+  }
+  __syncthreads();
+  if (wave == 1) wave_scan_digits<R>(dtot, dbase, lane);  // digit bases in the whole output
+  __syncthreads();
+  // Elements read by this pass: all slots (first pass) or the active ones,
+  // whose count is the sum of this pass's digit totals.
+  const int64_t n_in = FIRST ? M : (int64_t)dbase[R - 1] + dtot[R - 1];
+  const int64_t base = (int64_t)blockIdx.x * kSortTile + (int64_t)wave * PER_WAVE;
 
   unsigned key[kSortItems];
   int val[kSortItems];
   unsigned rank[kSortItems];
+  bool act[kSortItems];
 #pragma unroll
   for (int i = 0; i < kSortItems; ++i) {
-    const int64_t e = base + (int64_t)i * kBlock + tid;
+    const int64_t e = base + (int64_t)i * kWave + lane;
     key[i] = 0;
     val[i] = 0;
-    if (e < M) {
+    act[i] = false;
+    if (e < n_in) {
       key[i] = FIRST ? sk.key(e) : kin[e];
       val[i] = FIRST ? sk.pos(e) : vin[e];
+      act[i] = !FIRST || key[i] < sk.sentinel;
     }
   }
-  __syncthreads();
-
-  // Stable ranks within the tile: slot order is (round i, wave, lane).
+  unsigned *my = wrun[wave];
 #pragma unroll
   for (int i = 0; i < kSortItems; ++i) {
-    const bool valid = i * kBlock + tid < count;
-    const unsigned d = (key[i] >> shift) & (kRadix - 1);
-    const uint64_t peers = match_digit(d, valid);
-    if (valid && (int)(__ffsll((unsigned long long)peers) - 1) == lane) wcnt[wave][d] = (unsigned)__popcll(peers);
-    __syncthreads();
-    if (valid) {
-      unsigned r = running[d] + (unsigned)popc_below(peers);
-      for (int w = 0; w < wave; ++w) r += wcnt[w][d];
-      rank[i] = r;
-    }
-    __syncthreads();
-    unsigned tot = 0;
+    const unsigned d = (key[i] >> shift) & (R - 1);
+    const uint64_t peers = match_digit<RB>(d, act[i]);
+    if (act[i]) rank[i] = my[d] + (unsigned)popc_below(peers);
+    __builtin_amdgcn_wave_barrier();
+    if (act[i] && (int)(__ffsll((unsigned long long)peers) - 1) == lane) my[d] += (unsigned)__popcll(peers);
+    __builtin_amdgcn_wave_barrier();
+  }
+  __syncthreads();
+  // Per digit: counts of earlier waves (rank bases) and the tile total.
+  for (int d = tid; d < R; d += kBlock) {
+    unsigned run = 0;
 #pragma unroll
     for (int w = 0; w < kWavesPerBlock; ++w) {
-      tot += wcnt[w][tid];
-      wcnt[w][tid] = 0;
+      const unsigned c = wrun[w][d];
+      wrun[w][d] = run;
+      run += c;
     }
-    running[tid] += tot;
-    __syncthreads();
+    dtot[d] = run;  // reuse: digit count of this tile
   }
-
-  // Digit starts inside the tile, and of each digit in the whole output.
-  if (wave == 0) wave_scan_256(running, dstart, lane);
-  if (wave == 1) wave_scan_256(dtot, dbase, lane);
   __syncthreads();
-
+  if (wave == 0) wave_scan_digits<R>(dtot, dstart, lane);
+  __syncthreads();
 #pragma unroll
   for (int i = 0; i < kSortItems; ++i) {
-    if (i * kBlock + tid < count) {
-      const unsigned d = (key[i] >> shift) & (kRadix - 1);
-      const unsigned p = dstart[d] + rank[i];
+    if (act[i]) {
+      const unsigned d = (key[i] >> shift) & (R - 1);
+      const unsigned p = dstart[d] + my[d] + rank[i];
       s_keys[p] = key[i];
       s_vals[p] = val[i];
     }
   }
+  const int kept = (int)(dstart[R - 1] + dtot[R - 1]);  // active elements of the tile
   __syncthreads();
 
-  for (int j = tid; j < count; j += kBlock) {
+  for (int j = tid; j < kept; j += kBlock) {
     const unsigned k = s_keys[j];
-    const unsigned d = (k >> shift) & (kRadix - 1);
+    const unsigned d = (k >> shift) & (R - 1);
     const int64_t dst = (int64_t)dbase[d] + offs[(int64_t)d * ntiles + blockIdx.x] + (j - dstart[d]);
     kout[dst] = k;
     vout[dst] = s_vals[j];
@@ -228,55 +271,74 @@ __global__ __launch_bounds__(kBlock) void radix_downsweep(SlotKey sk, const unsi
 
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
-}  // namespace
-
-unsigned sort_key_bits(int64_t maxkey) {
+unsigned key_bits(int64_t maxkey) {
   unsigned bits = 1;
   while (((int64_t)1 << bits) <= maxkey) ++bits;  // keys lie in [0, maxkey]
   return bits;
 }
 
+template <int RB>
+int run_passes(const SlotKey &sk, int64_t M, int passes, unsigned *kbuf[2], int *vbuf[2], unsigned *hist,
+               unsigned *totals, int ntiles, hipStream_t s) {
+  for (int p = 0; p < passes; ++p) {
+    const int shift = p * RB;
+    const unsigned *kin = p == 0 ? nullptr : kbuf[(p - 1) & 1];
+    const int *vin = p == 0 ? nullptr : vbuf[(p - 1) & 1];
+    unsigned *kout = kbuf[p & 1];
+    int *vout = vbuf[p & 1];
+    if (p == 0)
+      hipLaunchKernelGGL((radix_upsweep<RB, true>), dim3(ntiles), dim3(kBlock), 0, s, sk, kin, M, totals, ntiles,
+                         shift, hist);
+    else
+      hipLaunchKernelGGL((radix_upsweep<RB, false>), dim3(ntiles), dim3(kBlock), 0, s, sk, kin, M, totals, ntiles,
+                         shift, hist);
+    hipLaunchKernelGGL(radix_scan_digits, dim3(1 << RB), dim3(kBlock), 0, s, hist, ntiles, totals);
+    if (p == 0)
+      hipLaunchKernelGGL((radix_downsweep<RB, true>), dim3(ntiles), dim3(kBlock), 0, s, sk, kin, vin, kout, vout,
+                         hist, totals, M, ntiles, shift);
+    else
+      hipLaunchKernelGGL((radix_downsweep<RB, false>), dim3(ntiles), dim3(kBlock), 0, s, sk, kin, vin, kout, vout,
+                         hist, totals, M, ntiles, shift);
+    const int rc = check_launch("slot radix sort");
+    if (rc != SFT_OK) return rc;
+  }
+  return SFT_OK;
+}
+
+}  // namespace
+
 // Workspace: two key/position buffer pairs (ping-pong), the histograms and
-// the digit totals.
+// the digit totals (the active-slot count is their sum).
 size_t slot_sort_workspace(int64_t M) {
   const int64_t ntiles = ceil_div(std::max<int64_t>(M, 1), kSortTile);
-  return 4 * align256((size_t)M * 4) + align256((size_t)(kRadix * ntiles) * 4) + align256(kRadix * 4);
+  return 4 * align256((size_t)M * 4) + align256((size_t)(kMaxRadix * ntiles) * 4) + align256(kMaxRadix * 4);
 }
 
 int slot_sort(const int32_t *idx, int64_t M, int K, int64_t N, int chunk_rows, int nchunks, void *ws,
-              unsigned **keys_sorted, int **pos_sorted, hipStream_t s) {
+              unsigned **keys_sorted, int **pos_sorted, unsigned **digit_totals, int *digit_count,
+              hipStream_t s) {
   char *w = static_cast<char *>(ws);
   const size_t a = align256((size_t)M * 4);
   unsigned *kbuf[2] = {reinterpret_cast<unsigned *>(w), reinterpret_cast<unsigned *>(w + 2 * a)};
   int *vbuf[2] = {reinterpret_cast<int *>(w + a), reinterpret_cast<int *>(w + 3 * a)};
   const int ntiles = (int)ceil_div(std::max<int64_t>(M, 1), kSortTile);
   unsigned *hist = reinterpret_cast<unsigned *>(w + 4 * a);
-  unsigned *totals = reinterpret_cast<unsigned *>(w + 4 * a + align256((size_t)(kRadix * ntiles) * 4));
-  const unsigned sentinel = (unsigned)((int64_t)nchunks * N);
-  const SlotKey sk{idx, (unsigned)N, FastDiv((uint32_t)K), FastDiv((uint32_t)chunk_rows), sentinel};
-  const int passes = (int)ceil_div(sort_key_bits(sentinel), kRadixBits);
-  for (int p = 0; p < passes; ++p) {
-    const int shift = p * kRadixBits;
-    const unsigned *kin = p == 0 ? nullptr : kbuf[(p - 1) & 1];
-    const int *vin = p == 0 ? nullptr : vbuf[(p - 1) & 1];
-    unsigned *kout = kbuf[p & 1];
-    int *vout = vbuf[p & 1];
-    if (p == 0)
-      hipLaunchKernelGGL(radix_upsweep<true>, dim3(ntiles), dim3(kBlock), 0, s, sk, kin, M, ntiles, shift, hist);
-    else
-      hipLaunchKernelGGL(radix_upsweep<false>, dim3(ntiles), dim3(kBlock), 0, s, sk, kin, M, ntiles, shift, hist);
-    hipLaunchKernelGGL(radix_scan_digits, dim3(kRadix), dim3(kBlock), 0, s, hist, ntiles, totals);
-    if (p == 0)
-      hipLaunchKernelGGL(radix_downsweep<true>, dim3(ntiles), dim3(kBlock), 0, s, sk, kin, vin, kout, vout, hist,
-                         totals, M, ntiles, shift);
-    else
-      hipLaunchKernelGGL(radix_downsweep<false>, dim3(ntiles), dim3(kBlock), 0, s, sk, kin, vin, kout, vout, hist,
-                         totals, M, ntiles, shift);
-    const int rc = check_launch("slot radix sort");
-    if (rc != SFT_OK) return rc;
+  unsigned *totals = reinterpret_cast<unsigned *>(w + 4 * a + align256((size_t)(kMaxRadix * ntiles) * 4));
+  const unsigned nkeys = (unsigned)((int64_t)nchunks * N);
+  const SlotKey sk{idx, (unsigned)N, FastDiv((uint32_t)K), FastDiv((uint32_t)chunk_rows), nkeys};
+  const unsigned bits = key_bits((int64_t)nkeys - 1 > 0 ? (int64_t)nkeys - 1 : 1);  // real keys < nkeys
+  int rb = 8, passes = (int)ceil_div(bits, 8);
+  if (passes > 1 && ceil_div(bits, 9) < passes) {
+    rb = 9;
+    passes = (int)ceil_div(bits, 9);
   }
+  const int rc = rb == 9 ? run_passes<9>(sk, M, passes, kbuf, vbuf, hist, totals, ntiles, s)
+                         : run_passes<8>(sk, M, passes, kbuf, vbuf, hist, totals, ntiles, s);
+  if (rc != SFT_OK) return rc;
   *keys_sorted = kbuf[(passes - 1) & 1];
   *pos_sorted = vbuf[(passes - 1) & 1];
+  *digit_totals = totals;
+  *digit_count = 1 << rb;
   return SFT_OK;
 }
 
