@@ -25,6 +25,8 @@ SHAPES = [
     (10, 5, 3, 70, 12, 0, 3, False),          # K > 64: two compaction rounds
     (11, 1000, 24576, 32, 256, 0, 32, False),  # largest table the tiled gather takes; 8 tiles
     (12, 77, 900, 13, 1040, 0, 13, False),    # K = 13: four rows per ballot
+    (13, 700, 40000, 32, 1048, 16, 32, True),  # 32-column tile > 4 MB: 16-column tiles
+    (14, 300, 85296, 160, 1048, 32, 160, False),  # threat-sized table, 16-column tiles
 ]
 
 
