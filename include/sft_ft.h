@@ -158,6 +158,62 @@ int sft_ft_fwd_i16_ex(const int32_t *idx, int64_t batch, int32_t max_active,
                       void *workspace, size_t workspace_bytes, uint32_t flags, void *stream);
 
 /*
+ * ---- Composed table, both perspectives in one call ----
+ * The table is num_blocks (1..4) row blocks concatenated in order (the feature
+ * sets of a composed transformer, FEAT/composed.py:49-50).  Block s has
+ * block_rows[s] rows; when block_virtual_rows[s] > 0 it also has a virtual
+ * table and its merged row r is weight_s[r] + virtual_s[r % block_virtual_rows[s]]
+ * (HalfKAv2_hm's weight + virtual_weight.repeat(32, 1), FEAT/halfka_v2_hm.py:69-70;
+ * block_rows[s] must be a multiple of block_virtual_rows[s]).  num_inputs is the
+ * sum of block_rows.
+ *
+ * Bytes of workspace the forward and the backward pair calls need.  Returns
+ * SFT_EUNSUPPORTED (nothing is launched by the pair calls) unless
+ * output_size % 4 == 0, output_size >= 256 and num_inputs * 128 <= 64 MiB; the
+ * caller then materialises the table and uses sft_ft_fwd_f32_ex / sft_ft_bwd_f32.
+ * Host-only computation.  No reference counterpart.
+ */
+int sft_ft_pair_workspace_size(int64_t batch, int32_t max_active, int32_t num_blocks,
+                               const int64_t *block_rows, const int64_t *block_virtual_rows,
+                               int32_t output_size, size_t *fwd_bytes, size_t *bwd_bytes);
+
+/*
+ * Forward of both perspectives over the composed table:
+ *   out0 = fwd(idx0, merged, bias), out1 = fwd(idx1, merged, bias)
+ * with merged as above, each bit for bit as sft_ft_fwd_f32 on the materialised
+ * table.  The merged table is built once, directly in the 32-column tiles of
+ * the workspace (the table itself is never written).  Pointers 16-byte aligned.
+ * Replaces ComposedFeatureTransformer.forward (FEAT/composed.py:49-54): its
+ * merged_weight (FEAT/halfka_v2_hm.py:69-70, FEAT/full_threats.py:27-28, torch.cat)
+ * and its two SparseLinearFunction.apply calls (FT/functions.py:12-48).
+ */
+int sft_ft_fwd_pair_f32(const int32_t *idx0, const int32_t *idx1, int64_t batch, int32_t max_active,
+                        int32_t num_blocks, const float *const *block_weight,
+                        const float *const *block_virtual, const int64_t *block_rows,
+                        const int64_t *block_virtual_rows, int32_t output_size, const float *bias,
+                        float *out0, float *out1, void *workspace, size_t workspace_bytes,
+                        void *stream);
+
+/*
+ * Backward of the pair (overwrites every output):
+ *   block_weight_grad[s] = rows of dW_0 + dW_1 for block s, where dW_p is the
+ *                          reference-order weight grad of perspective p (as
+ *                          sft_ft_bwd_f32 computes it, bit for bit) and the sum is
+ *                          one binary32 add, as autograd sums the two grads;
+ *   block_virtual_grad[s] = sum over repeats i of block_weight_grad[s][i * V + j]
+ *                          (blocks with virtual rows; NULL entries otherwise);
+ *   bias_grad             = sum_b grad0[b] + sum_b grad1[b].
+ * Replaces the backward of the same composition: FT/functions.py:50-72 twice,
+ * autograd's sum of the two table grads, the cat split and repeat's reduction.
+ */
+int sft_ft_bwd_pair_f32(const int32_t *idx0, const int32_t *idx1, int64_t batch, int32_t max_active,
+                        const float *grad0, const float *grad1, int32_t num_blocks,
+                        const int64_t *block_rows, const int64_t *block_virtual_rows,
+                        int32_t output_size, float *const *block_weight_grad,
+                        float *const *block_virtual_grad, float *bias_grad, void *workspace,
+                        size_t workspace_bytes, void *stream);
+
+/*
  * Export quantization on the device (src/model/quantize.py:83-84):
  * out[i] = round_half_even(float32(x[i] * scale)) saturated to int16.
  * No reference counterpart as a kernel (the reference runs it as torch ops).

@@ -26,6 +26,15 @@ int fwd_i16_tiled(const int32_t *idx, int64_t B, int K, const int16_t *W, int64_
                   size_t ws_bytes, hipStream_t s);
 int bwd_f32(const int32_t *idx, int64_t B, int K, const float *grad, int64_t N, int L, float *dW, float *db,
             void *ws, size_t ws_bytes, uint32_t flags, hipStream_t s);
+size_t index_lds_bytes(int G, int K);
+int fwd_pair_f32(const int32_t *idx0, const int32_t *idx1, int64_t B, int K, const FoldSrc &src, int64_t N, int L,
+                 const float *bias, float *out0, float *out1, void *ws, size_t ws_bytes, hipStream_t s);
+size_t bwd_pair_workspace(int64_t B, int K, int64_t N, int L);
+int bwd_pair_f32(const int32_t *idx0, const int32_t *idx1, int64_t B, int K, const float *grad0, const float *grad1,
+                 int64_t N, int L, const RowDst &dst, const float *const *vgrad_src, float *const *vgrad,
+                 const int64_t *vperiod, const int64_t *vreps, int nvirt, float *db, void *ws, size_t ws_bytes,
+                 hipStream_t s);
+void zero_f32(float *p, int64_t n, hipStream_t s);
 
 namespace {
 thread_local std::string t_error;
@@ -109,6 +118,7 @@ const char *const kKindNames[kProfNumKinds] = {
     "fwd_f32_gather",   "bwd_feature_sort",  "bwd_segment_offsets", "bwd_feature_gather", "bwd_bias_partial",
     "bwd_bias_final",   "bwd_atomic_scatter", "bwd_zero_fill",      "fwd_i16_gather",     "quantize_i16",
     "fwd_tile_relayout", "fwd_f32_tiled_gather", "bwd_tiled_gather", "bwd_grad_relayout", "fwd_i16_tiled_gather",
+    "fwd_fold_relayout", "bwd_virtual_reduce",
 };
 }  // namespace
 
@@ -217,6 +227,128 @@ int sft_ft_bwd_f32(const int32_t *idx, int64_t batch, int32_t max_active, const 
   if (flags & ~(SFT_BWD_OVERWRITE | SFT_BWD_ATOMIC | SFT_BWD_ROWS)) return fail(SFT_EINVAL, "sft_ft_bwd_f32: unknown flags");
   return bwd_f32(idx, batch, max_active, grad_out, num_inputs, output_size, weight_grad, bias_grad, workspace,
                  workspace_bytes, flags, (hipStream_t)stream);
+}
+
+// Validates the block description of a composed table and its shape; sets *N.
+static int check_pair_shape(const char *who, int64_t batch, int32_t max_active, int32_t num_blocks,
+                            const int64_t *block_rows, const int64_t *block_virtual_rows, int32_t output_size,
+                            int64_t *N) {
+  const std::string w(who);
+  if (num_blocks < 1 || num_blocks > kMaxBlocks) return fail(SFT_EINVAL, w + ": num_blocks must be in [1, 4]");
+  if (!block_rows || !block_virtual_rows) return fail(SFT_EINVAL, w + ": null pointer");
+  int64_t n = 0;
+  for (int s = 0; s < num_blocks; ++s) {
+    const int64_t r = block_rows[s], v = block_virtual_rows[s];
+    if (r <= 0 || r >= INT32_MAX) return fail(SFT_EINVAL, w + ": block_rows must be in [1, 2^31-1)");
+    if (v < 0 || (v > 0 && r % v != 0))
+      return fail(SFT_EINVAL, w + ": block_virtual_rows must be 0 or divide block_rows");
+    n += r;
+  }
+  std::string why;
+  if (bad_sizes(batch, max_active, n, output_size, why)) return fail(SFT_EINVAL, w + ": " + why);
+  if (output_size % 4 != 0 || output_size < 256)
+    return fail(SFT_EUNSUPPORTED, w + ": output_size must be a multiple of 4 and >= 256");
+  if (!fwd_tiled_supported(n, output_size, nullptr, nullptr, nullptr) || n * (int64_t)(output_size / 4) >= INT32_MAX)
+    return fail(SFT_EUNSUPPORTED, w + ": table too large for the tiled composed path");
+  if (index_lds_bytes(8, max_active) > kMaxIndexLds)
+    return fail(SFT_EUNSUPPORTED, w + ": max_active too large for the LDS index lists");
+  *N = n;
+  return SFT_OK;
+}
+
+static bool misaligned16(const void *p) { return (uintptr_t)p % 16 != 0; }
+
+int sft_ft_pair_workspace_size(int64_t batch, int32_t max_active, int32_t num_blocks, const int64_t *block_rows,
+                               const int64_t *block_virtual_rows, int32_t output_size, size_t *fwd_bytes,
+                               size_t *bwd_bytes) {
+  clear_error();
+  if (!fwd_bytes || !bwd_bytes) return fail(SFT_EINVAL, "sft_ft_pair_workspace_size: null pointer");
+  int64_t N = 0;
+  const int rc = check_pair_shape("sft_ft_pair_workspace_size", batch, max_active, num_blocks, block_rows,
+                                  block_virtual_rows, output_size, &N);
+  if (rc != SFT_OK) return rc;
+  *fwd_bytes = fwd_tiled_workspace(N, output_size);
+  *bwd_bytes = bwd_pair_workspace(batch, max_active, N, output_size);
+  return SFT_OK;
+}
+
+int sft_ft_fwd_pair_f32(const int32_t *idx0, const int32_t *idx1, int64_t batch, int32_t max_active,
+                        int32_t num_blocks, const float *const *block_weight, const float *const *block_virtual,
+                        const int64_t *block_rows, const int64_t *block_virtual_rows, int32_t output_size,
+                        const float *bias, float *out0, float *out1, void *workspace, size_t workspace_bytes,
+                        void *stream) {
+  clear_error();
+  const char *who = "sft_ft_fwd_pair_f32";
+  int64_t N = 0;
+  int rc = check_pair_shape(who, batch, max_active, num_blocks, block_rows, block_virtual_rows, output_size, &N);
+  if (rc != SFT_OK) return rc;
+  if (!block_weight || !block_virtual || !bias || (batch > 0 && (!idx0 || !idx1 || !out0 || !out1)))
+    return fail(SFT_EINVAL, std::string(who) + ": null pointer");
+  FoldSrc src{};
+  src.n = num_blocks;
+  for (int s = 0; s < num_blocks; ++s) {
+    if (!block_weight[s] || (block_virtual_rows[s] > 0 && !block_virtual[s]))
+      return fail(SFT_EINVAL, std::string(who) + ": null block pointer");
+    if (misaligned16(block_weight[s]) || (block_virtual_rows[s] > 0 && misaligned16(block_virtual[s])))
+      return fail(SFT_EINVAL, std::string(who) + ": block tables must be 16-byte aligned");
+    src.start[s + 1] = src.start[s] + block_rows[s];
+    src.w[s] = reinterpret_cast<const f32x4 *>(block_weight[s]);
+    src.v[s] = block_virtual_rows[s] > 0 ? reinterpret_cast<const f32x4 *>(block_virtual[s]) : nullptr;
+    src.period[s] = block_virtual_rows[s] > 0 ? block_virtual_rows[s] : 1;
+  }
+  if (misaligned16(bias) || (batch > 0 && (misaligned16(out0) || misaligned16(out1))))
+    return fail(SFT_EINVAL, std::string(who) + ": bias and outputs must be 16-byte aligned");
+  if (batch == 0) return SFT_OK;
+  return fwd_pair_f32(idx0, idx1, batch, max_active, src, N, output_size, bias, out0, out1, workspace,
+                      workspace_bytes, (hipStream_t)stream);
+}
+
+int sft_ft_bwd_pair_f32(const int32_t *idx0, const int32_t *idx1, int64_t batch, int32_t max_active,
+                        const float *grad0, const float *grad1, int32_t num_blocks, const int64_t *block_rows,
+                        const int64_t *block_virtual_rows, int32_t output_size, float *const *block_weight_grad,
+                        float *const *block_virtual_grad, float *bias_grad, void *workspace, size_t workspace_bytes,
+                        void *stream) {
+  clear_error();
+  const char *who = "sft_ft_bwd_pair_f32";
+  int64_t N = 0;
+  int rc = check_pair_shape(who, batch, max_active, num_blocks, block_rows, block_virtual_rows, output_size, &N);
+  if (rc != SFT_OK) return rc;
+  if (!block_weight_grad || !block_virtual_grad || !bias_grad || (batch > 0 && (!idx0 || !idx1 || !grad0 || !grad1)))
+    return fail(SFT_EINVAL, std::string(who) + ": null pointer");
+  RowDst dst{};
+  dst.n = num_blocks;
+  const float *vsrc[kMaxBlocks];
+  float *vdst[kMaxBlocks];
+  int64_t vperiod[kMaxBlocks], vreps[kMaxBlocks];
+  int nvirt = 0;
+  for (int s = 0; s < num_blocks; ++s) {
+    if (!block_weight_grad[s] || (block_virtual_rows[s] > 0 && !block_virtual_grad[s]))
+      return fail(SFT_EINVAL, std::string(who) + ": null block pointer");
+    if (misaligned16(block_weight_grad[s]) || (block_virtual_rows[s] > 0 && misaligned16(block_virtual_grad[s])))
+      return fail(SFT_EINVAL, std::string(who) + ": block grads must be 16-byte aligned");
+    dst.start[s + 1] = dst.start[s] + block_rows[s];
+    dst.p[s] = reinterpret_cast<f32x4 *>(block_weight_grad[s]);
+    if (block_virtual_rows[s] > 0) {
+      vsrc[nvirt] = block_weight_grad[s];
+      vdst[nvirt] = block_virtual_grad[s];
+      vperiod[nvirt] = block_virtual_rows[s];
+      vreps[nvirt] = block_rows[s] / block_virtual_rows[s];
+      ++nvirt;
+    }
+  }
+  if (misaligned16(bias_grad) || (batch > 0 && (misaligned16(grad0) || misaligned16(grad1))))
+    return fail(SFT_EINVAL, std::string(who) + ": bias_grad and grads must be 16-byte aligned");
+  const hipStream_t st = (hipStream_t)stream;
+  if (batch == 0) {  // no positions: every grad is zero
+    for (int s = 0; s < num_blocks; ++s) {
+      zero_f32(block_weight_grad[s], block_rows[s] * output_size, st);
+      if (block_virtual_rows[s] > 0) zero_f32(block_virtual_grad[s], block_virtual_rows[s] * output_size, st);
+    }
+    zero_f32(bias_grad, output_size, st);
+    return check_launch("sft_ft_bwd_pair_f32 (zero fill)");
+  }
+  return bwd_pair_f32(idx0, idx1, batch, max_active, grad0, grad1, N, output_size, dst, vsrc, vdst, vperiod, vreps,
+                      nvirt, bias_grad, workspace, workspace_bytes, st);
 }
 
 static int check_i16_args(const char *who, const int32_t *idx, int64_t batch, int32_t max_active,

@@ -44,6 +44,8 @@ enum ProfKind : int {
   kProfBwdTiled,
   kProfBwdRelayout,
   kProfFwdI16Tiled,
+  kProfFwdFold,
+  kProfBwdVirtual,
   kProfNumKinds
 };
 struct ProfScope {
@@ -158,6 +160,40 @@ __device__ __forceinline__ TileItem tile_sched_item(int64_t bid, int ntiles, int
   if (j < fj) return TileItem{xcd + kXcds * (int)(j / nchunks), (int)(j % nchunks)};
   const int64_t g = (j - fj) * kXcds + xcd;
   return TileItem{kXcds * full + (int)(g / nchunks), (int)(g % nchunks)};  // tile >= ntiles: no work
+}
+
+// ---- composed tables ----
+// A composed feature transformer's table is the concatenation of up to
+// kMaxBlocks row blocks (one per feature set); block s covers merged rows
+// [start[s], start[s + 1]).  A block may carry virtual rows: merged row r of
+// the block then reads w[r] + v[r % period].
+constexpr int kMaxBlocks = 4;
+struct FoldSrc {
+  int n;
+  int64_t start[kMaxBlocks + 1];
+  const f32x4 *w[kMaxBlocks];
+  const f32x4 *v[kMaxBlocks];  // null: no virtual rows
+  int64_t period[kMaxBlocks];
+};
+// Where the grad of each merged row goes (row-major blocks of cols4 chunks).
+struct RowDst {
+  int n;
+  int64_t start[kMaxBlocks + 1];
+  f32x4 *p[kMaxBlocks];
+};
+// a[s] for a run-time s without indexing the kernel-argument array (selects).
+template <typename T, int M>
+__device__ __forceinline__ T pick(const T (&a)[M], int s) {
+  T x = a[0];
+#pragma unroll
+  for (int j = 1; j < M; ++j) x = (s == j) ? a[j] : x;
+  return x;
+}
+__device__ __forceinline__ int block_of(int64_t r, int n, const int64_t *start) {
+  int s = 0;
+#pragma unroll
+  for (int j = 1; j < kMaxBlocks; ++j) s += (j < n && r >= start[j]) ? 1 : 0;
+  return s;
 }
 
 __host__ __device__ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }

@@ -229,11 +229,23 @@ __device__ __forceinline__ void bwd_tile_sum(const int32_t *list, int n, int nmi
 // coalesced loads and read from there, which keeps the position reads off the
 // in-order vector-memory counter the row loads wait on.  Ranges longer than
 // kBwdPosLds entries read their positions from global memory instead.
+//
+// Where a launch starts and leaves each feature's sum:
+//   src_mode kSrcZero: acc = 0;  kSrcDst: acc = dst row;  kSrcTmp: acc = tmp row
+//   dst_mode kDstOut: dst row = acc (skipped for untouched features when the
+//            sum continues from dst);  kDstTmp: tmp row = acc;
+//            kDstOutPlus: dst row = dst row + acc (every feature).
+// One perspective: (zero, out), then (dst, out) per further position chunk.
+// A second perspective sums onto 0 in tmp and its last launch adds its total
+// to the first's: dW = dW_0 + dW_1, the sum autograd forms for the composed
+// table (FEAT/composed.py:52-53).  dst rows are split into blocks (RowDst).
+enum { kSrcZero = 0, kSrcDst = 1, kSrcTmp = 2 };
+enum { kDstOut = 0, kDstTmp = 1, kDstOutPlus = 2 };
 __global__ __launch_bounds__(kBlock) void bwd_tiled_gather_kernel(const int32_t *__restrict__ seg,
                                                                   const int32_t *__restrict__ sorted_pos, int64_t N,
                                                                   const f32x4 *__restrict__ gt, int64_t B,
-                                                                  int64_t cols4, f32x4 *__restrict__ dW, int first,
-                                                                  int ntiles, int ngroups) {
+                                                                  int64_t cols4, RowDst dst, f32x4 *__restrict__ tmp,
+                                                                  int src_mode, int dst_mode, int ntiles, int ngroups) {
   __shared__ int spos[kBwdPosLds];
   const TileItem it = tile_sched_item(blockIdx.x, ntiles, ngroups);
   if (it.tile >= ntiles) return;  // whole block: uniform
@@ -258,23 +270,60 @@ __global__ __launch_bounds__(kBlock) void bwd_tiled_gather_kernel(const int32_t 
   }
   const int n = s1 - s0;
   const bool wave_has_work = ballot(n > 0) != 0;  // wave-uniform
-  if (!first && !wave_has_work) return;             // nothing to add anywhere in the wave
+  const bool skip_untouched = src_mode == kSrcDst && dst_mode == kDstOut;
+  if (skip_untouched && !wave_has_work) return;  // nothing to change anywhere in the wave
   int nmin, nmax;
   group_minmax<kBwdTileCh>(n, nmin, nmax);
   const f32x4 *gcol = gt + (int64_t)it.tile * B * kBwdTileCh + t;
-  f32x4 *d = dW + f * cols4 + col4;
+  const int blk = block_of(f, dst.n, dst.start);
+  f32x4 *d = pick(dst.p, blk) + (f - pick(dst.start, blk)) * cols4 + col4;
+  f32x4 *tp = tmp + f * cols4 + col4;
+  const bool mine = f < N && colok;
   f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
-  if (!first && n > 0 && f < N && colok) acc = *d;
+  if (mine) {
+    if (src_mode == kSrcDst && (n > 0 || !skip_untouched)) acc = *d;
+    else if (src_mode == kSrcTmp) acc = *tp;
+  }
   if (staged)
     bwd_tile_sum<true>(spos + (s0 - r0), n, nmin, nmax, t, colok, gcol, acc);
   else
     bwd_tile_sum<false>(sorted_pos + s0, n, nmin, nmax, t, colok, gcol, acc);
-  if (f >= N || !colok) return;
+  if (!mine) return;
+  if (dst_mode == kDstTmp) {
+    *tp = acc;
+  } else if (dst_mode == kDstOutPlus) {
+    const f32x4 prev = *d;
+    *d = prev + acc;
+  } else if (!skip_untouched || n > 0) {
 #if SFT_BWD_NT_STORE
-  if (first || n > 0) __builtin_nontemporal_store(acc, d);
+    __builtin_nontemporal_store(acc, d);
 #else
-  if (first || n > 0) *d = acc;
+    *d = acc;
 #endif
+  }
+}
+
+// dV[j, :] = sum over i < reps of dWb[i * period + j, :], i ascending (the
+// reduction behind virtual_weight.repeat(32, 1), FEAT/halfka_v2_hm.py:69-70).
+// One thread per 16-byte chunk of dV; rows of consecutive threads are
+// consecutive, so every step reads contiguous memory.
+__global__ __launch_bounds__(kBlock) void virtual_reduce_kernel(const f32x4 *__restrict__ dWb, int64_t period,
+                                                                int reps, int64_t cols4, f32x4 *__restrict__ dV) {
+  constexpr int U = 8;
+  const int64_t total = period * cols4;
+  for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < total; i += (int64_t)gridDim.x * kBlock) {
+    f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+    int r = 0;
+    for (; r + U <= reps; r += U) {
+      f32x4 x[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) x[u] = dWb[(int64_t)(r + u) * total + i];
+#pragma unroll
+      for (int u = 0; u < U; ++u) acc += x[u];
+    }
+    for (; r < reps; ++r) acc += dWb[(int64_t)r * total + i];
+    dV[i] = acc;
+  }
 }
 
 // Position-major fp32 atomic scatter.  One wave per position (lanes over
@@ -480,6 +529,49 @@ int make_layout(int64_t B, int K, int64_t N, int L, uint32_t flags, BwdLayout &l
   return SFT_OK;
 }
 
+int launch_bias_partial(const float *grad, int64_t B, int L, int nparts, float *partial, f32x4 *gt, bool vec,
+                        hipStream_t s) {
+  const int64_t cols = vec ? L / 4 : L;
+  const int64_t rows = ceil_div(std::max<int64_t>(B, 1), nparts);
+  const int cpl = (int)std::min<int64_t>(ceil_div(cols, kWave), kMaxCpl);
+  const dim3 pgrid((unsigned)nparts, (unsigned)ceil_div(cols, (int64_t)kWave * cpl));
+  ProfScope prof(kProfBwdBiasPartial, s);
+#define SFT_BIAS_CASE(T, C)                                                                                  \
+  hipLaunchKernelGGL((bias_partial_kernel<T, C>), pgrid, dim3(kBlock), 0, s, reinterpret_cast<const T *>(grad), \
+                     B, cols, rows, reinterpret_cast<T *>(partial), reinterpret_cast<T *>(gt))
+#define SFT_BIAS_SWITCH(T)               \
+  switch (cpl) {                         \
+    case 1: SFT_BIAS_CASE(T, 1); break;  \
+    case 2: SFT_BIAS_CASE(T, 2); break;  \
+    case 3: SFT_BIAS_CASE(T, 3); break;  \
+    case 4: SFT_BIAS_CASE(T, 4); break;  \
+    case 5: SFT_BIAS_CASE(T, 5); break;  \
+    case 6: SFT_BIAS_CASE(T, 6); break;  \
+    case 7: SFT_BIAS_CASE(T, 7); break;  \
+    default: SFT_BIAS_CASE(T, 8); break; \
+  }
+  if (vec) {
+    SFT_BIAS_SWITCH(f32x4)
+  } else {
+    SFT_BIAS_SWITCH(float)
+  }
+#undef SFT_BIAS_SWITCH
+#undef SFT_BIAS_CASE
+  return check_launch("bias partial sums");
+}
+
+int launch_bias_final(const float *partial, int nparts, int L, float *db, int overwrite, bool vec, hipStream_t s) {
+  const int64_t cols = vec ? L / 4 : L;
+  ProfScope prof(kProfBwdBiasFinal, s);
+  const dim3 grid((unsigned)ceil_div(cols, kWavesPerBlock));
+  if (vec)
+    hipLaunchKernelGGL(bias_final_kernel<f32x4>, grid, dim3(kBlock), 0, s, reinterpret_cast<const f32x4 *>(partial),
+                       nparts, cols, reinterpret_cast<f32x4 *>(db), overwrite);
+  else
+    hipLaunchKernelGGL(bias_final_kernel<float>, grid, dim3(kBlock), 0, s, partial, nparts, cols, db, overwrite);
+  return check_launch("bias reduction");
+}
+
 }  // namespace
 
 int bwd_workspace(int64_t B, int K, int64_t N, int L, uint32_t flags, size_t *bytes) {
@@ -511,47 +603,12 @@ int bwd_f32(const int32_t *idx, int64_t B, int K, const float *grad, int64_t N, 
   // ---- bias grad ----
   {
     const bool vec = (L % 4 == 0) && ((uintptr_t)grad % 16 == 0) && ((uintptr_t)db % 16 == 0);
-    const int64_t cols = vec ? L / 4 : L;
-    const int64_t rows = ceil_div(std::max<int64_t>(B, 1), lay.nparts);
-    const int cpl = (int)std::min<int64_t>(ceil_div(cols, kWave), kMaxCpl);
-    const dim3 pgrid((unsigned)lay.nparts, (unsigned)ceil_div(cols, (int64_t)kWave * cpl));
-    {
-      ProfScope prof(kProfBwdBiasPartial, s);
-#define SFT_BIAS_CASE(T, C)                                                                                  \
-  hipLaunchKernelGGL((bias_partial_kernel<T, C>), pgrid, dim3(kBlock), 0, s, reinterpret_cast<const T *>(grad), \
-                     B, cols, rows, reinterpret_cast<T *>(w + lay.partial), reinterpret_cast<T *>(gt))
-#define SFT_BIAS_SWITCH(T)               \
-  switch (cpl) {                         \
-    case 1: SFT_BIAS_CASE(T, 1); break;  \
-    case 2: SFT_BIAS_CASE(T, 2); break;  \
-    case 3: SFT_BIAS_CASE(T, 3); break;  \
-    case 4: SFT_BIAS_CASE(T, 4); break;  \
-    case 5: SFT_BIAS_CASE(T, 5); break;  \
-    case 6: SFT_BIAS_CASE(T, 6); break;  \
-    case 7: SFT_BIAS_CASE(T, 7); break;  \
-    default: SFT_BIAS_CASE(T, 8); break; \
-  }
-      if (vec) {
-        SFT_BIAS_SWITCH(f32x4)
-      } else {
-        SFT_BIAS_SWITCH(float)
-      }
-#undef SFT_BIAS_SWITCH
-#undef SFT_BIAS_CASE
-    }
-    if ((rc = check_launch("bias partial sums")) != SFT_OK) return rc;
-    {
-      ProfScope prof(kProfBwdBiasFinal, s);
-      const dim3 grid((unsigned)ceil_div(cols, kWavesPerBlock));
-      if (vec)
-        hipLaunchKernelGGL(bias_final_kernel<f32x4>, grid, dim3(kBlock), 0, s,
-                           reinterpret_cast<const f32x4 *>(w + lay.partial), lay.nparts, cols,
-                           reinterpret_cast<f32x4 *>(db), overwrite);
-      else
-        hipLaunchKernelGGL(bias_final_kernel<float>, grid, dim3(kBlock), 0, s,
-                           reinterpret_cast<const float *>(w + lay.partial), lay.nparts, cols, db, overwrite);
-    }
-    if ((rc = check_launch("bias reduction")) != SFT_OK) return rc;
+    if ((rc = launch_bias_partial(grad, B, L, lay.nparts, reinterpret_cast<float *>(w + lay.partial), gt, vec, s)) !=
+        SFT_OK)
+      return rc;
+    if ((rc = launch_bias_final(reinterpret_cast<const float *>(w + lay.partial), lay.nparts, L, db, overwrite, vec,
+                                s)) != SFT_OK)
+      return rc;
   }
 
   if (flags & SFT_BWD_ATOMIC) {
@@ -616,10 +673,15 @@ int bwd_f32(const int32_t *idx, int64_t B, int K, const float *grad, int64_t N, 
     const int ntiles = (int)ceil_div(cols4, kBwdTileCh);
     const int ngroups = (int)ceil_div(N, kBwdFeatPerBlock);
     const int64_t blocks = tile_sched_items_per_xcd(ntiles, ngroups) * kXcds;
+    RowDst dst{};
+    dst.n = 1;
+    dst.start[1] = N;
+    dst.p[0] = reinterpret_cast<f32x4 *>(dW);
     for (int h = 0; h < nc; ++h) {
       ProfScope prof(kProfBwdTiled, s);
       hipLaunchKernelGGL(bwd_tiled_gather_kernel, dim3((unsigned)blocks), dim3(kBlock), 0, s, seg + (int64_t)h * N,
-                         pos, N, gt, B, cols4, reinterpret_cast<f32x4 *>(dW), h == 0 ? 1 : 0, ntiles, ngroups);
+                         pos, N, gt, B, cols4, dst, (f32x4 *)nullptr, h == 0 ? kSrcZero : kSrcDst, kDstOut, ntiles,
+                         ngroups);
       if ((rc = check_launch("tiled feature gather")) != SFT_OK) return rc;
     }
     return SFT_OK;
@@ -638,6 +700,115 @@ int bwd_f32(const int32_t *idx, int64_t B, int K, const float *grad, int64_t N, 
     }
   }
   return check_launch("feature row gather");
+}
+
+
+// ------------------------------------------- composed table, two perspectives ----
+// Workspace: bias partials of both grads | sort buffers | segment starts |
+// grad tiles | tmp (the second perspective's sums, [N, L]).
+struct PairLayout {
+  size_t partial, sort, seg, gt, tmp, total;
+  int nparts, nc;
+};
+
+void make_pair_layout(int64_t B, int K, int64_t N, int L, PairLayout &lay) {
+  const int64_t M = B * K;
+  lay.nparts = bias_parts(B);
+  lay.nc = sort_chunks(B, L, SFT_BWD_OVERWRITE);
+  size_t off = 0;
+  lay.partial = off;
+  off = align256(off + (size_t)2 * lay.nparts * (size_t)L * sizeof(float));
+  lay.sort = off;
+  off = align256(off + slot_sort_workspace(std::max<int64_t>(M, 1)));
+  lay.seg = off;
+  off = align256(off + (size_t)(lay.nc * N + 1) * sizeof(int32_t));
+  lay.gt = off;
+  off = align256(off + (size_t)(ceil_div(L, 32) * B * 32) * sizeof(float));
+  lay.tmp = off;
+  off = align256(off + (size_t)N * (size_t)L * sizeof(float));
+  lay.total = off;
+}
+
+size_t bwd_pair_workspace(int64_t B, int K, int64_t N, int L) {
+  PairLayout lay;
+  make_pair_layout(B, K, N, L, lay);
+  return lay.total;
+}
+
+int bwd_pair_f32(const int32_t *idx0, const int32_t *idx1, int64_t B, int K, const float *grad0, const float *grad1,
+                 int64_t N, int L, const RowDst &dst, const float *const *vgrad_src, float *const *vgrad,
+                 const int64_t *vperiod, const int64_t *vreps, int nvirt, float *db, void *ws, size_t ws_bytes,
+                 hipStream_t s) {
+  PairLayout lay;
+  make_pair_layout(B, K, N, L, lay);
+  if (ws_bytes < lay.total || ws == nullptr || (uintptr_t)ws % 256 != 0)
+    return fail(SFT_EWORKSPACE, "sft_ft_bwd_pair_f32: workspace smaller than sft_ft_pair_workspace_size() "
+                                "or not 256-byte aligned");
+  char *w = static_cast<char *>(ws);
+  const int64_t M = B * K;
+  const int64_t cols4 = L / 4;
+  float *partial = reinterpret_cast<float *>(w + lay.partial);
+  f32x4 *gt = reinterpret_cast<f32x4 *>(w + lay.gt);
+  f32x4 *tmp = reinterpret_cast<f32x4 *>(w + lay.tmp);
+  int32_t *seg = reinterpret_cast<int32_t *>(w + lay.seg);
+  const int ntiles = (int)ceil_div(cols4, kBwdTileCh);
+  const int ngroups = (int)ceil_div(N, kBwdFeatPerBlock);
+  const int64_t blocks = tile_sched_items_per_xcd(ntiles, ngroups) * kXcds;
+  const int nc = lay.nc;
+  const int chunk_rows = (int)(nc > 1 ? half_rows(B) : B);
+  int rc;
+  for (int p = 0; p < 2; ++p) {
+    const float *grad = p == 0 ? grad0 : grad1;
+    if ((rc = launch_bias_partial(grad, B, L, lay.nparts, partial + (size_t)p * lay.nparts * L, gt, true, s)) !=
+        SFT_OK)
+      return rc;
+    unsigned *keys = nullptr, *totals = nullptr;
+    int32_t *pos = nullptr;
+    int ntot = 0;
+    {
+      ProfScope prof(kProfBwdSort, s);
+      if ((rc = slot_sort(p == 0 ? idx0 : idx1, M, K, N, chunk_rows, nc, w + lay.sort, &keys, &pos, &totals, &ntot,
+                          s)) != SFT_OK)
+        return rc;
+    }
+    {
+      ProfScope prof(kProfBwdOffsets, s);
+      hipLaunchKernelGGL(seg_offsets_kernel, dim3((unsigned)ceil_div(M + 1, kBlock)), dim3(kBlock), 0, s, keys,
+                         (int64_t)nc * N, totals, ntot, seg);
+      if ((rc = check_launch("segment offsets")) != SFT_OK) return rc;
+    }
+    for (int h = 0; h < nc; ++h) {
+      int src_mode, dst_mode;
+      if (p == 0) {
+        src_mode = h == 0 ? kSrcZero : kSrcDst;
+        dst_mode = kDstOut;
+      } else {
+        src_mode = h == 0 ? kSrcZero : kSrcTmp;
+        dst_mode = h == nc - 1 ? kDstOutPlus : kDstTmp;
+      }
+      ProfScope prof(kProfBwdTiled, s);
+      hipLaunchKernelGGL(bwd_tiled_gather_kernel, dim3((unsigned)blocks), dim3(kBlock), 0, s, seg + (int64_t)h * N,
+                         pos, N, gt, B, cols4, dst, tmp, src_mode, dst_mode, ntiles, ngroups);
+      if ((rc = check_launch("tiled feature gather")) != SFT_OK) return rc;
+    }
+  }
+  if ((rc = launch_bias_final(partial, 2 * lay.nparts, L, db, 1, true, s)) != SFT_OK) return rc;
+  for (int v = 0; v < nvirt; ++v) {
+    const int64_t total = vperiod[v] * cols4;
+    ProfScope prof(kProfBwdVirtual, s);
+    hipLaunchKernelGGL(virtual_reduce_kernel, dim3((unsigned)std::min<int64_t>(ceil_div(total, kBlock), 1 << 16)),
+                       dim3(kBlock), 0, s, reinterpret_cast<const f32x4 *>(vgrad_src[v]), vperiod[v], (int)vreps[v],
+                       cols4, reinterpret_cast<f32x4 *>(vgrad[v]));
+    if ((rc = check_launch("virtual row reduction")) != SFT_OK) return rc;
+  }
+  return SFT_OK;
+}
+
+void zero_f32(float *p, int64_t n, hipStream_t s) {
+  if (n <= 0) return;
+  ProfScope prof(kProfBwdZero, s);
+  hipLaunchKernelGGL(zero_kernel, dim3((unsigned)std::min<int64_t>(ceil_div(n, kBlock), 1 << 16)), dim3(kBlock), 0, s,
+                     p, n);
 }
 
 }  // namespace sft

@@ -247,15 +247,25 @@ constexpr int kTiledRounds = SFT_TILED_ROUNDS;                        // positio
 constexpr int kTiledPosPerRound = kWavesPerBlock * (kWave / kTileCh);  // 32
 constexpr int kTiledPosPerBlock = kTiledPosPerRound * kTiledRounds;
 
-__global__ __launch_bounds__(kBlock) void fwd_tiled_kernel(const int32_t *__restrict__ idx, int64_t B, int K, int N,
+// Two perspectives share one launch: chunks [0, nchunks_p) read idx0 and write
+// out0, chunks [nchunks_p, 2 nchunks_p) idx1 and out1, so an XCD gathers both
+// perspectives from a tile while it is in L2.  A single-perspective call passes
+// the same arrays twice and nchunks_p = nchunks.
+__global__ __launch_bounds__(kBlock) void fwd_tiled_kernel(const int32_t *__restrict__ idx0,
+                                                           const int32_t *__restrict__ idx1, int64_t B, int K, int N,
                                                            const f32x4 *__restrict__ Wt, int64_t cols4,
-                                                           const f32x4 *__restrict__ bias, f32x4 *__restrict__ out,
-                                                           int kpad, int ntiles, int nchunks) {
+                                                           const f32x4 *__restrict__ bias, f32x4 *__restrict__ out0,
+                                                           f32x4 *__restrict__ out1, int kpad, int ntiles, int nchunks,
+                                                           int nchunks_p) {
   constexpr int U = SFT_FWD_TILED_U;
   constexpr int PPW = kWave / kTileCh;  // 8 positions per wave per round
   extern __shared__ int smem[];
-  const TileItem it = tile_sched_item(blockIdx.x, ntiles, nchunks);
+  TileItem it = tile_sched_item(blockIdx.x, ntiles, nchunks);
   if (it.tile >= ntiles) return;  // whole block: uniform
+  const bool second = it.chunk >= nchunks_p;
+  if (second) it.chunk -= nchunks_p;
+  const int32_t *__restrict__ idx = second ? idx1 : idx0;
+  f32x4 *__restrict__ out = second ? out1 : out0;
   const int wave = uniform(threadIdx.x / kWave);
   const int lane = threadIdx.x % kWave;
   int *list = smem + wave * PPW * kpad;
@@ -441,6 +451,28 @@ void launch_tile_relayout(const f32x4 *src, int64_t rows, int64_t cols4, f32x4 *
                      dim3(kBlock), 0, s, src, rows, cols4, dst);
 }
 
+// Composed-table re-layout: merged row r of block s is w_s[r'] (+ v_s[r' %
+// period_s] when the block has virtual rows; r' = r - start_s), added in
+// binary32 exactly as the table the reference materialises
+// (FEAT/halfka_v2_hm.py:69-70, FEAT/composed.py:49-50), and stored straight into
+// the 32-column tiles of the tiled gather.  total = N * cols4 < 2^31.
+static __global__ __launch_bounds__(kBlock) void fold_relayout_kernel(FoldSrc src, int N, int cols4,
+                                                                      f32x4 *__restrict__ Wt) {
+  const int total = N * cols4;
+  for (int i = blockIdx.x * kBlock + threadIdx.x; i < total; i += gridDim.x * kBlock) {
+    const int r = i / cols4, c = i - r * cols4;
+    const int s = block_of(r, src.n, src.start);
+    const int rl = r - (int)pick(src.start, s);
+    f32x4 x = pick(src.w, s)[(int64_t)rl * cols4 + c];
+    const f32x4 *v = pick(src.v, s);
+    if (v != nullptr) {
+      const f32x4 y = v[(int64_t)(rl % (int)pick(src.period, s)) * cols4 + c];
+      x += y;
+    }
+    Wt[((int64_t)(c >> 3) * N + r) * 8 + (c & 7)] = x;
+  }
+}
+
 size_t index_lds_bytes(int G, int K) {
   const int ppw = kWave / G;
   return (size_t)(kWavesPerBlock * ppw * round_up4(K) + kWavesPerBlock * ppw) * sizeof(int);
@@ -501,10 +533,41 @@ int fwd_f32_tiled(const int32_t *idx, int64_t B, int K, const float *W, int64_t 
   const int64_t blocks = tile_sched_items_per_xcd(ntiles, nchunks) * kXcds;
   {
     ProfScope prof(kProfFwdTiled, s);
-    hipLaunchKernelGGL(fwd_tiled_kernel, dim3((unsigned)blocks), dim3(kBlock), lds, s, idx, B, K, (int)N, wt, cols4,
-                       reinterpret_cast<const f32x4 *>(bias), reinterpret_cast<f32x4 *>(out), kpad, ntiles, nchunks);
+    hipLaunchKernelGGL(fwd_tiled_kernel, dim3((unsigned)blocks), dim3(kBlock), lds, s, idx, idx, B, K, (int)N, wt,
+                       cols4, reinterpret_cast<const f32x4 *>(bias), reinterpret_cast<f32x4 *>(out),
+                       reinterpret_cast<f32x4 *>(out), kpad, ntiles, nchunks, nchunks);
   }
   return check_launch("sft_ft_fwd_f32_ex (tiled gather)");
+}
+
+int fwd_pair_f32(const int32_t *idx0, const int32_t *idx1, int64_t B, int K, const FoldSrc &src, int64_t N, int L,
+                 const float *bias, float *out0, float *out1, void *ws, size_t ws_bytes, hipStream_t s) {
+  if (ws_bytes < fwd_tiled_workspace(N, L) || ws == nullptr || (uintptr_t)ws % 256 != 0)
+    return fail(SFT_EWORKSPACE, "sft_ft_fwd_pair_f32: workspace smaller than sft_ft_pair_workspace_size() "
+                                "or not 256-byte aligned");
+  const int64_t cols4 = L / 4;
+  const int ntiles = (int)ceil_div(L, kTileF);
+  const int kpad = round_up4(K);
+  const size_t lds = index_lds_bytes(kTileCh, K);
+  if (lds > kMaxIndexLds) return fail(SFT_EUNSUPPORTED, "sft_ft_fwd_pair_f32: max_active too large for the LDS index lists");
+  f32x4 *wt = static_cast<f32x4 *>(ws);
+  {
+    const int64_t total = N * cols4;
+    ProfScope prof(kProfFwdFold, s);
+    hipLaunchKernelGGL(fold_relayout_kernel, dim3((unsigned)std::min<int64_t>(ceil_div(total, kBlock), 1 << 16)),
+                       dim3(kBlock), 0, s, src, (int)N, (int)cols4, wt);
+  }
+  int rc = check_launch("sft_ft_fwd_pair_f32 (fold re-layout)");
+  if (rc != SFT_OK || B == 0) return rc;
+  const int nchunks_p = (int)ceil_div(B, kTiledPosPerBlock);
+  const int64_t blocks = tile_sched_items_per_xcd(ntiles, 2 * nchunks_p) * kXcds;
+  {
+    ProfScope prof(kProfFwdTiled, s);
+    hipLaunchKernelGGL(fwd_tiled_kernel, dim3((unsigned)blocks), dim3(kBlock), lds, s, idx0, idx1, B, K, (int)N, wt,
+                       cols4, reinterpret_cast<const f32x4 *>(bias), reinterpret_cast<f32x4 *>(out0),
+                       reinterpret_cast<f32x4 *>(out1), kpad, ntiles, 2 * nchunks_p, nchunks_p);
+  }
+  return check_launch("sft_ft_fwd_pair_f32 (tiled gather)");
 }
 
 size_t fwd_i16_tiled_workspace(int64_t N, int L) {

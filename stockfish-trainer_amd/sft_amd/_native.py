@@ -18,6 +18,7 @@ PKG_ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 LIB_PATH = os.path.join(PKG_ROOT, "lib", "libsft_ft.so")
 
 SFT_OK = 0
+SFT_EUNSUPPORTED = -4
 SFT_FWD_AUTO = 0x0
 SFT_FWD_ROWS = 0x1
 SFT_BWD_ACCUMULATE = 0x0
@@ -55,6 +56,18 @@ SIGNATURES = {
     "sft_ft_fwd_i16_ex": (
         ctypes.c_int,
         [_vp, _i64, _i32, _vp, _i64, _i32, _vp, _vp, _i32, _vp, _vp, _i32, _i32, _vp, ctypes.c_size_t, _u32, _vp]),
+    "sft_ft_pair_workspace_size": (
+        ctypes.c_int,
+        [_i64, _i32, _i32, ctypes.POINTER(_i64), ctypes.POINTER(_i64), _i32, ctypes.POINTER(ctypes.c_size_t),
+         ctypes.POINTER(ctypes.c_size_t)]),
+    "sft_ft_fwd_pair_f32": (
+        ctypes.c_int,
+        [_vp, _vp, _i64, _i32, _i32, ctypes.POINTER(_vp), ctypes.POINTER(_vp), ctypes.POINTER(_i64),
+         ctypes.POINTER(_i64), _i32, _vp, _vp, _vp, _vp, ctypes.c_size_t, _vp]),
+    "sft_ft_bwd_pair_f32": (
+        ctypes.c_int,
+        [_vp, _vp, _i64, _i32, _vp, _vp, _i32, ctypes.POINTER(_i64), ctypes.POINTER(_i64), _i32,
+         ctypes.POINTER(_vp), ctypes.POINTER(_vp), _vp, _vp, ctypes.c_size_t, _vp]),
     "sft_quantize_i16": (ctypes.c_int, [_vp, _i64, ctypes.c_float, _vp, _vp]),
     "sft_prof_enable": (ctypes.c_int, [ctypes.c_int]),
     "sft_prof_num_kinds": (ctypes.c_int, []),
@@ -227,6 +240,91 @@ def ft_fwd_i16(idx: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor, out:
         _check(lib().sft_ft_fwd_i16_ex(_ptr(idx), B, K, _ptr(weight), N, L, _ptr(bias), _ptr(psqt_weight), P,
                                        _ptr(out), _ptr(psqt_out), clip_lo, clip_hi, ptr, nbytes, flags,
                                        _stream(idx.device)), "sft_ft_fwd_i16_ex")
+    del ws
+
+
+# ---- composed table, both perspectives ----
+def _i64_array(vals):
+    return (_i64 * len(vals))(*[int(v) for v in vals])
+
+
+def _ptr_array(tensors):
+    return (_vp * len(tensors))(*[None if t is None else t.data_ptr() for t in tensors])
+
+
+def pair_workspace_bytes(B: int, K: int, rows, virtual_rows, L: int):
+    """(forward bytes, backward bytes) of the composed-table pair calls, or None
+    when the library does not run this shape fused (then the caller composes the
+    table itself)."""
+    key = ("pair", B, K, tuple(rows), tuple(virtual_rows), L)
+    if key in _ws_cache:
+        return _ws_cache[key]
+    fb, bb = ctypes.c_size_t(0), ctypes.c_size_t(0)
+    rc = lib().sft_ft_pair_workspace_size(B, K, len(rows), _i64_array(rows), _i64_array(virtual_rows), L,
+                                          ctypes.byref(fb), ctypes.byref(bb))
+    if rc == SFT_EUNSUPPORTED:
+        got = None
+    else:
+        _check(rc, "sft_ft_pair_workspace_size")
+        got = (int(fb.value), int(bb.value))
+    _ws_cache[key] = got
+    return got
+
+
+def _pair_shapes(idx0, idx1, tables, virtuals):
+    _require(idx0.dim() == 2 and idx0.dtype == torch.int32, "idx0 must be int32 [B, K]")
+    _require(idx1.shape == idx0.shape and idx1.dtype == torch.int32, "idx1 must be int32 [B, K] like idx0")
+    _require(1 <= len(tables) <= 4 and len(virtuals) == len(tables), "1 to 4 table blocks, one virtual entry each")
+    L = tables[0].shape[1]
+    rows, vrows = [], []
+    for w, v in zip(tables, virtuals):
+        _require(w.dim() == 2 and w.shape[1] == L and w.dtype == torch.float32, "block tables must be float32 [R, L]")
+        rows.append(w.shape[0])
+        if v is None:
+            vrows.append(0)
+        else:
+            _require(v.dim() == 2 and v.shape[1] == L and v.dtype == torch.float32, "virtual tables must be float32 [V, L]")
+            _require(w.shape[0] % v.shape[0] == 0, "block rows must be a multiple of its virtual rows")
+            vrows.append(v.shape[0])
+    return idx0.shape[0], idx0.shape[1], L, rows, vrows
+
+
+def ft_fwd_pair_f32(idx0, idx1, tables, virtuals, bias, out0, out1) -> None:
+    """out_p = bias + sum of merged-table rows selected by idx_p, p = 0, 1; merged
+    row r of a block with virtual rows V is table[r] + V[r % len(V)]."""
+    B, K, L, rows, vrows = _pair_shapes(idx0, idx1, tables, virtuals)
+    _require(bias.shape == (L,) and bias.dtype == torch.float32, "bias must be float32 [L]")
+    for o in (out0, out1):
+        _require(o.shape == (B, L) and o.dtype == torch.float32, "outputs must be float32 [B, L]")
+    dev = idx0.device
+    _on_gpu(dev, idx0, idx1, bias, out0, out1, *tables, *[v for v in virtuals if v is not None])
+    sizes = pair_workspace_bytes(B, K, rows, vrows, L)
+    _require(sizes is not None, f"sft: shape not supported by the composed pair path: {last_error()}")
+    ws, ptr = _workspace(sizes[0], dev)
+    with torch.cuda.device(dev):
+        _check(lib().sft_ft_fwd_pair_f32(_ptr(idx0), _ptr(idx1), B, K, len(rows), _ptr_array(tables),
+                                         _ptr_array(virtuals), _i64_array(rows), _i64_array(vrows), L, _ptr(bias),
+                                         _ptr(out0), _ptr(out1), ptr, sizes[0], _stream(dev)), "sft_ft_fwd_pair_f32")
+    del ws
+
+
+def ft_bwd_pair_f32(idx0, idx1, grad0, grad1, table_grads, virtual_grads, bias_grad) -> None:
+    """Overwrites table_grads (dW_0 + dW_1 per block), virtual_grads (sum over
+    repeats) and bias_grad (sum of both grads' rows)."""
+    B, K, L, rows, vrows = _pair_shapes(idx0, idx1, table_grads, virtual_grads)
+    _require(bias_grad.shape == (L,) and bias_grad.dtype == torch.float32, "bias_grad must be float32 [L]")
+    for g in (grad0, grad1):
+        _require(g.shape == (B, L) and g.dtype == torch.float32, "grads must be float32 [B, L]")
+    dev = idx0.device
+    _on_gpu(dev, idx0, idx1, grad0, grad1, bias_grad, *table_grads, *[v for v in virtual_grads if v is not None])
+    sizes = pair_workspace_bytes(B, K, rows, vrows, L)
+    _require(sizes is not None, f"sft: shape not supported by the composed pair path: {last_error()}")
+    ws, ptr = _workspace(sizes[1], dev)
+    with torch.cuda.device(dev):
+        _check(lib().sft_ft_bwd_pair_f32(_ptr(idx0), _ptr(idx1), B, K, _ptr(grad0), _ptr(grad1), len(rows),
+                                         _i64_array(rows), _i64_array(vrows), L, _ptr_array(table_grads),
+                                         _ptr_array(virtual_grads), _ptr(bias_grad), ptr, sizes[1], _stream(dev)),
+               "sft_ft_bwd_pair_f32")
     del ws
 
 

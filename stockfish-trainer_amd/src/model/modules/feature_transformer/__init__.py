@@ -1,5 +1,7 @@
 from .functions import SparseLinearFunction
+from .composed_function import ComposedSparseLinearFunction
 
 __all__ = [
     "SparseLinearFunction",
+    "ComposedSparseLinearFunction",
 ]

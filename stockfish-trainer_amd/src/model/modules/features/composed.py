@@ -7,12 +7,20 @@ import math
 import torch
 from torch import nn
 
-from ..feature_transformer import SparseLinearFunction
+from ..feature_transformer import ComposedSparseLinearFunction, SparseLinearFunction
+from ..feature_transformer.composed_function import composed_pair_supported
 from .input_feature import InputFeature
 
 
 class ComposedFeatureTransformer(nn.Module):
-    """Owns the shared bias; each feature block owns its weight rows."""
+    """Owns the shared bias; each feature block owns its weight rows.
+
+    forward() runs both perspectives through ComposedSparseLinearFunction (one
+    fused op, same values) when the library takes the shape; with
+    `fused = False`, or for shapes it does not take, it runs the reference
+    composition: merged_weight() and SparseLinearFunction per perspective."""
+
+    fused: bool = True
 
     def __init__(self, features: list):
         super().__init__()
@@ -44,6 +52,18 @@ class ComposedFeatureTransformer(nn.Module):
         return torch.cat([f.merged_weight() for f in self.features], dim=0)
 
     def forward(self, feature_indices_0, feature_indices_1):
+        if self.fused and feature_indices_0.is_cuda and feature_indices_0.shape == feature_indices_1.shape:
+            blocks = [f.table_blocks() for f in self.features]
+            B, K = feature_indices_0.shape
+            if composed_pair_supported(B, K, blocks, self.num_outputs):
+                tables, virtual_rows = [], []
+                for w, v in blocks:
+                    tables.append(w)
+                    if v is not None:
+                        tables.append(v)
+                    virtual_rows.append(0 if v is None else v.shape[0])
+                return ComposedSparseLinearFunction.apply(
+                    feature_indices_0, feature_indices_1, self.bias, tuple(virtual_rows), *tables)
         merged = self.merged_weight()
         return (
             SparseLinearFunction.apply(feature_indices_0, merged, self.bias),

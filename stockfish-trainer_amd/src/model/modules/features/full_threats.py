@@ -26,6 +26,9 @@ class FullThreats(InputFeature):
     def merged_weight(self) -> torch.Tensor:
         return self.weight
 
+    def table_blocks(self):
+        return self.weight, None
+
     @torch.no_grad()
     def coalesce(self) -> None:
         return None

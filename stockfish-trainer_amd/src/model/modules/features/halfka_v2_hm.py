@@ -71,6 +71,9 @@ class HalfKav2Hm(InputFeature):
     def merged_weight(self) -> torch.Tensor:
         return self.weight + self.virtual_weight.repeat(self.NUM_BUCKETS, 1)
 
+    def table_blocks(self):
+        return self.weight, self.virtual_weight
+
     @torch.no_grad()
     def coalesce(self) -> None:
         self.weight.add_(self.virtual_weight.repeat(self.NUM_BUCKETS, 1))

@@ -21,6 +21,12 @@ class InputFeature(nn.Module, ABC):
     def merged_weight(self) -> torch.Tensor:
         """Effective [NUM_INPUTS, num_outputs] table (virtual rows folded in)."""
 
+    def table_blocks(self):
+        """(weight, virtual table or None) whose fold is merged_weight(): row r of
+        the merged table is weight[r] (+ virtual[r % len(virtual)]).  The default
+        hands over merged_weight() itself, without virtual rows."""
+        return self.merged_weight(), None
+
     @abstractmethod
     def coalesce(self) -> None: ...
 

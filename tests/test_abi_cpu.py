@@ -120,3 +120,59 @@ def test_profiling_kinds_and_empty_collect():
     _native.prof_enable(True)
     assert _native.prof_collect() == {}
     _native.prof_enable(False)
+
+
+def _i64s(*v):
+    return (ctypes.c_int64 * len(v))(*v)
+
+
+def test_pair_workspace_size_and_shape_checks():
+    lib = _native.lib()
+    fb, bb = ctypes.c_size_t(0), ctypes.c_size_t(0)
+    # HalfKAv2_hm: 24576 rows folded with 768 virtual rows, L = 1048
+    rc = lib.sft_ft_pair_workspace_size(65536, 32, 1, _i64s(24576), _i64s(768), 1048, ctypes.byref(fb), ctypes.byref(bb))
+    assert rc == 0, _native.last_error()
+    assert fb.value == 33 * 24576 * 32 * 4  # the merged table in 32-column tiles
+    assert bb.value >= 24576 * 1048 * 4 + 33 * 65536 * 32 * 4  # tmp sums + grad tiles
+    # Full_Threats + HalfKAv2_hm
+    rc = lib.sft_ft_pair_workspace_size(65536, 160, 2, _i64s(60720, 24576), _i64s(0, 768), 1048, ctypes.byref(fb),
+                                        ctypes.byref(bb))
+    assert rc == 0 and fb.value == 33 * 85296 * 32 * 4
+    # shapes the fused path does not take
+    rc = lib.sft_ft_pair_workspace_size(65536, 32, 1, _i64s(24576), _i64s(768), 136, ctypes.byref(fb), ctypes.byref(bb))
+    assert rc == _native.SFT_EUNSUPPORTED and "output_size" in _native.last_error()
+    rc = lib.sft_ft_pair_workspace_size(16, 32, 1, _i64s(600000), _i64s(0), 1048, ctypes.byref(fb), ctypes.byref(bb))
+    assert rc == _native.SFT_EUNSUPPORTED
+    # invalid descriptions
+    for nb, rows, vrows, needle in ((0, (10,), (0,), "num_blocks"), (5, (1,) * 5, (0,) * 5, "num_blocks"),
+                                    (1, (1000,), (768,), "divide"), (1, (0,), (0,), "block_rows"),
+                                    (1, (100,), (-1,), "divide")):
+        rc = lib.sft_ft_pair_workspace_size(16, 32, nb, _i64s(*rows), _i64s(*vrows), 1048, ctypes.byref(fb),
+                                            ctypes.byref(bb))
+        assert rc == -1 and needle in _native.last_error()
+
+
+def test_pair_calls_reject_before_launch():
+    lib = _native.lib()
+    ptrs = (ctypes.c_void_p * 1)(0x1000)
+    nulls = (ctypes.c_void_p * 1)(None)
+    odd = (ctypes.c_void_p * 1)(0x1008)
+    rows, vrows = _i64s(24576), _i64s(768)
+    # null virtual table for a block that declares virtual rows
+    rc = lib.sft_ft_fwd_pair_f32(P, P, 4, 32, 1, ptrs, nulls, rows, vrows, 1048, P, P, P, P, 1 << 30, None)
+    assert rc == -1 and "null" in _native.last_error()
+    # misaligned table
+    rc = lib.sft_ft_fwd_pair_f32(P, P, 4, 32, 1, odd, ptrs, rows, vrows, 1048, P, P, P, P, 1 << 30, None)
+    assert rc == -1 and "aligned" in _native.last_error()
+    # unsupported output size
+    rc = lib.sft_ft_fwd_pair_f32(P, P, 4, 32, 1, ptrs, ptrs, rows, vrows, 136, P, P, P, P, 1 << 30, None)
+    assert rc == _native.SFT_EUNSUPPORTED
+    # missing second index tensor
+    rc = lib.sft_ft_fwd_pair_f32(P, None, 4, 32, 1, ptrs, ptrs, rows, vrows, 1048, P, P, P, P, 1 << 30, None)
+    assert rc == -1 and "null" in _native.last_error()
+    rc = lib.sft_ft_bwd_pair_f32(P, P, 4, 32, P, P, 1, rows, vrows, 1048, ptrs, nulls, P, P, 1 << 30, None)
+    assert rc == -1 and "null" in _native.last_error()
+    rc = lib.sft_ft_bwd_pair_f32(P, P, 4, 32, P, P, 1, rows, vrows, 1048, odd, ptrs, P, P, 1 << 30, None)
+    assert rc == -1 and "aligned" in _native.last_error()
+    rc = lib.sft_ft_bwd_pair_f32(P, P, 4, 32, P, None, 1, rows, vrows, 1048, ptrs, ptrs, P, P, 1 << 30, None)
+    assert rc == -1 and "null" in _native.last_error()
