@@ -10,6 +10,7 @@ restatement timed on a bounded sample of the same workload).
 
   python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--workload 1]
                   [--bwd sorted|atomic] [--cpu-seconds 12] [--no-cpu]
+  python bench.py --composed halfka|threats   (module surface, fused vs reference composition)
 """
 
 from __future__ import annotations
@@ -56,6 +57,10 @@ def kernel_step_bytes(kind: str, w, idx_pair) -> float | None:
         return 2 * 2 * 4.0 * w.B * w.L
     if kind == "bwd_bias_partial":
         return 2 * 4.0 * w.B * w.L
+    if kind == "fwd_fold_relayout":  # one launch per step: table (+ virtual rows) read, tiles written
+        return 4.0 * (2 * w.N + getattr(w, "virtual_rows", 0)) * w.L
+    if kind == "bwd_virtual_reduce":  # folded block's grad read, virtual grad written
+        return 4.0 * (getattr(w, "folded_rows", 0) + getattr(w, "virtual_rows", 0)) * w.L
     return None
 
 
@@ -166,6 +171,103 @@ def bench_q16(args, w, dev) -> int:
     return 0
 
 
+COMPOSED = {"halfka": ("HalfKAv2_hm^", 16, 32), "threats": ("Full_Threats+HalfKAv2_hm^", 32, 160)}
+
+
+def bench_composed(args, dev) -> int:
+    """ComposedFeatureTransformer forward + backward of both perspectives at
+    B=65536, L=1048 through the module surface: the fused pair op (default)
+    timed against the reference composition (merged_weight, then
+    SparseLinearFunction per perspective) on the same kernels."""
+    import types
+
+    import numpy as np
+    import torch
+
+    from sft_amd import _native, workloads
+    from src.model.modules.features import get_feature_cls
+
+    name, lo, hi = COMPOSED[args.composed]
+    B, L = 65536, 1048
+    torch.manual_seed(0)
+    ft = get_feature_cls(name)(L).to(dev)
+    vrows = folded = 0
+    for f in ft.features:
+        if hasattr(f, "virtual_weight"):
+            with torch.no_grad():
+                f.virtual_weight.normal_(0, 0.01)
+            vrows += f.virtual_weight.shape[0]
+            folded += f.weight.shape[0]
+    N, K = ft.NUM_INPUTS, ft.MAX_ACTIVE_FEATURES
+    log(f"[bench] composed {name}: B={B} N={N} K={K} active U[{lo},{hi}] L={L}")
+    idx = [workloads.make_indices(np.random.default_rng([200 + K, s]), B, N, K, lo, hi) for s in (0, 1)]
+    iw, ib = (torch.from_numpy(i).to(dev) for i in idx)
+    gw = torch.randn(B, L, device=dev)
+    gb = torch.randn(B, L, device=dev)
+
+    def step():
+        for p in ft.parameters():
+            p.grad = None
+        ow, ob = ft(iw, ib)
+        torch.autograd.backward([ow, ob], [gw, gb])
+
+    def timed(fused: bool, prof: bool):
+        ft.fused = fused
+        for _ in range(args.warmup):
+            step()
+        torch.cuda.synchronize()
+        if prof:
+            _native.prof_enable(True)
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(args.steps):
+            step()
+        e1.record()
+        torch.cuda.synchronize()
+        out = _native.prof_collect() if prof else None
+        _native.prof_enable(False)
+        return e0.elapsed_time(e1) / args.steps, out
+
+    ref_ms, _ = timed(False, False)
+    ms, prof = timed(True, True)
+    log(f"[bench] fused {ms:.3f} ms/step, reference composition {ref_ms:.3f} ms/step")
+    w = types.SimpleNamespace(N=N, L=L, B=B, virtual_rows=vrows, folded_rows=folded)
+    kern = {}
+    for kind, (tot, cnt) in prof.items():
+        sb = kernel_step_bytes(kind, w, idx)
+        per_launch = sb / (cnt / args.steps) if sb else None
+        avg = tot / cnt
+        kern[kind] = {"avg_ms": avg, "launches_per_step": cnt / args.steps, "bytes_per_launch": per_launch,
+                      "gbs": (per_launch / (avg * 1e-3) / 1e9) if per_launch else None}
+        log(f"[bench]   {kind:22s} {avg:8.4f} ms x {cnt / args.steps:.0f}/step")
+    dom = max(prof, key=lambda k: prof[k][0])
+    dom_avg = prof[dom][0] / prof[dom][1]
+    dom_bytes = kern[dom]["bytes_per_launch"]
+    achieved = dom_bytes / (dom_avg * 1e-3) / 1e9
+    step_bytes = workloads.step_bytes(idx[0], idx[1], N, L)
+    result = {
+        "metric": "composed FT module fwd+bwd positions/sec @B=65536,L1=1040",
+        "value": B / (ms * 1e-3), "unit": "positions/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "fp32", "data": "synthetic",
+        "config": {"workload": f"composed_{args.composed}_b65536", "feature_set": name, "batch": B,
+                   "num_inputs": N, "virtual_rows": vrows, "max_active": K, "active": [lo, hi],
+                   "output_size": L, "parallelism": "single-gpu"},
+        "reference_composition": {"ms_per_step": ref_ms, "value": B / (ref_ms * 1e-3)},
+        "speedup_vs_reference_composition": ref_ms / ms,
+        "step_bytes": step_bytes,
+        "step_gbs": step_bytes / (ms * 1e-3) / 1e9,
+        "roofline": {"kernel": dom, "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": None,
+                     "algorithmic_bytes_per_launch": dom_bytes, "avg_launch_ms": dom_avg},
+        "kernels": kern,
+        "cpu_baseline": None,
+    }
+    print(json.dumps(result), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -175,6 +277,8 @@ def main() -> int:
     ap.add_argument("--bwd", choices=["sorted", "atomic"], default="sorted")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--composed", choices=sorted(COMPOSED), default=None,
+                    help="time ComposedFeatureTransformer (fused vs reference composition) instead")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -192,6 +296,8 @@ def main() -> int:
     w = workloads.WORKLOADS[args.workload]
     dev = torch.device("cuda:0")
     _native.lib()  # fail loudly if the library is missing
+    if args.composed:
+        return bench_composed(args, dev)
     if w.quantized:
         return bench_q16(args, w, dev)
     log(f"[bench] generating {w.name}: B={w.B} N={w.N} K={w.K} active U[{w.lo},{w.hi}] L={w.L}")
