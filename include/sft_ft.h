@@ -214,6 +214,52 @@ int sft_ft_bwd_pair_f32(const int32_t *idx0, const int32_t *idx1, int64_t batch,
                         size_t workspace_bytes, void *stream);
 
 /*
+ * ---- Composed table + post-FT epilogue, both perspectives ----
+ * NNUEModel._transform_inputs (src/model/model.py:86-115) on top of the
+ * composed forward above, with L1 = l1 and P = output_size - l1 PSQT columns:
+ *   pw_p  = clamp(x_p[:, :L1/2], 0, 1) * clamp(x_p[:, L1/2:L1], 0, 1)  (x_p: FT output of
+ *           perspective p, white = idx0, black = idx1)
+ *   l0    = cat(where(us, pw_white, pw_black), where(us, pw_black, pw_white)) * 127/128
+ *   psqt  = (x_white[b, L1 + k] - x_black[b, L1 + k]) * (us[b] - 0.5), k = psqt_indices[b]
+ * us is float [batch] (nonzero: white to move), psqt_indices int64 [batch]
+ * (an index outside [0, P) gives psqt 0 and no PSQT grad).  The FT outputs
+ * themselves are never written: the forward keeps the pre-activations of both
+ * perspectives in `saved` (an opaque buffer the caller holds until the
+ * backward), and the backward turns grad_l0 / grad_psqt straight into the
+ * weight, virtual and bias grads.  Every value is bit-identical to the
+ * reference ops run on the composed forward (elementwise ops in autograd's
+ * order); the virtual and bias grads are fixed-order sums (<= 1e-5 of binary64).
+ * Requires l1 % 8 == 0, 0 < l1 < output_size, the shape conditions of
+ * sft_ft_pair_workspace_size, and 16-byte aligned l0 / grad_l0.
+ */
+int sft_ft_transform_workspace_size(int64_t batch, int32_t max_active, int32_t num_blocks,
+                                    const int64_t *block_rows, const int64_t *block_virtual_rows,
+                                    int32_t output_size, int32_t l1, size_t *saved_bytes,
+                                    size_t *fwd_bytes, size_t *bwd_bytes);
+
+/* Replaces src/model/model.py:86-115 with the composed forward it calls
+   (FEAT/composed.py:49-54, FT/functions.py:12-48). */
+int sft_ft_fwd_transform_f32(const int32_t *idx0, const int32_t *idx1, int64_t batch,
+                             int32_t max_active, int32_t num_blocks,
+                             const float *const *block_weight, const float *const *block_virtual,
+                             const int64_t *block_rows, const int64_t *block_virtual_rows,
+                             int32_t output_size, int32_t l1, const float *bias, const float *us,
+                             const int64_t *psqt_indices, float *l0, float *psqt, void *saved,
+                             size_t saved_bytes, void *workspace, size_t workspace_bytes,
+                             void *stream);
+
+/* Backward of the same (autograd through src/model/model.py:93-115 and the
+   composed backward, FT/functions.py:50-72); overwrites every grad output. */
+int sft_ft_bwd_transform_f32(const int32_t *idx0, const int32_t *idx1, int64_t batch,
+                             int32_t max_active, const float *grad_l0, const float *grad_psqt,
+                             const float *us, const int64_t *psqt_indices, const void *saved,
+                             size_t saved_bytes, int32_t num_blocks, const int64_t *block_rows,
+                             const int64_t *block_virtual_rows, int32_t output_size, int32_t l1,
+                             float *const *block_weight_grad, float *const *block_virtual_grad,
+                             float *bias_grad, void *workspace, size_t workspace_bytes,
+                             void *stream);
+
+/*
  * Export quantization on the device (src/model/quantize.py:83-84):
  * out[i] = round_half_even(float32(x[i] * scale)) saturated to int16.
  * No reference counterpart as a kernel (the reference runs it as torch ops).

@@ -35,6 +35,16 @@ int bwd_pair_f32(const int32_t *idx0, const int32_t *idx1, int64_t B, int K, con
                  const int64_t *vperiod, const int64_t *vreps, int nvirt, float *db, void *ws, size_t ws_bytes,
                  hipStream_t s);
 void zero_f32(float *p, int64_t n, hipStream_t s);
+size_t map_tiles_workspace(const ColMap &m, int64_t rows);
+int fwd_transform_f32(const int32_t *idx0, const int32_t *idx1, int64_t B, int K, const FoldSrc &src, int64_t N,
+                      int L, int L1, const float *bias, const float *us, const int64_t *psqt_idx, float *l0,
+                      float *psqt, void *saved, size_t saved_bytes, void *ws, size_t ws_bytes, hipStream_t s);
+size_t bwd_transform_workspace(int64_t B, int K, int64_t N, int L, int L1);
+int bwd_transform_f32(const int32_t *idx0, const int32_t *idx1, int64_t B, int K, const float *g_l0,
+                      const float *g_psqt, const float *us, const int64_t *psqt_idx, const void *saved,
+                      size_t saved_bytes, int64_t N, int L, int L1, const RowDst &dst, const float *const *vgrad_src,
+                      float *const *vgrad, const int64_t *vperiod, const int64_t *vreps, int nvirt, float *db,
+                      void *ws, size_t ws_bytes, hipStream_t s);
 
 namespace {
 thread_local std::string t_error;
@@ -118,7 +128,7 @@ const char *const kKindNames[kProfNumKinds] = {
     "fwd_f32_gather",   "bwd_feature_sort",  "bwd_segment_offsets", "bwd_feature_gather", "bwd_bias_partial",
     "bwd_bias_final",   "bwd_atomic_scatter", "bwd_zero_fill",      "fwd_i16_gather",     "quantize_i16",
     "fwd_tile_relayout", "fwd_f32_tiled_gather", "bwd_tiled_gather", "bwd_grad_relayout", "fwd_i16_tiled_gather",
-    "fwd_fold_relayout", "bwd_virtual_reduce",
+    "fwd_fold_relayout", "bwd_virtual_reduce", "bwd_epilogue",
 };
 }  // namespace
 
@@ -349,6 +359,141 @@ int sft_ft_bwd_pair_f32(const int32_t *idx0, const int32_t *idx1, int64_t batch,
   }
   return bwd_pair_f32(idx0, idx1, batch, max_active, grad0, grad1, N, output_size, dst, vsrc, vdst, vperiod, vreps,
                       nvirt, bias_grad, workspace, workspace_bytes, st);
+}
+
+static int check_l1(const char *who, int32_t output_size, int32_t l1) {
+  if (l1 <= 0 || l1 >= output_size || l1 % 8 != 0)
+    return fail(SFT_EUNSUPPORTED, std::string(who) + ": l1 must be a positive multiple of 8 below output_size");
+  return SFT_OK;
+}
+
+static int make_fold_src(const char *who, int32_t num_blocks, const float *const *block_weight,
+                         const float *const *block_virtual, const int64_t *block_rows,
+                         const int64_t *block_virtual_rows, FoldSrc &src) {
+  if (!block_weight || !block_virtual) return fail(SFT_EINVAL, std::string(who) + ": null pointer");
+  src = FoldSrc{};
+  src.n = num_blocks;
+  for (int s = 0; s < num_blocks; ++s) {
+    if (!block_weight[s] || (block_virtual_rows[s] > 0 && !block_virtual[s]))
+      return fail(SFT_EINVAL, std::string(who) + ": null block pointer");
+    if (misaligned16(block_weight[s]) || (block_virtual_rows[s] > 0 && misaligned16(block_virtual[s])))
+      return fail(SFT_EINVAL, std::string(who) + ": block tables must be 16-byte aligned");
+    src.start[s + 1] = src.start[s] + block_rows[s];
+    src.w[s] = reinterpret_cast<const f32x4 *>(block_weight[s]);
+    src.v[s] = block_virtual_rows[s] > 0 ? reinterpret_cast<const f32x4 *>(block_virtual[s]) : nullptr;
+    src.period[s] = block_virtual_rows[s] > 0 ? block_virtual_rows[s] : 1;
+  }
+  return SFT_OK;
+}
+
+struct GradDst {
+  RowDst dst;
+  const float *vsrc[kMaxBlocks];
+  float *vdst[kMaxBlocks];
+  int64_t vperiod[kMaxBlocks], vreps[kMaxBlocks];
+  int nvirt;
+};
+
+static int make_grad_dst(const char *who, int32_t num_blocks, const int64_t *block_rows,
+                         const int64_t *block_virtual_rows, float *const *block_weight_grad,
+                         float *const *block_virtual_grad, GradDst &g) {
+  if (!block_weight_grad || !block_virtual_grad) return fail(SFT_EINVAL, std::string(who) + ": null pointer");
+  g = GradDst{};
+  g.dst.n = num_blocks;
+  for (int s = 0; s < num_blocks; ++s) {
+    if (!block_weight_grad[s] || (block_virtual_rows[s] > 0 && !block_virtual_grad[s]))
+      return fail(SFT_EINVAL, std::string(who) + ": null block pointer");
+    if (misaligned16(block_weight_grad[s]) || (block_virtual_rows[s] > 0 && misaligned16(block_virtual_grad[s])))
+      return fail(SFT_EINVAL, std::string(who) + ": block grads must be 16-byte aligned");
+    g.dst.start[s + 1] = g.dst.start[s] + block_rows[s];
+    g.dst.p[s] = reinterpret_cast<f32x4 *>(block_weight_grad[s]);
+    if (block_virtual_rows[s] > 0) {
+      g.vsrc[g.nvirt] = block_weight_grad[s];
+      g.vdst[g.nvirt] = block_virtual_grad[s];
+      g.vperiod[g.nvirt] = block_virtual_rows[s];
+      g.vreps[g.nvirt] = block_rows[s] / block_virtual_rows[s];
+      ++g.nvirt;
+    }
+  }
+  return SFT_OK;
+}
+
+static int zero_grads(int32_t num_blocks, const int64_t *block_rows, const int64_t *block_virtual_rows,
+                      int32_t output_size, float *const *block_weight_grad, float *const *block_virtual_grad,
+                      float *bias_grad, hipStream_t st, const char *who) {
+  for (int s = 0; s < num_blocks; ++s) {
+    zero_f32(block_weight_grad[s], block_rows[s] * output_size, st);
+    if (block_virtual_rows[s] > 0) zero_f32(block_virtual_grad[s], block_virtual_rows[s] * output_size, st);
+  }
+  zero_f32(bias_grad, output_size, st);
+  return check_launch(who);
+}
+
+int sft_ft_transform_workspace_size(int64_t batch, int32_t max_active, int32_t num_blocks, const int64_t *block_rows,
+                                    const int64_t *block_virtual_rows, int32_t output_size, int32_t l1,
+                                    size_t *saved_bytes, size_t *fwd_bytes, size_t *bwd_bytes) {
+  clear_error();
+  const char *who = "sft_ft_transform_workspace_size";
+  if (!saved_bytes || !fwd_bytes || !bwd_bytes) return fail(SFT_EINVAL, std::string(who) + ": null pointer");
+  int64_t N = 0;
+  int rc = check_pair_shape(who, batch, max_active, num_blocks, block_rows, block_virtual_rows, output_size, &N);
+  if (rc != SFT_OK || (rc = check_l1(who, output_size, l1)) != SFT_OK) return rc;
+  const ColMap map = paired_map(output_size / 4, l1 / 8);
+  *saved_bytes = 2 * map_tiles_workspace(map, batch);
+  *fwd_bytes = map_tiles_workspace(map, N);
+  *bwd_bytes = bwd_transform_workspace(batch, max_active, N, output_size, l1);
+  return SFT_OK;
+}
+
+int sft_ft_fwd_transform_f32(const int32_t *idx0, const int32_t *idx1, int64_t batch, int32_t max_active,
+                             int32_t num_blocks, const float *const *block_weight, const float *const *block_virtual,
+                             const int64_t *block_rows, const int64_t *block_virtual_rows, int32_t output_size,
+                             int32_t l1, const float *bias, const float *us, const int64_t *psqt_indices, float *l0,
+                             float *psqt, void *saved, size_t saved_bytes, void *workspace, size_t workspace_bytes,
+                             void *stream) {
+  clear_error();
+  const char *who = "sft_ft_fwd_transform_f32";
+  int64_t N = 0;
+  int rc = check_pair_shape(who, batch, max_active, num_blocks, block_rows, block_virtual_rows, output_size, &N);
+  if (rc != SFT_OK || (rc = check_l1(who, output_size, l1)) != SFT_OK) return rc;
+  if (!bias || (batch > 0 && (!idx0 || !idx1 || !us || !psqt_indices || !l0 || !psqt)))
+    return fail(SFT_EINVAL, std::string(who) + ": null pointer");
+  FoldSrc src;
+  if ((rc = make_fold_src(who, num_blocks, block_weight, block_virtual, block_rows, block_virtual_rows, src)) != SFT_OK)
+    return rc;
+  if (misaligned16(bias) || (batch > 0 && misaligned16(l0)))
+    return fail(SFT_EINVAL, std::string(who) + ": bias and l0 must be 16-byte aligned");
+  if (batch == 0) return SFT_OK;
+  return fwd_transform_f32(idx0, idx1, batch, max_active, src, N, output_size, l1, bias, us, psqt_indices, l0, psqt,
+                           saved, saved_bytes, workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+int sft_ft_bwd_transform_f32(const int32_t *idx0, const int32_t *idx1, int64_t batch, int32_t max_active,
+                             const float *grad_l0, const float *grad_psqt, const float *us,
+                             const int64_t *psqt_indices, const void *saved, size_t saved_bytes, int32_t num_blocks,
+                             const int64_t *block_rows, const int64_t *block_virtual_rows, int32_t output_size,
+                             int32_t l1, float *const *block_weight_grad, float *const *block_virtual_grad,
+                             float *bias_grad, void *workspace, size_t workspace_bytes, void *stream) {
+  clear_error();
+  const char *who = "sft_ft_bwd_transform_f32";
+  int64_t N = 0;
+  int rc = check_pair_shape(who, batch, max_active, num_blocks, block_rows, block_virtual_rows, output_size, &N);
+  if (rc != SFT_OK || (rc = check_l1(who, output_size, l1)) != SFT_OK) return rc;
+  if (!bias_grad || (batch > 0 && (!idx0 || !idx1 || !grad_l0 || !grad_psqt || !us || !psqt_indices)))
+    return fail(SFT_EINVAL, std::string(who) + ": null pointer");
+  GradDst g;
+  if ((rc = make_grad_dst(who, num_blocks, block_rows, block_virtual_rows, block_weight_grad, block_virtual_grad,
+                          g)) != SFT_OK)
+    return rc;
+  if (misaligned16(bias_grad) || (batch > 0 && misaligned16(grad_l0)))
+    return fail(SFT_EINVAL, std::string(who) + ": bias_grad and grad_l0 must be 16-byte aligned");
+  const hipStream_t st = (hipStream_t)stream;
+  if (batch == 0)
+    return zero_grads(num_blocks, block_rows, block_virtual_rows, output_size, block_weight_grad, block_virtual_grad,
+                      bias_grad, st, who);
+  return bwd_transform_f32(idx0, idx1, batch, max_active, grad_l0, grad_psqt, us, psqt_indices, saved, saved_bytes, N,
+                           output_size, l1, g.dst, g.vsrc, g.vdst, g.vperiod, g.vreps, g.nvirt, bias_grad, workspace,
+                           workspace_bytes, st);
 }
 
 static int check_i16_args(const char *who, const int32_t *idx, int64_t batch, int32_t max_active,

@@ -46,6 +46,7 @@ enum ProfKind : int {
   kProfFwdI16Tiled,
   kProfFwdFold,
   kProfBwdVirtual,
+  kProfBwdEpilogue,
   kProfNumKinds
 };
 struct ProfScope {
@@ -181,6 +182,56 @@ struct RowDst {
   int64_t start[kMaxBlocks + 1];
   f32x4 *p[kMaxBlocks];
 };
+// ---- column maps of the 32-column tiles ----
+// Tile t, lane q (one 16-byte chunk of 4 columns) of a tile row holds chunk
+// tile_col(m, t, q) of the row-major table (-1: padding).
+//   plain  (half4 == 0): chunks 8t .. 8t+7.
+//   paired (half4 > 0):  for t < t1, chunks 4t .. 4t+3 of the first half
+//     (lanes 0-3) and the same chunks of the second half (lanes 4-7), where a
+//     half is half4 chunks; tiles t >= t1 hold the chunks after both halves
+//     (the PSQT columns), 8 per tile.  Columns j and j + L1/2 of a row, which
+//     the post-FT epilogue multiplies together, then sit in lanes q and q ^ 4.
+struct ColMap {
+  int half4;  // chunks per half (0: plain map)
+  int t1;     // paired tiles
+  int cols4;  // chunks per row
+};
+__host__ __device__ inline int tile_col(const ColMap &m, int t, int q) {
+  if (m.half4 == 0) {
+    const int c = 8 * t + q;
+    return c < m.cols4 ? c : -1;
+  }
+  if (t < m.t1) {
+    const int j = 4 * t + (q & 3);
+    return j < m.half4 ? j + (q >> 2) * m.half4 : -1;
+  }
+  const int c = 2 * m.half4 + 8 * (t - m.t1) + q;
+  return c < m.cols4 ? c : -1;
+}
+// Inverse: tile and lane of chunk c.
+__host__ __device__ inline void tile_of_col(const ColMap &m, int c, int &t, int &q) {
+  if (m.half4 == 0) {
+    t = c >> 3;
+    q = c & 7;
+  } else if (c < 2 * m.half4) {
+    const int h = c >= m.half4 ? 1 : 0;
+    const int j = c - h * m.half4;
+    t = j >> 2;
+    q = (j & 3) + 4 * h;
+  } else {
+    const int k = c - 2 * m.half4;
+    t = m.t1 + (k >> 3);
+    q = k & 7;
+  }
+}
+inline ColMap plain_map(int cols4) { return ColMap{0, 0, cols4}; }
+inline ColMap paired_map(int cols4, int half4) {
+  return ColMap{half4, (half4 + 3) / 4, cols4};
+}
+inline int map_tiles(const ColMap &m) {
+  return m.half4 == 0 ? (m.cols4 + 7) / 8 : m.t1 + (m.cols4 - 2 * m.half4 + 7) / 8;
+}
+
 // a[s] for a run-time s without indexing the kernel-argument array (selects).
 template <typename T, int M>
 __device__ __forceinline__ T pick(const T (&a)[M], int s) {

@@ -244,7 +244,7 @@ enum { kDstOut = 0, kDstTmp = 1, kDstOutPlus = 2 };
 __global__ __launch_bounds__(kBlock) void bwd_tiled_gather_kernel(const int32_t *__restrict__ seg,
                                                                   const int32_t *__restrict__ sorted_pos, int64_t N,
                                                                   const f32x4 *__restrict__ gt, int64_t B,
-                                                                  int64_t cols4, RowDst dst, f32x4 *__restrict__ tmp,
+                                                                  ColMap map, RowDst dst, f32x4 *__restrict__ tmp,
                                                                   int src_mode, int dst_mode, int ntiles, int ngroups) {
   __shared__ int spos[kBwdPosLds];
   const TileItem it = tile_sched_item(blockIdx.x, ntiles, ngroups);
@@ -260,8 +260,10 @@ __global__ __launch_bounds__(kBlock) void bwd_tiled_gather_kernel(const int32_t 
   const int wave = uniform(threadIdx.x / kWave);
   const int lane = threadIdx.x % kWave;
   const int g = lane / kBwdTileCh, t = lane % kBwdTileCh;
-  const int64_t col4 = (int64_t)it.tile * kBwdTileCh + t;
-  const bool colok = col4 < cols4;
+  const int colm = tile_col(map, it.tile, t);
+  const bool colok = colm >= 0;
+  const int64_t col4 = colm;
+  const int64_t cols4 = map.cols4;
   const int64_t f = fb + wave * (kWave / kBwdTileCh) + g;
   int s0 = 0, s1 = 0;
   if (f < N) {
@@ -323,6 +325,90 @@ __global__ __launch_bounds__(kBlock) void virtual_reduce_kernel(const f32x4 *__r
     }
     for (; r < reps; ++r) acc += dWb[(int64_t)r * total + i];
     dV[i] = acc;
+  }
+}
+
+// Backward of the post-FT epilogue (src/model/model.py:93-115), elementwise
+// and in the order autograd evaluates it, so every grad is bit-identical:
+//   d_sel  = g_l0[b, half + j] * (127/128)         half chosen by us[b] and the perspective
+//   d_pw   = d_sel + 0        (the two where() grads are summed; one is +0)
+//   d_c    = d_pw * clamp(partner) + 0   (mul backward; the two select() grads summed)
+//   d_raw  = (0 <= raw <= 1) ? d_c : 0   (clamp backward)
+//   PSQT column k: (k == psqt_idx[b]) ? 0 + (+/-)(g_psqt[b] * (us[b] - 0.5)) : 0
+//                  (mul, sub and gather backward; + for white, - for black)
+// The grads go straight to the grad tiles of the weight-grad gather (paired
+// map), and their column sums over the block's positions of both perspectives
+// to partial[blockIdx.x] for the bias grad.  Lane group lg of the block takes
+// rows r0 + lg + 32 i.
+struct BwdEpilogue {
+  const float *g_l0;         // [B, L1]
+  const float *g_psqt;       // [B]
+  const float *us;           // [B]
+  const int64_t *psqt_idx;   // [B]
+  const f32x4 *raw0, *raw1;  // pre-activations, paired tiles
+  f32x4 *gt0, *gt1;          // grad tiles out
+  f32x4 *partial;            // [gridDim.x][cols4]
+  int P;
+};
+constexpr int kEpiRows = 128;  // positions per workgroup
+__device__ __forceinline__ float clamp01f(float x) { return x < 0.f ? 0.f : (x > 1.f ? 1.f : x); }
+
+__global__ __launch_bounds__(kBlock) void bwd_epilogue_kernel(BwdEpilogue e, ColMap map, int64_t B) {
+  __shared__ f32x4 red[kBlock / kBwdTileCh][kBwdTileCh];
+  const int tile = blockIdx.y;
+  const int lg = threadIdx.x / kBwdTileCh, q = threadIdx.x % kBwdTileCh;
+  const int colm = tile_col(map, tile, q);
+  const bool colok = colm >= 0;
+  const bool paired = tile < map.t1;  // block-uniform
+  const int64_t j = 4 * (int64_t)tile + (q & 3);  // first-half chunk of a paired lane
+  const int64_t l0_row = 2 * (int64_t)map.half4;
+  const float k127 = 127.0f / 128.0f;
+  f32x4 bsum = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int64_t r0 = (int64_t)blockIdx.x * kEpiRows;
+  for (int i = 0; i < kEpiRows / (kBlock / kBwdTileCh); ++i) {
+    const int64_t b = r0 + lg + (int64_t)(kBlock / kBwdTileCh) * i;
+    const bool rowok = b < B;
+    const int64_t bb = rowok ? b : 0;
+    const bool wtm = e.us[bb] != 0.f;
+    const int64_t at = ((int64_t)tile * B + bb) * kBwdTileCh + q;
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      const f32x4 a = (p == 0 ? e.raw0 : e.raw1)[at];
+      f32x4 d = f32x4{0.f, 0.f, 0.f, 0.f};
+      if (paired) {
+        const f32x4 partner = f32x4{__shfl_xor(a.x, 4), __shfl_xor(a.y, 4), __shfl_xor(a.z, 4), __shfl_xor(a.w, 4)};
+        if (colok) {
+          const int64_t half = ((p == 1) ? wtm : !wtm) ? map.half4 : 0;
+          const f32x4 gsel = reinterpret_cast<const f32x4 *>(e.g_l0)[bb * l0_row + half + j];
+          const f32x4 dpw = gsel * k127 + 0.0f;
+          const f32x4 cp = f32x4{clamp01f(partner.x), clamp01f(partner.y), clamp01f(partner.z), clamp01f(partner.w)};
+          const f32x4 dc = dpw * cp + 0.0f;
+          d.x = (a.x >= 0.f && a.x <= 1.f) ? dc.x : 0.f;
+          d.y = (a.y >= 0.f && a.y <= 1.f) ? dc.y : 0.f;
+          d.z = (a.z >= 0.f && a.z <= 1.f) ? dc.z : 0.f;
+          d.w = (a.w >= 0.f && a.w <= 1.f) ? dc.w : 0.f;
+        }
+      } else if (colok) {
+        const int64_t kq = 4 * (int64_t)(colm - 2 * map.half4);  // PSQT column of element 0
+        const int64_t k = e.psqt_idx[bb];
+        if (k >= kq && k < kq + 4) {
+          const float dp = e.g_psqt[bb] * (e.us[bb] - 0.5f);
+          d[(int)(k - kq)] = 0.0f + (p == 0 ? dp : -dp);
+        }
+      }
+      if (rowok) {
+        (p == 0 ? e.gt0 : e.gt1)[at] = d;
+        bsum += d;
+      }
+    }
+  }
+  red[lg][q] = bsum;
+  __syncthreads();
+  if (threadIdx.x < kBwdTileCh) {
+    f32x4 s = red[0][threadIdx.x];
+    for (int r = 1; r < kBlock / kBwdTileCh; ++r) s += red[r][threadIdx.x];
+    const int c = tile_col(map, tile, threadIdx.x);
+    if (c >= 0) e.partial[(int64_t)blockIdx.x * map.cols4 + c] = s;
   }
 }
 
@@ -680,8 +766,8 @@ int bwd_f32(const int32_t *idx, int64_t B, int K, const float *grad, int64_t N, 
     for (int h = 0; h < nc; ++h) {
       ProfScope prof(kProfBwdTiled, s);
       hipLaunchKernelGGL(bwd_tiled_gather_kernel, dim3((unsigned)blocks), dim3(kBlock), 0, s, seg + (int64_t)h * N,
-                         pos, N, gt, B, cols4, dst, (f32x4 *)nullptr, h == 0 ? kSrcZero : kSrcDst, kDstOut, ntiles,
-                         ngroups);
+                         pos, N, gt, B, plain_map((int)cols4), dst, (f32x4 *)nullptr, h == 0 ? kSrcZero : kSrcDst,
+                         kDstOut, ntiles, ngroups);
       if ((rc = check_launch("tiled feature gather")) != SFT_OK) return rc;
     }
     return SFT_OK;
@@ -735,6 +821,61 @@ size_t bwd_pair_workspace(int64_t B, int K, int64_t N, int L) {
   return lay.total;
 }
 
+// Sort one perspective's slots, find its segments and run its position-chunk
+// launches of the tiled gather: perspective 0 stores to dst, perspective 1 sums
+// onto 0 in tmp and its last launch stores dst + tmp.
+static int pair_gather_perspective(int p, const int32_t *idx, int64_t B, int K, int64_t N, const ColMap &map,
+                                   const f32x4 *gt, const RowDst &dst, f32x4 *tmp, int nc, char *sort_ws,
+                                   int32_t *seg, hipStream_t s) {
+  const int64_t M = B * K;
+  const int ntiles = map_tiles(map);
+  const int ngroups = (int)ceil_div(N, kBwdFeatPerBlock);
+  const int64_t blocks = tile_sched_items_per_xcd(ntiles, ngroups) * kXcds;
+  const int chunk_rows = (int)(nc > 1 ? half_rows(B) : B);
+  unsigned *keys = nullptr, *totals = nullptr;
+  int32_t *pos = nullptr;
+  int ntot = 0, rc;
+  {
+    ProfScope prof(kProfBwdSort, s);
+    if ((rc = slot_sort(idx, M, K, N, chunk_rows, nc, sort_ws, &keys, &pos, &totals, &ntot, s)) != SFT_OK) return rc;
+  }
+  {
+    ProfScope prof(kProfBwdOffsets, s);
+    hipLaunchKernelGGL(seg_offsets_kernel, dim3((unsigned)ceil_div(M + 1, kBlock)), dim3(kBlock), 0, s, keys,
+                       (int64_t)nc * N, totals, ntot, seg);
+    if ((rc = check_launch("segment offsets")) != SFT_OK) return rc;
+  }
+  for (int h = 0; h < nc; ++h) {
+    int src_mode, dst_mode;
+    if (p == 0) {
+      src_mode = h == 0 ? kSrcZero : kSrcDst;
+      dst_mode = kDstOut;
+    } else {
+      src_mode = h == 0 ? kSrcZero : kSrcTmp;
+      dst_mode = h == nc - 1 ? kDstOutPlus : kDstTmp;
+    }
+    ProfScope prof(kProfBwdTiled, s);
+    hipLaunchKernelGGL(bwd_tiled_gather_kernel, dim3((unsigned)blocks), dim3(kBlock), 0, s, seg + (int64_t)h * N, pos,
+                       N, gt, B, map, dst, tmp, src_mode, dst_mode, ntiles, ngroups);
+    if ((rc = check_launch("tiled feature gather")) != SFT_OK) return rc;
+  }
+  return SFT_OK;
+}
+
+static int virtual_reduce(const float *const *vgrad_src, float *const *vgrad, const int64_t *vperiod,
+                          const int64_t *vreps, int nvirt, int64_t cols4, hipStream_t s) {
+  for (int v = 0; v < nvirt; ++v) {
+    const int64_t total = vperiod[v] * cols4;
+    ProfScope prof(kProfBwdVirtual, s);
+    hipLaunchKernelGGL(virtual_reduce_kernel, dim3((unsigned)std::min<int64_t>(ceil_div(total, kBlock), 1 << 16)),
+                       dim3(kBlock), 0, s, reinterpret_cast<const f32x4 *>(vgrad_src[v]), vperiod[v], (int)vreps[v],
+                       cols4, reinterpret_cast<f32x4 *>(vgrad[v]));
+    int rc = check_launch("virtual row reduction");
+    if (rc != SFT_OK) return rc;
+  }
+  return SFT_OK;
+}
+
 int bwd_pair_f32(const int32_t *idx0, const int32_t *idx1, int64_t B, int K, const float *grad0, const float *grad1,
                  int64_t N, int L, const RowDst &dst, const float *const *vgrad_src, float *const *vgrad,
                  const int64_t *vperiod, const int64_t *vreps, int nvirt, float *db, void *ws, size_t ws_bytes,
@@ -745,63 +886,104 @@ int bwd_pair_f32(const int32_t *idx0, const int32_t *idx1, int64_t B, int K, con
     return fail(SFT_EWORKSPACE, "sft_ft_bwd_pair_f32: workspace smaller than sft_ft_pair_workspace_size() "
                                 "or not 256-byte aligned");
   char *w = static_cast<char *>(ws);
-  const int64_t M = B * K;
-  const int64_t cols4 = L / 4;
+  const ColMap map = plain_map(L / 4);
   float *partial = reinterpret_cast<float *>(w + lay.partial);
   f32x4 *gt = reinterpret_cast<f32x4 *>(w + lay.gt);
   f32x4 *tmp = reinterpret_cast<f32x4 *>(w + lay.tmp);
   int32_t *seg = reinterpret_cast<int32_t *>(w + lay.seg);
-  const int ntiles = (int)ceil_div(cols4, kBwdTileCh);
-  const int ngroups = (int)ceil_div(N, kBwdFeatPerBlock);
-  const int64_t blocks = tile_sched_items_per_xcd(ntiles, ngroups) * kXcds;
-  const int nc = lay.nc;
-  const int chunk_rows = (int)(nc > 1 ? half_rows(B) : B);
   int rc;
   for (int p = 0; p < 2; ++p) {
     const float *grad = p == 0 ? grad0 : grad1;
     if ((rc = launch_bias_partial(grad, B, L, lay.nparts, partial + (size_t)p * lay.nparts * L, gt, true, s)) !=
         SFT_OK)
       return rc;
-    unsigned *keys = nullptr, *totals = nullptr;
-    int32_t *pos = nullptr;
-    int ntot = 0;
-    {
-      ProfScope prof(kProfBwdSort, s);
-      if ((rc = slot_sort(p == 0 ? idx0 : idx1, M, K, N, chunk_rows, nc, w + lay.sort, &keys, &pos, &totals, &ntot,
-                          s)) != SFT_OK)
-        return rc;
-    }
-    {
-      ProfScope prof(kProfBwdOffsets, s);
-      hipLaunchKernelGGL(seg_offsets_kernel, dim3((unsigned)ceil_div(M + 1, kBlock)), dim3(kBlock), 0, s, keys,
-                         (int64_t)nc * N, totals, ntot, seg);
-      if ((rc = check_launch("segment offsets")) != SFT_OK) return rc;
-    }
-    for (int h = 0; h < nc; ++h) {
-      int src_mode, dst_mode;
-      if (p == 0) {
-        src_mode = h == 0 ? kSrcZero : kSrcDst;
-        dst_mode = kDstOut;
-      } else {
-        src_mode = h == 0 ? kSrcZero : kSrcTmp;
-        dst_mode = h == nc - 1 ? kDstOutPlus : kDstTmp;
-      }
-      ProfScope prof(kProfBwdTiled, s);
-      hipLaunchKernelGGL(bwd_tiled_gather_kernel, dim3((unsigned)blocks), dim3(kBlock), 0, s, seg + (int64_t)h * N,
-                         pos, N, gt, B, cols4, dst, tmp, src_mode, dst_mode, ntiles, ngroups);
-      if ((rc = check_launch("tiled feature gather")) != SFT_OK) return rc;
-    }
+    if ((rc = pair_gather_perspective(p, p == 0 ? idx0 : idx1, B, K, N, map, gt, dst, tmp, lay.nc, w + lay.sort, seg,
+                                      s)) != SFT_OK)
+      return rc;
   }
   if ((rc = launch_bias_final(partial, 2 * lay.nparts, L, db, 1, true, s)) != SFT_OK) return rc;
-  for (int v = 0; v < nvirt; ++v) {
-    const int64_t total = vperiod[v] * cols4;
-    ProfScope prof(kProfBwdVirtual, s);
-    hipLaunchKernelGGL(virtual_reduce_kernel, dim3((unsigned)std::min<int64_t>(ceil_div(total, kBlock), 1 << 16)),
-                       dim3(kBlock), 0, s, reinterpret_cast<const f32x4 *>(vgrad_src[v]), vperiod[v], (int)vreps[v],
-                       cols4, reinterpret_cast<f32x4 *>(vgrad[v]));
-    if ((rc = check_launch("virtual row reduction")) != SFT_OK) return rc;
+  return virtual_reduce(vgrad_src, vgrad, vperiod, vreps, nvirt, L / 4, s);
+}
+
+// ------------------------------------------- composed table + post-FT epilogue ----
+// Workspace: bias partials | sort buffers | segment starts | grad tiles of both
+// perspectives (paired map) | tmp [N, L].
+struct TransformLayout {
+  size_t partial, sort, seg, gt0, gt1, tmp, total;
+  int nparts, nc;
+};
+
+void make_transform_layout(int64_t B, int K, int64_t N, int L, int L1, TransformLayout &lay) {
+  const ColMap map = paired_map(L / 4, L1 / 8);
+  const int64_t M = B * K;
+  lay.nparts = (int)std::max<int64_t>(1, ceil_div(B, kEpiRows));
+  lay.nc = sort_chunks(B, L, SFT_BWD_OVERWRITE);
+  const size_t gtb = (size_t)map_tiles(map) * (size_t)B * 128;
+  size_t off = 0;
+  lay.partial = off;
+  off = align256(off + (size_t)lay.nparts * (size_t)L * sizeof(float));
+  lay.sort = off;
+  off = align256(off + slot_sort_workspace(std::max<int64_t>(M, 1)));
+  lay.seg = off;
+  off = align256(off + (size_t)(lay.nc * N + 1) * sizeof(int32_t));
+  lay.gt0 = off;
+  off = align256(off + gtb);
+  lay.gt1 = off;
+  off = align256(off + gtb);
+  lay.tmp = off;
+  off = align256(off + (size_t)N * (size_t)L * sizeof(float));
+  lay.total = off;
+}
+
+size_t bwd_transform_workspace(int64_t B, int K, int64_t N, int L, int L1) {
+  TransformLayout lay;
+  make_transform_layout(B, K, N, L, L1, lay);
+  return lay.total;
+}
+
+int bwd_transform_f32(const int32_t *idx0, const int32_t *idx1, int64_t B, int K, const float *g_l0,
+                      const float *g_psqt, const float *us, const int64_t *psqt_idx, const void *saved,
+                      size_t saved_bytes, int64_t N, int L, int L1, const RowDst &dst, const float *const *vgrad_src,
+                      float *const *vgrad, const int64_t *vperiod, const int64_t *vreps, int nvirt, float *db,
+                      void *ws, size_t ws_bytes, hipStream_t s) {
+  TransformLayout lay;
+  make_transform_layout(B, K, N, L, L1, lay);
+  const ColMap map = paired_map(L / 4, L1 / 8);
+  const size_t raw_bytes = (size_t)map_tiles(map) * (size_t)B * 128;
+  if (ws_bytes < lay.total || ws == nullptr || (uintptr_t)ws % 256 != 0 || saved == nullptr ||
+      saved_bytes < 2 * raw_bytes || (uintptr_t)saved % 256 != 0)
+    return fail(SFT_EWORKSPACE, "sft_ft_bwd_transform_f32: saved or workspace buffer smaller than "
+                                "sft_ft_transform_workspace_size() or not 256-byte aligned");
+  char *w = static_cast<char *>(ws);
+  f32x4 *gt0 = reinterpret_cast<f32x4 *>(w + lay.gt0), *gt1 = reinterpret_cast<f32x4 *>(w + lay.gt1);
+  BwdEpilogue e;
+  e.g_l0 = g_l0;
+  e.g_psqt = g_psqt;
+  e.us = us;
+  e.psqt_idx = psqt_idx;
+  e.raw0 = static_cast<const f32x4 *>(saved);
+  e.raw1 = reinterpret_cast<const f32x4 *>(static_cast<const char *>(saved) + raw_bytes);
+  e.gt0 = gt0;
+  e.gt1 = gt1;
+  e.partial = reinterpret_cast<f32x4 *>(w + lay.partial);
+  e.P = L - L1;
+  int rc;
+  {
+    ProfScope prof(kProfBwdEpilogue, s);
+    hipLaunchKernelGGL(bwd_epilogue_kernel, dim3((unsigned)lay.nparts, (unsigned)map_tiles(map)), dim3(kBlock), 0, s,
+                       e, map, B);
+    if ((rc = check_launch("epilogue backward")) != SFT_OK) return rc;
   }
-  return SFT_OK;
+  if ((rc = launch_bias_final(reinterpret_cast<const float *>(w + lay.partial), lay.nparts, L, db, 1, true, s)) !=
+      SFT_OK)
+    return rc;
+  f32x4 *tmp = reinterpret_cast<f32x4 *>(w + lay.tmp);
+  int32_t *seg = reinterpret_cast<int32_t *>(w + lay.seg);
+  for (int p = 0; p < 2; ++p)
+    if ((rc = pair_gather_perspective(p, p == 0 ? idx0 : idx1, B, K, N, map, p == 0 ? gt0 : gt1, dst, tmp, lay.nc,
+                                      w + lay.sort, seg, s)) != SFT_OK)
+      return rc;
+  return virtual_reduce(vgrad_src, vgrad, vperiod, vreps, nvirt, L / 4, s);
 }
 
 void zero_f32(float *p, int64_t n, hipStream_t s) {

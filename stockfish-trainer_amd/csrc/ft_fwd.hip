@@ -247,16 +247,39 @@ constexpr int kTiledRounds = SFT_TILED_ROUNDS;                        // positio
 constexpr int kTiledPosPerRound = kWavesPerBlock * (kWave / kTileCh);  // 32
 constexpr int kTiledPosPerBlock = kTiledPosPerRound * kTiledRounds;
 
+// Post-FT epilogue of the forward (src/model/model.py:93-115), applied in
+// registers by the EPI instantiation over the paired column map: the
+// pre-activations are stored to raw0/raw1 in tile layout (kept for the
+// backward), and for the paired tiles lane q < 4 multiplies its clamped chunk
+// with the partner chunk of the other half (lane q + 4), scales by 127/128 and
+// stores it to the half of l0 the side to move selects:
+//   l0 = cat(where(us, pw_white, pw_black), where(us, pw_black, pw_white)) * 127/128.
+struct FwdEpilogue {
+  const float *us;     // [B]; nonzero: white to move
+  f32x4 *l0;           // [B, 2 * half4] chunks
+  f32x4 *raw0, *raw1;  // [ntiles][B][8] chunks per perspective
+};
+
+// torch.clamp(x, 0, 1): NaN passes through.
+__device__ __forceinline__ float clamp01(float x) { return x < 0.f ? 0.f : (x > 1.f ? 1.f : x); }
+__device__ __forceinline__ f32x4 clamp01(f32x4 v) {
+  return f32x4{clamp01(v.x), clamp01(v.y), clamp01(v.z), clamp01(v.w)};
+}
+__device__ __forceinline__ f32x4 shfl_xor4(f32x4 v, int m) {
+  return f32x4{__shfl_xor(v.x, m), __shfl_xor(v.y, m), __shfl_xor(v.z, m), __shfl_xor(v.w, m)};
+}
+
 // Two perspectives share one launch: chunks [0, nchunks_p) read idx0 and write
 // out0, chunks [nchunks_p, 2 nchunks_p) idx1 and out1, so an XCD gathers both
 // perspectives from a tile while it is in L2.  A single-perspective call passes
 // the same arrays twice and nchunks_p = nchunks.
+template <bool EPI>
 __global__ __launch_bounds__(kBlock) void fwd_tiled_kernel(const int32_t *__restrict__ idx0,
                                                            const int32_t *__restrict__ idx1, int64_t B, int K, int N,
-                                                           const f32x4 *__restrict__ Wt, int64_t cols4,
+                                                           const f32x4 *__restrict__ Wt, ColMap map,
                                                            const f32x4 *__restrict__ bias, f32x4 *__restrict__ out0,
-                                                           f32x4 *__restrict__ out1, int kpad, int ntiles, int nchunks,
-                                                           int nchunks_p) {
+                                                           f32x4 *__restrict__ out1, FwdEpilogue epi, int kpad,
+                                                           int ntiles, int nchunks, int nchunks_p) {
   constexpr int U = SFT_FWD_TILED_U;
   constexpr int PPW = kWave / kTileCh;  // 8 positions per wave per round
   extern __shared__ int smem[];
@@ -265,14 +288,15 @@ __global__ __launch_bounds__(kBlock) void fwd_tiled_kernel(const int32_t *__rest
   const bool second = it.chunk >= nchunks_p;
   if (second) it.chunk -= nchunks_p;
   const int32_t *__restrict__ idx = second ? idx1 : idx0;
-  f32x4 *__restrict__ out = second ? out1 : out0;
   const int wave = uniform(threadIdx.x / kWave);
   const int lane = threadIdx.x % kWave;
   int *list = smem + wave * PPW * kpad;
   int *count = smem + kWavesPerBlock * PPW * kpad + wave * PPW;
   const int g = lane / kTileCh, t = lane % kTileCh;
-  const int64_t col4 = (int64_t)it.tile * kTileCh + t;
-  const bool colok = col4 < cols4;
+  const int col = tile_col(map, it.tile, t);
+  const bool colok = col >= 0;
+  const int64_t col4 = col;
+  const int64_t cols4 = map.cols4;
   const f32x4 b4 = colok ? bias[col4] : f32x4{0.f, 0.f, 0.f, 0.f};
   const f32x4 *wtile = Wt + (int64_t)it.tile * N * kTileCh + t;
 
@@ -314,9 +338,47 @@ __global__ __launch_bounds__(kBlock) void fwd_tiled_kernel(const int32_t *__rest
       for (int u = 0; u < UT; ++u)
         if (k + u < n) acc += w[u];
     }
-    if (pos < B && colok) __builtin_nontemporal_store(acc, out + pos * cols4 + col4);
+    if (!EPI) {
+      f32x4 *__restrict__ out = second ? out1 : out0;
+      if (pos < B && colok) __builtin_nontemporal_store(acc, out + pos * cols4 + col4);
+    } else {
+      f32x4 *__restrict__ raw = second ? epi.raw1 : epi.raw0;
+      if (pos < B) __builtin_nontemporal_store(acc, raw + ((int64_t)it.tile * B + pos) * kTileCh + t);
+      if (it.tile < map.t1) {  // block-uniform
+        const f32x4 partner = shfl_xor4(acc, 4);
+        if (t < 4 && colok && pos < B) {
+          const bool white_to_move = epi.us[pos] != 0.f;
+          const int64_t half = (second ? white_to_move : !white_to_move) ? map.half4 : 0;
+          const f32x4 pw = clamp01(acc) * clamp01(partner);
+          const f32x4 v = pw * (127.0f / 128.0f);
+          __builtin_nontemporal_store(v, epi.l0 + pos * (2 * (int64_t)map.half4) + half + col4);
+        }
+      }
+    }
     __syncthreads();
   }
+}
+
+// psqt[b] = (white[b, L1 + k] - black[b, L1 + k]) * (us[b] - 0.5), k = psqt_idx[b]
+// (src/model/model.py:110-114), read from the raw tiles; an index outside
+// [0, P) gives 0.
+__global__ __launch_bounds__(kBlock) void psqt_out_kernel(const f32x4 *__restrict__ raw0,
+                                                          const f32x4 *__restrict__ raw1, ColMap map, int64_t B,
+                                                          const float *__restrict__ us,
+                                                          const int64_t *__restrict__ psqt_idx, int P,
+                                                          float *__restrict__ psqt) {
+  const int64_t b = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  if (b >= B) return;
+  const int64_t k = psqt_idx[b];
+  float v = 0.f;
+  if (k >= 0 && k < P) {
+    int t, q;
+    tile_of_col(map, 2 * map.half4 + (int)(k >> 2), t, q);
+    const int64_t at = ((int64_t)t * B + b) * kTileCh + q;
+    const float w = raw0[at][k & 3], bl = raw1[at][k & 3];
+    v = (w - bl) * (us[b] - 0.5f);
+  }
+  psqt[b] = v;
 }
 
 // ----------------------------------------------------- tiled int16 gather ----
@@ -456,8 +518,9 @@ void launch_tile_relayout(const f32x4 *src, int64_t rows, int64_t cols4, f32x4 *
 // binary32 exactly as the table the reference materialises
 // (FEAT/halfka_v2_hm.py:69-70, FEAT/composed.py:49-50), and stored straight into
 // the 32-column tiles of the tiled gather.  total = N * cols4 < 2^31.
-static __global__ __launch_bounds__(kBlock) void fold_relayout_kernel(FoldSrc src, int N, int cols4,
+static __global__ __launch_bounds__(kBlock) void fold_relayout_kernel(FoldSrc src, int N, ColMap map,
                                                                       f32x4 *__restrict__ Wt) {
+  const int cols4 = map.cols4;
   const int total = N * cols4;
   for (int i = blockIdx.x * kBlock + threadIdx.x; i < total; i += gridDim.x * kBlock) {
     const int r = i / cols4, c = i - r * cols4;
@@ -469,7 +532,9 @@ static __global__ __launch_bounds__(kBlock) void fold_relayout_kernel(FoldSrc sr
       const f32x4 y = v[(int64_t)(rl % (int)pick(src.period, s)) * cols4 + c];
       x += y;
     }
-    Wt[((int64_t)(c >> 3) * N + r) * 8 + (c & 7)] = x;
+    int t, q;
+    tile_of_col(map, c, t, q);
+    Wt[((int64_t)t * N + r) * 8 + q] = x;
   }
 }
 
@@ -533,41 +598,82 @@ int fwd_f32_tiled(const int32_t *idx, int64_t B, int K, const float *W, int64_t 
   const int64_t blocks = tile_sched_items_per_xcd(ntiles, nchunks) * kXcds;
   {
     ProfScope prof(kProfFwdTiled, s);
-    hipLaunchKernelGGL(fwd_tiled_kernel, dim3((unsigned)blocks), dim3(kBlock), lds, s, idx, idx, B, K, (int)N, wt,
-                       cols4, reinterpret_cast<const f32x4 *>(bias), reinterpret_cast<f32x4 *>(out),
-                       reinterpret_cast<f32x4 *>(out), kpad, ntiles, nchunks, nchunks);
+    hipLaunchKernelGGL(fwd_tiled_kernel<false>, dim3((unsigned)blocks), dim3(kBlock), lds, s, idx, idx, B, K,
+                       (int)N, wt, plain_map((int)cols4), reinterpret_cast<const f32x4 *>(bias),
+                       reinterpret_cast<f32x4 *>(out), reinterpret_cast<f32x4 *>(out), FwdEpilogue{}, kpad, ntiles,
+                       nchunks, nchunks);
   }
   return check_launch("sft_ft_fwd_f32_ex (tiled gather)");
 }
 
-int fwd_pair_f32(const int32_t *idx0, const int32_t *idx1, int64_t B, int K, const FoldSrc &src, int64_t N, int L,
-                 const float *bias, float *out0, float *out1, void *ws, size_t ws_bytes, hipStream_t s) {
-  if (ws_bytes < fwd_tiled_workspace(N, L) || ws == nullptr || (uintptr_t)ws % 256 != 0)
-    return fail(SFT_EWORKSPACE, "sft_ft_fwd_pair_f32: workspace smaller than sft_ft_pair_workspace_size() "
-                                "or not 256-byte aligned");
-  const int64_t cols4 = L / 4;
-  const int ntiles = (int)ceil_div(L, kTileF);
+size_t map_tiles_workspace(const ColMap &m, int64_t rows) { return (size_t)map_tiles(m) * (size_t)rows * 128; }
+
+// Fold re-layout of the composed table into `wt`, then one tiled gather of both
+// perspectives (plain outputs, or the post-FT epilogue when epi.l0 is set).
+static int pair_gather(const int32_t *idx0, const int32_t *idx1, int64_t B, int K, const FoldSrc &src, int64_t N,
+                       const ColMap &map, const float *bias, float *out0, float *out1, const FwdEpilogue &epi,
+                       f32x4 *wt, hipStream_t s, const char *who) {
+  const int ntiles = map_tiles(map);
   const int kpad = round_up4(K);
   const size_t lds = index_lds_bytes(kTileCh, K);
-  if (lds > kMaxIndexLds) return fail(SFT_EUNSUPPORTED, "sft_ft_fwd_pair_f32: max_active too large for the LDS index lists");
-  f32x4 *wt = static_cast<f32x4 *>(ws);
+  if (lds > kMaxIndexLds) return fail(SFT_EUNSUPPORTED, std::string(who) + ": max_active too large for the LDS index lists");
   {
-    const int64_t total = N * cols4;
+    const int64_t total = N * map.cols4;
     ProfScope prof(kProfFwdFold, s);
     hipLaunchKernelGGL(fold_relayout_kernel, dim3((unsigned)std::min<int64_t>(ceil_div(total, kBlock), 1 << 16)),
-                       dim3(kBlock), 0, s, src, (int)N, (int)cols4, wt);
+                       dim3(kBlock), 0, s, src, (int)N, map, wt);
   }
-  int rc = check_launch("sft_ft_fwd_pair_f32 (fold re-layout)");
+  int rc = check_launch(who);
   if (rc != SFT_OK || B == 0) return rc;
   const int nchunks_p = (int)ceil_div(B, kTiledPosPerBlock);
   const int64_t blocks = tile_sched_items_per_xcd(ntiles, 2 * nchunks_p) * kXcds;
   {
     ProfScope prof(kProfFwdTiled, s);
-    hipLaunchKernelGGL(fwd_tiled_kernel, dim3((unsigned)blocks), dim3(kBlock), lds, s, idx0, idx1, B, K, (int)N, wt,
-                       cols4, reinterpret_cast<const f32x4 *>(bias), reinterpret_cast<f32x4 *>(out0),
-                       reinterpret_cast<f32x4 *>(out1), kpad, ntiles, 2 * nchunks_p, nchunks_p);
+    if (epi.l0 != nullptr)
+      hipLaunchKernelGGL(fwd_tiled_kernel<true>, dim3((unsigned)blocks), dim3(kBlock), lds, s, idx0, idx1, B, K,
+                         (int)N, wt, map, reinterpret_cast<const f32x4 *>(bias), (f32x4 *)nullptr, (f32x4 *)nullptr,
+                         epi, kpad, ntiles, 2 * nchunks_p, nchunks_p);
+    else
+      hipLaunchKernelGGL(fwd_tiled_kernel<false>, dim3((unsigned)blocks), dim3(kBlock), lds, s, idx0, idx1, B, K,
+                         (int)N, wt, map, reinterpret_cast<const f32x4 *>(bias), reinterpret_cast<f32x4 *>(out0),
+                         reinterpret_cast<f32x4 *>(out1), epi, kpad, ntiles, 2 * nchunks_p, nchunks_p);
   }
-  return check_launch("sft_ft_fwd_pair_f32 (tiled gather)");
+  return check_launch(who);
+}
+
+int fwd_pair_f32(const int32_t *idx0, const int32_t *idx1, int64_t B, int K, const FoldSrc &src, int64_t N, int L,
+                 const float *bias, float *out0, float *out1, void *ws, size_t ws_bytes, hipStream_t s) {
+  const ColMap map = plain_map(L / 4);
+  if (ws_bytes < map_tiles_workspace(map, N) || ws == nullptr || (uintptr_t)ws % 256 != 0)
+    return fail(SFT_EWORKSPACE, "sft_ft_fwd_pair_f32: workspace smaller than sft_ft_pair_workspace_size() "
+                                "or not 256-byte aligned");
+  return pair_gather(idx0, idx1, B, K, src, N, map, bias, out0, out1, FwdEpilogue{}, static_cast<f32x4 *>(ws), s,
+                     "sft_ft_fwd_pair_f32");
+}
+
+// Forward of the composed table with the post-FT epilogue.  `saved` holds the
+// raw pre-activations of both perspectives in paired tiles (map_tiles x B x
+// 128 B each) for the backward; `ws` the table tiles.
+int fwd_transform_f32(const int32_t *idx0, const int32_t *idx1, int64_t B, int K, const FoldSrc &src, int64_t N,
+                      int L, int L1, const float *bias, const float *us, const int64_t *psqt_idx, float *l0,
+                      float *psqt, void *saved, size_t saved_bytes, void *ws, size_t ws_bytes, hipStream_t s) {
+  const ColMap map = paired_map(L / 4, L1 / 8);
+  const size_t raw_bytes = map_tiles_workspace(map, B);
+  if (ws_bytes < map_tiles_workspace(map, N) || ws == nullptr || (uintptr_t)ws % 256 != 0 ||
+      saved_bytes < 2 * raw_bytes || saved == nullptr || (uintptr_t)saved % 256 != 0)
+    return fail(SFT_EWORKSPACE, "sft_ft_fwd_transform_f32: saved or workspace buffer smaller than "
+                                "sft_ft_transform_workspace_size() or not 256-byte aligned");
+  FwdEpilogue epi;
+  epi.us = us;
+  epi.l0 = reinterpret_cast<f32x4 *>(l0);
+  epi.raw0 = static_cast<f32x4 *>(saved);
+  epi.raw1 = reinterpret_cast<f32x4 *>(static_cast<char *>(saved) + raw_bytes);
+  int rc = pair_gather(idx0, idx1, B, K, src, N, map, bias, nullptr, nullptr, epi, static_cast<f32x4 *>(ws), s,
+                       "sft_ft_fwd_transform_f32");
+  if (rc != SFT_OK || B == 0) return rc;
+  hipLaunchKernelGGL(psqt_out_kernel, dim3((unsigned)ceil_div(B, kBlock)), dim3(kBlock), 0, s, epi.raw0, epi.raw1,
+                     map, B, us, psqt_idx, L - L1, psqt);
+  return check_launch("sft_ft_fwd_transform_f32 (psqt)");
 }
 
 size_t fwd_i16_tiled_workspace(int64_t N, int L) {

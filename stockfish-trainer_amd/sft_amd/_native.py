@@ -68,6 +68,18 @@ SIGNATURES = {
         ctypes.c_int,
         [_vp, _vp, _i64, _i32, _vp, _vp, _i32, ctypes.POINTER(_i64), ctypes.POINTER(_i64), _i32,
          ctypes.POINTER(_vp), ctypes.POINTER(_vp), _vp, _vp, ctypes.c_size_t, _vp]),
+    "sft_ft_transform_workspace_size": (
+        ctypes.c_int,
+        [_i64, _i32, _i32, ctypes.POINTER(_i64), ctypes.POINTER(_i64), _i32, _i32, ctypes.POINTER(ctypes.c_size_t),
+         ctypes.POINTER(ctypes.c_size_t), ctypes.POINTER(ctypes.c_size_t)]),
+    "sft_ft_fwd_transform_f32": (
+        ctypes.c_int,
+        [_vp, _vp, _i64, _i32, _i32, ctypes.POINTER(_vp), ctypes.POINTER(_vp), ctypes.POINTER(_i64),
+         ctypes.POINTER(_i64), _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, ctypes.c_size_t, _vp, ctypes.c_size_t, _vp]),
+    "sft_ft_bwd_transform_f32": (
+        ctypes.c_int,
+        [_vp, _vp, _i64, _i32, _vp, _vp, _vp, _vp, _vp, ctypes.c_size_t, _i32, ctypes.POINTER(_i64),
+         ctypes.POINTER(_i64), _i32, _i32, ctypes.POINTER(_vp), ctypes.POINTER(_vp), _vp, _vp, ctypes.c_size_t, _vp]),
     "sft_quantize_i16": (ctypes.c_int, [_vp, _i64, ctypes.c_float, _vp, _vp]),
     "sft_prof_enable": (ctypes.c_int, [ctypes.c_int]),
     "sft_prof_num_kinds": (ctypes.c_int, []),
@@ -325,6 +337,78 @@ def ft_bwd_pair_f32(idx0, idx1, grad0, grad1, table_grads, virtual_grads, bias_g
                                          _i64_array(rows), _i64_array(vrows), L, _ptr_array(table_grads),
                                          _ptr_array(virtual_grads), _ptr(bias_grad), ptr, sizes[1], _stream(dev)),
                "sft_ft_bwd_pair_f32")
+    del ws
+
+
+# ---- composed table + post-FT epilogue ----
+def transform_workspace_bytes(B: int, K: int, rows, virtual_rows, L: int, L1: int):
+    """(saved, forward workspace, backward workspace) bytes of the transform
+    calls, or None when the library does not run this shape fused."""
+    key = ("transform", B, K, tuple(rows), tuple(virtual_rows), L, L1)
+    if key in _ws_cache:
+        return _ws_cache[key]
+    sb, fb, bb = ctypes.c_size_t(0), ctypes.c_size_t(0), ctypes.c_size_t(0)
+    rc = lib().sft_ft_transform_workspace_size(B, K, len(rows), _i64_array(rows), _i64_array(virtual_rows), L, L1,
+                                               ctypes.byref(sb), ctypes.byref(fb), ctypes.byref(bb))
+    if rc == SFT_EUNSUPPORTED:
+        got = None
+    else:
+        _check(rc, "sft_ft_transform_workspace_size")
+        got = (int(sb.value), int(fb.value), int(bb.value))
+    _ws_cache[key] = got
+    return got
+
+
+def _transform_checks(idx0, idx1, tables, virtuals, us, psqt_idx, L1):
+    B, K, L, rows, vrows = _pair_shapes(idx0, idx1, tables, virtuals)
+    _require(us.dtype == torch.float32 and us.numel() == B, "us must be float32 with one value per position")
+    _require(psqt_idx.dtype == torch.int64 and psqt_idx.numel() == B, "psqt_indices must be int64 [B]")
+    sizes = transform_workspace_bytes(B, K, rows, vrows, L, L1)
+    _require(sizes is not None, f"sft: shape not supported by the fused transform: {last_error()}")
+    return B, K, L, rows, vrows, sizes
+
+
+def ft_fwd_transform_f32(idx0, idx1, tables, virtuals, bias, us, psqt_idx, L1: int, l0, psqt):
+    """l0 [B, L1] and psqt [B] of the post-FT epilogue over the composed forward.
+    Returns the saved pre-activations (a uint8 tensor and the aligned pointer
+    into it) that ft_bwd_transform_f32 needs."""
+    B, K, L, rows, vrows, (sbytes, fbytes, _) = _transform_checks(idx0, idx1, tables, virtuals, us, psqt_idx, L1)
+    _require(l0.shape == (B, L1) and l0.dtype == torch.float32, "l0 must be float32 [B, L1]")
+    _require(psqt.numel() == B and psqt.dtype == torch.float32, "psqt must be float32 [B]")
+    dev = idx0.device
+    _on_gpu(dev, idx0, idx1, bias, us, psqt_idx, l0, psqt, *tables, *[v for v in virtuals if v is not None])
+    saved, sptr = _workspace(sbytes, dev)
+    ws, ptr = _workspace(fbytes, dev)
+    with torch.cuda.device(dev):
+        _check(lib().sft_ft_fwd_transform_f32(_ptr(idx0), _ptr(idx1), B, K, len(rows), _ptr_array(tables),
+                                              _ptr_array(virtuals), _i64_array(rows), _i64_array(vrows), L, L1,
+                                              _ptr(bias), _ptr(us), _ptr(psqt_idx), _ptr(l0), _ptr(psqt), sptr,
+                                              sbytes, ptr, fbytes, _stream(dev)), "sft_ft_fwd_transform_f32")
+    del ws
+    return saved, sptr
+
+
+def ft_bwd_transform_f32(idx0, idx1, g_l0, g_psqt, us, psqt_idx, saved, L1: int, table_grads, virtual_grads,
+                         bias_grad) -> None:
+    """Overwrites table_grads, virtual_grads and bias_grad with the grads of the
+    transform given the grads of l0 and psqt and the forward's saved buffer."""
+    B, K, L, rows, vrows, (sbytes, _, bbytes) = _transform_checks(idx0, idx1, table_grads, virtual_grads, us,
+                                                                   psqt_idx, L1)
+    _require(g_l0.shape == (B, L1) and g_l0.dtype == torch.float32, "grad of l0 must be float32 [B, L1]")
+    _require(g_psqt.numel() == B and g_psqt.dtype == torch.float32, "grad of psqt must be float32 [B]")
+    _require(bias_grad.shape == (L,) and bias_grad.dtype == torch.float32, "bias_grad must be float32 [L]")
+    dev = idx0.device
+    _on_gpu(dev, idx0, idx1, g_l0, g_psqt, us, psqt_idx, bias_grad, *table_grads,
+            *[v for v in virtual_grads if v is not None])
+    saved_tensor, sptr = saved
+    _require(saved_tensor is None or saved_tensor.device == dev, "saved buffer on another device")
+    ws, ptr = _workspace(bbytes, dev)
+    with torch.cuda.device(dev):
+        _check(lib().sft_ft_bwd_transform_f32(_ptr(idx0), _ptr(idx1), B, K, _ptr(g_l0), _ptr(g_psqt), _ptr(us),
+                                              _ptr(psqt_idx), sptr, sbytes, len(rows), _i64_array(rows),
+                                              _i64_array(vrows), L, L1, _ptr_array(table_grads),
+                                              _ptr_array(virtual_grads), _ptr(bias_grad), ptr, bbytes,
+                                              _stream(dev)), "sft_ft_bwd_transform_f32")
     del ws
 
 

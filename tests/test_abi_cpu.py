@@ -176,3 +176,40 @@ def test_pair_calls_reject_before_launch():
     assert rc == -1 and "aligned" in _native.last_error()
     rc = lib.sft_ft_bwd_pair_f32(P, P, 4, 32, P, None, 1, rows, vrows, 1048, ptrs, ptrs, P, P, 1 << 30, None)
     assert rc == -1 and "null" in _native.last_error()
+
+
+def test_transform_workspace_size_and_checks():
+    lib = _native.lib()
+    sb, fb, bb = ctypes.c_size_t(0), ctypes.c_size_t(0), ctypes.c_size_t(0)
+    args = lambda l1, L=1048: (65536, 32, 1, _i64s(24576), _i64s(768), L, l1, ctypes.byref(sb), ctypes.byref(fb),
+                               ctypes.byref(bb))
+    assert lib.sft_ft_transform_workspace_size(*args(1040)) == 0, _native.last_error()
+    # paired map: 33 tiles for the 2 x 130 chunks of L1 plus one PSQT tile, 128 B per row
+    assert sb.value == 2 * 34 * 65536 * 128 and fb.value == 34 * 24576 * 128
+    assert bb.value >= 2 * 34 * 65536 * 128 + 24576 * 1048 * 4
+    for l1 in (1044, 1048, 0, -8):
+        assert lib.sft_ft_transform_workspace_size(*args(l1)) == _native.SFT_EUNSUPPORTED
+        assert "l1" in _native.last_error()
+    assert lib.sft_ft_transform_workspace_size(*args(128, L=136)) == _native.SFT_EUNSUPPORTED
+
+
+def test_transform_calls_reject_before_launch():
+    lib = _native.lib()
+    ptrs = (ctypes.c_void_p * 1)(0x1000)
+    odd = (ctypes.c_void_p * 1)(0x1008)
+    rows, vrows = _i64s(24576), _i64s(768)
+    fwd = lambda *a: lib.sft_ft_fwd_transform_f32(*a)
+    # null side-to-move, misaligned l0, misaligned table, bad l1
+    assert fwd(P, P, 4, 32, 1, ptrs, ptrs, rows, vrows, 1048, 1040, P, None, P, P, P, P, 1 << 30, P, 1 << 30,
+               None) == -1 and "null" in _native.last_error()
+    assert fwd(P, P, 4, 32, 1, ptrs, ptrs, rows, vrows, 1048, 1040, P, P, P, ctypes.c_void_p(0x1004), P, P, 1 << 30,
+               P, 1 << 30, None) == -1 and "aligned" in _native.last_error()
+    assert fwd(P, P, 4, 32, 1, odd, ptrs, rows, vrows, 1048, 1040, P, P, P, P, P, P, 1 << 30, P, 1 << 30,
+               None) == -1 and "aligned" in _native.last_error()
+    assert fwd(P, P, 4, 32, 1, ptrs, ptrs, rows, vrows, 1048, 1036, P, P, P, P, P, P, 1 << 30, P, 1 << 30,
+               None) == _native.SFT_EUNSUPPORTED
+    bwd = lambda *a: lib.sft_ft_bwd_transform_f32(*a)
+    assert bwd(P, P, 4, 32, P, None, P, P, P, 1 << 30, 1, rows, vrows, 1048, 1040, ptrs, ptrs, P, P, 1 << 30,
+               None) == -1 and "null" in _native.last_error()
+    assert bwd(P, P, 4, 32, P, P, P, P, P, 1 << 30, 1, rows, vrows, 1048, 1040, odd, ptrs, P, P, 1 << 30,
+               None) == -1 and "aligned" in _native.last_error()
