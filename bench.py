@@ -11,6 +11,7 @@ restatement timed on a bounded sample of the same workload).
   python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--workload 1]
                   [--bwd sorted|atomic] [--cpu-seconds 12] [--no-cpu]
   python bench.py --composed halfka|threats   (module surface, fused vs reference composition)
+  python bench.py --transform halfka|threats  (FT + post-FT epilogue, fused vs reference ops)
 """
 
 from __future__ import annotations
@@ -268,6 +269,110 @@ def bench_composed(args, dev) -> int:
     return 0
 
 
+def bench_transform(args, dev) -> int:
+    """NNUEModel._transform_inputs forward + backward (FT of both perspectives
+    and the post-FT epilogue) at B=65536, L1=1040, 8 PSQT buckets, three ways on
+    the same kernels: the reference ops over the reference composition, the
+    reference ops over the fused composed op, and the fused transform."""
+    import types
+
+    import numpy as np
+    import torch
+
+    from sft_amd import _native, workloads
+    from src.model.modules.features import get_feature_cls
+    from src.model.transform_inputs import transform_inputs
+
+    name, lo, hi = COMPOSED[args.transform]
+    B, L1, P = 65536, 1040, 8
+    L = L1 + P
+    torch.manual_seed(0)
+    ft = get_feature_cls(name)(L).to(dev)
+    vrows = folded = 0
+    with torch.no_grad():
+        for f in ft.features:
+            f.weight.normal_(0, 0.05)
+            if hasattr(f, "virtual_weight"):
+                f.virtual_weight.normal_(0, 0.02)
+                vrows += f.virtual_weight.shape[0]
+                folded += f.weight.shape[0]
+        ft.bias.uniform_(0.0, 0.6)
+    N, K = ft.NUM_INPUTS, ft.MAX_ACTIVE_FEATURES
+    log(f"[bench] transform {name}: B={B} N={N} K={K} active U[{lo},{hi}] L1={L1} P={P}")
+    g = np.random.default_rng([300 + K, 0])
+    idx = [workloads.make_indices(np.random.default_rng([200 + K, s]), B, N, K, lo, hi) for s in (0, 1)]
+    iw, ib = (torch.from_numpy(i).to(dev) for i in idx)
+    us = torch.from_numpy(g.integers(0, 2, (B, 1)).astype(np.float32)).to(dev)
+    k = torch.from_numpy(g.integers(0, P, B).astype(np.int64)).to(dev)
+    g_l0 = torch.randn(B, L1, device=dev)
+    g_psqt = torch.randn(B, 1, device=dev)
+
+    def run(mode: str, prof: bool):
+        ft.fused = mode != "reference"
+
+        def step():
+            for p in ft.parameters():
+                p.grad = None
+            l0, psqt = transform_inputs(ft, L1, us, iw, ib, k, fused=mode == "fused")
+            torch.autograd.backward([l0, psqt], [g_l0, g_psqt])
+
+        for _ in range(args.warmup):
+            step()
+        torch.cuda.synchronize()
+        if prof:
+            _native.prof_enable(True)
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(args.steps):
+            step()
+        e1.record()
+        torch.cuda.synchronize()
+        out = _native.prof_collect() if prof else None
+        _native.prof_enable(False)
+        return e0.elapsed_time(e1) / args.steps, out
+
+    ref_ms, _ = run("reference", False)
+    f1_ms, _ = run("composed", False)
+    ms, prof = run("fused", True)
+    log(f"[bench] fused transform {ms:.3f} ms/step; reference ops over the composed op {f1_ms:.3f}; "
+        f"over the reference composition {ref_ms:.3f}")
+    w = types.SimpleNamespace(N=N, L=L, B=B, virtual_rows=vrows, folded_rows=folded)
+    kern = {}
+    for kind, (tot, cnt) in prof.items():
+        sb = kernel_step_bytes(kind, w, idx)
+        if kind == "bwd_epilogue":  # raw tiles and grad tiles of both perspectives + the l0 grad
+            sb = 2 * 4.0 * B * L * 2 + 4.0 * B * L1
+        per_launch = sb / (cnt / args.steps) if sb else None
+        avg = tot / cnt
+        kern[kind] = {"avg_ms": avg, "launches_per_step": cnt / args.steps, "bytes_per_launch": per_launch,
+                      "gbs": (per_launch / (avg * 1e-3) / 1e9) if per_launch else None}
+        log(f"[bench]   {kind:22s} {avg:8.4f} ms x {cnt / args.steps:.0f}/step")
+    dom = max(prof, key=lambda kk: prof[kk][0])
+    dom_avg = prof[dom][0] / prof[dom][1]
+    dom_bytes = kern[dom]["bytes_per_launch"]
+    achieved = dom_bytes / (dom_avg * 1e-3) / 1e9
+    result = {
+        "metric": "FT + post-FT epilogue fwd+bwd positions/sec @B=65536,L1=1040",
+        "value": B / (ms * 1e-3), "unit": "positions/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "fp32", "data": "synthetic",
+        "config": {"workload": f"transform_{args.transform}_b65536", "feature_set": name, "batch": B,
+                   "num_inputs": N, "virtual_rows": vrows, "max_active": K, "active": [lo, hi], "l1": L1,
+                   "psqt_buckets": P, "parallelism": "single-gpu"},
+        "reference_ops_over_reference_composition": {"ms_per_step": ref_ms, "value": B / (ref_ms * 1e-3)},
+        "reference_ops_over_composed_op": {"ms_per_step": f1_ms, "value": B / (f1_ms * 1e-3)},
+        "speedup_vs_reference": ref_ms / ms,
+        "roofline": {"kernel": dom, "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": None,
+                     "algorithmic_bytes_per_launch": dom_bytes, "avg_launch_ms": dom_avg},
+        "kernels": kern,
+        "cpu_baseline": None,
+    }
+    print(json.dumps(result), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -279,6 +384,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--composed", choices=sorted(COMPOSED), default=None,
                     help="time ComposedFeatureTransformer (fused vs reference composition) instead")
+    ap.add_argument("--transform", choices=sorted(COMPOSED), default=None,
+                    help="time the FT + post-FT epilogue (fused vs the reference ops) instead")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -298,6 +405,8 @@ def main() -> int:
     _native.lib()  # fail loudly if the library is missing
     if args.composed:
         return bench_composed(args, dev)
+    if args.transform:
+        return bench_transform(args, dev)
     if w.quantized:
         return bench_q16(args, w, dev)
     log(f"[bench] generating {w.name}: B={w.B} N={w.N} K={w.K} active U[{w.lo},{w.hi}] L={w.L}")
