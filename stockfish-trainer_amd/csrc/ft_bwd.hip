@@ -338,8 +338,14 @@ __global__ __launch_bounds__(kBlock) void virtual_reduce_kernel(const f32x4 *__r
 //                  (mul, sub and gather backward; + for white, - for black)
 // The grads go straight to the grad tiles of the weight-grad gather (paired
 // map), and their column sums over the block's positions of both perspectives
-// to partial[blockIdx.x] for the bias grad.  Lane group lg of the block takes
-// rows r0 + lg + 32 i.
+// to partial[blockIdx.x] for the bias grad.
+//
+// Mapping: wave w of a workgroup takes rows r0 + w, r0 + w + 4, ...; lane
+// group g of the wave takes tiles g, g + 8, ... (kEpiIt per pass), so the
+// eight lane groups of a wave read 8 consecutive 64-byte chunks of each half
+// of the row's l0 grad (512 contiguous bytes) and each lane group one whole
+// 128-byte line of the pre-activation and grad tiles.  All loads of a row are
+// issued before any arithmetic.
 struct BwdEpilogue {
   const float *g_l0;         // [B, L1]
   const float *g_psqt;       // [B]
@@ -350,65 +356,90 @@ struct BwdEpilogue {
   f32x4 *partial;            // [gridDim.x][cols4]
   int P;
 };
-constexpr int kEpiRows = 128;  // positions per workgroup
+constexpr int kEpiRows = 64;  // positions per workgroup
+constexpr int kEpiIt = 5;     // tile slots per lane group and pass (40 tiles per pass)
 __device__ __forceinline__ float clamp01f(float x) { return x < 0.f ? 0.f : (x > 1.f ? 1.f : x); }
+__device__ __forceinline__ f32x4 shfl_xor4(f32x4 v, int m) {
+  return f32x4{__shfl_xor(v.x, m), __shfl_xor(v.y, m), __shfl_xor(v.z, m), __shfl_xor(v.w, m)};
+}
 
-__global__ __launch_bounds__(kBlock) void bwd_epilogue_kernel(BwdEpilogue e, ColMap map, int64_t B) {
-  __shared__ f32x4 red[kBlock / kBwdTileCh][kBwdTileCh];
-  const int tile = blockIdx.y;
-  const int lg = threadIdx.x / kBwdTileCh, q = threadIdx.x % kBwdTileCh;
-  const int colm = tile_col(map, tile, q);
-  const bool colok = colm >= 0;
-  const bool paired = tile < map.t1;  // block-uniform
-  const int64_t j = 4 * (int64_t)tile + (q & 3);  // first-half chunk of a paired lane
+__global__ __launch_bounds__(kBlock) void bwd_epilogue_kernel(BwdEpilogue e, ColMap map, int64_t B, int ntiles) {
+  __shared__ f32x4 red[kWavesPerBlock][kEpiIt][kWave];
+  const int wave = uniform(threadIdx.x / kWave);
+  const int lane = threadIdx.x % kWave;
+  const int g = lane / kBwdTileCh, q = lane % kBwdTileCh;
   const int64_t l0_row = 2 * (int64_t)map.half4;
   const float k127 = 127.0f / 128.0f;
-  f32x4 bsum = f32x4{0.f, 0.f, 0.f, 0.f};
   const int64_t r0 = (int64_t)blockIdx.x * kEpiRows;
-  for (int i = 0; i < kEpiRows / (kBlock / kBwdTileCh); ++i) {
-    const int64_t b = r0 + lg + (int64_t)(kBlock / kBwdTileCh) * i;
-    const bool rowok = b < B;
-    const int64_t bb = rowok ? b : 0;
-    const bool wtm = e.us[bb] != 0.f;
-    const int64_t at = ((int64_t)tile * B + bb) * kBwdTileCh + q;
+  for (int t0 = 0; t0 < ntiles; t0 += kBwdTileCh * kEpiIt) {
+    int tile[kEpiIt], colm[kEpiIt];
 #pragma unroll
-    for (int p = 0; p < 2; ++p) {
-      const f32x4 a = (p == 0 ? e.raw0 : e.raw1)[at];
-      f32x4 d = f32x4{0.f, 0.f, 0.f, 0.f};
-      if (paired) {
-        const f32x4 partner = f32x4{__shfl_xor(a.x, 4), __shfl_xor(a.y, 4), __shfl_xor(a.z, 4), __shfl_xor(a.w, 4)};
-        if (colok) {
-          const int64_t half = ((p == 1) ? wtm : !wtm) ? map.half4 : 0;
-          const f32x4 gsel = reinterpret_cast<const f32x4 *>(e.g_l0)[bb * l0_row + half + j];
-          const f32x4 dpw = gsel * k127 + 0.0f;
-          const f32x4 cp = f32x4{clamp01f(partner.x), clamp01f(partner.y), clamp01f(partner.z), clamp01f(partner.w)};
-          const f32x4 dc = dpw * cp + 0.0f;
-          d.x = (a.x >= 0.f && a.x <= 1.f) ? dc.x : 0.f;
-          d.y = (a.y >= 0.f && a.y <= 1.f) ? dc.y : 0.f;
-          d.z = (a.z >= 0.f && a.z <= 1.f) ? dc.z : 0.f;
-          d.w = (a.w >= 0.f && a.w <= 1.f) ? dc.w : 0.f;
-        }
-      } else if (colok) {
-        const int64_t kq = 4 * (int64_t)(colm - 2 * map.half4);  // PSQT column of element 0
-        const int64_t k = e.psqt_idx[bb];
-        if (k >= kq && k < kq + 4) {
-          const float dp = e.g_psqt[bb] * (e.us[bb] - 0.5f);
-          d[(int)(k - kq)] = 0.0f + (p == 0 ? dp : -dp);
-        }
+    for (int i = 0; i < kEpiIt; ++i) {
+      tile[i] = t0 + g + kBwdTileCh * i;
+      colm[i] = tile[i] < ntiles ? tile_col(map, tile[i], q) : -1;
+    }
+    f32x4 bsum[kEpiIt];
+#pragma unroll
+    for (int i = 0; i < kEpiIt; ++i) bsum[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int r = wave; r < kEpiRows; r += kWavesPerBlock) {
+      const int64_t b = r0 + r;
+      if (b >= B) break;  // wave-uniform
+      const bool wtm = e.us[b] != 0.f;
+      const int64_t half0 = wtm ? 0 : map.half4, half1 = wtm ? map.half4 : 0;
+      f32x4 a[2][kEpiIt], gs[2][kEpiIt];
+#pragma unroll
+      for (int i = 0; i < kEpiIt; ++i) {
+        const bool ok = colm[i] >= 0;
+        const bool paired = tile[i] < map.t1;
+        const int64_t at = ((int64_t)tile[i] * B + b) * kBwdTileCh + q;
+        const int64_t j = 4 * (int64_t)tile[i] + (q & 3);
+        const f32x4 zero = f32x4{0.f, 0.f, 0.f, 0.f};
+        a[0][i] = ok ? e.raw0[at] : zero;
+        a[1][i] = ok ? e.raw1[at] : zero;
+        gs[0][i] = (ok && paired) ? reinterpret_cast<const f32x4 *>(e.g_l0)[b * l0_row + half0 + j] : zero;
+        gs[1][i] = (ok && paired) ? reinterpret_cast<const f32x4 *>(e.g_l0)[b * l0_row + half1 + j] : zero;
       }
-      if (rowok) {
-        (p == 0 ? e.gt0 : e.gt1)[at] = d;
-        bsum += d;
+      const int64_t k = e.psqt_idx[b];
+      const float dp = e.g_psqt[b] * (e.us[b] - 0.5f);
+#pragma unroll
+      for (int i = 0; i < kEpiIt; ++i) {
+        const bool paired = tile[i] < map.t1;
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+          const f32x4 av = a[p][i];
+          const f32x4 partner = shfl_xor4(av, 4);
+          f32x4 d = f32x4{0.f, 0.f, 0.f, 0.f};
+          if (colm[i] >= 0) {
+            if (paired) {
+              const f32x4 dpw = gs[p][i] * k127 + 0.0f;
+              const f32x4 cp = f32x4{clamp01f(partner.x), clamp01f(partner.y), clamp01f(partner.z),
+                                     clamp01f(partner.w)};
+              const f32x4 dc = dpw * cp + 0.0f;
+              d.x = (av.x >= 0.f && av.x <= 1.f) ? dc.x : 0.f;
+              d.y = (av.y >= 0.f && av.y <= 1.f) ? dc.y : 0.f;
+              d.z = (av.z >= 0.f && av.z <= 1.f) ? dc.z : 0.f;
+              d.w = (av.w >= 0.f && av.w <= 1.f) ? dc.w : 0.f;
+            } else {
+              const int64_t kq = 4 * (int64_t)(colm[i] - 2 * map.half4);  // PSQT column of element 0
+              if (k >= kq && k < kq + 4) d[(int)(k - kq)] = 0.0f + (p == 0 ? dp : -dp);
+            }
+            (p == 0 ? e.gt0 : e.gt1)[((int64_t)tile[i] * B + b) * kBwdTileCh + q] = d;
+          }
+          bsum[i] += d;
+        }
       }
     }
-  }
-  red[lg][q] = bsum;
-  __syncthreads();
-  if (threadIdx.x < kBwdTileCh) {
-    f32x4 s = red[0][threadIdx.x];
-    for (int r = 1; r < kBlock / kBwdTileCh; ++r) s += red[r][threadIdx.x];
-    const int c = tile_col(map, tile, threadIdx.x);
-    if (c >= 0) e.partial[(int64_t)blockIdx.x * map.cols4 + c] = s;
+#pragma unroll
+    for (int i = 0; i < kEpiIt; ++i) red[wave][i][lane] = bsum[i];
+    __syncthreads();
+    for (int x = threadIdx.x; x < kEpiIt * kWave; x += kBlock) {
+      const int i = x / kWave, l = x % kWave;
+      const int t = t0 + l / kBwdTileCh + kBwdTileCh * i;
+      const int c = t < ntiles ? tile_col(map, t, l % kBwdTileCh) : -1;
+      if (c >= 0)
+        e.partial[(int64_t)blockIdx.x * map.cols4 + c] = (red[0][i][l] + red[1][i][l]) + (red[2][i][l] + red[3][i][l]);
+    }
+    __syncthreads();
   }
 }
 
@@ -970,8 +1001,8 @@ int bwd_transform_f32(const int32_t *idx0, const int32_t *idx1, int64_t B, int K
   int rc;
   {
     ProfScope prof(kProfBwdEpilogue, s);
-    hipLaunchKernelGGL(bwd_epilogue_kernel, dim3((unsigned)lay.nparts, (unsigned)map_tiles(map)), dim3(kBlock), 0, s,
-                       e, map, B);
+    hipLaunchKernelGGL(bwd_epilogue_kernel, dim3((unsigned)lay.nparts), dim3(kBlock), 0, s, e, map, B,
+                       map_tiles(map));
     if ((rc = check_launch("epilogue backward")) != SFT_OK) return rc;
   }
   if ((rc = launch_bias_final(reinterpret_cast<const float *>(w + lay.partial), lay.nparts, L, db, 1, true, s)) !=

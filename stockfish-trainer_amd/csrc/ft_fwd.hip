@@ -618,8 +618,8 @@ static int pair_gather(const int32_t *idx0, const int32_t *idx1, int64_t B, int 
   const size_t lds = index_lds_bytes(kTileCh, K);
   if (lds > kMaxIndexLds) return fail(SFT_EUNSUPPORTED, std::string(who) + ": max_active too large for the LDS index lists");
   {
-    const int64_t total = N * map.cols4;
     ProfScope prof(kProfFwdFold, s);
+    const int64_t total = N * map.cols4;
     hipLaunchKernelGGL(fold_relayout_kernel, dim3((unsigned)std::min<int64_t>(ceil_div(total, kBlock), 1 << 16)),
                        dim3(kBlock), 0, s, src, (int)N, map, wt);
   }
