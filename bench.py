@@ -12,6 +12,7 @@ restatement timed on a bounded sample of the same workload).
                   [--bwd sorted|atomic] [--cpu-seconds 12] [--no-cpu]
   python bench.py --composed halfka|threats   (module surface, fused vs reference composition)
   python bench.py --transform halfka|threats  (FT + post-FT epilogue, fused vs reference ops)
+  python bench.py --optimizer                 (fused Ranger22 update of the FT parameters)
 """
 
 from __future__ import annotations
@@ -373,6 +374,92 @@ def bench_transform(args, dev) -> int:
     return 0
 
 
+def bench_optimizer(args, dev) -> int:
+    """Ranger22 full update of the HalfKAv2_hm^ FT parameters (weight
+    [24576, 1048], virtual weight [768, 1048], bias [1048]) per step: the fused
+    kernel against the reference function's ops run eagerly in torch (the
+    reference compiles them with torch.compile, which this build does not use)."""
+    import numpy as np
+    import torch
+
+    from sft_amd import _native
+    from src.ranger22.fused_update import get_fused_full_update
+
+    L = 1048
+    shapes = [(24576, L), (768, L), (L,)]
+    g = torch.Generator(device=dev).manual_seed(0)
+    tensors = []
+    for shp in shapes:
+        mk = lambda scale: torch.randn(shp, device=dev, generator=g) * scale
+        tensors.append([mk(0.05), mk(1e-3), mk(1e-3).abs() * 1e-3, mk(1e-3), mk(1e-3)])
+    step, beta1, beta2, lr, eps = 7, 0.9, 0.999, 8.75e-4, 1e-7
+    host = [lr, 1 / np.sqrt(1 - beta2 ** step), eps, 2e-4, 1 / np.sqrt((1 + beta2) ** 2 + beta2 ** 2), 2.0, -1.0,
+            lr / (1 - beta1 ** step), beta2, 1 - beta2, beta1 * beta1, 1 - beta1 * beta1]
+    scalars = torch.tensor(host, dtype=torch.float32, device=dev)
+
+    def reference(p, grad, v, m, mp, s):
+        v.mul_(s[8])
+        v.add_(grad * grad * s[9])
+        m.mul_(s[10])
+        m.add_(grad * s[11])
+        if p.dim() == 2:
+            unorm = torch.linalg.vector_norm(p, ord=2, dim=1, keepdim=True)
+        else:
+            unorm = torch.linalg.vector_norm(p, ord=2)
+        correction = s[3] * (1 - 1 / (unorm + s[2]))
+        denom = v.sqrt() * s[1] + s[2]
+        pn = (m * s[5] + mp * s[6]) * s[4]
+        p.mul_(1 - s[0] * correction)
+        p.sub_((pn / denom) * s[7])
+
+    def timed(fn, prof):
+        for _ in range(args.warmup):
+            for t in tensors:
+                fn(*t, scalars)
+        torch.cuda.synchronize()
+        if prof:
+            _native.prof_enable(True)
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(args.steps):
+            for t in tensors:
+                fn(*t, scalars)
+        e1.record()
+        torch.cuda.synchronize()
+        out = _native.prof_collect() if prof else None
+        _native.prof_enable(False)
+        return e0.elapsed_time(e1) / args.steps, out
+
+    ref_ms, _ = timed(reference, False)
+    fused = lambda p, gr, v, m, mp, s: get_fused_full_update(p.dim())(p, gr, v, m, mp, s)
+    ms, prof = timed(fused, True)
+    elems = sum(int(np.prod(s)) for s in shapes)
+    step_bytes = 8 * 4 * elems  # p, grad, v, m, m_prev read; p, v, m written
+    tot, cnt = prof["ranger22_update"]
+    # the weight table dominates: its launch is the first of each step's three
+    big = 8 * 4 * shapes[0][0] * shapes[0][1]
+    log(f"[bench] fused Ranger22 update {ms * 1e3:.1f} us/step, reference ops eager {ref_ms * 1e3:.1f} us/step")
+    achieved = step_bytes / (tot / cnt * 3 * 1e-3) / 1e9
+    result = {
+        "metric": "Ranger22 FT-parameter update, GB/s (HalfKAv2_hm^ weight + virtual + bias, L=1048)",
+        "value": step_bytes / (ms * 1e-3) / 1e9, "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "fp32", "data": "synthetic",
+        "config": {"workload": "ranger22_halfka_ft_params", "shapes": shapes, "elements": elems,
+                   "parallelism": "single-gpu"},
+        "reference_ops_eager": {"ms_per_step": ref_ms, "value": step_bytes / (ref_ms * 1e-3) / 1e9},
+        "speedup_vs_reference_ops_eager": ref_ms / ms,
+        "roofline": {"kernel": "ranger22_update", "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS, "traffic": None,
+                     "algorithmic_bytes_per_step": step_bytes, "weight_table_bytes": big,
+                     "avg_launch_ms": tot / cnt},
+        "cpu_baseline": None,
+    }
+    print(json.dumps(result), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -386,6 +473,8 @@ def main() -> int:
                     help="time ComposedFeatureTransformer (fused vs reference composition) instead")
     ap.add_argument("--transform", choices=sorted(COMPOSED), default=None,
                     help="time the FT + post-FT epilogue (fused vs the reference ops) instead")
+    ap.add_argument("--optimizer", action="store_true",
+                    help="time the fused Ranger22 update of the FT parameters instead")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -407,6 +496,8 @@ def main() -> int:
         return bench_composed(args, dev)
     if args.transform:
         return bench_transform(args, dev)
+    if args.optimizer:
+        return bench_optimizer(args, dev)
     if w.quantized:
         return bench_q16(args, w, dev)
     log(f"[bench] generating {w.name}: B={w.B} N={w.N} K={w.K} active U[{w.lo},{w.hi}] L={w.L}")

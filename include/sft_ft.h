@@ -260,6 +260,28 @@ int sft_ft_bwd_transform_f32(const int32_t *idx0, const int32_t *idx1, int64_t b
                              void *stream);
 
 /*
+ * Ranger22 parameter update of one table (or any fp32 tensor), in place:
+ *   variance_ma = variance_ma * beta2 + (grad * grad) * (1 - beta2)
+ *   grad_ma_cur = grad_ma_cur * beta1^2 + grad * (1 - beta1^2)
+ *   c           = two_nl_factor * (1 - 1 / (||p_row||_2 + eps))   (p before the update)
+ *   p           = p * (1 - lr * c)
+ *                 - ((grad_ma_cur * pnm_a + grad_ma_prev * pnm_b) * noise_norm_recip
+ *                    / (sqrt(variance_ma) * inv_sqrt_bc2 + eps)) * step_size
+ * p, grad and the states are [rows, cols] row-major; the norm is per row
+ * (a 1-D tensor is passed as rows = 1).  scalars is a device array of 12
+ * floats in the reference's order: lr, inv_sqrt_bc2, eps, two_nl_factor,
+ * noise_norm_recip, pnm_a, pnm_b, step_size, beta2, 1 - beta2, beta1^2,
+ * 1 - beta1^2.  Each element's operations round to binary32 in this order (no
+ * FMA contraction); the row norm is a fixed-order fp32 sum.
+ * Replaces the torch.compile'd full update of Ranger22
+ * (src/ranger22/optimizer.py:46-77 for 1-D, :80-111 for 2-D tensors), called
+ * from Ranger22.step (src/ranger22/optimizer.py:472-480).
+ */
+int sft_ranger22_update_f32(float *p, const float *grad, float *variance_ma, float *grad_ma_cur,
+                            const float *grad_ma_prev, int64_t rows, int64_t cols,
+                            const float *scalars, void *stream);
+
+/*
  * Export quantization on the device (src/model/quantize.py:83-84):
  * out[i] = round_half_even(float32(x[i] * scale)) saturated to int16.
  * No reference counterpart as a kernel (the reference runs it as torch ops).

@@ -35,6 +35,8 @@ int bwd_pair_f32(const int32_t *idx0, const int32_t *idx1, int64_t B, int K, con
                  const int64_t *vperiod, const int64_t *vreps, int nvirt, float *db, void *ws, size_t ws_bytes,
                  hipStream_t s);
 void zero_f32(float *p, int64_t n, hipStream_t s);
+int ranger_update_f32(float *p, const float *grad, float *variance_ma, float *gma_cur, const float *gma_prev,
+                      int64_t rows, int64_t cols, const float *scalars, hipStream_t s);
 size_t map_tiles_workspace(const ColMap &m, int64_t rows);
 int fwd_transform_f32(const int32_t *idx0, const int32_t *idx1, int64_t B, int K, const FoldSrc &src, int64_t N,
                       int L, int L1, const float *bias, const float *us, const int64_t *psqt_idx, float *l0,
@@ -128,7 +130,7 @@ const char *const kKindNames[kProfNumKinds] = {
     "fwd_f32_gather",   "bwd_feature_sort",  "bwd_segment_offsets", "bwd_feature_gather", "bwd_bias_partial",
     "bwd_bias_final",   "bwd_atomic_scatter", "bwd_zero_fill",      "fwd_i16_gather",     "quantize_i16",
     "fwd_tile_relayout", "fwd_f32_tiled_gather", "bwd_tiled_gather", "bwd_grad_relayout", "fwd_i16_tiled_gather",
-    "fwd_fold_relayout", "bwd_virtual_reduce", "bwd_epilogue",
+    "fwd_fold_relayout", "bwd_virtual_reduce", "bwd_epilogue", "ranger22_update",
 };
 }  // namespace
 
@@ -494,6 +496,18 @@ int sft_ft_bwd_transform_f32(const int32_t *idx0, const int32_t *idx1, int64_t b
   return bwd_transform_f32(idx0, idx1, batch, max_active, grad_l0, grad_psqt, us, psqt_indices, saved, saved_bytes, N,
                            output_size, l1, g.dst, g.vsrc, g.vdst, g.vperiod, g.vreps, g.nvirt, bias_grad, workspace,
                            workspace_bytes, st);
+}
+
+int sft_ranger22_update_f32(float *p, const float *grad, float *variance_ma, float *grad_ma_cur,
+                            const float *grad_ma_prev, int64_t rows, int64_t cols, const float *scalars,
+                            void *stream) {
+  clear_error();
+  if (!p || !grad || !variance_ma || !grad_ma_cur || !grad_ma_prev || !scalars)
+    return fail(SFT_EINVAL, "sft_ranger22_update_f32: null pointer");
+  if (rows < 0 || cols <= 0 || rows >= INT32_MAX || rows * cols >= ((int64_t)1 << 40))
+    return fail(SFT_EINVAL, "sft_ranger22_update_f32: rows must be in [0, 2^31-1), cols > 0");
+  if (rows == 0) return SFT_OK;
+  return ranger_update_f32(p, grad, variance_ma, grad_ma_cur, grad_ma_prev, rows, cols, scalars, (hipStream_t)stream);
 }
 
 static int check_i16_args(const char *who, const int32_t *idx, int64_t batch, int32_t max_active,

@@ -47,6 +47,7 @@ enum ProfKind : int {
   kProfFwdFold,
   kProfBwdVirtual,
   kProfBwdEpilogue,
+  kProfOptim,
   kProfNumKinds
 };
 struct ProfScope {

@@ -80,6 +80,7 @@ SIGNATURES = {
         ctypes.c_int,
         [_vp, _vp, _i64, _i32, _vp, _vp, _vp, _vp, _vp, ctypes.c_size_t, _i32, ctypes.POINTER(_i64),
          ctypes.POINTER(_i64), _i32, _i32, ctypes.POINTER(_vp), ctypes.POINTER(_vp), _vp, _vp, ctypes.c_size_t, _vp]),
+    "sft_ranger22_update_f32": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _vp, _vp]),
     "sft_quantize_i16": (ctypes.c_int, [_vp, _i64, ctypes.c_float, _vp, _vp]),
     "sft_prof_enable": (ctypes.c_int, [ctypes.c_int]),
     "sft_prof_num_kinds": (ctypes.c_int, []),
@@ -410,6 +411,20 @@ def ft_bwd_transform_f32(idx0, idx1, g_l0, g_psqt, us, psqt_idx, saved, L1: int,
                                               _ptr_array(virtual_grads), _ptr(bias_grad), ptr, bbytes,
                                               _stream(dev)), "sft_ft_bwd_transform_f32")
     del ws
+
+
+def ranger22_update_f32(p, grad, variance_ma, gma_cur, gma_prev, scalars) -> None:
+    """In-place Ranger22 full update of one fp32 tensor (row norms for 2-D,
+    whole-tensor norm for 1-D); scalars is the reference's 12-float device tensor."""
+    _require(p.dim() in (1, 2) and p.dtype == torch.float32, "p must be a 1-D or 2-D float32 tensor")
+    for t in (grad, variance_ma, gma_cur, gma_prev):
+        _require(t.shape == p.shape and t.dtype == torch.float32, "grad and states must match p")
+    _require(scalars.numel() == 12 and scalars.dtype == torch.float32, "scalars must be 12 float32 values")
+    _on_gpu(p.device, p, grad, variance_ma, gma_cur, gma_prev, scalars)
+    rows, cols = (1, p.shape[0]) if p.dim() == 1 else p.shape
+    with torch.cuda.device(p.device):
+        _check(lib().sft_ranger22_update_f32(_ptr(p), _ptr(grad), _ptr(variance_ma), _ptr(gma_cur), _ptr(gma_prev),
+                                             rows, cols, _ptr(scalars), _stream(p.device)), "sft_ranger22_update_f32")
 
 
 def quantize_i16(x: torch.Tensor, scale: float) -> torch.Tensor:
