@@ -229,7 +229,7 @@ inline ColMap plain_map(int cols4) { return ColMap{0, 0, cols4}; }
 inline ColMap paired_map(int cols4, int half4) {
   return ColMap{half4, (half4 + 3) / 4, cols4};
 }
-inline int map_tiles(const ColMap &m) {
+__host__ __device__ inline int map_tiles(const ColMap &m) {
   return m.half4 == 0 ? (m.cols4 + 7) / 8 : m.t1 + (m.cols4 - 2 * m.half4 + 7) / 8;
 }
 

@@ -351,13 +351,16 @@ struct BwdEpilogue {
   const float *g_psqt;       // [B]
   const float *us;           // [B]
   const int64_t *psqt_idx;   // [B]
-  const f32x4 *raw0, *raw1;  // pre-activations, paired tiles
+  const f32x4 *raw0, *raw1;  // pre-activations, [B][ntiles][8] paired-tile chunks
   f32x4 *gt0, *gt1;          // grad tiles out
   f32x4 *partial;            // [gridDim.x][cols4]
   int P;
 };
 constexpr int kEpiRows = 64;  // positions per workgroup
-constexpr int kEpiIt = 5;     // tile slots per lane group and pass (40 tiles per pass)
+#ifndef SFT_EPI_IT
+#define SFT_EPI_IT 3
+#endif
+constexpr int kEpiIt = SFT_EPI_IT;  // tile slots per lane group and pass (8 kEpiIt tiles per pass)
 __device__ __forceinline__ float clamp01f(float x) { return x < 0.f ? 0.f : (x > 1.f ? 1.f : x); }
 __device__ __forceinline__ f32x4 shfl_xor4(f32x4 v, int m) {
   return f32x4{__shfl_xor(v.x, m), __shfl_xor(v.y, m), __shfl_xor(v.z, m), __shfl_xor(v.w, m)};
@@ -385,33 +388,34 @@ __global__ __launch_bounds__(kBlock) void bwd_epilogue_kernel(BwdEpilogue e, Col
       const int64_t b = r0 + r;
       if (b >= B) break;  // wave-uniform
       const bool wtm = e.us[b] != 0.f;
-      const int64_t half0 = wtm ? 0 : map.half4, half1 = wtm ? map.half4 : 0;
-      f32x4 a[2][kEpiIt], gs[2][kEpiIt];
-#pragma unroll
-      for (int i = 0; i < kEpiIt; ++i) {
-        const bool ok = colm[i] >= 0;
-        const bool paired = tile[i] < map.t1;
-        const int64_t at = ((int64_t)tile[i] * B + b) * kBwdTileCh + q;
-        const int64_t j = 4 * (int64_t)tile[i] + (q & 3);
-        const f32x4 zero = f32x4{0.f, 0.f, 0.f, 0.f};
-        a[0][i] = ok ? e.raw0[at] : zero;
-        a[1][i] = ok ? e.raw1[at] : zero;
-        gs[0][i] = (ok && paired) ? reinterpret_cast<const f32x4 *>(e.g_l0)[b * l0_row + half0 + j] : zero;
-        gs[1][i] = (ok && paired) ? reinterpret_cast<const f32x4 *>(e.g_l0)[b * l0_row + half1 + j] : zero;
-      }
       const int64_t k = e.psqt_idx[b];
       const float dp = e.g_psqt[b] * (e.us[b] - 0.5f);
+      // One perspective at a time: its loads for all kEpiIt tile slots are
+      // issued together, which bounds the live registers to one perspective.
+#pragma unroll 1
+      for (int p = 0; p < 2; ++p) {
+        const int64_t half = ((p == 1) ? wtm : !wtm) ? map.half4 : 0;
+        const f32x4 *__restrict__ raw = p == 0 ? e.raw0 : e.raw1;
+        f32x4 *__restrict__ gt = p == 0 ? e.gt0 : e.gt1;
+        f32x4 a[kEpiIt], gs[kEpiIt];
 #pragma unroll
-      for (int i = 0; i < kEpiIt; ++i) {
-        const bool paired = tile[i] < map.t1;
+        for (int i = 0; i < kEpiIt; ++i) {
+          const bool ok = colm[i] >= 0;
+          const bool paired = tile[i] < map.t1;
+          const int64_t j = 4 * (int64_t)tile[i] + (q & 3);
+          const f32x4 zero = f32x4{0.f, 0.f, 0.f, 0.f};
+          a[i] = ok ? raw[(b * ntiles + tile[i]) * kBwdTileCh + q] : zero;
+          gs[i] = (ok && paired) ? reinterpret_cast<const f32x4 *>(e.g_l0)[b * l0_row + half + j] : zero;
+        }
 #pragma unroll
-        for (int p = 0; p < 2; ++p) {
-          const f32x4 av = a[p][i];
+        for (int i = 0; i < kEpiIt; ++i) {
+          const bool paired = tile[i] < map.t1;
+          const f32x4 av = a[i];
           const f32x4 partner = shfl_xor4(av, 4);
           f32x4 d = f32x4{0.f, 0.f, 0.f, 0.f};
           if (colm[i] >= 0) {
             if (paired) {
-              const f32x4 dpw = gs[p][i] * k127 + 0.0f;
+              const f32x4 dpw = gs[i] * k127 + 0.0f;
               const f32x4 cp = f32x4{clamp01f(partner.x), clamp01f(partner.y), clamp01f(partner.z),
                                      clamp01f(partner.w)};
               const f32x4 dc = dpw * cp + 0.0f;
@@ -423,7 +427,7 @@ __global__ __launch_bounds__(kBlock) void bwd_epilogue_kernel(BwdEpilogue e, Col
               const int64_t kq = 4 * (int64_t)(colm[i] - 2 * map.half4);  // PSQT column of element 0
               if (k >= kq && k < kq + 4) d[(int)(k - kq)] = 0.0f + (p == 0 ? dp : -dp);
             }
-            (p == 0 ? e.gt0 : e.gt1)[((int64_t)tile[i] * B + b) * kBwdTileCh + q] = d;
+            gt[((int64_t)tile[i] * B + b) * kBwdTileCh + q] = d;
           }
           bsum[i] += d;
         }

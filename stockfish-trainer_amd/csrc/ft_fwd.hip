@@ -249,7 +249,7 @@ constexpr int kTiledPosPerBlock = kTiledPosPerRound * kTiledRounds;
 
 // Post-FT epilogue of the forward (src/model/model.py:93-115), applied in
 // registers by the EPI instantiation over the paired column map: the
-// pre-activations are stored to raw0/raw1 in tile layout (kept for the
+// pre-activations are stored to raw0/raw1 position-major (kept for the
 // backward), and for the paired tiles lane q < 4 multiplies its clamped chunk
 // with the partner chunk of the other half (lane q + 4), scales by 127/128 and
 // stores it to the half of l0 the side to move selects:
@@ -257,7 +257,7 @@ constexpr int kTiledPosPerBlock = kTiledPosPerRound * kTiledRounds;
 struct FwdEpilogue {
   const float *us;     // [B]; nonzero: white to move
   f32x4 *l0;           // [B, 2 * half4] chunks
-  f32x4 *raw0, *raw1;  // [ntiles][B][8] chunks per perspective
+  f32x4 *raw0, *raw1;  // [B][ntiles][8] chunks per perspective (position-major)
 };
 
 // torch.clamp(x, 0, 1): NaN passes through.
@@ -343,7 +343,7 @@ __global__ __launch_bounds__(kBlock) void fwd_tiled_kernel(const int32_t *__rest
       if (pos < B && colok) __builtin_nontemporal_store(acc, out + pos * cols4 + col4);
     } else {
       f32x4 *__restrict__ raw = second ? epi.raw1 : epi.raw0;
-      if (pos < B) __builtin_nontemporal_store(acc, raw + ((int64_t)it.tile * B + pos) * kTileCh + t);
+      if (pos < B) __builtin_nontemporal_store(acc, raw + (pos * ntiles + it.tile) * kTileCh + t);
       if (it.tile < map.t1) {  // block-uniform
         const f32x4 partner = shfl_xor4(acc, 4);
         if (t < 4 && colok && pos < B) {
@@ -374,7 +374,7 @@ __global__ __launch_bounds__(kBlock) void psqt_out_kernel(const f32x4 *__restric
   if (k >= 0 && k < P) {
     int t, q;
     tile_of_col(map, 2 * map.half4 + (int)(k >> 2), t, q);
-    const int64_t at = ((int64_t)t * B + b) * kTileCh + q;
+    const int64_t at = (b * map_tiles(map) + t) * kTileCh + q;
     const float w = raw0[at][k & 3], bl = raw1[at][k & 3];
     v = (w - bl) * (us[b] - 0.5f);
   }
