@@ -282,6 +282,36 @@ int sft_ranger22_update_f32(float *p, const float *grad, float *variance_ma, flo
                             const float *scalars, void *stream);
 
 /*
+ * ---- Feature-index encoder ----
+ * Positions -> the FT's index rows of both perspectives, in the reference's
+ * order (FeatureSet::fill_feature_indices_sparse and
+ * fill_row_from_position_without_values, src/rust/feature_extraction.rs:209-236,
+ * 442-477; HalfKAv2_hm :389-402, 677-685; Full_Threats :572-675, 687-833).
+ *   boards:       uint8 [batch][64], piece id per square (a1 = 0 .. h8 = 63;
+ *                 id = 2 * type + color, pawn..king = 0..5, white = 0; 255 empty)
+ *   side_to_move: uint8 [batch], 0 = white
+ *   components:   host array of SFT_FEATURES_* in feature-set order, e.g.
+ *                 {SFT_FEATURES_THREATS, SFT_FEATURES_HALFKA} = "Full_Threats+HalfKAv2_hm"
+ *   white_indices / black_indices: int32 [batch][max_active], max_active = the
+ *                 components' maxima summed (128 threats, 32 HalfKAv2_hm); each
+ *                 component's features follow the previous one's, offset by its
+ *                 input count; -1 after the last
+ *   us (float), psqt_indices, layer_stack_indices (int64): [batch], optional
+ *                 (NULL): 1.0 for white to move, (pieces - 1) / 4
+ *   white_count / black_count: int32 [batch], optional: features found per
+ *                 row; above a component's maximum the row keeps the first ones
+ * Positions need one king per side and no pawn on the first or last rank (as
+ * any chess position); other boards give unspecified rows, never a fault.
+ */
+#define SFT_FEATURES_THREATS 1
+#define SFT_FEATURES_HALFKA 2
+int sft_encode_features(const uint8_t *boards, const uint8_t *side_to_move, int64_t batch,
+                        const int32_t *components, int32_t num_components, int32_t *white_indices,
+                        int32_t *black_indices, int32_t max_active, float *us,
+                        int64_t *psqt_indices, int64_t *layer_stack_indices,
+                        int32_t *white_count, int32_t *black_count, void *stream);
+
+/*
  * Export quantization on the device (src/model/quantize.py:83-84):
  * out[i] = round_half_even(float32(x[i] * scale)) saturated to int16.
  * No reference counterpart as a kernel (the reference runs it as torch ops).

@@ -37,6 +37,9 @@ int bwd_pair_f32(const int32_t *idx0, const int32_t *idx1, int64_t B, int K, con
 void zero_f32(float *p, int64_t n, hipStream_t s);
 int ranger_update_f32(float *p, const float *grad, float *variance_ma, float *gma_cur, const float *gma_prev,
                       int64_t rows, int64_t cols, const float *scalars, hipStream_t s);
+int encode_features(const uint8_t *boards, const uint8_t *stm, int64_t B, const int32_t *comps, int ncomp,
+                    int32_t *white, int32_t *black, int K, float *us, int64_t *psqt, int64_t *ls, int32_t *count_w,
+                    int32_t *count_b, hipStream_t s);
 size_t map_tiles_workspace(const ColMap &m, int64_t rows);
 int fwd_transform_f32(const int32_t *idx0, const int32_t *idx1, int64_t B, int K, const FoldSrc &src, int64_t N,
                       int L, int L1, const float *bias, const float *us, const int64_t *psqt_idx, float *l0,
@@ -130,7 +133,7 @@ const char *const kKindNames[kProfNumKinds] = {
     "fwd_f32_gather",   "bwd_feature_sort",  "bwd_segment_offsets", "bwd_feature_gather", "bwd_bias_partial",
     "bwd_bias_final",   "bwd_atomic_scatter", "bwd_zero_fill",      "fwd_i16_gather",     "quantize_i16",
     "fwd_tile_relayout", "fwd_f32_tiled_gather", "bwd_tiled_gather", "bwd_grad_relayout", "fwd_i16_tiled_gather",
-    "fwd_fold_relayout", "bwd_virtual_reduce", "bwd_epilogue", "ranger22_update",
+    "fwd_fold_relayout", "bwd_virtual_reduce", "bwd_epilogue", "ranger22_update", "encode_features",
 };
 }  // namespace
 
@@ -508,6 +511,32 @@ int sft_ranger22_update_f32(float *p, const float *grad, float *variance_ma, flo
     return fail(SFT_EINVAL, "sft_ranger22_update_f32: rows must be in [0, 2^31-1), cols > 0");
   if (rows == 0) return SFT_OK;
   return ranger_update_f32(p, grad, variance_ma, grad_ma_cur, grad_ma_prev, rows, cols, scalars, (hipStream_t)stream);
+}
+
+int sft_encode_features(const uint8_t *boards, const uint8_t *side_to_move, int64_t batch, const int32_t *components,
+                        int32_t num_components, int32_t *white_indices, int32_t *black_indices, int32_t max_active,
+                        float *us, int64_t *psqt_indices, int64_t *layer_stack_indices, int32_t *white_count,
+                        int32_t *black_count, void *stream) {
+  clear_error();
+  const char *who = "sft_encode_features";
+  if (batch < 0 || batch >= ((int64_t)1 << 30)) return fail(SFT_EINVAL, std::string(who) + ": batch out of range");
+  if (!components || num_components < 1 || num_components > 2)
+    return fail(SFT_EINVAL, std::string(who) + ": 1 or 2 components");
+  int K = 0;
+  for (int i = 0; i < num_components; ++i) {
+    if (components[i] != SFT_FEATURES_THREATS && components[i] != SFT_FEATURES_HALFKA)
+      return fail(SFT_EINVAL, std::string(who) + ": unknown component");
+    if (i > 0 && components[i] == components[0]) return fail(SFT_EINVAL, std::string(who) + ": repeated component");
+    K += components[i] == SFT_FEATURES_THREATS ? 128 : 32;
+  }
+  if (max_active != K) return fail(SFT_EINVAL, std::string(who) + ": max_active must be the components' sum");
+  if (batch == 0) return SFT_OK;
+  if (!boards || !side_to_move || !white_indices || !black_indices)
+    return fail(SFT_EINVAL, std::string(who) + ": null pointer");
+  if (misaligned16(boards) || misaligned16(white_indices) || misaligned16(black_indices))
+    return fail(SFT_EINVAL, std::string(who) + ": boards and index rows must be 16-byte aligned");
+  return encode_features(boards, side_to_move, batch, components, num_components, white_indices, black_indices, K, us,
+                         psqt_indices, layer_stack_indices, white_count, black_count, (hipStream_t)stream);
 }
 
 static int check_i16_args(const char *who, const int32_t *idx, int64_t batch, int32_t max_active,

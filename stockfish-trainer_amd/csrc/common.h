@@ -14,6 +14,7 @@ namespace sft {
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef short i16x8 __attribute__((ext_vector_type(8)));
 typedef int i32x8 __attribute__((ext_vector_type(8)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kWave = 64;          // CDNA wavefront width
 constexpr int kWavesPerBlock = 4;  // 256-thread workgroups
@@ -48,6 +49,7 @@ enum ProfKind : int {
   kProfBwdVirtual,
   kProfBwdEpilogue,
   kProfOptim,
+  kProfEncode,
   kProfNumKinds
 };
 struct ProfScope {

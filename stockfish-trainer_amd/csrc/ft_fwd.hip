@@ -21,7 +21,6 @@ namespace sft {
 
 namespace {
 
-typedef int i32x4 __attribute__((ext_vector_type(4)));
 
 template <typename T>
 __device__ __forceinline__ T zero_of() {

@@ -29,6 +29,8 @@ SFT_BWD_ROWS = 0x2
 SFT_Q16_ACC32 = 0x0
 SFT_Q16_WRAP16 = 0x1
 SFT_Q16_ROWS = 0x2
+SFT_FEATURES_THREATS = 1
+SFT_FEATURES_HALFKA = 2
 
 _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -81,6 +83,8 @@ SIGNATURES = {
         [_vp, _vp, _i64, _i32, _vp, _vp, _vp, _vp, _vp, ctypes.c_size_t, _i32, ctypes.POINTER(_i64),
          ctypes.POINTER(_i64), _i32, _i32, ctypes.POINTER(_vp), ctypes.POINTER(_vp), _vp, _vp, ctypes.c_size_t, _vp]),
     "sft_ranger22_update_f32": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _vp, _vp]),
+    "sft_encode_features": (
+        ctypes.c_int, [_vp, _vp, _i64, ctypes.POINTER(_i32), _i32, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp]),
     "sft_quantize_i16": (ctypes.c_int, [_vp, _i64, ctypes.c_float, _vp, _vp]),
     "sft_prof_enable": (ctypes.c_int, [ctypes.c_int]),
     "sft_prof_num_kinds": (ctypes.c_int, []),
@@ -425,6 +429,25 @@ def ranger22_update_f32(p, grad, variance_ma, gma_cur, gma_prev, scalars) -> Non
     with torch.cuda.device(p.device):
         _check(lib().sft_ranger22_update_f32(_ptr(p), _ptr(grad), _ptr(variance_ma), _ptr(gma_cur), _ptr(gma_prev),
                                              rows, cols, _ptr(scalars), _stream(p.device)), "sft_ranger22_update_f32")
+
+
+def encode_features(boards, side_to_move, components, white, black, us=None, psqt=None, layer_stack=None,
+                    white_count=None, black_count=None) -> None:
+    """Index rows of both perspectives from positions (uint8 boards [B, 64],
+    side to move [B]); components: SFT_FEATURES_* in feature-set order."""
+    _require(boards.dim() == 2 and boards.shape[1] == 64 and boards.dtype == torch.uint8, "boards must be uint8 [B, 64]")
+    B = boards.shape[0]
+    _require(side_to_move.dtype == torch.uint8 and side_to_move.numel() == B, "side_to_move must be uint8 [B]")
+    K = white.shape[1] if white.dim() == 2 else -1
+    for t in (white, black):
+        _require(t.dtype == torch.int32 and t.shape == (B, K), "index rows must be int32 [B, K]")
+    opt = [t for t in (us, psqt, layer_stack, white_count, black_count) if t is not None]
+    _on_gpu(boards.device, boards, side_to_move, white, black, *opt)
+    comps = (_i32 * len(components))(*components)
+    with torch.cuda.device(boards.device):
+        _check(lib().sft_encode_features(_ptr(boards), _ptr(side_to_move), B, comps, len(components), _ptr(white),
+                                         _ptr(black), K, _ptr(us), _ptr(psqt), _ptr(layer_stack), _ptr(white_count),
+                                         _ptr(black_count), _stream(boards.device)), "sft_encode_features")
 
 
 def quantize_i16(x: torch.Tensor, scale: float) -> torch.Tensor:
