@@ -13,6 +13,7 @@ restatement timed on a bounded sample of the same workload).
   python bench.py --composed halfka|threats   (module surface, fused vs reference composition)
   python bench.py --transform halfka|threats  (FT + post-FT epilogue, fused vs reference ops)
   python bench.py --optimizer                 (fused Ranger22 update of the FT parameters)
+  python bench.py --encode halfka|threats     (GPU feature-index encoder)
 """
 
 from __future__ import annotations
@@ -460,6 +461,81 @@ def bench_optimizer(args, dev) -> int:
     return 0
 
 
+def bench_encode(args, dev) -> int:
+    """Feature-index encoding of B=65536 positions (both perspectives, index rows
+    plus side to move and buckets) on the GPU, positions already in HBM; the C
+    oracle on the host cores is the CPU baseline."""
+    import os as _os
+
+    import numpy as np
+    import torch
+
+    from oracle import feature_oracle
+    from sft_amd import _native, positions
+    from sft_amd.encode import encode_batch, parse_feature_set
+
+    name = {"halfka": "HalfKAv2_hm", "threats": "Full_Threats+HalfKAv2_hm"}[args.encode]
+    B = 65536
+    log(f"[bench] encode {name}: generating {B} positions")
+    boards_np, stm_np = positions.random_positions(B, seed=7)
+    boards = torch.from_numpy(boards_np).to(dev)
+    stm = torch.from_numpy(stm_np).to(dev)
+    for _ in range(args.warmup):
+        encode_batch(boards, stm, name)
+    torch.cuda.synchronize()
+    _native.prof_enable(True)
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(args.steps):
+        out = encode_batch(boards, stm, name)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / args.steps
+    tot, cnt = _native.prof_collect()["encode_features"]
+    _native.prof_enable(False)
+    comps, K = parse_feature_set(name)
+    active = int((out["white"] >= 0).sum().item() + (out["black"] >= 0).sum().item())
+    # algorithmic bytes: boards + side to move read; both index rows, us, psqt and layer-stack buckets written
+    step_bytes = B * (64 + 1) + B * (2 * K * 4 + 4 + 8 + 8)
+    kern_ms = tot / cnt
+    achieved = step_bytes / (kern_ms * 1e-3) / 1e9
+    log(f"[bench] encode {ms * 1e3:.1f} us/batch ({B / (ms * 1e-3) / 1e6:.1f} M positions/s), "
+        f"{active / B:.1f} features per position")
+    cpu = None
+    if not args.no_cpu:
+        threads = min(len(_os.sched_getaffinity(0)), int(_os.environ.get("OMP_NUM_THREADS", "64")))
+        _os.environ["OMP_NUM_THREADS"] = str(threads)
+        n = 16384
+        comps_names = name.split("+")
+        feature_oracle.encode(boards_np[:256], stm_np[:256], comps_names)
+        t0 = time.perf_counter()
+        reps = 0
+        while time.perf_counter() - t0 < min(args.cpu_seconds, 10.0):
+            feature_oracle.encode(boards_np[:n], stm_np[:n], comps_names)
+            reps += 1
+        el = time.perf_counter() - t0
+        cpu = {"value": reps * n / el, "unit": "positions/s", "cores": threads, "kind": "port",
+               "sample": f"{reps} x {n} positions of the same batch, oracle/feature_oracle.c with OpenMP, "
+                         f"{el:.1f} s"}
+        log(f"[bench] cpu baseline {cpu['value'] / 1e6:.2f} M positions/s on {threads} threads")
+    result = {
+        "metric": f"feature-index encode positions/sec ({name}, both perspectives) @B=65536",
+        "value": B / (ms * 1e-3), "unit": "positions/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "int32", "data": "synthetic",
+        "config": {"workload": f"encode_{args.encode}_b65536", "feature_set": name, "batch": B, "max_active": K,
+                   "positions": "random armies (sft_amd.positions.random_positions, seed 7)",
+                   "features_per_position": active / B, "parallelism": "single-gpu"},
+        "roofline": {"kernel": "encode_features", "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS, "traffic": None,
+                     "algorithmic_bytes_per_launch": step_bytes, "avg_launch_ms": kern_ms},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(result), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -475,6 +551,8 @@ def main() -> int:
                     help="time the FT + post-FT epilogue (fused vs the reference ops) instead")
     ap.add_argument("--optimizer", action="store_true",
                     help="time the fused Ranger22 update of the FT parameters instead")
+    ap.add_argument("--encode", choices=["halfka", "threats"], default=None,
+                    help="time the GPU feature-index encoder instead")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -498,6 +576,8 @@ def main() -> int:
         return bench_transform(args, dev)
     if args.optimizer:
         return bench_optimizer(args, dev)
+    if args.encode:
+        return bench_encode(args, dev)
     if w.quantized:
         return bench_q16(args, w, dev)
     log(f"[bench] generating {w.name}: B={w.B} N={w.N} K={w.K} active U[{w.lo},{w.hi}] L={w.L}")

@@ -107,18 +107,24 @@ __device__ uint64_t empty_mask(int piece, int from) {
 }
 
 __device__ void build_tables(EncodeTables &T) {
+  __shared__ int sizes[12];
   for (int i = threadIdx.x; i < 10 * 64; i += blockDim.x) T.mask[i / 64][i % 64] = empty_mask(i / 64, i % 64);
   __syncthreads();
-  if (threadIdx.x < 12) {
-    // piece ids in the reference's order: colour outer, type inner
-    // (src/rust/feature_extraction.rs:800-828); offsets need the earlier pieces' sizes.
+  if (threadIdx.x < 12) {  // per piece: from-square offsets within its block
     const int p = threadIdx.x;
-    int sizes[12];
-    for (int q = 0; q < 12; ++q) {
-      int sz = 0;
-      for (int s = 0; s < 64; ++s) sz += (q >> 1) == kKing ? popc64(step_attacks(s, kKingD, 8)) : popc64(T.mask[q][s]);
-      sizes[q] = sz;
+    int off = 0;
+    for (int s = 0; s < 64; ++s) {
+      T.table[p][s] = off;
+      off += (p >> 1) == kKing ? popc64(step_attacks(s, kKingD, 8)) : popc64(T.mask[p][s]);
     }
+    T.table[p][64] = off;
+    sizes[p] = off;
+  }
+  __syncthreads();
+  if (threadIdx.x < 12) {
+    // base offsets in the reference's piece order: colour outer, type inner
+    // (src/rust/feature_extraction.rs:800-828)
+    const int p = threadIdx.x;
     int base = 0;
     for (int color = 0; color < 2; ++color)
       for (int t = 0; t < 6; ++t) {
@@ -126,12 +132,6 @@ __device__ void build_tables(EncodeTables &T) {
         if (q == p) T.table[p][65] = base;
         base += kNumValidTargets[q] * sizes[q];
       }
-    int off = 0;
-    for (int s = 0; s < 64; ++s) {
-      T.table[p][s] = off;
-      off += (p >> 1) == kKing ? popc64(step_attacks(s, kKingD, 8)) : popc64(T.mask[p][s]);
-    }
-    T.table[p][64] = off;
   }
   __syncthreads();
 }
@@ -194,7 +194,7 @@ __global__ __launch_bounds__(kBlock) void encode_kernel(const uint8_t *__restric
                                                         int64_t *__restrict__ ls, int32_t *__restrict__ count_w,
                                                         int32_t *__restrict__ count_b) {
   __shared__ EncodeTables T;
-  build_tables(T);
+  if (enc.comp[0] == 1 || (enc.ncomp > 1 && enc.comp[1] == 1)) build_tables(T);  // block-uniform
   const int64_t t = (int64_t)blockIdx.x * kBlock + threadIdx.x;
   const int64_t b = t >> 1;
   const int persp = (int)(t & 1);
