@@ -32,27 +32,30 @@ constexpr int kBiasMaxParts = 512;
 
 // seg_start[k] for k in [0, N]: index of the first sorted key >= k, N = key
 // count.  The sorted array holds the active slots only; their number is the
-// sum of the sort's last digit totals (read here, on the device).
+// sum of the sort's last digit totals (read here, on the device, once per
+// workgroup by one wave).  Grid-stride over the sorted slots.
 __global__ __launch_bounds__(kBlock) void seg_offsets_kernel(const unsigned *__restrict__ keys, int64_t N,
                                                              const unsigned *__restrict__ totals, int ntot,
                                                              int32_t *__restrict__ seg_start) {
-  __shared__ unsigned red[kBlock];
-  unsigned v = 0;
-  for (int d = threadIdx.x; d < ntot; d += kBlock) v += totals[d];
-  red[threadIdx.x] = v;
-  __syncthreads();
-  for (int off = kBlock / 2; off > 0; off >>= 1) {
-    if ((int)threadIdx.x < off) red[threadIdx.x] += red[threadIdx.x + off];
-    __syncthreads();
+  __shared__ unsigned s_active;
+  if (threadIdx.x < kWave) {
+    unsigned v = 0;
+    for (int d = threadIdx.x; d < ntot; d += kWave) v += totals[d];
+#pragma unroll
+    for (int m = 1; m < kWave; m <<= 1) v += __shfl_xor(v, m);
+    if (threadIdx.x == 0) s_active = v;
   }
-  const int64_t M = red[0];
-  const int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
-  if (i > M) return;
-  const int64_t cur = i < M ? (int64_t)keys[i] : N + 1;
-  const int64_t prev = i > 0 ? (int64_t)keys[i - 1] : -1;
-  const int64_t hi = cur < N ? cur : N;
-  for (int64_t f = prev + 1; f <= hi; ++f) seg_start[f] = (int32_t)i;
+  __syncthreads();
+  const int64_t M = s_active;
+  for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i <= M; i += (int64_t)gridDim.x * kBlock) {
+    const int64_t cur = i < M ? (int64_t)keys[i] : N + 1;
+    const int64_t prev = i > 0 ? (int64_t)keys[i - 1] : -1;
+    const int64_t hi = cur < N ? cur : N;
+    for (int64_t f = prev + 1; f <= hi; ++f) seg_start[f] = (int32_t)i;
+  }
 }
+
+constexpr int kSegBlocks = 2048;
 
 template <int G>
 __device__ __forceinline__ void group_minmax(int v, int &vmin, int &vmax) {
@@ -785,7 +788,7 @@ int bwd_f32(const int32_t *idx, int64_t B, int K, const float *grad, int64_t N, 
   }
   {
     ProfScope prof(kProfBwdOffsets, s);
-    hipLaunchKernelGGL(seg_offsets_kernel, dim3((unsigned)ceil_div(M + 1, kBlock)), dim3(kBlock), 0, s, keys, nkeys,
+    hipLaunchKernelGGL(seg_offsets_kernel, dim3((unsigned)std::min<int64_t>(ceil_div(M + 1, kBlock), kSegBlocks)), dim3(kBlock), 0, s, keys, nkeys,
                        totals, ntot, seg);
     if ((rc = check_launch("segment offsets")) != SFT_OK) return rc;
   }
@@ -876,7 +879,7 @@ static int pair_gather_perspective(int p, const int32_t *idx, int64_t B, int K, 
   }
   {
     ProfScope prof(kProfBwdOffsets, s);
-    hipLaunchKernelGGL(seg_offsets_kernel, dim3((unsigned)ceil_div(M + 1, kBlock)), dim3(kBlock), 0, s, keys,
+    hipLaunchKernelGGL(seg_offsets_kernel, dim3((unsigned)std::min<int64_t>(ceil_div(M + 1, kBlock), kSegBlocks)), dim3(kBlock), 0, s, keys,
                        (int64_t)nc * N, totals, ntot, seg);
     if ((rc = check_launch("segment offsets")) != SFT_OK) return rc;
   }
