@@ -14,6 +14,7 @@ restatement timed on a bounded sample of the same workload).
   python bench.py --transform halfka|threats  (FT + post-FT epilogue, fused vs reference ops)
   python bench.py --optimizer                 (fused Ranger22 update of the FT parameters)
   python bench.py --encode halfka|threats     (GPU feature-index encoder)
+  python bench.py --export                    (GPU LEB128 of the .nnue FT weights)
 """
 
 from __future__ import annotations
@@ -536,6 +537,61 @@ def bench_encode(args, dev) -> int:
     return 0
 
 
+def bench_export(args, dev) -> int:
+    """Signed LEB128 of the exported HalfKAv2_hm FT weights (22528 x 1040 int16,
+    the largest tensor of the .nnue file) on the GPU; the per-value loop of the
+    reference's encoder (restated in the oracle) on a bounded sample is the CPU
+    baseline."""
+    import numpy as np
+    import torch
+
+    from oracle import leb128_oracle
+    from sft_amd import _native
+
+    g = np.random.default_rng(11)
+    w = np.clip(np.rint(g.standard_normal((22528, 1040)) * 40), -32768, 32767).astype(np.int16)
+    t = torch.from_numpy(w).to(dev)
+    for _ in range(args.warmup):
+        _native.leb128_encode(t)
+    torch.cuda.synchronize()
+    _native.prof_enable(True)
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        out = _native.leb128_encode(t)
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / args.steps
+    tot, cnt = _native.prof_collect()["leb128_encode"]
+    _native.prof_enable(False)
+    kern = tot / cnt
+    n = w.size
+    nbytes = int(out.numel())
+    algo = n * 2 + nbytes  # values read, code bytes written
+    log(f"[bench] LEB128 {n} int16 -> {nbytes} bytes: kernels {kern * 1e3:.1f} us, call {wall * 1e6:.1f} us")
+    cpu = None
+    if not args.no_cpu:
+        sample = w.reshape(-1)[:200000]
+        t0 = time.perf_counter()
+        leb128_oracle.encode(sample)
+        el = time.perf_counter() - t0
+        cpu = {"value": sample.size / el, "unit": "values/s", "cores": 1, "kind": "port",
+               "sample": f"{sample.size} values through the per-value loop of the reference encoder (Python), "
+                         f"{el:.1f} s"}
+    result = {
+        "metric": "signed LEB128 encode values/sec (HalfKAv2_hm FT weights 22528 x 1040 int16)",
+        "value": n / (kern * 1e-3), "unit": "values/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": kern, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int16",
+        "data": "synthetic", "config": {"workload": "leb128_halfka_export_weights", "values": n,
+                                        "encoded_bytes": nbytes, "parallelism": "single-gpu"},
+        "call_ms_including_length_readback": wall * 1e3,
+        "roofline": {"kernel": "leb128_encode", "bound": "hbm", "achieved": algo / (kern * 1e-3) / 1e9,
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": algo / (kern * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                     "traffic": None, "algorithmic_bytes_per_launch": algo, "avg_launch_ms": kern},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(result), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -553,6 +609,7 @@ def main() -> int:
                     help="time the fused Ranger22 update of the FT parameters instead")
     ap.add_argument("--encode", choices=["halfka", "threats"], default=None,
                     help="time the GPU feature-index encoder instead")
+    ap.add_argument("--export", action="store_true", help="time the GPU LEB128 encoder of the .nnue export instead")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -578,6 +635,8 @@ def main() -> int:
         return bench_optimizer(args, dev)
     if args.encode:
         return bench_encode(args, dev)
+    if args.export:
+        return bench_export(args, dev)
     if w.quantized:
         return bench_q16(args, w, dev)
     log(f"[bench] generating {w.name}: B={w.B} N={w.N} K={w.K} active U[{w.lo},{w.hi}] L={w.L}")

@@ -312,6 +312,21 @@ int sft_encode_features(const uint8_t *boards, const uint8_t *side_to_move, int6
                         int32_t *white_count, int32_t *black_count, void *stream);
 
 /*
+ * ---- .nnue export: signed LEB128 ----
+ * Encodes n signed integers (elem_bytes 1, 2 or 4: int8 / int16 / int32) as the
+ * concatenation of their signed LEB128 codes, in element order, into out
+ * (device, out_capacity >= n * 2 / 3 / 5 bytes), and the byte count into
+ * *out_len (a device int64, written by the last kernel on the stream).
+ * Replaces _encode_leb_128_array (src/scripts/serialize.py:61-93), the
+ * payload of _write_leb_128_array (:254-257) for the FT bias, weights and PSQT
+ * weights of the .nnue file.
+ */
+int sft_leb128_workspace_size(int64_t n, size_t *bytes);
+int sft_leb128_encode(const void *values, int32_t elem_bytes, int64_t n, uint8_t *out,
+                      size_t out_capacity, int64_t *out_len, void *workspace,
+                      size_t workspace_bytes, void *stream);
+
+/*
  * Export quantization on the device (src/model/quantize.py:83-84):
  * out[i] = round_half_even(float32(x[i] * scale)) saturated to int16.
  * No reference counterpart as a kernel (the reference runs it as torch ops).

@@ -37,6 +37,8 @@ int bwd_pair_f32(const int32_t *idx0, const int32_t *idx1, int64_t B, int K, con
 void zero_f32(float *p, int64_t n, hipStream_t s);
 int ranger_update_f32(float *p, const float *grad, float *variance_ma, float *gma_cur, const float *gma_prev,
                       int64_t rows, int64_t cols, const float *scalars, hipStream_t s);
+size_t leb128_workspace(int64_t n);
+int leb128_encode(const void *values, int elem, int64_t n, uint8_t *out, int64_t *out_len, void *ws, hipStream_t s);
 int encode_features(const uint8_t *boards, const uint8_t *stm, int64_t B, const int32_t *comps, int ncomp,
                     int32_t *white, int32_t *black, int K, float *us, int64_t *psqt, int64_t *ls, int32_t *count_w,
                     int32_t *count_b, hipStream_t s);
@@ -133,7 +135,7 @@ const char *const kKindNames[kProfNumKinds] = {
     "fwd_f32_gather",   "bwd_feature_sort",  "bwd_segment_offsets", "bwd_feature_gather", "bwd_bias_partial",
     "bwd_bias_final",   "bwd_atomic_scatter", "bwd_zero_fill",      "fwd_i16_gather",     "quantize_i16",
     "fwd_tile_relayout", "fwd_f32_tiled_gather", "bwd_tiled_gather", "bwd_grad_relayout", "fwd_i16_tiled_gather",
-    "fwd_fold_relayout", "bwd_virtual_reduce", "bwd_epilogue", "ranger22_update", "encode_features",
+    "fwd_fold_relayout", "bwd_virtual_reduce", "bwd_epilogue", "ranger22_update", "encode_features", "leb128_encode",
 };
 }  // namespace
 
@@ -537,6 +539,32 @@ int sft_encode_features(const uint8_t *boards, const uint8_t *side_to_move, int6
     return fail(SFT_EINVAL, std::string(who) + ": boards and index rows must be 16-byte aligned");
   return encode_features(boards, side_to_move, batch, components, num_components, white_indices, black_indices, K, us,
                          psqt_indices, layer_stack_indices, white_count, black_count, (hipStream_t)stream);
+}
+
+int sft_leb128_workspace_size(int64_t n, size_t *bytes) {
+  clear_error();
+  if (!bytes) return fail(SFT_EINVAL, "sft_leb128_workspace_size: null pointer");
+  if (n < 0 || n >= ((int64_t)1 << 40)) return fail(SFT_EINVAL, "sft_leb128_workspace_size: n out of range");
+  *bytes = leb128_workspace(n);
+  return SFT_OK;
+}
+
+int sft_leb128_encode(const void *values, int32_t elem_bytes, int64_t n, uint8_t *out, size_t out_capacity,
+                      int64_t *out_len, void *workspace, size_t workspace_bytes, void *stream) {
+  clear_error();
+  const char *who = "sft_leb128_encode";
+  if (elem_bytes != 1 && elem_bytes != 2 && elem_bytes != 4)
+    return fail(SFT_EINVAL, std::string(who) + ": elem_bytes must be 1, 2 or 4");
+  if (n < 0 || n >= ((int64_t)1 << 40)) return fail(SFT_EINVAL, std::string(who) + ": n out of range");
+  if (!out_len || (n > 0 && (!values || !out))) return fail(SFT_EINVAL, std::string(who) + ": null pointer");
+  const int64_t max_bytes = elem_bytes == 1 ? 2 : elem_bytes == 2 ? 3 : 5;  // signed LEB128 of 8/16/32-bit values
+  if ((int64_t)out_capacity < n * max_bytes)
+    return fail(SFT_EINVAL, std::string(who) + ": out_capacity must be at least n * (2, 3 or 5)");
+  if (!workspace || workspace_bytes < leb128_workspace(n) || (uintptr_t)workspace % 8 != 0)
+    return fail(SFT_EWORKSPACE, std::string(who) + ": workspace smaller than sft_leb128_workspace_size()");
+  if ((uintptr_t)values % elem_bytes != 0 || (uintptr_t)out_len % 8 != 0)
+    return fail(SFT_EINVAL, std::string(who) + ": misaligned values or out_len");
+  return leb128_encode(values, elem_bytes, n, out, out_len, workspace, (hipStream_t)stream);
 }
 
 static int check_i16_args(const char *who, const int32_t *idx, int64_t batch, int32_t max_active,

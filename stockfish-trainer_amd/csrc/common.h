@@ -50,6 +50,7 @@ enum ProfKind : int {
   kProfBwdEpilogue,
   kProfOptim,
   kProfEncode,
+  kProfLeb128,
   kProfNumKinds
 };
 struct ProfScope {

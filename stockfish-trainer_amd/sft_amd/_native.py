@@ -18,6 +18,7 @@ PKG_ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 LIB_PATH = os.path.join(PKG_ROOT, "lib", "libsft_ft.so")
 
 SFT_OK = 0
+SFT_EWORKSPACE = -2
 SFT_EUNSUPPORTED = -4
 SFT_FWD_AUTO = 0x0
 SFT_FWD_ROWS = 0x1
@@ -85,6 +86,8 @@ SIGNATURES = {
     "sft_ranger22_update_f32": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _vp, _vp]),
     "sft_encode_features": (
         ctypes.c_int, [_vp, _vp, _i64, ctypes.POINTER(_i32), _i32, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "sft_leb128_workspace_size": (ctypes.c_int, [_i64, ctypes.POINTER(ctypes.c_size_t)]),
+    "sft_leb128_encode": (ctypes.c_int, [_vp, _i32, _i64, _vp, ctypes.c_size_t, _vp, _vp, ctypes.c_size_t, _vp]),
     "sft_quantize_i16": (ctypes.c_int, [_vp, _i64, ctypes.c_float, _vp, _vp]),
     "sft_prof_enable": (ctypes.c_int, [ctypes.c_int]),
     "sft_prof_num_kinds": (ctypes.c_int, []),
@@ -448,6 +451,28 @@ def encode_features(boards, side_to_move, components, white, black, us=None, psq
         _check(lib().sft_encode_features(_ptr(boards), _ptr(side_to_move), B, comps, len(components), _ptr(white),
                                          _ptr(black), K, _ptr(us), _ptr(psqt), _ptr(layer_stack), _ptr(white_count),
                                          _ptr(black_count), _stream(boards.device)), "sft_encode_features")
+
+
+def leb128_encode(values: torch.Tensor) -> torch.Tensor:
+    """Signed LEB128 codes of an int8 / int16 / int32 device tensor, concatenated
+    in element order: a uint8 device tensor of exactly the encoded length."""
+    elem = {torch.int8: 1, torch.int16: 2, torch.int32: 4}.get(values.dtype)
+    _require(elem is not None, "values must be int8, int16 or int32")
+    _on_gpu(values.device, values)
+    n = values.numel()
+    cap = n * {1: 2, 2: 3, 4: 5}[elem]
+    dev = values.device
+    out = torch.empty(max(cap, 1), dtype=torch.uint8, device=dev)
+    out_len = torch.zeros(1, dtype=torch.int64, device=dev)
+    nb = ctypes.c_size_t(0)
+    _check(lib().sft_leb128_workspace_size(n, ctypes.byref(nb)), "sft_leb128_workspace_size")
+    ws, ptr = _workspace(int(nb.value), dev)
+    with torch.cuda.device(dev):
+        _check(lib().sft_leb128_encode(_ptr(values), elem, n, _ptr(out), cap, _ptr(out_len), ptr, int(nb.value),
+                                       _stream(dev)), "sft_leb128_encode")
+    length = int(out_len.item())  # synchronises the stream
+    del ws
+    return out[:length]
 
 
 def quantize_i16(x: torch.Tensor, scale: float) -> torch.Tensor:

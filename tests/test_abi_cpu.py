@@ -213,3 +213,15 @@ def test_transform_calls_reject_before_launch():
                None) == -1 and "null" in _native.last_error()
     assert bwd(P, P, 4, 32, P, P, P, P, P, 1 << 30, 1, rows, vrows, 1048, 1040, odd, ptrs, P, P, 1 << 30,
                None) == -1 and "aligned" in _native.last_error()
+
+
+def test_leb128_rejects_before_launch():
+    lib = _native.lib()
+    n = ctypes.c_size_t(0)
+    assert lib.sft_leb128_workspace_size(100, ctypes.byref(n)) == 0 and n.value >= 8
+    ws = ctypes.c_void_p(0x1000)
+    # bad element size, too little output capacity, missing workspace, misaligned values
+    assert lib.sft_leb128_encode(P, 3, 10, P, 1000, P, ws, 1 << 20, None) == -1 and "elem_bytes" in _native.last_error()
+    assert lib.sft_leb128_encode(P, 2, 10, P, 29, P, ws, 1 << 20, None) == -1 and "capacity" in _native.last_error()
+    assert lib.sft_leb128_encode(P, 4, 10, P, 50, P, None, 0, None) == _native.SFT_EWORKSPACE
+    assert lib.sft_leb128_encode(ctypes.c_void_p(0x1001), 2, 10, P, 30, P, ws, 1 << 20, None) == -1
