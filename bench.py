@@ -3,13 +3,15 @@
 
 One step = forward and backward of both perspectives through
 SparseLinearFunction (two applies sharing W and b, autograd summing the two
-dense weight grads), on inputs already resident in HBM.  Prints one JSON line:
+dense weight grads), on inputs already resident in HBM, timed as replays of
+the step captured in a HIP graph (--no-graph: launched eagerly; the per-kernel
+durations always come from an eager pass).  Prints one JSON line:
 positions/s, the roofline of the dominant kernel (algorithmic bytes per launch
 over its average HIP-event duration), and a CPU baseline (the PyTorch-CPU
 restatement timed on a bounded sample of the same workload).
 
   python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--workload 1]
-                  [--bwd sorted|atomic] [--cpu-seconds 12] [--no-cpu]
+                  [--bwd sorted|atomic] [--cpu-seconds 12] [--no-cpu] [--no-graph]
   python bench.py --composed halfka|threats   (module surface, fused vs reference composition)
   python bench.py --transform halfka|threats  (FT + post-FT epilogue, fused vs reference ops)
   python bench.py --optimizer                 (fused Ranger22 update of the FT parameters)
@@ -260,6 +262,7 @@ def bench_composed(args, dev) -> int:
                    "output_size": L, "parallelism": "single-gpu"},
         "reference_composition": {"ms_per_step": ref_ms, "value": B / (ref_ms * 1e-3)},
         "speedup_vs_reference_composition": ref_ms / ms,
+        "eager_ms_per_step": eager_ms,
         "step_bytes": step_bytes,
         "step_gbs": step_bytes / (ms * 1e-3) / 1e9,
         "roofline": {"kernel": dom, "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -601,6 +604,8 @@ def main() -> int:
     ap.add_argument("--bwd", choices=["sorted", "atomic"], default="sorted")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--graph", action=argparse.BooleanOptionalAction, default=True,
+                    help="time the step as a captured HIP graph (default) or eagerly (--no-graph)")
     ap.add_argument("--composed", choices=sorted(COMPOSED), default=None,
                     help="time ComposedFeatureTransformer (fused vs reference composition) instead")
     ap.add_argument("--transform", choices=sorted(COMPOSED), default=None,
@@ -669,6 +674,7 @@ def main() -> int:
         step()
     torch.cuda.synchronize()
 
+    # Per-kernel durations: an eager pass with the library's launch events.
     _native.prof_enable(True)
     torch.cuda.synchronize()
     e0 = torch.cuda.Event(enable_timing=True)
@@ -680,10 +686,36 @@ def main() -> int:
     e1.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    ms = e0.elapsed_time(e1) / args.steps
+    eager_ms = e0.elapsed_time(e1) / args.steps
     prof = _native.prof_collect()
     _native.prof_enable(False)
-    log(f"[bench] timed {args.steps} steps: {ms:.3f} ms/step (wall {wall * 1e3 / args.steps:.3f} ms/step)")
+    log(f"[bench] eager {args.steps} steps: {eager_ms:.3f} ms/step (wall {wall * 1e3 / args.steps:.3f} ms/step)")
+    ms = eager_ms
+    if args.graph:
+        # The whole step (both forwards, autograd backward, the grad sum) as one
+        # HIP graph: the library makes no host synchronisation inside its calls.
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(2):
+                step()
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            step()
+        for _ in range(args.warmup):
+            graph.replay()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        e0.record()
+        for _ in range(args.steps):
+            graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        ms = e0.elapsed_time(e1) / args.steps
+        log(f"[bench] graph {args.steps} replays: {ms:.3f} ms/step (wall {wall * 1e3 / args.steps:.3f} ms/step)")
 
     step_bytes = workloads.step_bytes(d["idx_w"], d["idx_b"], w.N, w.L)
     kern = {}
@@ -718,6 +750,7 @@ def main() -> int:
         "config": {
             "workload": w.name, "feature_set": w.feature_set, "batch": w.B, "num_inputs": w.N,
             "max_active": w.K, "active": [w.lo, w.hi], "output_size": w.L, "bwd": args.bwd,
+            "launch": "hip_graph" if args.graph else "eager",
             "parallelism": "single-gpu",
             "input_sha256": {k: workloads.sha256(v) for k, v in d.items()},
         },
