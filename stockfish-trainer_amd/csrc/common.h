@@ -146,25 +146,38 @@ __device__ __forceinline__ void compact_rows(const int32_t *__restrict__ idx, in
 // MI355X runs a dispatch's workgroups round-robin over its 8 XCDs (workgroup i
 // on XCD i % 8), and each XCD has its own 4 MB L2.  Tiled kernels give every
 // XCD whole column tiles: workgroup i serves the (i / 8)-th item of XCD i % 8,
-// where XCD x owns tiles x, x + 8, ... (all chunks of one tile, then the next)
-// and the tiles left over after the last full round of 8 are split by chunks
-// across all XCDs.  Any other placement only costs locality, never results.
+// where XCD x owns tiles x, x + 8, ... (all chunks of one tile, then the next).
+// The rem = ntiles % 8 tiles left after the last full round each go to a
+// group of 8 / rem (rounded down or up) XCDs -- XCD x to leftover tile
+// x * rem / 8 -- whose members take its chunks in turn, so an XCD still reads
+// one tile.  Any other placement only costs locality, never results.
 constexpr int kXcds = 8;
+#ifndef SFT_MIN_TILES
+#define SFT_MIN_TILES 8
+#endif
+constexpr int kMinTiles = SFT_MIN_TILES;  // fewest column tiles for which the tiled kernels are used
 struct TileItem {
   int tile, chunk;
 };
 __host__ __device__ inline int64_t tile_sched_items_per_xcd(int ntiles, int nchunks) {
   const int full = ntiles / kXcds, rem = ntiles % kXcds;
-  return (int64_t)full * nchunks + ((int64_t)rem * nchunks + kXcds - 1) / kXcds;
+  if (rem == 0) return (int64_t)full * nchunks;
+  const int gmin = kXcds / rem;  // smallest group
+  return (int64_t)full * nchunks + ((int64_t)nchunks + gmin - 1) / gmin;
 }
 __device__ __forceinline__ TileItem tile_sched_item(int64_t bid, int ntiles, int nchunks) {
   const int xcd = (int)(bid % kXcds);
   const int64_t j = bid / kXcds;
-  const int full = ntiles / kXcds;
+  const int full = ntiles / kXcds, rem = ntiles % kXcds;
   const int64_t fj = (int64_t)full * nchunks;
   if (j < fj) return TileItem{xcd + kXcds * (int)(j / nchunks), (int)(j % nchunks)};
-  const int64_t g = (j - fj) * kXcds + xcd;
-  return TileItem{kXcds * full + (int)(g / nchunks), (int)(g % nchunks)};  // tile >= ntiles: no work
+  if (rem == 0) return TileItem{ntiles, 0};  // no work
+  const int t = xcd * rem / kXcds;                              // leftover tile of this XCD's group
+  const int x0 = (t * kXcds + rem - 1) / rem;                   // first XCD of the group
+  const int gs = ((t + 1) * kXcds + rem - 1) / rem - x0;        // group size
+  const int64_t c = (xcd - x0) + (j - fj) * gs;
+  if (c >= nchunks) return TileItem{ntiles, 0};  // no work
+  return TileItem{kXcds * full + t, (int)c};
 }
 
 // ---- composed tables ----

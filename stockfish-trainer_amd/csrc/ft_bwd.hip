@@ -614,7 +614,7 @@ int bias_parts(int64_t B) {
 
 bool tiled_shape(int L, uint32_t flags) {
   return !(flags & (SFT_BWD_ATOMIC | SFT_BWD_ROWS)) && (flags & SFT_BWD_OVERWRITE) && L % 4 == 0 &&
-         L >= 32 * kXcds;
+         ceil_div(L, 32) >= kMinTiles;
 }
 
 // Position chunks of the tiled gather (one launch each).

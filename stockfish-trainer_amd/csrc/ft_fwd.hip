@@ -572,7 +572,7 @@ size_t fwd_tiled_workspace(int64_t N, int L) {
 #define SFT_FWD_TILE_MAX_BYTES (64ll << 20)
 #endif
 bool fwd_tiled_supported(int64_t N, int L, const void *W, const void *bias, const void *out) {
-  return L % 4 == 0 && L >= kTileF * kXcds && N * kTileF * 4 <= (int64_t)(SFT_FWD_TILE_MAX_BYTES) &&
+  return L % 4 == 0 && ceil_div(L, kTileF) >= kMinTiles && N * kTileF * 4 <= (int64_t)(SFT_FWD_TILE_MAX_BYTES) &&
          (uintptr_t)W % 16 == 0 && (uintptr_t)bias % 16 == 0 && (uintptr_t)out % 16 == 0;
 }
 
@@ -682,7 +682,7 @@ size_t fwd_i16_tiled_workspace(int64_t N, int L) {
 }
 
 bool fwd_i16_tiled_supported(int64_t N, int L, int P, const void *W, const void *bias, const void *out) {
-  return L % 8 == 0 && ceil_div(L / 8, kTileCh) >= kXcds && N * 128 <= (int64_t)(SFT_FWD_TILE_MAX_BYTES) && P <= 8 &&
+  return L % 8 == 0 && ceil_div(L / 8, kTileCh) >= kMinTiles && N * 128 <= (int64_t)(SFT_FWD_TILE_MAX_BYTES) && P <= 8 &&
          (uintptr_t)W % 16 == 0 && (uintptr_t)bias % 16 == 0 && (uintptr_t)out % 16 == 0;
 }
 
