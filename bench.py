@@ -59,8 +59,6 @@ def kernel_step_bytes(kind: str, w, idx_pair) -> float | None:
         return float(sum(wl.fwd_kernel_bytes(i, w.N, w.L) for i in idx_pair))
     if kind == "fwd_tile_relayout":
         return 2 * 2 * 4.0 * w.N * w.L
-    if kind == "bwd_grad_relayout":
-        return 2 * 2 * 4.0 * w.B * w.L
     if kind == "bwd_bias_partial":
         return 2 * 4.0 * w.B * w.L
     if kind == "fwd_fold_relayout":  # one launch per step: table (+ virtual rows) read, tiles written

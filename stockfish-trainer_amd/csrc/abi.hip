@@ -131,12 +131,13 @@ struct ActiveScope {
   hipStream_t stream;
 };
 
-const char *const kKindNames[kProfNumKinds] = {
+const char *const kKindNames[] = {
     "fwd_f32_gather",   "bwd_feature_sort",  "bwd_segment_offsets", "bwd_feature_gather", "bwd_bias_partial",
     "bwd_bias_final",   "bwd_atomic_scatter", "bwd_zero_fill",      "fwd_i16_gather",     "quantize_i16",
-    "fwd_tile_relayout", "fwd_f32_tiled_gather", "bwd_tiled_gather", "bwd_grad_relayout", "fwd_i16_tiled_gather",
+    "fwd_tile_relayout", "fwd_f32_tiled_gather", "bwd_tiled_gather", "fwd_i16_tiled_gather",
     "fwd_fold_relayout", "bwd_virtual_reduce", "bwd_epilogue", "ranger22_update", "encode_features", "leb128_encode",
 };
+static_assert(sizeof(kKindNames) / sizeof(kKindNames[0]) == kProfNumKinds, "one name per profiling kind");
 }  // namespace
 
 ProfScope::ProfScope(int kind, hipStream_t stream) : slot_(nullptr) {

@@ -43,7 +43,6 @@ enum ProfKind : int {
   kProfFwdRelayout,
   kProfFwdTiled,
   kProfBwdTiled,
-  kProfBwdRelayout,
   kProfFwdI16Tiled,
   kProfFwdFold,
   kProfBwdVirtual,
