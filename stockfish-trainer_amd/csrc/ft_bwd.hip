@@ -177,6 +177,9 @@ __global__ __launch_bounds__(kBlock) void gather_rows_kernel(const int32_t *__re
 constexpr int kBwdTileCh = 8;  // float4 chunks per 32-column tile row
 constexpr int kBwdFeatPerBlock = kWavesPerBlock * (kWave / kBwdTileCh);  // 32
 
+#ifndef SFT_BWD_BALANCE
+#define SFT_BWD_BALANCE 1
+#endif
 #ifndef SFT_BWD_POS_LDS
 #define SFT_BWD_POS_LDS 4096
 #endif
@@ -250,16 +253,36 @@ __global__ __launch_bounds__(kBlock) void bwd_tiled_gather_kernel(const int32_t 
                                                                   ColMap map, RowDst dst, f32x4 *__restrict__ tmp,
                                                                   int src_mode, int dst_mode, int ntiles, int ngroups) {
   __shared__ int spos[kBwdPosLds];
+  __shared__ int s_len[kBwdFeatPerBlock], s_perm[kBwdFeatPerBlock];
   const TileItem it = tile_sched_item(blockIdx.x, ntiles, ngroups);
   if (it.tile >= ntiles) return;  // whole block: uniform
   const int64_t fb = (int64_t)it.chunk * kBwdFeatPerBlock;
   const int64_t fe = fb + kBwdFeatPerBlock < N ? fb + kBwdFeatPerBlock : N;
   const int r0 = seg[fb], r1 = seg[fe];
   const bool staged = (r1 - r0) <= kBwdPosLds;  // block-uniform
-  if (staged) {
-    for (int i = threadIdx.x; i < r1 - r0; i += kBlock) spos[i] = sorted_pos[r0 + i];
-    __syncthreads();
+#if SFT_BWD_BALANCE
+  if (threadIdx.x < kBwdFeatPerBlock) {
+    const int64_t fi = fb + threadIdx.x;
+    s_len[threadIdx.x] = fi < N ? seg[fi + 1] - seg[fi] : 0;
   }
+#endif
+  if (staged)
+    for (int i = threadIdx.x; i < r1 - r0; i += kBlock) spos[i] = sorted_pos[r0 + i];
+  __syncthreads();
+#if SFT_BWD_BALANCE
+  // A wave runs as long as its longest segment: rank the block's features by
+  // segment length (ties by index) and give each wave 8 consecutive ranks.
+  if (threadIdx.x < kBwdFeatPerBlock) {
+    const int me = s_len[threadIdx.x];
+    int rank = 0;
+    for (int j = 0; j < kBwdFeatPerBlock; ++j) {
+      const int o = s_len[j];
+      rank += (o > me || (o == me && j < (int)threadIdx.x)) ? 1 : 0;
+    }
+    s_perm[rank] = threadIdx.x;
+  }
+  __syncthreads();
+#endif
   const int wave = uniform(threadIdx.x / kWave);
   const int lane = threadIdx.x % kWave;
   const int g = lane / kBwdTileCh, t = lane % kBwdTileCh;
@@ -267,7 +290,11 @@ __global__ __launch_bounds__(kBlock) void bwd_tiled_gather_kernel(const int32_t 
   const bool colok = colm >= 0;
   const int64_t col4 = colm;
   const int64_t cols4 = map.cols4;
+#if SFT_BWD_BALANCE
+  const int64_t f = fb + s_perm[wave * (kWave / kBwdTileCh) + g];
+#else
   const int64_t f = fb + wave * (kWave / kBwdTileCh) + g;
+#endif
   int s0 = 0, s1 = 0;
   if (f < N) {
     s0 = seg[f];
