@@ -211,11 +211,12 @@ struct ColMap {
   int half4;  // chunks per half (0: plain map)
   int t1;     // paired tiles
   int cols4;  // chunks per row
+  int tch;    // plain map: chunks per tile row (8: 32 columns, 4: 16 columns)
 };
 __host__ __device__ inline int tile_col(const ColMap &m, int t, int q) {
   if (m.half4 == 0) {
-    const int c = 8 * t + q;
-    return c < m.cols4 ? c : -1;
+    const int c = m.tch * t + q;
+    return (q < m.tch && c < m.cols4) ? c : -1;
   }
   if (t < m.t1) {
     const int j = 4 * t + (q & 3);
@@ -227,8 +228,8 @@ __host__ __device__ inline int tile_col(const ColMap &m, int t, int q) {
 // Inverse: tile and lane of chunk c.
 __host__ __device__ inline void tile_of_col(const ColMap &m, int c, int &t, int &q) {
   if (m.half4 == 0) {
-    t = c >> 3;
-    q = c & 7;
+    t = c / m.tch;
+    q = c % m.tch;
   } else if (c < 2 * m.half4) {
     const int h = c >= m.half4 ? 1 : 0;
     const int j = c - h * m.half4;
@@ -240,12 +241,12 @@ __host__ __device__ inline void tile_of_col(const ColMap &m, int c, int &t, int 
     q = k & 7;
   }
 }
-inline ColMap plain_map(int cols4) { return ColMap{0, 0, cols4}; }
+inline ColMap plain_map(int cols4, int tch = 8) { return ColMap{0, 0, cols4, tch}; }
 inline ColMap paired_map(int cols4, int half4) {
-  return ColMap{half4, (half4 + 3) / 4, cols4};
+  return ColMap{half4, (half4 + 3) / 4, cols4, 8};
 }
 __host__ __device__ inline int map_tiles(const ColMap &m) {
-  return m.half4 == 0 ? (m.cols4 + 7) / 8 : m.t1 + (m.cols4 - 2 * m.half4 + 7) / 8;
+  return m.half4 == 0 ? (m.cols4 + m.tch - 1) / m.tch : m.t1 + (m.cols4 - 2 * m.half4 + 7) / 8;
 }
 
 // a[s] for a run-time s without indexing the kernel-argument array (selects).

@@ -171,11 +171,15 @@ __global__ __launch_bounds__(kBlock) void gather_rows_kernel(const int32_t *__re
 #ifndef SFT_BWD_NT_STORE
 #define SFT_BWD_NT_STORE 0
 #endif
-#ifndef SFT_BWD_TILED_U
-#define SFT_BWD_TILED_U 8
-#endif
 constexpr int kBwdTileCh = 8;  // float4 chunks per 32-column tile row
-constexpr int kBwdFeatPerBlock = kWavesPerBlock * (kWave / kBwdTileCh);  // 32
+// Grad tile width of the plain (single-perspective) tiled backward, in 16-byte chunks.
+#ifndef SFT_BWD_TCH
+#define SFT_BWD_TCH 8
+#endif
+template <int TCH>
+constexpr int bwd_feat_per_block() {
+  return kWavesPerBlock * (kWave / TCH);
+}
 
 #ifndef SFT_BWD_BALANCE
 #define SFT_BWD_BALANCE 1
@@ -185,12 +189,13 @@ constexpr int kBwdFeatPerBlock = kWavesPerBlock * (kWave / kBwdTileCh);  // 32
 #endif
 constexpr int kBwdPosLds = SFT_BWD_POS_LDS;  // staged positions per workgroup
 
-// Sums one lane group's positions from `list` (LDS or global) into acc.
-template <bool FROM_LDS>
+// Sums one lane group's positions from `list` (LDS or global) into acc.  A
+// lane group has TCH lanes (one 16-byte chunk of the tile row each) and keeps
+// TCH row loads in flight.
+template <bool FROM_LDS, int TCH>
 __device__ __forceinline__ void bwd_tile_sum(const int32_t *list, int n, int nmin, int nmax, int t, bool colok,
                                              const f32x4 *__restrict__ gcol, f32x4 &acc) {
-  constexpr int U = SFT_BWD_TILED_U;
-  static_assert(U == kBwdTileCh, "one position per lane of the group");
+  constexpr int U = TCH;  // one position per lane of the group when read from global memory
   int k = 0;
   for (; k + U <= nmin; k += U) {
     int b[U];
@@ -200,11 +205,11 @@ __device__ __forceinline__ void bwd_tile_sum(const int32_t *list, int n, int nmi
     } else {
       const int mine = list[k + t];
 #pragma unroll
-      for (int u = 0; u < U; ++u) b[u] = __shfl(mine, u, kBwdTileCh);
+      for (int u = 0; u < U; ++u) b[u] = __shfl(mine, u, TCH);
     }
     f32x4 w[U];
 #pragma unroll
-    for (int u = 0; u < U; ++u) w[u] = colok ? gcol[(int64_t)b[u] * kBwdTileCh] : f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int u = 0; u < U; ++u) w[u] = colok ? gcol[(int64_t)b[u] * TCH] : f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int u = 0; u < U; ++u) acc += w[u];
   }
@@ -216,13 +221,13 @@ __device__ __forceinline__ void bwd_tile_sum(const int32_t *list, int n, int nmi
     } else {
       const int mine = (k + t < n) ? list[k + t] : 0;
 #pragma unroll
-      for (int u = 0; u < U; ++u) b[u] = __shfl(mine, u, kBwdTileCh);
+      for (int u = 0; u < U; ++u) b[u] = __shfl(mine, u, TCH);
     }
     f32x4 w[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       w[u] = f32x4{0.f, 0.f, 0.f, 0.f};
-      if (k + u < n && colok) w[u] = gcol[(int64_t)b[u] * kBwdTileCh];
+      if (k + u < n && colok) w[u] = gcol[(int64_t)b[u] * TCH];
     }
 #pragma unroll
     for (int u = 0; u < U; ++u)
@@ -247,21 +252,23 @@ __device__ __forceinline__ void bwd_tile_sum(const int32_t *list, int n, int nmi
 // table (FEAT/composed.py:52-53).  dst rows are split into blocks (RowDst).
 enum { kSrcZero = 0, kSrcDst = 1, kSrcTmp = 2 };
 enum { kDstOut = 0, kDstTmp = 1, kDstOutPlus = 2 };
+template <int TCH>
 __global__ __launch_bounds__(kBlock) void bwd_tiled_gather_kernel(const int32_t *__restrict__ seg,
                                                                   const int32_t *__restrict__ sorted_pos, int64_t N,
                                                                   const f32x4 *__restrict__ gt, int64_t B,
                                                                   ColMap map, RowDst dst, f32x4 *__restrict__ tmp,
                                                                   int src_mode, int dst_mode, int ntiles, int ngroups) {
   __shared__ int spos[kBwdPosLds];
-  __shared__ int s_len[kBwdFeatPerBlock], s_perm[kBwdFeatPerBlock];
+  constexpr int FPB = bwd_feat_per_block<TCH>();
+  __shared__ int s_len[FPB], s_perm[FPB];
   const TileItem it = tile_sched_item(blockIdx.x, ntiles, ngroups);
   if (it.tile >= ntiles) return;  // whole block: uniform
-  const int64_t fb = (int64_t)it.chunk * kBwdFeatPerBlock;
-  const int64_t fe = fb + kBwdFeatPerBlock < N ? fb + kBwdFeatPerBlock : N;
+  const int64_t fb = (int64_t)it.chunk * FPB;
+  const int64_t fe = fb + FPB < N ? fb + FPB : N;
   const int r0 = seg[fb], r1 = seg[fe];
   const bool staged = (r1 - r0) <= kBwdPosLds;  // block-uniform
 #if SFT_BWD_BALANCE
-  if (threadIdx.x < kBwdFeatPerBlock) {
+  if (threadIdx.x < FPB) {
     const int64_t fi = fb + threadIdx.x;
     s_len[threadIdx.x] = fi < N ? seg[fi + 1] - seg[fi] : 0;
   }
@@ -272,10 +279,10 @@ __global__ __launch_bounds__(kBlock) void bwd_tiled_gather_kernel(const int32_t 
 #if SFT_BWD_BALANCE
   // A wave runs as long as its longest segment: rank the block's features by
   // segment length (ties by index) and give each wave 8 consecutive ranks.
-  if (threadIdx.x < kBwdFeatPerBlock) {
+  if (threadIdx.x < FPB) {
     const int me = s_len[threadIdx.x];
     int rank = 0;
-    for (int j = 0; j < kBwdFeatPerBlock; ++j) {
+    for (int j = 0; j < FPB; ++j) {
       const int o = s_len[j];
       rank += (o > me || (o == me && j < (int)threadIdx.x)) ? 1 : 0;
     }
@@ -285,15 +292,15 @@ __global__ __launch_bounds__(kBlock) void bwd_tiled_gather_kernel(const int32_t 
 #endif
   const int wave = uniform(threadIdx.x / kWave);
   const int lane = threadIdx.x % kWave;
-  const int g = lane / kBwdTileCh, t = lane % kBwdTileCh;
+  const int g = lane / TCH, t = lane % TCH;
   const int colm = tile_col(map, it.tile, t);
   const bool colok = colm >= 0;
   const int64_t col4 = colm;
   const int64_t cols4 = map.cols4;
 #if SFT_BWD_BALANCE
-  const int64_t f = fb + s_perm[wave * (kWave / kBwdTileCh) + g];
+  const int64_t f = fb + s_perm[wave * (kWave / TCH) + g];
 #else
-  const int64_t f = fb + wave * (kWave / kBwdTileCh) + g;
+  const int64_t f = fb + wave * (kWave / TCH) + g;
 #endif
   int s0 = 0, s1 = 0;
   if (f < N) {
@@ -305,8 +312,8 @@ __global__ __launch_bounds__(kBlock) void bwd_tiled_gather_kernel(const int32_t 
   const bool skip_untouched = src_mode == kSrcDst && dst_mode == kDstOut;
   if (skip_untouched && !wave_has_work) return;  // nothing to change anywhere in the wave
   int nmin, nmax;
-  group_minmax<kBwdTileCh>(n, nmin, nmax);
-  const f32x4 *gcol = gt + (int64_t)it.tile * B * kBwdTileCh + t;
+  group_minmax<TCH>(n, nmin, nmax);
+  const f32x4 *gcol = gt + (int64_t)it.tile * B * TCH + t;
   const int blk = block_of(f, dst.n, dst.start);
   f32x4 *d = pick(dst.p, blk) + (f - pick(dst.start, blk)) * cols4 + col4;
   f32x4 *tp = tmp + f * cols4 + col4;
@@ -317,9 +324,9 @@ __global__ __launch_bounds__(kBlock) void bwd_tiled_gather_kernel(const int32_t 
     else if (src_mode == kSrcTmp) acc = *tp;
   }
   if (staged)
-    bwd_tile_sum<true>(spos + (s0 - r0), n, nmin, nmax, t, colok, gcol, acc);
+    bwd_tile_sum<true, TCH>(spos + (s0 - r0), n, nmin, nmax, t, colok, gcol, acc);
   else
-    bwd_tile_sum<false>(sorted_pos + s0, n, nmin, nmax, t, colok, gcol, acc);
+    bwd_tile_sum<false, TCH>(sorted_pos + s0, n, nmin, nmax, t, colok, gcol, acc);
   if (!mine) return;
   if (dst_mode == kDstTmp) {
     *tp = acc;
@@ -518,12 +525,13 @@ __global__ __launch_bounds__(kBlock) void zero_kernel(float *__restrict__ p, int
 // are combined in a fixed order.  Deterministic.
 //
 // When gt is not null (T = f32x4 only), each grad chunk read is also stored to
-// the column-tile layout of the tiled gather: gt[(c / 8) * B + r][c % 8], so the
-// grad crosses HBM once for both the bias sum and the re-layout.
+// the column-tile layout of the tiled gather, tiles of 2^gt_shift chunks:
+// gt[(c >> gt_shift) * B + r][c mod 2^gt_shift], so the grad crosses HBM once
+// for both the bias sum and the re-layout.
 template <typename T, int CPL>
 __global__ __launch_bounds__(kBlock) void bias_partial_kernel(const T *__restrict__ grad, int64_t B, int64_t cols,
                                                               int64_t rows_per_block, T *__restrict__ partial,
-                                                              T *__restrict__ gt) {
+                                                              T *__restrict__ gt, int gt_shift) {
   constexpr int U = 4;
   __shared__ T red[kWavesPerBlock][kWave * CPL];
   const int wave = uniform(threadIdx.x / kWave);
@@ -557,7 +565,7 @@ __global__ __launch_bounds__(kBlock) void bias_partial_kernel(const T *__restric
 #pragma unroll
         for (int j = 0; j < CPL; ++j) {
           const int64_t c = c0 + kWave * j;
-          if (rr < r1 && colok[j]) gt[((c >> 3) * B + rr) * 8 + (c & 7)] = v[u][j];
+          if (rr < r1 && colok[j]) gt[(((c >> gt_shift) * B + rr) << gt_shift) + (c & ((1 << gt_shift) - 1))] = v[u][j];
         }
       }
     }
@@ -672,8 +680,8 @@ int make_layout(int64_t B, int K, int64_t N, int L, uint32_t flags, BwdLayout &l
     off = align256(off + (size_t)(nc * N + 1) * sizeof(int32_t));
     lay.gt = off;
     if (nc > 1) {
-      const int64_t ntiles = ceil_div(L, 32);
-      off = align256(off + (size_t)(ntiles * B * 32) * sizeof(float));
+      const int64_t ntiles = ceil_div(L / 4, SFT_BWD_TCH);
+      off = align256(off + (size_t)(ntiles * B * SFT_BWD_TCH) * 16);
     }
   }
   lay.total = off;
@@ -681,7 +689,8 @@ int make_layout(int64_t B, int K, int64_t N, int L, uint32_t flags, BwdLayout &l
 }
 
 int launch_bias_partial(const float *grad, int64_t B, int L, int nparts, float *partial, f32x4 *gt, bool vec,
-                        hipStream_t s) {
+                        hipStream_t s, int gt_tch = 8) {
+  const int gt_shift = gt_tch == 4 ? 2 : gt_tch == 16 ? 4 : 3;
   const int64_t cols = vec ? L / 4 : L;
   const int64_t rows = ceil_div(std::max<int64_t>(B, 1), nparts);
   const int cpl = (int)std::min<int64_t>(ceil_div(cols, kWave), kMaxCpl);
@@ -689,7 +698,7 @@ int launch_bias_partial(const float *grad, int64_t B, int L, int nparts, float *
   ProfScope prof(kProfBwdBiasPartial, s);
 #define SFT_BIAS_CASE(T, C)                                                                                  \
   hipLaunchKernelGGL((bias_partial_kernel<T, C>), pgrid, dim3(kBlock), 0, s, reinterpret_cast<const T *>(grad), \
-                     B, cols, rows, reinterpret_cast<T *>(partial), reinterpret_cast<T *>(gt))
+                     B, cols, rows, reinterpret_cast<T *>(partial), reinterpret_cast<T *>(gt), gt_shift)
 #define SFT_BIAS_SWITCH(T)               \
   switch (cpl) {                         \
     case 1: SFT_BIAS_CASE(T, 1); break;  \
@@ -754,8 +763,8 @@ int bwd_f32(const int32_t *idx, int64_t B, int K, const float *grad, int64_t N, 
   // ---- bias grad ----
   {
     const bool vec = (L % 4 == 0) && ((uintptr_t)grad % 16 == 0) && ((uintptr_t)db % 16 == 0);
-    if ((rc = launch_bias_partial(grad, B, L, lay.nparts, reinterpret_cast<float *>(w + lay.partial), gt, vec, s)) !=
-        SFT_OK)
+    if ((rc = launch_bias_partial(grad, B, L, lay.nparts, reinterpret_cast<float *>(w + lay.partial), gt, vec, s,
+                                  SFT_BWD_TCH)) != SFT_OK)
       return rc;
     if ((rc = launch_bias_final(reinterpret_cast<const float *>(w + lay.partial), lay.nparts, L, db, overwrite, vec,
                                 s)) != SFT_OK)
@@ -820,9 +829,11 @@ int bwd_f32(const int32_t *idx, int64_t B, int K, const float *grad, int64_t N, 
     if ((rc = check_launch("segment offsets")) != SFT_OK) return rc;
   }
   if (tiled) {
+    constexpr int TCH = SFT_BWD_TCH;
     const int64_t cols4 = L / 4;
-    const int ntiles = (int)ceil_div(cols4, kBwdTileCh);
-    const int ngroups = (int)ceil_div(N, kBwdFeatPerBlock);
+    const ColMap map = plain_map((int)cols4, TCH);
+    const int ntiles = map_tiles(map);
+    const int ngroups = (int)ceil_div(N, bwd_feat_per_block<TCH>());
     const int64_t blocks = tile_sched_items_per_xcd(ntiles, ngroups) * kXcds;
     RowDst dst{};
     dst.n = 1;
@@ -830,9 +841,9 @@ int bwd_f32(const int32_t *idx, int64_t B, int K, const float *grad, int64_t N, 
     dst.p[0] = reinterpret_cast<f32x4 *>(dW);
     for (int h = 0; h < nc; ++h) {
       ProfScope prof(kProfBwdTiled, s);
-      hipLaunchKernelGGL(bwd_tiled_gather_kernel, dim3((unsigned)blocks), dim3(kBlock), 0, s, seg + (int64_t)h * N,
-                         pos, N, gt, B, plain_map((int)cols4), dst, (f32x4 *)nullptr, h == 0 ? kSrcZero : kSrcDst,
-                         kDstOut, ntiles, ngroups);
+      hipLaunchKernelGGL(bwd_tiled_gather_kernel<TCH>, dim3((unsigned)blocks), dim3(kBlock), 0, s,
+                         seg + (int64_t)h * N, pos, N, gt, B, map, dst, (f32x4 *)nullptr,
+                         h == 0 ? kSrcZero : kSrcDst, kDstOut, ntiles, ngroups);
       if ((rc = check_launch("tiled feature gather")) != SFT_OK) return rc;
     }
     return SFT_OK;
@@ -894,7 +905,7 @@ static int pair_gather_perspective(int p, const int32_t *idx, int64_t B, int K, 
                                    int32_t *seg, hipStream_t s) {
   const int64_t M = B * K;
   const int ntiles = map_tiles(map);
-  const int ngroups = (int)ceil_div(N, kBwdFeatPerBlock);
+  const int ngroups = (int)ceil_div(N, bwd_feat_per_block<kBwdTileCh>());
   const int64_t blocks = tile_sched_items_per_xcd(ntiles, ngroups) * kXcds;
   const int chunk_rows = (int)(nc > 1 ? half_rows(B) : B);
   unsigned *keys = nullptr, *totals = nullptr;
@@ -920,8 +931,8 @@ static int pair_gather_perspective(int p, const int32_t *idx, int64_t B, int K, 
       dst_mode = h == nc - 1 ? kDstOutPlus : kDstTmp;
     }
     ProfScope prof(kProfBwdTiled, s);
-    hipLaunchKernelGGL(bwd_tiled_gather_kernel, dim3((unsigned)blocks), dim3(kBlock), 0, s, seg + (int64_t)h * N, pos,
-                       N, gt, B, map, dst, tmp, src_mode, dst_mode, ntiles, ngroups);
+    hipLaunchKernelGGL(bwd_tiled_gather_kernel<kBwdTileCh>, dim3((unsigned)blocks), dim3(kBlock), 0, s,
+                       seg + (int64_t)h * N, pos, N, gt, B, map, dst, tmp, src_mode, dst_mode, ntiles, ngroups);
     if ((rc = check_launch("tiled feature gather")) != SFT_OK) return rc;
   }
   return SFT_OK;

@@ -15,7 +15,8 @@ import threading
 import torch
 
 PKG_ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-LIB_PATH = os.path.join(PKG_ROOT, "lib", "libsft_ft.so")
+# SFT_LIB selects another build of the library (e.g. one compiled with other tuning constants).
+LIB_PATH = os.environ.get("SFT_LIB") or os.path.join(PKG_ROOT, "lib", "libsft_ft.so")
 
 SFT_OK = 0
 SFT_EWORKSPACE = -2
