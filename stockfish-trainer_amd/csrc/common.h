@@ -94,13 +94,23 @@ __device__ __forceinline__ uint64_t ballot(bool p) { return __builtin_amdgcn_bal
 
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
+// Orders a wave's LDS writes before its later LDS reads by other lanes of the
+// same wave (LDS operations of one wave complete in order; this keeps the
+// compiler from moving them across).
+__device__ __forceinline__ void wave_lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+}
+
+constexpr int kCompactRows = 8;  // most rows one compact_rows call takes
 // Compacts the active slots of `npos` consecutive index rows (row p at
 // idx + (pos0 + p) * K) into list[p * kpad + 0 .. count[p]), keeping slot order.
-// Called by one whole wave; rows at or past B get count 0.  A slot is active
+// Called by one whole wave with npos <= kCompactRows; rows at or past B get count 0.  A slot is active
 // when 0 <= v < N.  For K <= 64 one ballot covers 64 / Kp rows (Kp = K rounded
 // up to a power of two): lane l reads slot l % Kp of row l / Kp and ranks
 // itself among the active lanes of its own Kp-lane segment.  The wave owns
-// list/count; callers barrier before reading.
+// list/count; before other lanes of the wave read them it calls
+// wave_lds_barrier (the rows of one wave need no workgroup barrier).
 __device__ __forceinline__ void compact_rows(const int32_t *__restrict__ idx, int64_t B, int K, int N,
                                              int64_t pos0, int npos, int *list, int kpad, int *count) {
   const int lane = lane_id();
@@ -110,14 +120,23 @@ __device__ __forceinline__ void compact_rows(const int32_t *__restrict__ idx, in
     const int rows_per_ballot = kWave / kp;
     const int seg = lane / kp, slot = lane % kp;
     const uint64_t segmask = (kp == kWave) ? ~0ull : (((1ull << kp) - 1) << (seg * kp));
-    for (int p0 = 0; p0 < npos; p0 += rows_per_ballot) {
-      const int p = p0 + seg;
+    // All loads first (npos <= kCompactRows, so at most kCompactRows ballots),
+    // so that their latencies overlap instead of adding up.
+    int v[kCompactRows];
+#pragma unroll
+    for (int i = 0; i < kCompactRows; ++i) {
+      const int p = i * rows_per_ballot + seg;
       const int64_t pos = pos0 + p;
-      int v = -1;
-      if (p < npos && pos < B && slot < K) v = SFT_STREAM_LOAD(idx + pos * (int64_t)K + slot);
-      const bool ok = (unsigned)v < (unsigned)N;
+      v[i] = -1;
+      if (p < npos && pos < B && slot < K) v[i] = SFT_STREAM_LOAD(idx + pos * (int64_t)K + slot);
+    }
+#pragma unroll
+    for (int i = 0; i < kCompactRows; ++i) {
+      if (i * rows_per_ballot >= npos) break;  // wave-uniform
+      const int p = i * rows_per_ballot + seg;
+      const bool ok = (unsigned)v[i] < (unsigned)N;
       const uint64_t m = ballot(ok) & segmask;
-      if (ok) list[p * kpad + popc_below(m)] = v;
+      if (ok) list[p * kpad + popc_below(m)] = v[i];
       if (slot == 0 && p < npos) count[p] = __popcll(m);
     }
     return;

@@ -498,7 +498,7 @@ __global__ __launch_bounds__(kBlock) void scatter_atomic_kernel(const int32_t *_
   int *count = smem + kWavesPerBlock * kpad + wave;
   const int64_t pos = (int64_t)blockIdx.x * kWavesPerBlock + wave;
   compact_rows(idx, B, K, N, pos, 1, list, kpad, count);
-  __syncthreads();
+  wave_lds_barrier();
   if (pos >= B) return;
   const int n = uniform(count[0]);
   const int64_t c0 = (int64_t)blockIdx.y * (kWave * FPL) + lane;

@@ -51,6 +51,7 @@ __global__ __launch_bounds__(kBlock) void fwd_f32_kernel(const int32_t *__restri
                                                          const T *__restrict__ bias, T *__restrict__ out, int kpad) {
   static_assert(U == 4, "index reads are 4-wide");
   constexpr int PPW = kWave / G;
+  static_assert(PPW <= kCompactRows, "compact_rows takes at most kCompactRows rows");
   extern __shared__ int smem[];
   const int wave = uniform(threadIdx.x / kWave);
   const int lane = threadIdx.x % kWave;
@@ -58,7 +59,7 @@ __global__ __launch_bounds__(kBlock) void fwd_f32_kernel(const int32_t *__restri
   int *count = smem + kWavesPerBlock * PPW * kpad + wave * PPW;
   const int64_t pos0 = ((int64_t)blockIdx.x * kWavesPerBlock + wave) * PPW;
   compact_rows(idx, B, K, N, pos0, PPW, list, kpad, count);
-  __syncthreads();
+  wave_lds_barrier();
 
   const int g = lane / G, t = lane % G;
   const int64_t pos = pos0 + g;
@@ -163,6 +164,7 @@ __global__ __launch_bounds__(kBlock) void fwd_i16_kernel(const int32_t *__restri
   static_assert(U == 4, "index reads are 4-wide");
   typedef typename Q16<T>::Acc Acc;
   constexpr int PPW = kWave / G;
+  static_assert(PPW <= kCompactRows, "compact_rows takes at most kCompactRows rows");
   extern __shared__ int smem[];
   const int wave = uniform(threadIdx.x / kWave);
   const int lane = threadIdx.x % kWave;
@@ -170,7 +172,7 @@ __global__ __launch_bounds__(kBlock) void fwd_i16_kernel(const int32_t *__restri
   int *count = smem + kWavesPerBlock * PPW * kpad + wave * PPW;
   const int64_t pos0 = ((int64_t)blockIdx.x * kWavesPerBlock + wave) * PPW;
   compact_rows(idx, B, K, N, pos0, PPW, list, kpad, count);
-  __syncthreads();
+  wave_lds_barrier();
 
   const int g = lane / G, t = lane % G;
   const int64_t pos = pos0 + g;
@@ -281,6 +283,7 @@ __global__ __launch_bounds__(kBlock) void fwd_tiled_kernel(const int32_t *__rest
                                                            int ntiles, int nchunks, int nchunks_p) {
   constexpr int U = SFT_FWD_TILED_U;
   constexpr int PPW = kWave / kTileCh;  // 8 positions per wave per round
+  static_assert(PPW <= kCompactRows, "compact_rows takes at most kCompactRows rows");
   extern __shared__ int smem[];
   TileItem it = tile_sched_item(blockIdx.x, ntiles, nchunks);
   if (it.tile >= ntiles) return;  // whole block: uniform
@@ -302,7 +305,7 @@ __global__ __launch_bounds__(kBlock) void fwd_tiled_kernel(const int32_t *__rest
   for (int round = 0; round < kTiledRounds; ++round) {
     const int64_t pos0 = (int64_t)it.chunk * kTiledPosPerBlock + round * kTiledPosPerRound + wave * PPW;
     compact_rows(idx, B, K, N, pos0, PPW, list, kpad, count);
-    __syncthreads();
+    wave_lds_barrier();
     const int64_t pos = pos0 + g;
     const int n = count[g];
     int nmin, nmax;
@@ -354,7 +357,7 @@ __global__ __launch_bounds__(kBlock) void fwd_tiled_kernel(const int32_t *__rest
         }
       }
     }
-    __syncthreads();
+    wave_lds_barrier();
   }
 }
 
@@ -394,6 +397,7 @@ __global__ __launch_bounds__(kBlock) void fwd_i16_tiled_kernel(const int32_t *__
                                                                int ntiles, int nchunks) {
   constexpr int U = 4;
   constexpr int PPW = kWave / kTileCh;
+  static_assert(PPW <= kCompactRows, "compact_rows takes at most kCompactRows rows");
   extern __shared__ int smem[];
   const TileItem it = tile_sched_item(blockIdx.x, ntiles, nchunks);
   if (it.tile >= ntiles) return;
@@ -411,7 +415,7 @@ __global__ __launch_bounds__(kBlock) void fwd_i16_tiled_kernel(const int32_t *__
   for (int round = 0; round < kTiledRounds; ++round) {
     const int64_t pos0 = (int64_t)it.chunk * kTiledPosPerBlock + round * kTiledPosPerRound + wave * PPW;
     compact_rows(idx, B, K, N, pos0, PPW, list, kpad, count);
-    __syncthreads();
+    wave_lds_barrier();
     const int64_t pos = pos0 + g;
     const int n = count[g];
     int nmin, nmax;
@@ -442,7 +446,7 @@ __global__ __launch_bounds__(kBlock) void fwd_i16_tiled_kernel(const int32_t *__
       if (colok) __builtin_nontemporal_store(Q16<i16x8>::finish(acc, clip_lo, clip_hi, wrap16), out + pos * cols8 + col);
       if (do_psqt) psqt_out[pos * P + t] = pacc;
     }
-    __syncthreads();
+    wave_lds_barrier();
   }
 }
 
