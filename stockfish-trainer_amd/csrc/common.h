@@ -50,6 +50,7 @@ enum ProfKind : int {
   kProfOptim,
   kProfEncode,
   kProfLeb128,
+  kProfBwdLong,
   kProfNumKinds
 };
 struct ProfScope {

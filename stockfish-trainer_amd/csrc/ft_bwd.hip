@@ -30,13 +30,51 @@ namespace {
 constexpr int kBiasRowsPerBlock = 128;
 constexpr int kBiasMaxParts = 512;
 
+// ------------------------------------------------------- long segments ----
+// On real data a few features are active in a large share of the positions
+// (a quarter of them and more); one lane group summing such a segment would
+// run for the whole launch.  Long segments are summed by a whole workgroup
+// instead (bwd_long_kernel) and skipped by the gather kernels.  Whether
+// segment [s0, s1) of the sorted slots is long depends on its bounds alone,
+// so both sides agree without a list: it is long when it contains two
+// consecutive multiples of kLongSeg ("samples") of the sorted slot index.
+// Every segment of more than 2 kLongSeg slots is long, none of fewer than
+// kLongSeg + 2.  seg_offsets_kernel lists them (per position chunk) as it
+// finds them at their first sample m: keys[m + kLongSeg] == keys[m] !=
+// keys[m - kLongSeg].
+#ifndef SFT_BWD_LONG_SEG
+#define SFT_BWD_LONG_SEG 256
+#endif
+constexpr int kLongSeg = SFT_BWD_LONG_SEG;
+__host__ __device__ inline int64_t long_first_sample(int64_t s0) { return (s0 + kLongSeg - 1) / kLongSeg * kLongSeg; }
+__host__ __device__ inline bool long_segment(int64_t s0, int64_t s1) { return long_first_sample(s0) + kLongSeg < s1; }
+
+// Segment starts and the lists of long segments of one sort: seg[0 .. nc N]
+// (nc position chunks of nfeat features), then per chunk c a list of its long
+// features (list + c nfeat, count[c] entries; listed in no particular order).
+struct SegBufs {
+  int32_t *seg, *list;
+  int *count;
+};
+inline size_t seg_region_bytes(int nc, int64_t nfeat) {
+  return (size_t)(2 * nc * nfeat + 1 + nc) * sizeof(int32_t);
+}
+inline SegBufs seg_bufs(void *base, int nc, int64_t nfeat) {
+  int32_t *seg = static_cast<int32_t *>(base);
+  return SegBufs{seg, seg + nc * nfeat + 1, seg + 2 * nc * nfeat + 1};
+}
+
 // seg_start[k] for k in [0, N]: index of the first sorted key >= k, N = key
 // count.  The sorted array holds the active slots only; their number is the
 // sum of the sort's last digit totals (read here, on the device, once per
-// workgroup by one wave).  Grid-stride over the sorted slots.
+// workgroup by one wave).  Grid-stride over the sorted slots.  Long segments
+// are appended to their chunk's list (key = chunk * nfeat + feature; the
+// counts start at zero).
 __global__ __launch_bounds__(kBlock) void seg_offsets_kernel(const unsigned *__restrict__ keys, int64_t N,
                                                              const unsigned *__restrict__ totals, int ntot,
-                                                             int32_t *__restrict__ seg_start) {
+                                                             int32_t *__restrict__ seg_start, int64_t nfeat,
+                                                             int32_t *__restrict__ long_list,
+                                                             int *__restrict__ long_count) {
   __shared__ unsigned s_active;
   if (threadIdx.x < kWave) {
     unsigned v = 0;
@@ -52,6 +90,12 @@ __global__ __launch_bounds__(kBlock) void seg_offsets_kernel(const unsigned *__r
     const int64_t prev = i > 0 ? (int64_t)keys[i - 1] : -1;
     const int64_t hi = cur < N ? cur : N;
     for (int64_t f = prev + 1; f <= hi; ++f) seg_start[f] = (int32_t)i;
+    if (i % kLongSeg == 0 && i + kLongSeg < M && (int64_t)keys[i + kLongSeg] == cur &&
+        (i < kLongSeg || (int64_t)keys[i - kLongSeg] != cur)) {
+      const int64_t c = cur / nfeat;
+      const int at = atomicAdd(long_count + c, 1);
+      long_list[c * nfeat + at] = (int32_t)(cur - c * nfeat);
+    }
   }
 }
 
@@ -74,7 +118,7 @@ template <typename T, int G, int CPL, int U>
 __global__ __launch_bounds__(kBlock) void gather_rows_kernel(const int32_t *__restrict__ seg_start,
                                                              const int32_t *__restrict__ sorted_pos, int64_t N,
                                                              const T *__restrict__ grad, int64_t cols,
-                                                             T *__restrict__ dW, int overwrite) {
+                                                             T *__restrict__ dW, int overwrite, int skip_long) {
   constexpr int PPW = kWave / G;
   const int wave = uniform(threadIdx.x / kWave);
   const int lane = threadIdx.x % kWave;
@@ -90,7 +134,8 @@ __global__ __launch_bounds__(kBlock) void gather_rows_kernel(const int32_t *__re
     s0 = uniform(s0);
     s1 = uniform(s1);
   }
-  const int n = s1 - s0;
+  const bool is_long = skip_long && live && long_segment(s0, s1);  // summed by bwd_long_kernel
+  const int n = is_long ? 0 : s1 - s0;
   int nmin, nmax;
   group_minmax<G>(n, nmin, nmax);
 
@@ -145,7 +190,7 @@ __global__ __launch_bounds__(kBlock) void gather_rows_kernel(const int32_t *__re
     }
   }
 
-  if (live && (n > 0 || overwrite)) {
+  if (live && !is_long && (n > 0 || overwrite)) {
     T *d = dW + f * cols + c0;
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
@@ -180,6 +225,9 @@ template <int TCH>
 constexpr int bwd_feat_per_block() {
   return kWavesPerBlock * (kWave / TCH);
 }
+// Long segments go to bwd_long_kernel, which sums 32-column blocks.
+template <int TCH>
+constexpr bool kLongPath = TCH == 8;
 
 #ifndef SFT_BWD_BALANCE
 #define SFT_BWD_BALANCE 1
@@ -270,7 +318,8 @@ __global__ __launch_bounds__(kBlock) void bwd_tiled_gather_kernel(const int32_t 
 #if SFT_BWD_BALANCE
   if (threadIdx.x < FPB) {
     const int64_t fi = fb + threadIdx.x;
-    s_len[threadIdx.x] = fi < N ? seg[fi + 1] - seg[fi] : 0;
+    const int a = fi < N ? seg[fi] : 0, e = fi < N ? seg[fi + 1] : 0;
+    s_len[threadIdx.x] = (kLongPath<TCH> && long_segment(a, e)) ? 0 : e - a;
   }
 #endif
   if (staged)
@@ -307,7 +356,8 @@ __global__ __launch_bounds__(kBlock) void bwd_tiled_gather_kernel(const int32_t 
     s0 = seg[f];
     s1 = seg[f + 1];
   }
-  const int n = s1 - s0;
+  const bool is_long = kLongPath<TCH> && f < N && long_segment(s0, s1);  // summed by bwd_long_kernel
+  const int n = is_long ? 0 : s1 - s0;
   const bool wave_has_work = ballot(n > 0) != 0;  // wave-uniform
   const bool skip_untouched = src_mode == kSrcDst && dst_mode == kDstOut;
   if (skip_untouched && !wave_has_work) return;  // nothing to change anywhere in the wave
@@ -317,7 +367,7 @@ __global__ __launch_bounds__(kBlock) void bwd_tiled_gather_kernel(const int32_t 
   const int blk = block_of(f, dst.n, dst.start);
   f32x4 *d = pick(dst.p, blk) + (f - pick(dst.start, blk)) * cols4 + col4;
   f32x4 *tp = tmp + f * cols4 + col4;
-  const bool mine = f < N && colok;
+  const bool mine = f < N && colok && !is_long;
   f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
   if (mine) {
     if (src_mode == kSrcDst && (n > 0 || !skip_untouched)) acc = *d;
@@ -339,6 +389,119 @@ __global__ __launch_bounds__(kBlock) void bwd_tiled_gather_kernel(const int32_t 
 #else
     *d = acc;
 #endif
+  }
+}
+
+// A long segment is summed per 32-column block by one wave: the wave stages
+// kLongRows rows (lane l: 16 bytes of row l / 8 of every 8) into one of its two
+// LDS buffers while lanes 0-31 (one column each) add the rows of the other in
+// order.  The adds are the gather's: acc = start value, acc += row for the
+// positions ascending, so a feature's result does not depend on which kernel
+// summed it.  Waves work independently; each of a workgroup's four waves owns
+// 2 x 16 KB of LDS.
+//
+// Rows of column block cb for position p: 8 chunks at base + cb * blk_stride
+// + p * pos_stride (grad tiles: blk_stride = B * 8, pos_stride = 8; row-major
+// grad: blk_stride = 8, pos_stride = cols4); chunk q of block cb is column
+// chunk tile_col(map, cb, q) of dW.
+struct LongRows {
+  const f32x4 *base;
+  int64_t blk_stride, pos_stride;
+};
+constexpr int kLongRows = 128;    // rows per staged batch of a wave: 128 x 128 B = 16 KB
+constexpr int kLongBlocks = 256;  // one workgroup per CU (128 KB of LDS each); a multiple of kXcds
+
+__device__ __forceinline__ void long_segment_sum(const int32_t *__restrict__ sorted_pos, int64_t f, int s0, int n,
+                                                 int cb, const LongRows &rows, const ColMap &map,
+                                                 const RowDst &dst, f32x4 *__restrict__ tmp, int src_mode,
+                                                 int dst_mode, f32x4 (*buf)[kLongRows * 8]) {
+  constexpr int kRowsPerLoad = kWave / 8;  // rows one load instruction of the wave covers
+  constexpr int kPass = kLongRows / kRowsPerLoad;
+  const int lane = threadIdx.x % kWave;
+  // Summing lanes: lane l < 32 owns float l of the block row (chunk l / 4).
+  const int ccol = lane < 32 ? tile_col(map, cb, lane >> 2) : -1;
+  float *dp = nullptr, *tp = nullptr;
+  float acc = 0.f;
+  if (ccol >= 0) {
+    const int blk = block_of(f, dst.n, dst.start);
+    dp = reinterpret_cast<float *>(pick(dst.p, blk) + (f - pick(dst.start, blk)) * map.cols4 + ccol) + (lane & 3);
+    if (tmp != nullptr) tp = reinterpret_cast<float *>(tmp + f * map.cols4 + ccol) + (lane & 3);
+    if (src_mode == kSrcDst) acc = *dp;
+    else if (src_mode == kSrcTmp) acc = *tp;
+  }
+  // Staging lanes: chunk q of rows r0 + kRowsPerLoad * u.
+  const int q = lane & 7, r0 = lane >> 3;
+  const bool qok = tile_col(map, cb, q) >= 0;
+  const f32x4 *src = rows.base + cb * rows.blk_stride + q;
+  const int nb = (n + kLongRows - 1) / kLongRows;
+  int p[kPass];
+  f32x4 v[kPass];
+  auto load_pos = [&](int b) {
+#pragma unroll
+    for (int u = 0; u < kPass; ++u) {
+      const int r = b * kLongRows + r0 + kRowsPerLoad * u;
+      p[u] = r < n ? sorted_pos[s0 + r] : -1;
+    }
+  };
+  auto load_rows = [&]() {
+#pragma unroll
+    for (int u = 0; u < kPass; ++u)
+      v[u] = (p[u] >= 0 && qok) ? src[(int64_t)p[u] * rows.pos_stride] : f32x4{0.f, 0.f, 0.f, 0.f};
+  };
+  auto stage = [&](int which) {
+#pragma unroll
+    for (int u = 0; u < kPass; ++u) buf[which][(r0 + kRowsPerLoad * u) * 8 + q] = v[u];
+  };
+  load_pos(0);
+  load_rows();
+  stage(0);
+  if (nb > 1) load_pos(1);
+  wave_lds_barrier();
+  for (int b = 0; b < nb; ++b) {  // nb is wave-uniform
+    const bool more = b + 1 < nb;
+    if (more) {
+      load_rows();
+      if (b + 2 < nb) load_pos(b + 2);
+    }
+    if (ccol >= 0) {
+      const float *row = reinterpret_cast<const float *>(buf[b & 1]) + lane;
+      const int nrows = min(kLongRows, n - b * kLongRows);
+#pragma unroll 16
+      for (int r = 0; r < nrows; ++r) acc += row[r * 32];
+    }
+    wave_lds_barrier();  // the buffer staged next was read in the previous step
+    if (more) stage((b + 1) & 1);
+    wave_lds_barrier();
+  }
+  if (ccol >= 0) {
+    if (dst_mode == kDstTmp) *tp = acc;
+    else if (dst_mode == kDstOutPlus) *dp = *dp + acc;
+    else *dp = acc;
+  }
+}
+
+// Sums the listed long segments of one position chunk: items (segment e,
+// column block cb), cb on XCD cb % 8 (workgroup i runs on XCD i % 8), ordered
+// block-major so that an XCD's waves sum one block (one grad tile) at a time
+// while it is in their L2, and dealt round-robin to that XCD's waves.  src/dst
+// modes as in bwd_tiled_gather_kernel; long segments are never untouched.
+__global__ __launch_bounds__(kBlock) void bwd_long_kernel(const int32_t *__restrict__ list,
+                                                          const int *__restrict__ count,
+                                                          const int32_t *__restrict__ seg,
+                                                          const int32_t *__restrict__ sorted_pos, LongRows rows,
+                                                          ColMap map, int nblk, RowDst dst, f32x4 *__restrict__ tmp,
+                                                          int src_mode, int dst_mode) {
+  __shared__ f32x4 buf[kWavesPerBlock][2][kLongRows * 8];
+  const int wave = uniform(threadIdx.x / kWave);
+  const int64_t nseg = *count;
+  const int xcd = (int)(blockIdx.x % kXcds);
+  const int64_t slots = gridDim.x / kXcds * kWavesPerBlock, slot = blockIdx.x / kXcds * kWavesPerBlock + wave;
+  const int64_t xblk = xcd < nblk ? (nblk - xcd + kXcds - 1) / kXcds : 0;  // column blocks of this XCD
+  for (int64_t k = slot; k < xblk * nseg; k += slots) {  // wave-uniform
+    const int cb = xcd + kXcds * (int)(k / nseg);
+    const int64_t f = list[k % nseg];
+    const int s0 = seg[f];
+    long_segment_sum(sorted_pos, f, s0, seg[f + 1] - s0, cb, rows, map, dst, tmp, src_mode, dst_mode, buf[wave]);
   }
 }
 
@@ -611,9 +774,9 @@ __global__ __launch_bounds__(kBlock) void bias_final_kernel(const T *__restrict_
 
 template <typename T, int G, int CPL>
 void launch_gather(dim3 grid, hipStream_t s, const int32_t *seg_start, const int32_t *pos, int64_t N, const void *grad,
-                   int64_t cols, void *dW, int overwrite) {
+                   int64_t cols, void *dW, int overwrite, int skip_long) {
   hipLaunchKernelGGL((gather_rows_kernel<T, G, CPL, 4>), grid, dim3(kBlock), 0, s, seg_start, pos, N,
-                     static_cast<const T *>(grad), cols, static_cast<T *>(dW), overwrite);
+                     static_cast<const T *>(grad), cols, static_cast<T *>(dW), overwrite, skip_long);
 }
 
 #define SFT_CPL_CASES(FN, T, G, ...) \
@@ -677,7 +840,7 @@ int make_layout(int64_t B, int K, int64_t N, int L, uint32_t flags, BwdLayout &l
     lay.sort = off;
     off = align256(off + slot_sort_workspace(M));
     lay.seg = off;
-    off = align256(off + (size_t)(nc * N + 1) * sizeof(int32_t));
+    off = align256(off + seg_region_bytes(nc, N));
     lay.gt = off;
     if (nc > 1) {
       const int64_t ntiles = ceil_div(L / 4, SFT_BWD_TCH);
@@ -730,6 +893,27 @@ int launch_bias_final(const float *partial, int nparts, int L, float *db, int ov
   else
     hipLaunchKernelGGL(bias_final_kernel<float>, grid, dim3(kBlock), 0, s, partial, nparts, cols, db, overwrite);
   return check_launch("bias reduction");
+}
+
+// Segment starts of one sort and its lists of long segments (counts cleared
+// first, with a kernel rather than a memset so that the calls can be captured
+// in a graph).
+int launch_segments(const unsigned *keys, int64_t M, int nc, int64_t nfeat, const unsigned *totals, int ntot,
+                    const SegBufs &sb, hipStream_t s) {
+  ProfScope prof(kProfBwdOffsets, s);
+  hipLaunchKernelGGL(zero_kernel, dim3(1), dim3(kBlock), 0, s, reinterpret_cast<float *>(sb.count), (int64_t)nc);
+  hipLaunchKernelGGL(seg_offsets_kernel, dim3((unsigned)std::min<int64_t>(ceil_div(M + 1, kBlock), kSegBlocks)),
+                     dim3(kBlock), 0, s, keys, (int64_t)nc * nfeat, totals, ntot, sb.seg, nfeat, sb.list, sb.count);
+  return check_launch("segment offsets");
+}
+
+// The long segments of position chunk h (before that chunk's gather launch).
+int launch_long(const SegBufs &sb, int h, int64_t nfeat, const int32_t *pos, const LongRows &rows, const ColMap &map,
+                int nblk, const RowDst &dst, f32x4 *tmp, int src_mode, int dst_mode, hipStream_t s) {
+  ProfScope prof(kProfBwdLong, s);
+  hipLaunchKernelGGL(bwd_long_kernel, dim3(kLongBlocks), dim3(kBlock), 0, s, sb.list + h * nfeat, sb.count + h,
+                     sb.seg + h * nfeat, pos, rows, map, nblk, dst, tmp, src_mode, dst_mode);
+  return check_launch("long segments");
 }
 
 }  // namespace
@@ -822,12 +1006,9 @@ int bwd_f32(const int32_t *idx, int64_t B, int K, const float *grad, int64_t N, 
     if ((rc = slot_sort(idx, M, K, N, chunk_rows, nc, w + lay.sort, &keys, &pos, &totals, &ntot, s)) != SFT_OK)
       return rc;
   }
-  {
-    ProfScope prof(kProfBwdOffsets, s);
-    hipLaunchKernelGGL(seg_offsets_kernel, dim3((unsigned)std::min<int64_t>(ceil_div(M + 1, kBlock), kSegBlocks)), dim3(kBlock), 0, s, keys, nkeys,
-                       totals, ntot, seg);
-    if ((rc = check_launch("segment offsets")) != SFT_OK) return rc;
-  }
+  (void)nkeys;
+  const SegBufs sb = seg_bufs(seg, nc, N);
+  if ((rc = launch_segments(keys, M, nc, N, totals, ntot, sb, s)) != SFT_OK) return rc;
   if (tiled) {
     constexpr int TCH = SFT_BWD_TCH;
     const int64_t cols4 = L / 4;
@@ -840,10 +1021,15 @@ int bwd_f32(const int32_t *idx, int64_t B, int K, const float *grad, int64_t N, 
     dst.start[1] = N;
     dst.p[0] = reinterpret_cast<f32x4 *>(dW);
     for (int h = 0; h < nc; ++h) {
+      const int src_mode = h == 0 ? kSrcZero : kSrcDst;
+      if (kLongPath<TCH> &&
+          (rc = launch_long(sb, h, N, pos, LongRows{gt, B * TCH, TCH}, map, ntiles, dst, nullptr, src_mode, kDstOut,
+                            s)) != SFT_OK)
+        return rc;
       ProfScope prof(kProfBwdTiled, s);
       hipLaunchKernelGGL(bwd_tiled_gather_kernel<TCH>, dim3((unsigned)blocks), dim3(kBlock), 0, s,
-                         seg + (int64_t)h * N, pos, N, gt, B, map, dst, (f32x4 *)nullptr,
-                         h == 0 ? kSrcZero : kSrcDst, kDstOut, ntiles, ngroups);
+                         seg + (int64_t)h * N, pos, N, gt, B, map, dst, (f32x4 *)nullptr, src_mode, kDstOut,
+                         ntiles, ngroups);
       if ((rc = check_launch("tiled feature gather")) != SFT_OK) return rc;
     }
     return SFT_OK;
@@ -854,11 +1040,21 @@ int bwd_f32(const int32_t *idx, int64_t B, int K, const float *grad, int64_t N, 
     const Mapping m = choose_mapping(cols);
     const int fpb = kWavesPerBlock * (kWave / m.G);
     const dim3 grid((unsigned)ceil_div(N, fpb), (unsigned)m.slabs);
+    if (vec) {
+      const ColMap map = plain_map((int)cols, 8);
+      RowDst dst{};
+      dst.n = 1;
+      dst.start[1] = N;
+      dst.p[0] = reinterpret_cast<f32x4 *>(dW);
+      if ((rc = launch_long(sb, 0, N, pos, LongRows{reinterpret_cast<const f32x4 *>(grad), 8, cols}, map,
+                            map_tiles(map), dst, nullptr, kSrcZero, overwrite ? kDstOut : kDstOutPlus, s)) != SFT_OK)
+        return rc;
+    }
     ProfScope prof(kProfBwdGather, s);
     if (vec) {
-      SFT_G_CASES(launch_gather, f32x4, grid, s, seg, pos, N, grad, cols, dW, overwrite)
+      SFT_G_CASES(launch_gather, f32x4, grid, s, seg, pos, N, grad, cols, dW, overwrite, 1)
     } else {
-      SFT_G_CASES(launch_gather, float, grid, s, seg, pos, N, grad, cols, dW, overwrite)
+      SFT_G_CASES(launch_gather, float, grid, s, seg, pos, N, grad, cols, dW, overwrite, 0)
     }
   }
   return check_launch("feature row gather");
@@ -883,7 +1079,7 @@ void make_pair_layout(int64_t B, int K, int64_t N, int L, PairLayout &lay) {
   lay.sort = off;
   off = align256(off + slot_sort_workspace(std::max<int64_t>(M, 1)));
   lay.seg = off;
-  off = align256(off + (size_t)(lay.nc * N + 1) * sizeof(int32_t));
+  off = align256(off + seg_region_bytes(lay.nc, N));
   lay.gt = off;
   off = align256(off + (size_t)(ceil_div(L, 32) * B * 32) * sizeof(float));
   lay.tmp = off;
@@ -915,12 +1111,8 @@ static int pair_gather_perspective(int p, const int32_t *idx, int64_t B, int K, 
     ProfScope prof(kProfBwdSort, s);
     if ((rc = slot_sort(idx, M, K, N, chunk_rows, nc, sort_ws, &keys, &pos, &totals, &ntot, s)) != SFT_OK) return rc;
   }
-  {
-    ProfScope prof(kProfBwdOffsets, s);
-    hipLaunchKernelGGL(seg_offsets_kernel, dim3((unsigned)std::min<int64_t>(ceil_div(M + 1, kBlock), kSegBlocks)), dim3(kBlock), 0, s, keys,
-                       (int64_t)nc * N, totals, ntot, seg);
-    if ((rc = check_launch("segment offsets")) != SFT_OK) return rc;
-  }
+  const SegBufs sb = seg_bufs(seg, nc, N);
+  if ((rc = launch_segments(keys, M, nc, N, totals, ntot, sb, s)) != SFT_OK) return rc;
   for (int h = 0; h < nc; ++h) {
     int src_mode, dst_mode;
     if (p == 0) {
@@ -930,6 +1122,10 @@ static int pair_gather_perspective(int p, const int32_t *idx, int64_t B, int K, 
       src_mode = h == 0 ? kSrcZero : kSrcTmp;
       dst_mode = h == nc - 1 ? kDstOutPlus : kDstTmp;
     }
+    if ((rc = launch_long(sb, h, N, pos, LongRows{gt, B * kBwdTileCh, kBwdTileCh}, map, ntiles, dst, tmp, src_mode,
+                          dst_mode, s)) != SFT_OK)
+      return rc;
+    static_assert(kLongPath<kBwdTileCh>, "the pair gather relies on the long-segment kernel");
     ProfScope prof(kProfBwdTiled, s);
     hipLaunchKernelGGL(bwd_tiled_gather_kernel<kBwdTileCh>, dim3((unsigned)blocks), dim3(kBlock), 0, s,
                        seg + (int64_t)h * N, pos, N, gt, B, map, dst, tmp, src_mode, dst_mode, ntiles, ngroups);
@@ -1001,7 +1197,7 @@ void make_transform_layout(int64_t B, int K, int64_t N, int L, int L1, Transform
   lay.sort = off;
   off = align256(off + slot_sort_workspace(std::max<int64_t>(M, 1)));
   lay.seg = off;
-  off = align256(off + (size_t)(lay.nc * N + 1) * sizeof(int32_t));
+  off = align256(off + seg_region_bytes(lay.nc, N));
   lay.gt0 = off;
   off = align256(off + gtb);
   lay.gt1 = off;

@@ -56,6 +56,41 @@ def test_sorted_bwd_matches_reference_order(seed, B, N, K, L, lo, hi, sort, over
     assert rel_err(db, db_ref) <= 1e-5
 
 
+def skewed_indices(g, B, N, K, hot, p_hot):
+    """Rows whose first slots hold 'hot' features with probability p_hot each
+    (segment lengths from a few to thousands of slots, as for the most common
+    features of real positions), the rest uniform, -1 padded, rows unsorted."""
+    idx = np.full((B, K), -1, np.int32)
+    hot_ids = g.choice(N, hot, replace=False)
+    for b in range(B):
+        row = [int(f) for f in hot_ids if g.random() < p_hot]
+        rest = g.choice(N, K, replace=False)
+        row += [int(f) for f in rest if f not in row][: int(g.integers(0, K - len(row) + 1))]
+        g.shuffle(row)
+        idx[b, : len(row)] = row
+    return idx
+
+
+@pytest.mark.parametrize("seed,B,N,K,L,hot,p_hot", [
+    (21, 9000, 3000, 32, 1048, 12, 0.35),   # tiled: long segments in both position chunks
+    (22, 5000, 400, 24, 136, 40, 0.2),      # narrow rows (row gather)
+    (23, 1200, 50, 16, 520, 6, 0.9),        # segments just above and below the long threshold
+])
+@pytest.mark.parametrize("overwrite", [False, True])
+@pytest.mark.parametrize("rows", [False, True])
+def test_sorted_bwd_skewed_segments(seed, B, N, K, L, hot, p_hot, overwrite, rows):
+    announce(f"bwd skewed seed={seed} B={B} N={N} K={K} L={L} overwrite={overwrite} rows={rows}")
+    g = np.random.default_rng(seed)
+    idx = skewed_indices(g, B, N, K, hot, p_hot)
+    G = g.standard_normal((B, L)).astype(np.float32)
+    dW0 = None if overwrite else g.standard_normal((N, L)).astype(np.float32)
+    flags = (_native.SFT_BWD_OVERWRITE if overwrite else _native.SFT_BWD_ACCUMULATE) | (
+        _native.SFT_BWD_ROWS if rows else 0)
+    dW, _ = run_bwd(idx, G, N, flags, dW0, None if overwrite else np.zeros(L, np.float32))
+    rW, _ = ft_oracle.bwd_f32(idx, G, N, dW0)
+    assert np.array_equal(dW, rW)
+
+
 @pytest.mark.parametrize("seed,B,N,K,L,lo,hi,sort", SHAPES)
 @pytest.mark.parametrize("overwrite", [False, True])
 def test_atomic_bwd_within_tolerance(seed, B, N, K, L, lo, hi, sort, overwrite):

@@ -47,6 +47,7 @@ SHAPES = [
     (3, 1000, 32, 1048, 16, 32, [(2000, 0)]),           # no virtual rows
     (4, 257, 24, 260, 0, 24, [(960, 32), (500, 0), (64, 16), (100, 0)]),  # four blocks, partial last tile
     (5, 2048, 160, 1048, 32, 160, [(6072, 0), (3072, 768)]),  # threats-shaped composition
+    (6, 6000, 32, 520, 16, 32, [(40, 8), (24, 0)]),  # 64 rows: long segments in both position chunks
 ]
 
 

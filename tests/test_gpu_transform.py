@@ -27,6 +27,7 @@ SHAPES = [
     (3, 1000, 32, 1040, 8, 16, 32, [(2000, 0)]),                          # half of L1 = 130 chunks
     (4, 257, 24, 248, 12, 0, 24, [(960, 32), (500, 0), (64, 16), (100, 0)]),  # partial paired and PSQT tiles
     (5, 2048, 160, 1040, 8, 32, 160, [(6072, 0), (3072, 768)]),
+    (6, 6000, 32, 512, 8, 16, 32, [(40, 8), (24, 0)]),  # 64 rows: long segments
 ]
 
 
