@@ -612,6 +612,9 @@ def main() -> int:
     ap.add_argument("--encode", choices=["halfka", "threats"], default=None,
                     help="time the GPU feature-index encoder instead")
     ap.add_argument("--export", action="store_true", help="time the GPU LEB128 encoder of the .nnue export instead")
+    ap.add_argument("--zipf", type=float, default=None, metavar="ALPHA",
+                    help="skewed feature frequencies (probability ~ 1 / (rank + 10)^ALPHA) instead of uniform ones; "
+                         "a robustness run, not the headline")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -643,6 +646,12 @@ def main() -> int:
         return bench_q16(args, w, dev)
     log(f"[bench] generating {w.name}: B={w.B} N={w.N} K={w.K} active U[{w.lo},{w.hi}] L={w.L}")
     d = workloads.make_fp32_inputs(w)
+    if args.zipf is not None:
+        log(f"[bench] Zipf-like feature frequencies, alpha={args.zipf}")
+        d["idx_w"] = workloads.make_zipf_indices(workloads.rng(w.wid, workloads.S_WHITE), w.B, w.N, w.K, w.lo, w.hi,
+                                                 args.zipf)
+        d["idx_b"] = workloads.make_zipf_indices(workloads.rng(w.wid, workloads.S_BLACK), w.B, w.N, w.K, w.lo, w.hi,
+                                                 args.zipf)
     iw = torch.from_numpy(d["idx_w"]).to(dev)
     ib = torch.from_numpy(d["idx_b"]).to(dev)
     W = torch.from_numpy(d["W"]).to(dev).requires_grad_(True)
@@ -729,7 +738,7 @@ def main() -> int:
     dom_avg = prof[dom][0] / prof[dom][1]
     dom_bytes = kern[dom]["bytes_per_launch"]
     achieved = dom_bytes / (dom_avg * 1e-3) / 1e9
-    traffic = load_traffic(w.name, dom)
+    traffic = load_traffic(w.name, dom) if args.zipf is None else None
 
     result = {
         "metric": METRIC,
@@ -743,10 +752,11 @@ def main() -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "fp32",
-        "data": "synthetic",
+        "data": "synthetic" if args.zipf is None else f"synthetic, Zipf-like feature frequencies (alpha {args.zipf})",
         "config": {
             "workload": w.name, "feature_set": w.feature_set, "batch": w.B, "num_inputs": w.N,
             "max_active": w.K, "active": [w.lo, w.hi], "output_size": w.L, "bwd": args.bwd,
+            "feature_freq": "uniform" if args.zipf is None else f"1/(rank+10)^{args.zipf}",
             "launch": "hip_graph" if args.graph else "eager",
             "parallelism": "single-gpu",
             "input_sha256": {k: workloads.sha256(v) for k, v in d.items()},

@@ -98,6 +98,41 @@ def make_indices(g: np.random.Generator, B: int, N: int, K: int, lo: int, hi: in
     return out
 
 
+def make_zipf_indices(g: np.random.Generator, B: int, N: int, K: int, lo: int, hi: int, alpha: float,
+                      offset: float = 10.0, sort: bool = True) -> np.ndarray:
+    """Like make_indices, but with skewed feature frequencies, as on real
+    positions where a few features are active in a large share of them: the
+    features, in a random order, are drawn with probabilities proportional to
+    1 / (rank + offset)^alpha; each row keeps the first `count ~ U{lo..hi}`
+    distinct values of 2 * hi draws (fewer if the draws hold fewer)."""
+    if not (0 <= lo <= hi <= K and hi <= N):
+        raise ValueError("need 0 <= lo <= hi <= K and hi <= N")
+    perm = g.permutation(N)
+    cdf = np.cumsum(1.0 / (np.arange(N) + offset) ** alpha)
+    cdf /= cdf[-1]
+    D = 2 * hi
+    vals = perm[np.minimum(np.searchsorted(cdf, g.random((B, D)), side="right"), N - 1)]
+    order = np.argsort(vals, axis=1, kind="stable")  # equal values keep their draw order
+    sv = np.take_along_axis(vals, order, axis=1)
+    dup_sorted = np.zeros(sv.shape, bool)
+    dup_sorted[:, 1:] = sv[:, 1:] == sv[:, :-1]
+    dup = np.empty_like(dup_sorted)
+    np.put_along_axis(dup, order, dup_sorted, axis=1)
+    counts = g.integers(lo, hi + 1, size=B)
+    rank = np.cumsum(~dup, axis=1) - 1  # index among the row's distinct draws
+    keep = ~dup & (rank < counts[:, None])
+    r, c = np.nonzero(keep)
+    big = np.int64(N) + 1
+    out = np.full((B, hi), big, np.int64)
+    out[r, rank[r, c]] = vals[r, c]
+    if sort:
+        out = np.sort(out, axis=1)
+    out = np.where(out == big, -1, out)
+    res = np.full((B, K), -1, np.int32)
+    res[:, :hi] = out.astype(np.int32)
+    return res
+
+
 def make_fp32_inputs(w: Workload, with_grads: bool = True) -> dict:
     """numpy arrays of an fp32 workload: idx_w, idx_b, W, bias, (g_w, g_b)."""
     d = {

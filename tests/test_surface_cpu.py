@@ -125,6 +125,24 @@ def test_workload_indices_contract():
     assert np.array_equal(idx, again)
 
 
+def test_zipf_indices_contract_and_skew():
+    g = np.random.default_rng(3)
+    B, N = 4000, 2000
+    idx = workloads.make_zipf_indices(g, B, N, 32, 16, 32, alpha=1.0)
+    n = workloads.active_counts(idx, N)
+    assert n.min() >= 14 and n.max() <= 32 and n.mean() > 23
+    for r in idx[:300]:
+        a = r[r >= 0]
+        assert len(np.unique(a)) == len(a) and np.all(np.diff(a) > 0)
+        assert np.all(r[len(a):] == -1)
+    freq = np.bincount(idx[idx >= 0], minlength=N) / B
+    # rank 0 of 1 / (rank + 10): probability 1 / (10 H) per draw, H = sum over ranks
+    H = (1.0 / (np.arange(N) + 10.0)).sum()
+    assert freq.max() > 0.5 * 24 / (10 * H) and freq.max() > 20 * np.median(freq)
+    again = workloads.make_zipf_indices(np.random.default_rng(3), B, N, 32, 16, 32, alpha=1.0)
+    assert np.array_equal(idx, again)
+
+
 def test_step_bytes_formula():
     idx = np.array([[0, 1, -1], [2, -1, -1]], np.int32)
     # per perspective per direction: 4K + 4L(n+1); K=3, L=10: (12+120) + (12+80) = 224
