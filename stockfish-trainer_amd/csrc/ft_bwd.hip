@@ -43,7 +43,7 @@ constexpr int kBiasMaxParts = 512;
 // finds them at their first sample m: keys[m + kLongSeg] == keys[m] !=
 // keys[m - kLongSeg].
 #ifndef SFT_BWD_LONG_SEG
-#define SFT_BWD_LONG_SEG 256
+#define SFT_BWD_LONG_SEG 128
 #endif
 constexpr int kLongSeg = SFT_BWD_LONG_SEG;
 __host__ __device__ inline int64_t long_first_sample(int64_t s0) { return (s0 + kLongSeg - 1) / kLongSeg * kLongSeg; }
@@ -225,9 +225,14 @@ template <int TCH>
 constexpr int bwd_feat_per_block() {
   return kWavesPerBlock * (kWave / TCH);
 }
-// Long segments go to bwd_long_kernel, which sums 32-column blocks.
+// Long segments are summed in 32-column blocks by the tiled gather's
+// long-segment slots.
 template <int TCH>
 constexpr bool kLongPath = TCH == 8;
+#ifndef SFT_BWD_LONG_SLOTS
+#define SFT_BWD_LONG_SLOTS 128
+#endif
+constexpr int kLongSlots = SFT_BWD_LONG_SLOTS;  // long-segment workgroups per tile
 
 #ifndef SFT_BWD_BALANCE
 #define SFT_BWD_BALANCE 1
@@ -300,18 +305,135 @@ __device__ __forceinline__ void bwd_tile_sum(const int32_t *list, int n, int nmi
 // table (FEAT/composed.py:52-53).  dst rows are split into blocks (RowDst).
 enum { kSrcZero = 0, kSrcDst = 1, kSrcTmp = 2 };
 enum { kDstOut = 0, kDstTmp = 1, kDstOutPlus = 2 };
+
+// Rows of column block cb for position p: 8 chunks at base + cb * blk_stride
+// + p * pos_stride (grad tiles: blk_stride = B * 8, pos_stride = 8; row-major
+// grad: blk_stride = 8, pos_stride = cols4); chunk q of block cb is column
+// chunk tile_col(map, cb, q) of dW.
+struct LongRows {
+  const f32x4 *base;
+  int64_t blk_stride, pos_stride;
+};
+
+// Where a long segment's sum for block cb starts and goes (lanes 0-31 of the
+// calling wave; lane l owns float l of the block row); ccol < 0: no column.
+struct LongEnds {
+  float *dp, *tp;
+  int ccol;
+};
+__device__ __forceinline__ LongEnds long_ends(int64_t f, int cb, int lane, const ColMap &map, const RowDst &dst,
+                                              f32x4 *tmp) {
+  LongEnds e{nullptr, nullptr, lane < 32 ? tile_col(map, cb, lane >> 2) : -1};
+  if (e.ccol >= 0) {
+    const int blk = block_of(f, dst.n, dst.start);
+    e.dp = reinterpret_cast<float *>(pick(dst.p, blk) + (f - pick(dst.start, blk)) * map.cols4 + e.ccol) + (lane & 3);
+    if (tmp != nullptr) e.tp = reinterpret_cast<float *>(tmp + f * map.cols4 + e.ccol) + (lane & 3);
+  }
+  return e;
+}
+__device__ __forceinline__ float long_start(const LongEnds &e, int src_mode) {
+  if (e.ccol < 0) return 0.f;
+  if (src_mode == kSrcDst) return *e.dp;
+  if (src_mode == kSrcTmp) return *e.tp;
+  return 0.f;
+}
+__device__ __forceinline__ void long_store(const LongEnds &e, int dst_mode, float acc) {
+  if (e.ccol < 0) return;
+  if (dst_mode == kDstTmp) *e.tp = acc;
+  else if (dst_mode == kDstOutPlus) *e.dp = *e.dp + acc;
+  else *e.dp = acc;
+}
+
+// A long segment (see long_segment) summed for one column block by a whole
+// workgroup: its 256 threads stage kWgLongRows rows at a time into LDS (the
+// next batch's loads in flight meanwhile) and lanes 0-31 of wave 0 add them in
+// order: acc = start value, acc += row for the positions ascending -- the
+// gather's own sequence, so a feature's result does not depend on the path.
+constexpr int kWgLongRows = 128;  // 128 x 128 B = 16 KB of LDS
+__device__ __forceinline__ void long_segment_sum_wg(const int32_t *__restrict__ sorted_pos, int64_t f, int s0, int n,
+                                                    int cb, const LongRows &rows, const ColMap &map,
+                                                    const RowDst &dst, f32x4 *__restrict__ tmp, int src_mode,
+                                                    int dst_mode, f32x4 *buf) {
+  constexpr int kRowsPerPass = kBlock / 8;
+  constexpr int kPass = kWgLongRows / kRowsPerPass;
+  const LongEnds ends = long_ends(f, cb, (int)threadIdx.x, map, dst, tmp);
+  float acc = long_start(ends, src_mode);
+  const int q = threadIdx.x & 7, r0 = threadIdx.x >> 3;  // staging: chunk q of rows r0 + 32 u
+  const bool qok = tile_col(map, cb, q) >= 0;
+  const f32x4 *src = rows.base + cb * rows.blk_stride + q;
+  const int nb = (n + kWgLongRows - 1) / kWgLongRows;
+  int p[kPass];
+  f32x4 v[kPass];
+  auto load_pos = [&](int b) {
+#pragma unroll
+    for (int u = 0; u < kPass; ++u) {
+      const int r = b * kWgLongRows + r0 + kRowsPerPass * u;
+      p[u] = r < n ? sorted_pos[s0 + r] : -1;
+    }
+  };
+  auto load_rows = [&]() {
+#pragma unroll
+    for (int u = 0; u < kPass; ++u)
+      v[u] = (p[u] >= 0 && qok) ? src[(int64_t)p[u] * rows.pos_stride] : f32x4{0.f, 0.f, 0.f, 0.f};
+  };
+  auto stage = [&]() {
+#pragma unroll
+    for (int u = 0; u < kPass; ++u) buf[(r0 + kRowsPerPass * u) * 8 + q] = v[u];
+  };
+  load_pos(0);
+  load_rows();
+  if (nb > 1) load_pos(1);
+  stage();
+  __syncthreads();
+  for (int b = 0; b < nb; ++b) {  // nb is workgroup-uniform
+    const bool more = b + 1 < nb;
+    if (more) {
+      load_rows();
+      if (b + 2 < nb) load_pos(b + 2);
+    }
+    if (ends.ccol >= 0) {
+      const float *row = reinterpret_cast<const float *>(buf) + threadIdx.x;
+      const int nrows = min(kWgLongRows, n - b * kWgLongRows);
+#pragma unroll 16
+      for (int r = 0; r < nrows; ++r) acc += row[r * 32];
+    }
+    __syncthreads();
+    if (more) stage();
+    __syncthreads();
+  }
+  long_store(ends, dst_mode, acc);
+}
+
+//
+// Each tile's items start with nlong long-segment slots: slot j sums the
+// chunk's listed long segments j, j + nlong, ... for this tile with the
+// whole workgroup (long_segment_sum_wg), while the tile is in the XCD's L2;
+// the feature blocks follow.
 template <int TCH>
 __global__ __launch_bounds__(kBlock) void bwd_tiled_gather_kernel(const int32_t *__restrict__ seg,
                                                                   const int32_t *__restrict__ sorted_pos, int64_t N,
                                                                   const f32x4 *__restrict__ gt, int64_t B,
                                                                   ColMap map, RowDst dst, f32x4 *__restrict__ tmp,
-                                                                  int src_mode, int dst_mode, int ntiles, int ngroups) {
-  __shared__ int spos[kBwdPosLds];
+                                                                  int src_mode, int dst_mode, int ntiles, int ngroups,
+                                                                  const int32_t *__restrict__ long_list,
+                                                                  const int *__restrict__ long_count, int nlong) {
+  __shared__ __align__(16) int spos[kBwdPosLds];
   constexpr int FPB = bwd_feat_per_block<TCH>();
   __shared__ int s_len[FPB], s_perm[FPB];
-  const TileItem it = tile_sched_item(blockIdx.x, ntiles, ngroups);
+  const TileItem it = tile_sched_item(blockIdx.x, ntiles, ngroups + nlong);
   if (it.tile >= ntiles) return;  // whole block: uniform
-  const int64_t fb = (int64_t)it.chunk * FPB;
+  if (it.chunk < nlong) {         // whole block: uniform
+    static_assert(kWgLongRows * 8 * sizeof(f32x4) <= sizeof(spos), "long-segment batch must fit the LDS list");
+    const int cnt = *long_count;
+    for (int e = it.chunk; e < cnt; e += nlong) {
+      const int64_t f = long_list[e];
+      const int s0 = seg[f];
+      long_segment_sum_wg(sorted_pos, f, s0, seg[f + 1] - s0, it.tile, LongRows{gt, B * TCH, TCH}, map, dst, tmp,
+                          src_mode, dst_mode, reinterpret_cast<f32x4 *>(spos));
+    }
+    return;
+  }
+  const int64_t fb = (int64_t)(it.chunk - nlong) * FPB;
   const int64_t fe = fb + FPB < N ? fb + FPB : N;
   const int r0 = seg[fb], r1 = seg[fe];
   const bool staged = (r1 - r0) <= kBwdPosLds;  // block-uniform
@@ -392,22 +514,12 @@ __global__ __launch_bounds__(kBlock) void bwd_tiled_gather_kernel(const int32_t 
   }
 }
 
-// A long segment is summed per 32-column block by one wave: the wave stages
-// kLongRows rows (lane l: 16 bytes of row l / 8 of every 8) into one of its two
-// LDS buffers while lanes 0-31 (one column each) add the rows of the other in
-// order.  The adds are the gather's: acc = start value, acc += row for the
-// positions ascending, so a feature's result does not depend on which kernel
-// summed it.  Waves work independently; each of a workgroup's four waves owns
-// 2 x 16 KB of LDS.
-//
-// Rows of column block cb for position p: 8 chunks at base + cb * blk_stride
-// + p * pos_stride (grad tiles: blk_stride = B * 8, pos_stride = 8; row-major
-// grad: blk_stride = 8, pos_stride = cols4); chunk q of block cb is column
-// chunk tile_col(map, cb, q) of dW.
-struct LongRows {
-  const f32x4 *base;
-  int64_t blk_stride, pos_stride;
-};
+// Long segments of the row gather (narrow rows, row-major grad): each is
+// summed per 32-column block by one wave, which stages kLongRows rows (lane l:
+// 16 bytes of row l / 8 of every 8) into one of its two LDS buffers while lanes
+// 0-31 (one column each) add the rows of the other in order -- the same
+// sequence as long_segment_sum_wg.  Waves work independently; each of a
+// workgroup's four waves owns 2 x 16 KB of LDS.
 constexpr int kLongRows = 128;    // rows per staged batch of a wave: 128 x 128 B = 16 KB
 constexpr int kLongBlocks = 256;  // one workgroup per CU (128 KB of LDS each); a multiple of kXcds
 
@@ -418,17 +530,8 @@ __device__ __forceinline__ void long_segment_sum(const int32_t *__restrict__ sor
   constexpr int kRowsPerLoad = kWave / 8;  // rows one load instruction of the wave covers
   constexpr int kPass = kLongRows / kRowsPerLoad;
   const int lane = threadIdx.x % kWave;
-  // Summing lanes: lane l < 32 owns float l of the block row (chunk l / 4).
-  const int ccol = lane < 32 ? tile_col(map, cb, lane >> 2) : -1;
-  float *dp = nullptr, *tp = nullptr;
-  float acc = 0.f;
-  if (ccol >= 0) {
-    const int blk = block_of(f, dst.n, dst.start);
-    dp = reinterpret_cast<float *>(pick(dst.p, blk) + (f - pick(dst.start, blk)) * map.cols4 + ccol) + (lane & 3);
-    if (tmp != nullptr) tp = reinterpret_cast<float *>(tmp + f * map.cols4 + ccol) + (lane & 3);
-    if (src_mode == kSrcDst) acc = *dp;
-    else if (src_mode == kSrcTmp) acc = *tp;
-  }
+  const LongEnds ends = long_ends(f, cb, lane, map, dst, tmp);
+  float acc = long_start(ends, src_mode);
   // Staging lanes: chunk q of rows r0 + kRowsPerLoad * u.
   const int q = lane & 7, r0 = lane >> 3;
   const bool qok = tile_col(map, cb, q) >= 0;
@@ -463,7 +566,7 @@ __device__ __forceinline__ void long_segment_sum(const int32_t *__restrict__ sor
       load_rows();
       if (b + 2 < nb) load_pos(b + 2);
     }
-    if (ccol >= 0) {
+    if (ends.ccol >= 0) {
       const float *row = reinterpret_cast<const float *>(buf[b & 1]) + lane;
       const int nrows = min(kLongRows, n - b * kLongRows);
 #pragma unroll 16
@@ -473,18 +576,13 @@ __device__ __forceinline__ void long_segment_sum(const int32_t *__restrict__ sor
     if (more) stage((b + 1) & 1);
     wave_lds_barrier();
   }
-  if (ccol >= 0) {
-    if (dst_mode == kDstTmp) *tp = acc;
-    else if (dst_mode == kDstOutPlus) *dp = *dp + acc;
-    else *dp = acc;
-  }
+  long_store(ends, dst_mode, acc);
 }
 
-// Sums the listed long segments of one position chunk: items (segment e,
-// column block cb), cb on XCD cb % 8 (workgroup i runs on XCD i % 8), ordered
-// block-major so that an XCD's waves sum one block (one grad tile) at a time
-// while it is in their L2, and dealt round-robin to that XCD's waves.  src/dst
-// modes as in bwd_tiled_gather_kernel; long segments are never untouched.
+// Sums the listed long segments of the row gather: items (segment e, column
+// block cb), cb on XCD cb % 8 (workgroup i runs on XCD i % 8), ordered
+// block-major, dealt round-robin to that XCD's waves.  src/dst modes as in
+// bwd_tiled_gather_kernel; long segments are never untouched.
 __global__ __launch_bounds__(kBlock) void bwd_long_kernel(const int32_t *__restrict__ list,
                                                           const int *__restrict__ count,
                                                           const int32_t *__restrict__ seg,
@@ -1015,21 +1113,17 @@ int bwd_f32(const int32_t *idx, int64_t B, int K, const float *grad, int64_t N, 
     const ColMap map = plain_map((int)cols4, TCH);
     const int ntiles = map_tiles(map);
     const int ngroups = (int)ceil_div(N, bwd_feat_per_block<TCH>());
-    const int64_t blocks = tile_sched_items_per_xcd(ntiles, ngroups) * kXcds;
+    const int nlong = kLongPath<TCH> ? kLongSlots : 0;
+    const int64_t blocks = tile_sched_items_per_xcd(ntiles, ngroups + nlong) * kXcds;
     RowDst dst{};
     dst.n = 1;
     dst.start[1] = N;
     dst.p[0] = reinterpret_cast<f32x4 *>(dW);
     for (int h = 0; h < nc; ++h) {
-      const int src_mode = h == 0 ? kSrcZero : kSrcDst;
-      if (kLongPath<TCH> &&
-          (rc = launch_long(sb, h, N, pos, LongRows{gt, B * TCH, TCH}, map, ntiles, dst, nullptr, src_mode, kDstOut,
-                            s)) != SFT_OK)
-        return rc;
       ProfScope prof(kProfBwdTiled, s);
       hipLaunchKernelGGL(bwd_tiled_gather_kernel<TCH>, dim3((unsigned)blocks), dim3(kBlock), 0, s,
-                         seg + (int64_t)h * N, pos, N, gt, B, map, dst, (f32x4 *)nullptr, src_mode, kDstOut,
-                         ntiles, ngroups);
+                         seg + (int64_t)h * N, pos, N, gt, B, map, dst, (f32x4 *)nullptr, h == 0 ? kSrcZero : kSrcDst,
+                         kDstOut, ntiles, ngroups, sb.list + h * N, sb.count + h, nlong);
       if ((rc = check_launch("tiled feature gather")) != SFT_OK) return rc;
     }
     return SFT_OK;
@@ -1102,7 +1196,8 @@ static int pair_gather_perspective(int p, const int32_t *idx, int64_t B, int K, 
   const int64_t M = B * K;
   const int ntiles = map_tiles(map);
   const int ngroups = (int)ceil_div(N, bwd_feat_per_block<kBwdTileCh>());
-  const int64_t blocks = tile_sched_items_per_xcd(ntiles, ngroups) * kXcds;
+  static_assert(kLongPath<kBwdTileCh>, "the pair gather sums long segments in its long-segment slots");
+  const int64_t blocks = tile_sched_items_per_xcd(ntiles, ngroups + kLongSlots) * kXcds;
   const int chunk_rows = (int)(nc > 1 ? half_rows(B) : B);
   unsigned *keys = nullptr, *totals = nullptr;
   int32_t *pos = nullptr;
@@ -1122,13 +1217,10 @@ static int pair_gather_perspective(int p, const int32_t *idx, int64_t B, int K, 
       src_mode = h == 0 ? kSrcZero : kSrcTmp;
       dst_mode = h == nc - 1 ? kDstOutPlus : kDstTmp;
     }
-    if ((rc = launch_long(sb, h, N, pos, LongRows{gt, B * kBwdTileCh, kBwdTileCh}, map, ntiles, dst, tmp, src_mode,
-                          dst_mode, s)) != SFT_OK)
-      return rc;
-    static_assert(kLongPath<kBwdTileCh>, "the pair gather relies on the long-segment kernel");
     ProfScope prof(kProfBwdTiled, s);
     hipLaunchKernelGGL(bwd_tiled_gather_kernel<kBwdTileCh>, dim3((unsigned)blocks), dim3(kBlock), 0, s,
-                       seg + (int64_t)h * N, pos, N, gt, B, map, dst, tmp, src_mode, dst_mode, ntiles, ngroups);
+                       seg + (int64_t)h * N, pos, N, gt, B, map, dst, tmp, src_mode, dst_mode, ntiles, ngroups,
+                       sb.list + h * N, sb.count + h, kLongSlots);
     if ((rc = check_launch("tiled feature gather")) != SFT_OK) return rc;
   }
   return SFT_OK;
