@@ -136,7 +136,6 @@ const char *const kKindNames[] = {
     "bwd_bias_final",   "bwd_atomic_scatter", "bwd_zero_fill",      "fwd_i16_gather",     "quantize_i16",
     "fwd_tile_relayout", "fwd_f32_tiled_gather", "bwd_tiled_gather", "fwd_i16_tiled_gather",
     "fwd_fold_relayout", "bwd_virtual_reduce", "bwd_epilogue", "ranger22_update", "encode_features", "leb128_encode",
-    "bwd_long_segments",
 };
 static_assert(sizeof(kKindNames) / sizeof(kKindNames[0]) == kProfNumKinds, "one name per profiling kind");
 }  // namespace

@@ -50,7 +50,6 @@ enum ProfKind : int {
   kProfOptim,
   kProfEncode,
   kProfLeb128,
-  kProfBwdLong,
   kProfNumKinds
 };
 struct ProfScope {
@@ -261,7 +260,7 @@ __host__ __device__ inline void tile_of_col(const ColMap &m, int c, int &t, int 
     q = k & 7;
   }
 }
-inline ColMap plain_map(int cols4, int tch = 8) { return ColMap{0, 0, cols4, tch}; }
+__host__ __device__ inline ColMap plain_map(int cols4, int tch = 8) { return ColMap{0, 0, cols4, tch}; }
 inline ColMap paired_map(int cols4, int half4) {
   return ColMap{half4, (half4 + 3) / 4, cols4, 8};
 }

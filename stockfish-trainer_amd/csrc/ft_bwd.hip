@@ -14,6 +14,7 @@
 // Bias grad (FT/kernel.py:269): per-block column partial sums, then a fixed-
 // order reduction of the partials; deterministic.
 #include <algorithm>
+#include <type_traits>
 
 #include "common.h"
 
@@ -33,15 +34,15 @@ constexpr int kBiasMaxParts = 512;
 // ------------------------------------------------------- long segments ----
 // On real data a few features are active in a large share of the positions
 // (a quarter of them and more); one lane group summing such a segment would
-// run for the whole launch.  Long segments are summed by a whole workgroup
-// instead (bwd_long_kernel) and skipped by the gather kernels.  Whether
-// segment [s0, s1) of the sorted slots is long depends on its bounds alone,
-// so both sides agree without a list: it is long when it contains two
-// consecutive multiples of kLongSeg ("samples") of the sorted slot index.
-// Every segment of more than 2 kLongSeg slots is long, none of fewer than
-// kLongSeg + 2.  seg_offsets_kernel lists them (per position chunk) as it
-// finds them at their first sample m: keys[m + kLongSeg] == keys[m] !=
-// keys[m - kLongSeg].
+// run for the whole launch.  Long segments are summed by whole workgroups
+// (long_segment_sum_wg: reserved workgroups of the same gather launch) and
+// skipped by the per-feature lane groups.  Whether segment [s0, s1) of the
+// sorted slots is long depends on its bounds alone, so both sides agree: it
+// is long when it contains two consecutive multiples of kLongSeg ("samples")
+// of the sorted slot index.  Every segment of more than 2 kLongSeg slots is
+// long, none of fewer than kLongSeg + 2.  seg_offsets_kernel lists them (per
+// position chunk) as it finds them at their first sample m:
+// keys[m + kLongSeg] == keys[m] != keys[m - kLongSeg].
 #ifndef SFT_BWD_LONG_SEG
 #define SFT_BWD_LONG_SEG 128
 #endif
@@ -114,186 +115,6 @@ __device__ __forceinline__ void group_minmax(int v, int &vmin, int &vmax) {
   vmax = uniform(vmax);
 }
 
-template <typename T, int G, int CPL, int U>
-__global__ __launch_bounds__(kBlock) void gather_rows_kernel(const int32_t *__restrict__ seg_start,
-                                                             const int32_t *__restrict__ sorted_pos, int64_t N,
-                                                             const T *__restrict__ grad, int64_t cols,
-                                                             T *__restrict__ dW, int overwrite, int skip_long) {
-  constexpr int PPW = kWave / G;
-  const int wave = uniform(threadIdx.x / kWave);
-  const int lane = threadIdx.x % kWave;
-  const int g = lane / G, t = lane % G;
-  const int64_t f = ((int64_t)blockIdx.x * kWavesPerBlock + wave) * PPW + g;
-  const bool live = f < N;
-  int s0 = 0, s1 = 0;
-  if (live) {
-    s0 = seg_start[f];
-    s1 = seg_start[f + 1];
-  }
-  if (G == kWave) {
-    s0 = uniform(s0);
-    s1 = uniform(s1);
-  }
-  const bool is_long = skip_long && live && long_segment(s0, s1);  // summed by bwd_long_kernel
-  const int n = is_long ? 0 : s1 - s0;
-  int nmin, nmax;
-  group_minmax<G>(n, nmin, nmax);
-
-  const int64_t c0 = (int64_t)blockIdx.y * (G * CPL) + t;
-  bool colok[CPL];
-  T acc[CPL];
-#pragma unroll
-  for (int j = 0; j < CPL; ++j) {
-    colok[j] = (c0 + G * j) < cols;
-    acc[j] = T(0);
-  }
-  const int32_t *plist = sorted_pos + s0;
-
-  int k = 0;
-  for (; k + U <= nmin; k += U) {
-    T w[U][CPL];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      int b = plist[k + u];
-      if (G == kWave) b = uniform(b);
-      const T *row = grad + (int64_t)b * cols + c0;
-#pragma unroll
-      for (int j = 0; j < CPL; ++j)
-        if (colok[j]) w[u][j] = row[G * j];
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u)
-#pragma unroll
-      for (int j = 0; j < CPL; ++j)
-        if (colok[j]) acc[j] += w[u][j];
-  }
-  for (; k < nmax; k += U) {
-    T w[U][CPL];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const bool v = k + u < n;
-      int b = v ? plist[k + u] : 0;
-      if (G == kWave) b = uniform(b);
-      const T *row = grad + (int64_t)b * cols + c0;
-#pragma unroll
-      for (int j = 0; j < CPL; ++j) {
-        w[u][j] = T(0);
-        if (v && colok[j]) w[u][j] = row[G * j];
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const bool v = k + u < n;
-#pragma unroll
-      for (int j = 0; j < CPL; ++j)
-        if (v && colok[j]) acc[j] += w[u][j];
-    }
-  }
-
-  if (live && !is_long && (n > 0 || overwrite)) {
-    T *d = dW + f * cols + c0;
-#pragma unroll
-    for (int j = 0; j < CPL; ++j) {
-      if (!colok[j]) continue;
-      if (overwrite)
-        __builtin_nontemporal_store(acc[j], d + G * j);
-      else
-        d[G * j] = d[G * j] + acc[j];
-    }
-  }
-}
-
-// ---------------------------------------------------- tiled feature gather ----
-// dW[f, tile] for one 32-column tile, from the grad re-laid out as column
-// tiles (Gt: tile t holds columns [32t, 32t + 32) of every position, 128 B per
-// position).  The slots are sorted by (position half, feature), and the batch
-// is done in two launches: half 0 stores dW[f, tile] = its sum, half 1 loads
-// that value and keeps adding.  Either way a feature's sum is acc = 0,
-// acc += grad[b] over its positions ascending: the reference order
-// (FT/kernel.py:122, 178-181), bit for bit.  A lane group of 8 lanes x 16 B
-// owns one feature's tile row; tiles go to XCDs whole (tile_sched_item), so an
-// XCD reads one tile-half of Gt at a time: 32768 x 128 B = 4 MB, its L2.
-#ifndef SFT_BWD_NT_STORE
-#define SFT_BWD_NT_STORE 0
-#endif
-constexpr int kBwdTileCh = 8;  // float4 chunks per 32-column tile row
-// Grad tile width of the plain (single-perspective) tiled backward, in 16-byte chunks.
-#ifndef SFT_BWD_TCH
-#define SFT_BWD_TCH 8
-#endif
-template <int TCH>
-constexpr int bwd_feat_per_block() {
-  return kWavesPerBlock * (kWave / TCH);
-}
-// Long segments are summed in 32-column blocks by the tiled gather's
-// long-segment slots.
-template <int TCH>
-constexpr bool kLongPath = TCH == 8;
-#ifndef SFT_BWD_LONG_SLOTS
-#define SFT_BWD_LONG_SLOTS 128
-#endif
-constexpr int kLongSlots = SFT_BWD_LONG_SLOTS;  // long-segment workgroups per tile
-
-#ifndef SFT_BWD_BALANCE
-#define SFT_BWD_BALANCE 1
-#endif
-#ifndef SFT_BWD_POS_LDS
-#define SFT_BWD_POS_LDS 4096
-#endif
-constexpr int kBwdPosLds = SFT_BWD_POS_LDS;  // staged positions per workgroup
-
-// Sums one lane group's positions from `list` (LDS or global) into acc.  A
-// lane group has TCH lanes (one 16-byte chunk of the tile row each) and keeps
-// TCH row loads in flight.
-template <bool FROM_LDS, int TCH>
-__device__ __forceinline__ void bwd_tile_sum(const int32_t *list, int n, int nmin, int nmax, int t, bool colok,
-                                             const f32x4 *__restrict__ gcol, f32x4 &acc) {
-  constexpr int U = TCH;  // one position per lane of the group when read from global memory
-  int k = 0;
-  for (; k + U <= nmin; k += U) {
-    int b[U];
-    if (FROM_LDS) {
-#pragma unroll
-      for (int u = 0; u < U; ++u) b[u] = list[k + u];
-    } else {
-      const int mine = list[k + t];
-#pragma unroll
-      for (int u = 0; u < U; ++u) b[u] = __shfl(mine, u, TCH);
-    }
-    f32x4 w[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) w[u] = colok ? gcol[(int64_t)b[u] * TCH] : f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int u = 0; u < U; ++u) acc += w[u];
-  }
-  for (; k < nmax; k += U) {
-    int b[U];
-    if (FROM_LDS) {
-#pragma unroll
-      for (int u = 0; u < U; ++u) b[u] = (k + u < n) ? list[k + u] : 0;
-    } else {
-      const int mine = (k + t < n) ? list[k + t] : 0;
-#pragma unroll
-      for (int u = 0; u < U; ++u) b[u] = __shfl(mine, u, TCH);
-    }
-    f32x4 w[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      w[u] = f32x4{0.f, 0.f, 0.f, 0.f};
-      if (k + u < n && colok) w[u] = gcol[(int64_t)b[u] * TCH];
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u)
-      if (k + u < n) acc += w[u];
-  }
-}
-
-// The 32 features of a workgroup are consecutive, so their position lists
-// form one contiguous range of the sorted array; it is copied to LDS with
-// coalesced loads and read from there, which keeps the position reads off the
-// in-order vector-memory counter the row loads wait on.  Ranges longer than
-// kBwdPosLds entries read their positions from global memory instead.
-//
 // Where a launch starts and leaves each feature's sum:
 //   src_mode kSrcZero: acc = 0;  kSrcDst: acc = dst row;  kSrcTmp: acc = tmp row
 //   dst_mode kDstOut: dst row = acc (skipped for untouched features when the
@@ -404,6 +225,215 @@ __device__ __forceinline__ void long_segment_sum_wg(const int32_t *__restrict__ 
   long_store(ends, dst_mode, acc);
 }
 
+// Row gather: the first nlong workgroups (column slab 0) sum the listed long
+// segments in 32-column blocks (items e * nblk + cb dealt round-robin; the
+// float4 instantiation only); the others are feature blocks.
+template <typename T, int G, int CPL, int U>
+__global__ __launch_bounds__(kBlock) void gather_rows_kernel(const int32_t *__restrict__ seg_start,
+                                                             const int32_t *__restrict__ sorted_pos, int64_t N,
+                                                             const T *__restrict__ grad, int64_t cols,
+                                                             T *__restrict__ dW, int overwrite,
+                                                             const int32_t *__restrict__ long_list,
+                                                             const int *__restrict__ long_count, int nlong) {
+  if ((int)blockIdx.x < nlong) {  // whole block: uniform
+    if constexpr (std::is_same<T, f32x4>::value) {
+      __shared__ f32x4 lbuf[kWgLongRows * 8];
+      if (blockIdx.y != 0) return;
+      const ColMap map = plain_map((int)cols, 8);
+      const int nblk = map_tiles(map);
+      RowDst dst{};
+      dst.n = 1;
+      dst.start[1] = N;
+      dst.p[0] = dW;
+      const int64_t items = (int64_t)*long_count * nblk;
+      for (int64_t k = blockIdx.x; k < items; k += nlong) {
+        const int64_t f = long_list[k / nblk];
+        const int s0 = seg_start[f];
+        long_segment_sum_wg(sorted_pos, f, s0, seg_start[f + 1] - s0, (int)(k % nblk), LongRows{grad, 8, cols}, map,
+                            dst, nullptr, kSrcZero, overwrite ? kDstOut : kDstOutPlus, lbuf);
+      }
+    }
+    return;
+  }
+  const bool skip_long = nlong > 0;
+  constexpr int PPW = kWave / G;
+  const int wave = uniform(threadIdx.x / kWave);
+  const int lane = threadIdx.x % kWave;
+  const int g = lane / G, t = lane % G;
+  const int64_t f = ((int64_t)(blockIdx.x - nlong) * kWavesPerBlock + wave) * PPW + g;
+  const bool live = f < N;
+  int s0 = 0, s1 = 0;
+  if (live) {
+    s0 = seg_start[f];
+    s1 = seg_start[f + 1];
+  }
+  if (G == kWave) {
+    s0 = uniform(s0);
+    s1 = uniform(s1);
+  }
+  const bool is_long = skip_long && live && long_segment(s0, s1);  // summed by the long-segment blocks
+  const int n = is_long ? 0 : s1 - s0;
+  int nmin, nmax;
+  group_minmax<G>(n, nmin, nmax);
+
+  const int64_t c0 = (int64_t)blockIdx.y * (G * CPL) + t;
+  bool colok[CPL];
+  T acc[CPL];
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) {
+    colok[j] = (c0 + G * j) < cols;
+    acc[j] = T(0);
+  }
+  const int32_t *plist = sorted_pos + s0;
+
+  int k = 0;
+  for (; k + U <= nmin; k += U) {
+    T w[U][CPL];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      int b = plist[k + u];
+      if (G == kWave) b = uniform(b);
+      const T *row = grad + (int64_t)b * cols + c0;
+#pragma unroll
+      for (int j = 0; j < CPL; ++j)
+        if (colok[j]) w[u][j] = row[G * j];
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int j = 0; j < CPL; ++j)
+        if (colok[j]) acc[j] += w[u][j];
+  }
+  for (; k < nmax; k += U) {
+    T w[U][CPL];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const bool v = k + u < n;
+      int b = v ? plist[k + u] : 0;
+      if (G == kWave) b = uniform(b);
+      const T *row = grad + (int64_t)b * cols + c0;
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) {
+        w[u][j] = T(0);
+        if (v && colok[j]) w[u][j] = row[G * j];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const bool v = k + u < n;
+#pragma unroll
+      for (int j = 0; j < CPL; ++j)
+        if (v && colok[j]) acc[j] += w[u][j];
+    }
+  }
+
+  if (live && !is_long && (n > 0 || overwrite)) {
+    T *d = dW + f * cols + c0;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      if (!colok[j]) continue;
+      if (overwrite)
+        __builtin_nontemporal_store(acc[j], d + G * j);
+      else
+        d[G * j] = d[G * j] + acc[j];
+    }
+  }
+}
+
+// ---------------------------------------------------- tiled feature gather ----
+// dW[f, tile] for one 32-column tile, from the grad re-laid out as column
+// tiles (Gt: tile t holds columns [32t, 32t + 32) of every position, 128 B per
+// position).  The slots are sorted by (position half, feature), and the batch
+// is done in two launches: half 0 stores dW[f, tile] = its sum, half 1 loads
+// that value and keeps adding.  Either way a feature's sum is acc = 0,
+// acc += grad[b] over its positions ascending: the reference order
+// (FT/kernel.py:122, 178-181), bit for bit.  A lane group of 8 lanes x 16 B
+// owns one feature's tile row; tiles go to XCDs whole (tile_sched_item), so an
+// XCD reads one tile-half of Gt at a time: 32768 x 128 B = 4 MB, its L2.
+#ifndef SFT_BWD_NT_STORE
+#define SFT_BWD_NT_STORE 0
+#endif
+constexpr int kBwdTileCh = 8;  // float4 chunks per 32-column tile row
+// Grad tile width of the plain (single-perspective) tiled backward, in 16-byte chunks.
+#ifndef SFT_BWD_TCH
+#define SFT_BWD_TCH 8
+#endif
+template <int TCH>
+constexpr int bwd_feat_per_block() {
+  return kWavesPerBlock * (kWave / TCH);
+}
+// Long segments are summed in 32-column blocks by the tiled gather's
+// long-segment slots.
+template <int TCH>
+constexpr bool kLongPath = TCH == 8;
+#ifndef SFT_BWD_LONG_SLOTS
+#define SFT_BWD_LONG_SLOTS 128
+#endif
+constexpr int kLongSlots = SFT_BWD_LONG_SLOTS;  // long-segment workgroups per tile
+#ifndef SFT_BWD_ROW_LONG_BLOCKS
+#define SFT_BWD_ROW_LONG_BLOCKS 1024
+#endif
+constexpr int kRowLongBlocks = SFT_BWD_ROW_LONG_BLOCKS;  // long-segment workgroups of the row gather
+
+#ifndef SFT_BWD_BALANCE
+#define SFT_BWD_BALANCE 1
+#endif
+#ifndef SFT_BWD_POS_LDS
+#define SFT_BWD_POS_LDS 4096
+#endif
+constexpr int kBwdPosLds = SFT_BWD_POS_LDS;  // staged positions per workgroup
+
+// Sums one lane group's positions from `list` (LDS or global) into acc.  A
+// lane group has TCH lanes (one 16-byte chunk of the tile row each) and keeps
+// TCH row loads in flight.
+template <bool FROM_LDS, int TCH>
+__device__ __forceinline__ void bwd_tile_sum(const int32_t *list, int n, int nmin, int nmax, int t, bool colok,
+                                             const f32x4 *__restrict__ gcol, f32x4 &acc) {
+  constexpr int U = TCH;  // one position per lane of the group when read from global memory
+  int k = 0;
+  for (; k + U <= nmin; k += U) {
+    int b[U];
+    if (FROM_LDS) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) b[u] = list[k + u];
+    } else {
+      const int mine = list[k + t];
+#pragma unroll
+      for (int u = 0; u < U; ++u) b[u] = __shfl(mine, u, TCH);
+    }
+    f32x4 w[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) w[u] = colok ? gcol[(int64_t)b[u] * TCH] : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < U; ++u) acc += w[u];
+  }
+  for (; k < nmax; k += U) {
+    int b[U];
+    if (FROM_LDS) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) b[u] = (k + u < n) ? list[k + u] : 0;
+    } else {
+      const int mine = (k + t < n) ? list[k + t] : 0;
+#pragma unroll
+      for (int u = 0; u < U; ++u) b[u] = __shfl(mine, u, TCH);
+    }
+    f32x4 w[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      w[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+      if (k + u < n && colok) w[u] = gcol[(int64_t)b[u] * TCH];
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (k + u < n) acc += w[u];
+  }
+}
+
+// The 32 features of a workgroup are consecutive, so their position lists
+// form one contiguous range of the sorted array; it is copied to LDS with
+// coalesced loads and read from there, which keeps the position reads off the
+// in-order vector-memory counter the row loads wait on.  Ranges longer than
+// kBwdPosLds entries read their positions from global memory instead.
 //
 // Each tile's items start with nlong long-segment slots: slot j sums the
 // chunk's listed long segments j, j + nlong, ... for this tile with the
@@ -478,7 +508,7 @@ __global__ __launch_bounds__(kBlock) void bwd_tiled_gather_kernel(const int32_t 
     s0 = seg[f];
     s1 = seg[f + 1];
   }
-  const bool is_long = kLongPath<TCH> && f < N && long_segment(s0, s1);  // summed by bwd_long_kernel
+  const bool is_long = kLongPath<TCH> && f < N && long_segment(s0, s1);  // summed by the long-segment slots
   const int n = is_long ? 0 : s1 - s0;
   const bool wave_has_work = ballot(n > 0) != 0;  // wave-uniform
   const bool skip_untouched = src_mode == kSrcDst && dst_mode == kDstOut;
@@ -511,95 +541,6 @@ __global__ __launch_bounds__(kBlock) void bwd_tiled_gather_kernel(const int32_t 
 #else
     *d = acc;
 #endif
-  }
-}
-
-// Long segments of the row gather (narrow rows, row-major grad): each is
-// summed per 32-column block by one wave, which stages kLongRows rows (lane l:
-// 16 bytes of row l / 8 of every 8) into one of its two LDS buffers while lanes
-// 0-31 (one column each) add the rows of the other in order -- the same
-// sequence as long_segment_sum_wg.  Waves work independently; each of a
-// workgroup's four waves owns 2 x 16 KB of LDS.
-constexpr int kLongRows = 128;    // rows per staged batch of a wave: 128 x 128 B = 16 KB
-constexpr int kLongBlocks = 256;  // one workgroup per CU (128 KB of LDS each); a multiple of kXcds
-
-__device__ __forceinline__ void long_segment_sum(const int32_t *__restrict__ sorted_pos, int64_t f, int s0, int n,
-                                                 int cb, const LongRows &rows, const ColMap &map,
-                                                 const RowDst &dst, f32x4 *__restrict__ tmp, int src_mode,
-                                                 int dst_mode, f32x4 (*buf)[kLongRows * 8]) {
-  constexpr int kRowsPerLoad = kWave / 8;  // rows one load instruction of the wave covers
-  constexpr int kPass = kLongRows / kRowsPerLoad;
-  const int lane = threadIdx.x % kWave;
-  const LongEnds ends = long_ends(f, cb, lane, map, dst, tmp);
-  float acc = long_start(ends, src_mode);
-  // Staging lanes: chunk q of rows r0 + kRowsPerLoad * u.
-  const int q = lane & 7, r0 = lane >> 3;
-  const bool qok = tile_col(map, cb, q) >= 0;
-  const f32x4 *src = rows.base + cb * rows.blk_stride + q;
-  const int nb = (n + kLongRows - 1) / kLongRows;
-  int p[kPass];
-  f32x4 v[kPass];
-  auto load_pos = [&](int b) {
-#pragma unroll
-    for (int u = 0; u < kPass; ++u) {
-      const int r = b * kLongRows + r0 + kRowsPerLoad * u;
-      p[u] = r < n ? sorted_pos[s0 + r] : -1;
-    }
-  };
-  auto load_rows = [&]() {
-#pragma unroll
-    for (int u = 0; u < kPass; ++u)
-      v[u] = (p[u] >= 0 && qok) ? src[(int64_t)p[u] * rows.pos_stride] : f32x4{0.f, 0.f, 0.f, 0.f};
-  };
-  auto stage = [&](int which) {
-#pragma unroll
-    for (int u = 0; u < kPass; ++u) buf[which][(r0 + kRowsPerLoad * u) * 8 + q] = v[u];
-  };
-  load_pos(0);
-  load_rows();
-  stage(0);
-  if (nb > 1) load_pos(1);
-  wave_lds_barrier();
-  for (int b = 0; b < nb; ++b) {  // nb is wave-uniform
-    const bool more = b + 1 < nb;
-    if (more) {
-      load_rows();
-      if (b + 2 < nb) load_pos(b + 2);
-    }
-    if (ends.ccol >= 0) {
-      const float *row = reinterpret_cast<const float *>(buf[b & 1]) + lane;
-      const int nrows = min(kLongRows, n - b * kLongRows);
-#pragma unroll 16
-      for (int r = 0; r < nrows; ++r) acc += row[r * 32];
-    }
-    wave_lds_barrier();  // the buffer staged next was read in the previous step
-    if (more) stage((b + 1) & 1);
-    wave_lds_barrier();
-  }
-  long_store(ends, dst_mode, acc);
-}
-
-// Sums the listed long segments of the row gather: items (segment e, column
-// block cb), cb on XCD cb % 8 (workgroup i runs on XCD i % 8), ordered
-// block-major, dealt round-robin to that XCD's waves.  src/dst modes as in
-// bwd_tiled_gather_kernel; long segments are never untouched.
-__global__ __launch_bounds__(kBlock) void bwd_long_kernel(const int32_t *__restrict__ list,
-                                                          const int *__restrict__ count,
-                                                          const int32_t *__restrict__ seg,
-                                                          const int32_t *__restrict__ sorted_pos, LongRows rows,
-                                                          ColMap map, int nblk, RowDst dst, f32x4 *__restrict__ tmp,
-                                                          int src_mode, int dst_mode) {
-  __shared__ f32x4 buf[kWavesPerBlock][2][kLongRows * 8];
-  const int wave = uniform(threadIdx.x / kWave);
-  const int64_t nseg = *count;
-  const int xcd = (int)(blockIdx.x % kXcds);
-  const int64_t slots = gridDim.x / kXcds * kWavesPerBlock, slot = blockIdx.x / kXcds * kWavesPerBlock + wave;
-  const int64_t xblk = xcd < nblk ? (nblk - xcd + kXcds - 1) / kXcds : 0;  // column blocks of this XCD
-  for (int64_t k = slot; k < xblk * nseg; k += slots) {  // wave-uniform
-    const int cb = xcd + kXcds * (int)(k / nseg);
-    const int64_t f = list[k % nseg];
-    const int s0 = seg[f];
-    long_segment_sum(sorted_pos, f, s0, seg[f + 1] - s0, cb, rows, map, dst, tmp, src_mode, dst_mode, buf[wave]);
   }
 }
 
@@ -872,9 +813,9 @@ __global__ __launch_bounds__(kBlock) void bias_final_kernel(const T *__restrict_
 
 template <typename T, int G, int CPL>
 void launch_gather(dim3 grid, hipStream_t s, const int32_t *seg_start, const int32_t *pos, int64_t N, const void *grad,
-                   int64_t cols, void *dW, int overwrite, int skip_long) {
+                   int64_t cols, void *dW, int overwrite, const SegBufs &sb, int nlong) {
   hipLaunchKernelGGL((gather_rows_kernel<T, G, CPL, 4>), grid, dim3(kBlock), 0, s, seg_start, pos, N,
-                     static_cast<const T *>(grad), cols, static_cast<T *>(dW), overwrite, skip_long);
+                     static_cast<const T *>(grad), cols, static_cast<T *>(dW), overwrite, sb.list, sb.count, nlong);
 }
 
 #define SFT_CPL_CASES(FN, T, G, ...) \
@@ -1005,15 +946,6 @@ int launch_segments(const unsigned *keys, int64_t M, int nc, int64_t nfeat, cons
   return check_launch("segment offsets");
 }
 
-// The long segments of position chunk h (before that chunk's gather launch).
-int launch_long(const SegBufs &sb, int h, int64_t nfeat, const int32_t *pos, const LongRows &rows, const ColMap &map,
-                int nblk, const RowDst &dst, f32x4 *tmp, int src_mode, int dst_mode, hipStream_t s) {
-  ProfScope prof(kProfBwdLong, s);
-  hipLaunchKernelGGL(bwd_long_kernel, dim3(kLongBlocks), dim3(kBlock), 0, s, sb.list + h * nfeat, sb.count + h,
-                     sb.seg + h * nfeat, pos, rows, map, nblk, dst, tmp, src_mode, dst_mode);
-  return check_launch("long segments");
-}
-
 }  // namespace
 
 int bwd_workspace(int64_t B, int K, int64_t N, int L, uint32_t flags, size_t *bytes) {
@@ -1133,22 +1065,13 @@ int bwd_f32(const int32_t *idx, int64_t B, int K, const float *grad, int64_t N, 
     const int64_t cols = vec ? L / 4 : L;
     const Mapping m = choose_mapping(cols);
     const int fpb = kWavesPerBlock * (kWave / m.G);
-    const dim3 grid((unsigned)ceil_div(N, fpb), (unsigned)m.slabs);
-    if (vec) {
-      const ColMap map = plain_map((int)cols, 8);
-      RowDst dst{};
-      dst.n = 1;
-      dst.start[1] = N;
-      dst.p[0] = reinterpret_cast<f32x4 *>(dW);
-      if ((rc = launch_long(sb, 0, N, pos, LongRows{reinterpret_cast<const f32x4 *>(grad), 8, cols}, map,
-                            map_tiles(map), dst, nullptr, kSrcZero, overwrite ? kDstOut : kDstOutPlus, s)) != SFT_OK)
-        return rc;
-    }
+    const int nlong = vec ? kRowLongBlocks : 0;
+    const dim3 grid((unsigned)(nlong + ceil_div(N, fpb)), (unsigned)m.slabs);
     ProfScope prof(kProfBwdGather, s);
     if (vec) {
-      SFT_G_CASES(launch_gather, f32x4, grid, s, seg, pos, N, grad, cols, dW, overwrite, 1)
+      SFT_G_CASES(launch_gather, f32x4, grid, s, seg, pos, N, grad, cols, dW, overwrite, sb, nlong)
     } else {
-      SFT_G_CASES(launch_gather, float, grid, s, seg, pos, N, grad, cols, dW, overwrite, 0)
+      SFT_G_CASES(launch_gather, float, grid, s, seg, pos, N, grad, cols, dW, overwrite, sb, 0)
     }
   }
   return check_launch("feature row gather");
