@@ -22,9 +22,11 @@ namespace sft {
 
 size_t index_lds_bytes(int G, int K);
 size_t slot_sort_workspace(int64_t M);
+// Stable sort of the active slots by (position chunk, feature); also zeroes
+// clear[0 .. nclear) before it returns (stream-ordered).
 int slot_sort(const int32_t *idx, int64_t M, int K, int64_t N, int chunk_rows, int nchunks, void *ws,
-              unsigned **keys_sorted, int **pos_sorted, unsigned **digit_totals, int *digit_count,
-              hipStream_t s);
+              unsigned **keys_sorted, int **pos_sorted, unsigned **digit_totals, int *digit_count, int *clear,
+              int nclear, hipStream_t s);
 
 namespace {
 
@@ -934,13 +936,11 @@ int launch_bias_final(const float *partial, int nparts, int L, float *db, int ov
   return check_launch("bias reduction");
 }
 
-// Segment starts of one sort and its lists of long segments (counts cleared
-// first, with a kernel rather than a memset so that the calls can be captured
-// in a graph).
+// Segment starts of one sort and its lists of long segments (the counts
+// were zeroed by the sort).
 int launch_segments(const unsigned *keys, int64_t M, int nc, int64_t nfeat, const unsigned *totals, int ntot,
                     const SegBufs &sb, hipStream_t s) {
   ProfScope prof(kProfBwdOffsets, s);
-  hipLaunchKernelGGL(zero_kernel, dim3(1), dim3(kBlock), 0, s, reinterpret_cast<float *>(sb.count), (int64_t)nc);
   hipLaunchKernelGGL(seg_offsets_kernel, dim3((unsigned)std::min<int64_t>(ceil_div(M + 1, kBlock), kSegBlocks)),
                      dim3(kBlock), 0, s, keys, (int64_t)nc * nfeat, totals, ntot, sb.seg, nfeat, sb.list, sb.count);
   return check_launch("segment offsets");
@@ -1026,6 +1026,7 @@ int bwd_f32(const int32_t *idx, int64_t B, int K, const float *grad, int64_t N, 
     return check_launch("weight grad zero fill");
   }
   const int nc = tiled ? sort_chunks(B, L, flags) : 1;
+  const SegBufs sb = seg_bufs(seg, nc, N);
   const int chunk_rows = (int)(nc > 1 ? half_rows(B) : B);
   const int64_t nkeys = (int64_t)nc * N;
   unsigned *keys = nullptr, *totals = nullptr;
@@ -1033,11 +1034,11 @@ int bwd_f32(const int32_t *idx, int64_t B, int K, const float *grad, int64_t N, 
   int ntot = 0;
   {
     ProfScope prof(kProfBwdSort, s);
-    if ((rc = slot_sort(idx, M, K, N, chunk_rows, nc, w + lay.sort, &keys, &pos, &totals, &ntot, s)) != SFT_OK)
+    if ((rc = slot_sort(idx, M, K, N, chunk_rows, nc, w + lay.sort, &keys, &pos, &totals, &ntot, sb.count, nc,
+                        s)) != SFT_OK)
       return rc;
   }
   (void)nkeys;
-  const SegBufs sb = seg_bufs(seg, nc, N);
   if ((rc = launch_segments(keys, M, nc, N, totals, ntot, sb, s)) != SFT_OK) return rc;
   if (tiled) {
     constexpr int TCH = SFT_BWD_TCH;
@@ -1125,11 +1126,13 @@ static int pair_gather_perspective(int p, const int32_t *idx, int64_t B, int K, 
   unsigned *keys = nullptr, *totals = nullptr;
   int32_t *pos = nullptr;
   int ntot = 0, rc;
+  const SegBufs sb = seg_bufs(seg, nc, N);
   {
     ProfScope prof(kProfBwdSort, s);
-    if ((rc = slot_sort(idx, M, K, N, chunk_rows, nc, sort_ws, &keys, &pos, &totals, &ntot, s)) != SFT_OK) return rc;
+    if ((rc = slot_sort(idx, M, K, N, chunk_rows, nc, sort_ws, &keys, &pos, &totals, &ntot, sb.count, nc, s)) !=
+        SFT_OK)
+      return rc;
   }
-  const SegBufs sb = seg_bufs(seg, nc, N);
   if ((rc = launch_segments(keys, M, nc, N, totals, ntot, sb, s)) != SFT_OK) return rc;
   for (int h = 0; h < nc; ++h) {
     int src_mode, dst_mode;

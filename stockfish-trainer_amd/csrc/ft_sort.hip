@@ -129,9 +129,12 @@ __global__ __launch_bounds__(kBlock) void radix_upsweep(SlotKey sk, const unsign
 // Per digit d (one block each): exclusive scan of hist[d][0 .. ntiles) in
 // place, and the digit's total into totals[d].
 __global__ __launch_bounds__(kBlock) void radix_scan_digits(unsigned *__restrict__ hist, int ntiles,
-                                                            unsigned *__restrict__ totals) {
+                                                            unsigned *__restrict__ totals, int *__restrict__ clear,
+                                                            int nclear) {
   __shared__ unsigned part[kBlock];
   const int tid = threadIdx.x;
+  if (blockIdx.x == 0)  // the caller's counters, zeroed here to save a launch
+    for (int i = tid; i < nclear; i += kBlock) clear[i] = 0;
   unsigned *h = hist + (int64_t)blockIdx.x * ntiles;
   const int per = (ntiles + kBlock - 1) / kBlock;
   const int lo = std::min(ntiles, tid * per), hi = std::min(ntiles, lo + per);
@@ -285,7 +288,7 @@ unsigned key_bits(int64_t maxkey) {
 
 template <int RB, int IT>
 int run_passes(const SlotKey &sk, int64_t M, int passes, unsigned *kbuf[2], int *vbuf[2], unsigned *hist,
-               unsigned *totals, int ntiles, hipStream_t s) {
+               unsigned *totals, int ntiles, int *clear, int nclear, hipStream_t s) {
   for (int p = 0; p < passes; ++p) {
     const int shift = p * RB;
     const unsigned *kin = p == 0 ? nullptr : kbuf[(p - 1) & 1];
@@ -298,7 +301,8 @@ int run_passes(const SlotKey &sk, int64_t M, int passes, unsigned *kbuf[2], int 
     else
       hipLaunchKernelGGL((radix_upsweep<RB, false, IT>), dim3(ntiles), dim3(kBlock), 0, s, sk, kin, M, totals, ntiles,
                          shift, hist);
-    hipLaunchKernelGGL(radix_scan_digits, dim3(1 << RB), dim3(kBlock), 0, s, hist, ntiles, totals);
+    hipLaunchKernelGGL(radix_scan_digits, dim3(1 << RB), dim3(kBlock), 0, s, hist, ntiles, totals, clear,
+                       p == 0 ? nclear : 0);
     if (p == 0)
       hipLaunchKernelGGL((radix_downsweep<RB, true, IT>), dim3(ntiles), dim3(kBlock), 0, s, sk, kin, vin, kout, vout,
                          hist, totals, M, ntiles, shift);
@@ -321,8 +325,8 @@ size_t slot_sort_workspace(int64_t M) {
 }
 
 int slot_sort(const int32_t *idx, int64_t M, int K, int64_t N, int chunk_rows, int nchunks, void *ws,
-              unsigned **keys_sorted, int **pos_sorted, unsigned **digit_totals, int *digit_count,
-              hipStream_t s) {
+              unsigned **keys_sorted, int **pos_sorted, unsigned **digit_totals, int *digit_count, int *clear,
+              int nclear, hipStream_t s) {
   char *w = static_cast<char *>(ws);
   const size_t a = align256((size_t)M * 4);
   unsigned *kbuf[2] = {reinterpret_cast<unsigned *>(w), reinterpret_cast<unsigned *>(w + 2 * a)};
@@ -342,11 +346,11 @@ int slot_sort(const int32_t *idx, int64_t M, int K, int64_t N, int chunk_rows, i
   }
   int rc;
   if (big)
-    rc = rb == 9 ? run_passes<9, kSortItemsBig>(sk, M, passes, kbuf, vbuf, hist, totals, ntiles, s)
-                 : run_passes<8, kSortItemsBig>(sk, M, passes, kbuf, vbuf, hist, totals, ntiles, s);
+    rc = rb == 9 ? run_passes<9, kSortItemsBig>(sk, M, passes, kbuf, vbuf, hist, totals, ntiles, clear, nclear, s)
+                 : run_passes<8, kSortItemsBig>(sk, M, passes, kbuf, vbuf, hist, totals, ntiles, clear, nclear, s);
   else
-    rc = rb == 9 ? run_passes<9, kSortItems>(sk, M, passes, kbuf, vbuf, hist, totals, ntiles, s)
-                 : run_passes<8, kSortItems>(sk, M, passes, kbuf, vbuf, hist, totals, ntiles, s);
+    rc = rb == 9 ? run_passes<9, kSortItems>(sk, M, passes, kbuf, vbuf, hist, totals, ntiles, clear, nclear, s)
+                 : run_passes<8, kSortItems>(sk, M, passes, kbuf, vbuf, hist, totals, ntiles, clear, nclear, s);
   if (rc != SFT_OK) return rc;
   *keys_sorted = kbuf[(passes - 1) & 1];
   *pos_sorted = vbuf[(passes - 1) & 1];
