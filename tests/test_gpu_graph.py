@@ -62,6 +62,31 @@ def test_graph_two_perspectives_slf():
     _capture_and_compare(step, 4)
 
 
+@pytest.mark.parametrize("L", [1048, 136])
+def test_graph_skewed_segments(L):
+    """Long segments (listed by the segment pass with atomics, summed by the
+    gathers' long-segment workgroups) replay bit-identically."""
+    announce(f"graph: SparseLinearFunction fwd+bwd, skewed feature frequencies, L={L}")
+    B, N, K = 6000, 3000, 32
+    g = np.random.default_rng(41)
+    iw_t = dev(workloads.make_zipf_indices(g, B, N, K, 16, 32, alpha=1.0))
+    ib_t = dev(workloads.make_zipf_indices(g, B, N, K, 16, 32, alpha=1.0))
+    Wt = dev((g.standard_normal((N, L)) * 0.01).astype(np.float32)).requires_grad_(True)
+    bt = dev(g.uniform(-0.1, 0.1, L).astype(np.float32)).requires_grad_(True)
+    gw = dev(g.standard_normal((B, L)).astype(np.float32))
+    gb = dev(g.standard_normal((B, L)).astype(np.float32))
+
+    def step():
+        Wt.grad = None
+        bt.grad = None
+        ow = SparseLinearFunction.apply(iw_t, Wt, bt)
+        ob = SparseLinearFunction.apply(ib_t, Wt, bt)
+        torch.autograd.backward([ow, ob], [gw, gb])
+        return [ow, ob, Wt.grad, bt.grad]
+
+    _capture_and_compare(step, 4)
+
+
 def test_graph_fused_transform():
     announce("graph: fused composed transform fwd+bwd")
     B, L1 = 2048, 1040
