@@ -2,6 +2,7 @@
 // reporting and the optional per-launch event timing.
 #include <atomic>
 #include <climits>
+#include <memory>
 #include <mutex>
 #include <vector>
 
@@ -68,6 +69,74 @@ int check_launch(const char *what) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(SFT_EHIP, std::string(what) + ": " + hipGetErrorString(e));
   return SFT_OK;
+}
+
+// ------------------------------------------------------- side stream ----
+// One non-blocking stream (default priority), a fork event and kSideMarks
+// join events per thread and device, created on first use and kept until the
+// thread ends: a call forks independent work onto the side stream and makes
+// its own stream wait for marks recorded there before the work that needs it.
+// Per thread, so that concurrent callers (and a caller capturing a graph)
+// never share one.
+namespace {
+struct SideState {
+  hipStream_t stream = nullptr;
+  hipEvent_t fork = nullptr;
+  hipEvent_t mark[kSideMarks] = {};
+  ~SideState() {
+    for (hipEvent_t &e : mark)
+      if (e) (void)hipEventDestroy(e);
+    if (fork) (void)hipEventDestroy(fork);
+    if (stream) (void)hipStreamDestroy(stream);
+  }
+};
+thread_local std::vector<std::unique_ptr<SideState>> t_side;
+
+SideState *side_state(bool create) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+  if ((int)t_side.size() <= dev) {
+    if (!create) return nullptr;
+    t_side.resize(dev + 1);
+  }
+  if (!t_side[dev] && create) {
+    auto st = std::make_unique<SideState>();
+    bool ok = hipStreamCreateWithFlags(&st->stream, hipStreamNonBlocking) == hipSuccess &&
+              hipEventCreateWithFlags(&st->fork, hipEventDisableTiming) == hipSuccess;
+    for (hipEvent_t &e : st->mark) ok = ok && hipEventCreateWithFlags(&e, hipEventDisableTiming) == hipSuccess;
+    if (!ok) return nullptr;
+    t_side[dev] = std::move(st);
+  }
+  return t_side[dev].get();
+}
+}  // namespace
+
+int fork_side(hipStream_t s, hipStream_t *side) {
+  SideState *st = side_state(true);
+  if (!st) return fail(SFT_EHIP, "side stream: creation failed");
+  if (hipEventRecord(st->fork, s) != hipSuccess || hipStreamWaitEvent(st->stream, st->fork, 0) != hipSuccess)
+    return fail(SFT_EHIP, "side stream: fork failed");
+  *side = st->stream;
+  return SFT_OK;
+}
+
+int mark_side(int slot) {
+  SideState *st = side_state(false);
+  if (!st || slot < 0 || slot >= kSideMarks) return fail(SFT_EHIP, "side stream: mark without fork");
+  if (hipEventRecord(st->mark[slot], st->stream) != hipSuccess) return fail(SFT_EHIP, "side stream: mark failed");
+  return SFT_OK;
+}
+
+int wait_side(hipStream_t s, int slot) {
+  SideState *st = side_state(false);
+  if (!st || slot < 0 || slot >= kSideMarks) return fail(SFT_EHIP, "side stream: wait without fork");
+  if (hipStreamWaitEvent(s, st->mark[slot], 0) != hipSuccess) return fail(SFT_EHIP, "side stream: wait failed");
+  return SFT_OK;
+}
+
+int join_side(hipStream_t s) {
+  const int rc = mark_side(0);
+  return rc != SFT_OK ? rc : wait_side(s, 0);
 }
 
 Mapping choose_mapping(int64_t chunks, int min_group) {

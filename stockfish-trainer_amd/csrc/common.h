@@ -28,6 +28,18 @@ void clear_error();
 int fail(int code, const std::string &msg);
 int check_launch(const char *what);
 
+// ---- fork/join with the calling thread's side stream on the current device ----
+// fork_side: work enqueued on *side after the call runs after everything
+// already enqueued on s.  mark_side(k) records mark k on the side stream (after
+// the work enqueued there so far); wait_side(s, k): work enqueued on s after
+// the call runs after that mark.  join_side(s) = mark 0 + wait.  All are stream
+// operations (event record / wait), so they capture into a graph like kernels.
+constexpr int kSideMarks = 2;
+int fork_side(hipStream_t s, hipStream_t *side);
+int mark_side(int slot);
+int wait_side(hipStream_t s, int slot);
+int join_side(hipStream_t s);
+
 // ---- kernel timing hooks (active only between sft_prof_enable(1) and (0)) ----
 enum ProfKind : int {
   kProfFwdF32 = 0,

@@ -974,6 +974,27 @@ int bwd_f32(const int32_t *idx, int64_t B, int K, const float *grad, int64_t N, 
                      (uintptr_t)dW % 16 == 0 && (uintptr_t)db % 16 == 0;
   f32x4 *gt = tiled ? reinterpret_cast<f32x4 *>(w + lay.gt) : nullptr;
 
+  // ---- sort of the slots and their segments: they need only the indices, so
+  // they run on the side stream while the bias pass streams the grad ----
+  const bool sorted = !(flags & SFT_BWD_ATOMIC) && M > 0;
+  const int nc = tiled ? sort_chunks(B, L, flags) : 1;
+  int32_t *seg = reinterpret_cast<int32_t *>(w + lay.seg);
+  const SegBufs sb = seg_bufs(seg, nc, N);
+  unsigned *keys = nullptr, *totals = nullptr;
+  int32_t *pos = nullptr;
+  int ntot = 0;
+  if (sorted) {
+    hipStream_t side;
+    if ((rc = fork_side(s, &side)) != SFT_OK) return rc;
+    {
+      ProfScope prof(kProfBwdSort, side);
+      if ((rc = slot_sort(idx, M, K, N, (int)(nc > 1 ? half_rows(B) : B), nc, w + lay.sort, &keys, &pos, &totals,
+                          &ntot, sb.count, nc, side)) != SFT_OK)
+        return rc;
+    }
+    if ((rc = launch_segments(keys, M, nc, N, totals, ntot, sb, side)) != SFT_OK) return rc;
+  }
+
   // ---- bias grad ----
   {
     const bool vec = (L % 4 == 0) && ((uintptr_t)grad % 16 == 0) && ((uintptr_t)db % 16 == 0);
@@ -984,6 +1005,7 @@ int bwd_f32(const int32_t *idx, int64_t B, int K, const float *grad, int64_t N, 
                                 s)) != SFT_OK)
       return rc;
   }
+  if (sorted && (rc = join_side(s)) != SFT_OK) return rc;
 
   if (flags & SFT_BWD_ATOMIC) {
     if (overwrite) {
@@ -1016,7 +1038,6 @@ int bwd_f32(const int32_t *idx, int64_t B, int K, const float *grad, int64_t N, 
   }
 
   // ---- sorted (deterministic) weight grad ----
-  int32_t *seg = reinterpret_cast<int32_t *>(w + lay.seg);
   if (M == 0) {
     if (!overwrite) return SFT_OK;  // nothing active: dW untouched
     const int64_t n = N * (int64_t)L;  // overwrite with no slots at all: every row is zero
@@ -1025,21 +1046,6 @@ int bwd_f32(const int32_t *idx, int64_t B, int K, const float *grad, int64_t N, 
                        s, dW, n);
     return check_launch("weight grad zero fill");
   }
-  const int nc = tiled ? sort_chunks(B, L, flags) : 1;
-  const SegBufs sb = seg_bufs(seg, nc, N);
-  const int chunk_rows = (int)(nc > 1 ? half_rows(B) : B);
-  const int64_t nkeys = (int64_t)nc * N;
-  unsigned *keys = nullptr, *totals = nullptr;
-  int32_t *pos = nullptr;
-  int ntot = 0;
-  {
-    ProfScope prof(kProfBwdSort, s);
-    if ((rc = slot_sort(idx, M, K, N, chunk_rows, nc, w + lay.sort, &keys, &pos, &totals, &ntot, sb.count, nc,
-                        s)) != SFT_OK)
-      return rc;
-  }
-  (void)nkeys;
-  if ((rc = launch_segments(keys, M, nc, N, totals, ntot, sb, s)) != SFT_OK) return rc;
   if (tiled) {
     constexpr int TCH = SFT_BWD_TCH;
     const int64_t cols4 = L / 4;
@@ -1083,7 +1089,7 @@ int bwd_f32(const int32_t *idx, int64_t B, int K, const float *grad, int64_t N, 
 // Workspace: bias partials of both grads | sort buffers | segment starts |
 // grad tiles | tmp (the second perspective's sums, [N, L]).
 struct PairLayout {
-  size_t partial, sort, seg, gt, tmp, total;
+  size_t partial, sort[2], seg[2], gt, tmp, total;
   int nparts, nc;
 };
 
@@ -1094,10 +1100,12 @@ void make_pair_layout(int64_t B, int K, int64_t N, int L, PairLayout &lay) {
   size_t off = 0;
   lay.partial = off;
   off = align256(off + (size_t)2 * lay.nparts * (size_t)L * sizeof(float));
-  lay.sort = off;
-  off = align256(off + slot_sort_workspace(std::max<int64_t>(M, 1)));
-  lay.seg = off;
-  off = align256(off + seg_region_bytes(lay.nc, N));
+  for (int p = 0; p < 2; ++p) {  // each perspective sorts into its own buffers
+    lay.sort[p] = off;
+    off = align256(off + slot_sort_workspace(std::max<int64_t>(M, 1)));
+    lay.seg[p] = off;
+    off = align256(off + seg_region_bytes(lay.nc, N));
+  }
   lay.gt = off;
   off = align256(off + (size_t)(ceil_div(L, 32) * B * 32) * sizeof(float));
   lay.tmp = off;
@@ -1111,29 +1119,35 @@ size_t bwd_pair_workspace(int64_t B, int K, int64_t N, int L) {
   return lay.total;
 }
 
-// Sort one perspective's slots, find its segments and run its position-chunk
-// launches of the tiled gather: perspective 0 stores to dst, perspective 1 sums
-// onto 0 in tmp and its last launch stores dst + tmp.
-static int pair_gather_perspective(int p, const int32_t *idx, int64_t B, int K, int64_t N, const ColMap &map,
-                                   const f32x4 *gt, const RowDst &dst, f32x4 *tmp, int nc, char *sort_ws,
-                                   int32_t *seg, hipStream_t s) {
+// One perspective's slots sorted, with their segments (on the side stream).
+struct SortedSlots {
+  SegBufs sb;
+  int32_t *pos;
+};
+static int pair_sort_perspective(const int32_t *idx, int64_t B, int K, int64_t N, int nc, char *sort_ws,
+                                 int32_t *seg, SortedSlots &out, hipStream_t s) {
   const int64_t M = B * K;
+  unsigned *keys = nullptr, *totals = nullptr;
+  int ntot = 0, rc;
+  out.sb = seg_bufs(seg, nc, N);
+  {
+    ProfScope prof(kProfBwdSort, s);
+    if ((rc = slot_sort(idx, M, K, N, (int)(nc > 1 ? half_rows(B) : B), nc, sort_ws, &keys, &out.pos, &totals,
+                        &ntot, out.sb.count, nc, s)) != SFT_OK)
+      return rc;
+  }
+  return launch_segments(keys, M, nc, N, totals, ntot, out.sb, s);
+}
+
+// One perspective's position-chunk launches of the tiled gather: perspective 0
+// stores to dst, perspective 1 sums onto 0 in tmp and its last launch stores
+// dst + tmp.
+static int pair_gather_perspective(int p, const SortedSlots &ss, int64_t B, int64_t N, const ColMap &map,
+                                   const f32x4 *gt, const RowDst &dst, f32x4 *tmp, int nc, hipStream_t s) {
   const int ntiles = map_tiles(map);
   const int ngroups = (int)ceil_div(N, bwd_feat_per_block<kBwdTileCh>());
   static_assert(kLongPath<kBwdTileCh>, "the pair gather sums long segments in its long-segment slots");
   const int64_t blocks = tile_sched_items_per_xcd(ntiles, ngroups + kLongSlots) * kXcds;
-  const int chunk_rows = (int)(nc > 1 ? half_rows(B) : B);
-  unsigned *keys = nullptr, *totals = nullptr;
-  int32_t *pos = nullptr;
-  int ntot = 0, rc;
-  const SegBufs sb = seg_bufs(seg, nc, N);
-  {
-    ProfScope prof(kProfBwdSort, s);
-    if ((rc = slot_sort(idx, M, K, N, chunk_rows, nc, sort_ws, &keys, &pos, &totals, &ntot, sb.count, nc, s)) !=
-        SFT_OK)
-      return rc;
-  }
-  if ((rc = launch_segments(keys, M, nc, N, totals, ntot, sb, s)) != SFT_OK) return rc;
   for (int h = 0; h < nc; ++h) {
     int src_mode, dst_mode;
     if (p == 0) {
@@ -1145,9 +1159,28 @@ static int pair_gather_perspective(int p, const int32_t *idx, int64_t B, int K, 
     }
     ProfScope prof(kProfBwdTiled, s);
     hipLaunchKernelGGL(bwd_tiled_gather_kernel<kBwdTileCh>, dim3((unsigned)blocks), dim3(kBlock), 0, s,
-                       seg + (int64_t)h * N, pos, N, gt, B, map, dst, tmp, src_mode, dst_mode, ntiles, ngroups,
-                       sb.list + h * N, sb.count + h, kLongSlots);
-    if ((rc = check_launch("tiled feature gather")) != SFT_OK) return rc;
+                       ss.sb.seg + (int64_t)h * N, ss.pos, N, gt, B, map, dst, tmp, src_mode, dst_mode, ntiles,
+                       ngroups, ss.sb.list + h * N, ss.sb.count + h, kLongSlots);
+    const int rc = check_launch("tiled feature gather");
+    if (rc != SFT_OK) return rc;
+  }
+  return SFT_OK;
+}
+
+// Both perspectives' sorts on the side stream, into their own buffers; mark p
+// follows perspective p's sort, so its gathers wait for that sort only.
+static int pair_sort_both(const int32_t *idx0, const int32_t *idx1, int64_t B, int K, int64_t N, int nc,
+                          char *w, const size_t (&sort_off)[2], const size_t (&seg_off)[2], SortedSlots (&ss)[2],
+                          hipStream_t s) {
+  static_assert(kSideMarks >= 2, "one mark per perspective");
+  hipStream_t side;
+  int rc = fork_side(s, &side);
+  if (rc != SFT_OK) return rc;
+  for (int p = 0; p < 2; ++p) {
+    if ((rc = pair_sort_perspective(p == 0 ? idx0 : idx1, B, K, N, nc, w + sort_off[p],
+                                    reinterpret_cast<int32_t *>(w + seg_off[p]), ss[p], side)) != SFT_OK)
+      return rc;
+    if ((rc = mark_side(p)) != SFT_OK) return rc;
   }
   return SFT_OK;
 }
@@ -1180,16 +1213,16 @@ int bwd_pair_f32(const int32_t *idx0, const int32_t *idx1, int64_t B, int K, con
   float *partial = reinterpret_cast<float *>(w + lay.partial);
   f32x4 *gt = reinterpret_cast<f32x4 *>(w + lay.gt);
   f32x4 *tmp = reinterpret_cast<f32x4 *>(w + lay.tmp);
-  int32_t *seg = reinterpret_cast<int32_t *>(w + lay.seg);
-  int rc;
+  SortedSlots ss[2];
+  int rc = pair_sort_both(idx0, idx1, B, K, N, lay.nc, w, lay.sort, lay.seg, ss, s);
+  if (rc != SFT_OK) return rc;
   for (int p = 0; p < 2; ++p) {
     const float *grad = p == 0 ? grad0 : grad1;
     if ((rc = launch_bias_partial(grad, B, L, lay.nparts, partial + (size_t)p * lay.nparts * L, gt, true, s)) !=
         SFT_OK)
       return rc;
-    if ((rc = pair_gather_perspective(p, p == 0 ? idx0 : idx1, B, K, N, map, gt, dst, tmp, lay.nc, w + lay.sort, seg,
-                                      s)) != SFT_OK)
-      return rc;
+    if ((rc = wait_side(s, p)) != SFT_OK) return rc;
+    if ((rc = pair_gather_perspective(p, ss[p], B, N, map, gt, dst, tmp, lay.nc, s)) != SFT_OK) return rc;
   }
   if ((rc = launch_bias_final(partial, 2 * lay.nparts, L, db, 1, true, s)) != SFT_OK) return rc;
   return virtual_reduce(vgrad_src, vgrad, vperiod, vreps, nvirt, L / 4, s);
@@ -1199,7 +1232,7 @@ int bwd_pair_f32(const int32_t *idx0, const int32_t *idx1, int64_t B, int K, con
 // Workspace: bias partials | sort buffers | segment starts | grad tiles of both
 // perspectives (paired map) | tmp [N, L].
 struct TransformLayout {
-  size_t partial, sort, seg, gt0, gt1, tmp, total;
+  size_t partial, sort[2], seg[2], gt0, gt1, tmp, total;
   int nparts, nc;
 };
 
@@ -1212,10 +1245,12 @@ void make_transform_layout(int64_t B, int K, int64_t N, int L, int L1, Transform
   size_t off = 0;
   lay.partial = off;
   off = align256(off + (size_t)lay.nparts * (size_t)L * sizeof(float));
-  lay.sort = off;
-  off = align256(off + slot_sort_workspace(std::max<int64_t>(M, 1)));
-  lay.seg = off;
-  off = align256(off + seg_region_bytes(lay.nc, N));
+  for (int p = 0; p < 2; ++p) {
+    lay.sort[p] = off;
+    off = align256(off + slot_sort_workspace(std::max<int64_t>(M, 1)));
+    lay.seg[p] = off;
+    off = align256(off + seg_region_bytes(lay.nc, N));
+  }
   lay.gt0 = off;
   off = align256(off + gtb);
   lay.gt1 = off;
@@ -1257,7 +1292,9 @@ int bwd_transform_f32(const int32_t *idx0, const int32_t *idx1, int64_t B, int K
   e.gt1 = gt1;
   e.partial = reinterpret_cast<f32x4 *>(w + lay.partial);
   e.P = L - L1;
-  int rc;
+  SortedSlots ss[2];  // sorted on the side stream while the epilogue runs
+  int rc = pair_sort_both(idx0, idx1, B, K, N, lay.nc, w, lay.sort, lay.seg, ss, s);
+  if (rc != SFT_OK) return rc;
   {
     ProfScope prof(kProfBwdEpilogue, s);
     hipLaunchKernelGGL(bwd_epilogue_kernel, dim3((unsigned)lay.nparts), dim3(kBlock), 0, s, e, map, B,
@@ -1268,11 +1305,11 @@ int bwd_transform_f32(const int32_t *idx0, const int32_t *idx1, int64_t B, int K
       SFT_OK)
     return rc;
   f32x4 *tmp = reinterpret_cast<f32x4 *>(w + lay.tmp);
-  int32_t *seg = reinterpret_cast<int32_t *>(w + lay.seg);
-  for (int p = 0; p < 2; ++p)
-    if ((rc = pair_gather_perspective(p, p == 0 ? idx0 : idx1, B, K, N, map, p == 0 ? gt0 : gt1, dst, tmp, lay.nc,
-                                      w + lay.sort, seg, s)) != SFT_OK)
+  for (int p = 0; p < 2; ++p) {
+    if ((rc = wait_side(s, p)) != SFT_OK) return rc;
+    if ((rc = pair_gather_perspective(p, ss[p], B, N, map, p == 0 ? gt0 : gt1, dst, tmp, lay.nc, s)) != SFT_OK)
       return rc;
+  }
   return virtual_reduce(vgrad_src, vgrad, vperiod, vreps, nvirt, L / 4, s);
 }
 
