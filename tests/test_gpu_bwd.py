@@ -91,6 +91,25 @@ def test_sorted_bwd_skewed_segments(seed, B, N, K, L, hot, p_hot, overwrite, row
     assert np.array_equal(dW, rW)
 
 
+@pytest.mark.parametrize("L,rows", [(1048, False), (136, True)])
+def test_sorted_bwd_long_segments_with_repeated_slots(L, rows):
+    """A feature repeated within rows: its long segment holds each such
+    position several times, added once per slot (FT/kernel.py:122, 178-181)."""
+    announce(f"bwd long segments with repeated slots L={L} rows={rows}")
+    g = np.random.default_rng(77)
+    B, N, K = 3000, 900, 12
+    idx = workloads.make_indices(g, B, N, K, 4, 8, sort=False)
+    rep = g.random(B) < 0.6
+    idx[rep, 8] = 7
+    idx[rep & (g.random(B) < 0.5), 9] = 7  # some rows hold feature 7 three times
+    idx[g.random(B) < 0.3, 10] = 11
+    G = g.standard_normal((B, L)).astype(np.float32)
+    flags = _native.SFT_BWD_OVERWRITE | (_native.SFT_BWD_ROWS if rows else 0)
+    dW, _ = run_bwd(idx, G, N, flags)
+    rW, _ = ft_oracle.bwd_f32(idx, G, N)
+    assert np.array_equal(dW, rW)
+
+
 @pytest.mark.parametrize("seed,B,N,K,L,lo,hi,sort", SHAPES)
 @pytest.mark.parametrize("overwrite", [False, True])
 def test_atomic_bwd_within_tolerance(seed, B, N, K, L, lo, hi, sort, overwrite):
