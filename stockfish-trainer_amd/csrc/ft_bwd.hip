@@ -8,7 +8,11 @@
 //   2. seg_start[f] = first sorted slot with key >= f, for f = 0..N.
 //   3. one lane group per feature row: acc = 0, acc += grad[b] over the
 //      feature's positions in ascending order, then one store of the row
-//      (dW[f] + acc, or acc when overwriting).  No atomics touch dW.
+//      (dW[f] + acc, or acc when overwriting).  No atomics touch dW.  Long
+//      segments (features active in many positions) are summed by whole
+//      workgroups in the same order.
+// Steps 1-2 need only the indices and run on a side stream beside the bias
+// pass, which streams the grad (fork/join by events).
 // Alternative (SFT_BWD_ATOMIC): position-major scatter, each active slot adds
 // the position's grad row into dW[f] with fp32 atomics.
 // Bias grad (FT/kernel.py:269): per-block column partial sums, then a fixed-
