@@ -763,7 +763,7 @@ __global__ __launch_bounds__(kBlock) void bias_partial_kernel(const T *__restric
 #pragma unroll
       for (int j = 0; j < CPL; ++j) {
         v[u][j] = T(0);
-        if (rr < r1 && colok[j]) v[u][j] = row[kWave * j];
+        if (rr < r1 && colok[j]) v[u][j] = __builtin_nontemporal_load(row + kWave * j);  // read once
       }
     }
     if (gt != nullptr) {
