@@ -78,6 +78,25 @@ def load_traffic(workload_name: str, kind: str):
     return d.get("traffic_bytes_per_launch")
 
 
+def attainable(dev) -> dict:
+    """The measured HBM ceiling beside the 8 TB/s peak: a 1 GiB device-to-device
+    copy, bytes read + written per second."""
+    import torch
+
+    src = torch.empty(1 << 28, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(10):
+        dst.copy_(src)
+    e1.record()
+    torch.cuda.synchronize()
+    return {"copy_gbs": 2 * src.numel() * 4 / (e0.elapsed_time(e1) / 10 * 1e-3) / 1e9, "copy_bytes": 1 << 30}
+
+
 def cpu_baseline(w, d, seconds: float) -> dict:
     import numpy as np
     import torch
@@ -778,6 +797,8 @@ def main() -> int:
         },
         "kernels": kern,
     }
+    result["attainable"] = attainable(dev)
+    log(f"[bench] attainable: 1 GiB device copy {result['attainable']['copy_gbs']:.0f} GB/s")
     if not args.no_cpu:
         log(f"[bench] cpu baseline ({args.cpu_seconds:.0f} s budget)")
         result["cpu_baseline"] = cpu_baseline(w, d, args.cpu_seconds)
