@@ -139,7 +139,9 @@ int sft_ft_fwd_i16(const int32_t *idx, int64_t batch, int32_t max_active, const 
 
 /*
  * Bytes of device workspace sft_ft_fwd_i16_ex uses (0 when the shape runs the
- * row gather).  Host-only computation.  No reference counterpart.
+ * row gather); it grows with psqt_size, whose PSQT columns are stored in the
+ * tiles beside the int16 columns, so query with the psqt_size of the call.
+ * Host-only computation.  No reference counterpart.
  */
 int sft_ft_fwd_i16_workspace_size(int64_t batch, int32_t max_active, int64_t num_inputs,
                                   int32_t output_size, int32_t psqt_size, uint32_t flags,
@@ -148,8 +150,9 @@ int sft_ft_fwd_i16_workspace_size(int64_t batch, int32_t max_active, int64_t num
 /*
  * int16 forward with a workspace: same results, bit for bit, as sft_ft_fwd_i16.
  * Unless SFT_Q16_ROWS is set, shapes with output_size % 8 == 0, at least 8
- * column tiles of 64 and psqt_size <= 8 copy the table into 64-column tiles in
- * the workspace and gather them XCD by XCD from L2.
+ * column tiles of 64 and psqt_size <= 8 copy the table, with the PSQT columns
+ * appended to each row, into 64-column tiles in the workspace and gather them
+ * XCD by XCD from L2.
  */
 int sft_ft_fwd_i16_ex(const int32_t *idx, int64_t batch, int32_t max_active,
                       const int16_t *weight, int64_t num_inputs, int32_t output_size,

@@ -270,6 +270,55 @@ __device__ __forceinline__ f32x4 shfl_xor4(f32x4 v, int m) {
   return f32x4{__shfl_xor(v.x, m), __shfl_xor(v.y, m), __shfl_xor(v.z, m), __shfl_xor(v.w, m)};
 }
 
+constexpr uint32_t kTileRowBytes = kTileCh * sizeof(f32x4);  // 128
+
+__device__ __forceinline__ f32x4 f32_row(const char *tbase, uint32_t lane_off, int f) {
+  return *reinterpret_cast<const f32x4 *>(tbase + ((uint32_t)f * kTileRowBytes + lane_off));
+}
+
+// Rows [0, n) of one position in one tile, added onto acc in list order (the
+// order of the reference's sum).  The main loop covers the rows every lane of
+// the 8-lane group has (nmin) without masks, a masked tail the rest up to nmax.
+// PARTIAL (block-uniform: the tile has padding lanes) masks the padding lanes'
+// loads so that they fetch nothing; in a full tile every lane loads.  Row
+// addresses are 32-bit offsets from the tile's base (a tile is N x 128 B).
+template <bool PARTIAL>
+__device__ __forceinline__ f32x4 f32_tile_rows(const int *mylist, int n, int nmin, int nmax, const char *tbase,
+                                               uint32_t lane_off, bool colok, f32x4 acc) {
+  constexpr int U = SFT_FWD_TILED_U;
+  static_assert(U % 4 == 0, "rows are read from the LDS list four at a time");
+  int k = 0;
+  for (; k + U <= nmin; k += U) {
+    int fi[U];
+#pragma unroll
+    for (int u = 0; u < U; u += 4) {
+      const i32x4 f4 = read4(mylist, k + u);
+      fi[u] = f4[0], fi[u + 1] = f4[1], fi[u + 2] = f4[2], fi[u + 3] = f4[3];
+    }
+    f32x4 w[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      w[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+      if (!PARTIAL || colok) w[u] = f32_row(tbase, lane_off, fi[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) acc += w[u];
+  }
+  for (; k < nmax; k += 4) {
+    const i32x4 f4 = read4(mylist, k);
+    f32x4 w[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      w[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+      if (k + u < n && (!PARTIAL || colok)) w[u] = f32_row(tbase, lane_off, f4[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      if (k + u < n) acc += w[u];
+  }
+  return acc;
+}
+
 // Two perspectives share one launch: chunks [0, nchunks_p) read idx0 and write
 // out0, chunks [nchunks_p, 2 nchunks_p) idx1 and out1, so an XCD gathers both
 // perspectives from a tile while it is in L2.  A single-perspective call passes
@@ -281,7 +330,6 @@ __global__ __launch_bounds__(kBlock) void fwd_tiled_kernel(const int32_t *__rest
                                                            const f32x4 *__restrict__ bias, f32x4 *__restrict__ out0,
                                                            f32x4 *__restrict__ out1, FwdEpilogue epi, int kpad,
                                                            int ntiles, int nchunks, int nchunks_p) {
-  constexpr int U = SFT_FWD_TILED_U;
   constexpr int PPW = kWave / kTileCh;  // 8 positions per wave per round
   static_assert(PPW <= kCompactRows, "compact_rows takes at most kCompactRows rows");
   extern __shared__ int smem[];
@@ -300,7 +348,10 @@ __global__ __launch_bounds__(kBlock) void fwd_tiled_kernel(const int32_t *__rest
   const int64_t col4 = col;
   const int64_t cols4 = map.cols4;
   const f32x4 b4 = colok ? bias[col4] : f32x4{0.f, 0.f, 0.f, 0.f};
-  const f32x4 *wtile = Wt + (int64_t)it.tile * N * kTileCh + t;
+  const char *tbase = reinterpret_cast<const char *>(Wt + (int64_t)it.tile * N * kTileCh);
+  const uint32_t lane_off = (uint32_t)t * (uint32_t)sizeof(f32x4);
+  bool partial = false;  // block-uniform
+  for (int q = 0; q < kTileCh; ++q) partial |= tile_col(map, it.tile, q) < 0;
 
   for (int round = 0; round < kTiledRounds; ++round) {
     const int64_t pos0 = (int64_t)it.chunk * kTiledPosPerBlock + round * kTiledPosPerRound + wave * PPW;
@@ -311,35 +362,8 @@ __global__ __launch_bounds__(kBlock) void fwd_tiled_kernel(const int32_t *__rest
     int nmin, nmax;
     group_minmax<kTileCh>(n, nmin, nmax);
     const int *mylist = list + g * kpad;
-    f32x4 acc = b4;
-    int k = 0;
-    for (; k + U <= nmin; k += U) {
-      int fi[U];
-#pragma unroll
-      for (int u = 0; u < U; u += 4) {
-        const i32x4 f4 = read4(mylist, k + u);
-        fi[u] = f4[0], fi[u + 1] = f4[1], fi[u + 2] = f4[2], fi[u + 3] = f4[3];
-      }
-      f32x4 w[U];
-#pragma unroll
-      for (int u = 0; u < U; ++u) w[u] = colok ? wtile[(int64_t)fi[u] * kTileCh] : f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int u = 0; u < U; ++u) acc += w[u];
-    }
-    for (; k < nmax; k += 4) {
-      constexpr int UT = 4;
-      const i32x4 f4 = read4(mylist, k);
-      f32x4 w[UT];
-#pragma unroll
-      for (int u = 0; u < UT; ++u) {
-        const bool v = k + u < n;
-        w[u] = f32x4{0.f, 0.f, 0.f, 0.f};
-        if (v && colok) w[u] = wtile[(int64_t)f4[u] * kTileCh];
-      }
-#pragma unroll
-      for (int u = 0; u < UT; ++u)
-        if (k + u < n) acc += w[u];
-    }
+    const f32x4 acc = partial ? f32_tile_rows<true>(mylist, n, nmin, nmax, tbase, lane_off, colok, b4)
+                              : f32_tile_rows<false>(mylist, n, nmin, nmax, tbase, lane_off, colok, b4);
     if (!EPI) {
       f32x4 *__restrict__ out = second ? out1 : out0;
       if (pos < B && colok) __builtin_nontemporal_store(acc, out + pos * cols4 + col4);
@@ -386,16 +410,97 @@ __global__ __launch_bounds__(kBlock) void psqt_out_kernel(const f32x4 *__restric
 // ----------------------------------------------------- tiled int16 gather ----
 // Same schedule as the fp32 tiled gather over an int16 table re-laid out in
 // 64-column tiles (128 B per row; 2.9 MB per tile at N = 22 528).  Lane t of
-// an 8-lane group owns 8 int16 columns, widened to int32 before adding (exact);
-// PSQT columns (P <= 8 int32 per row) are gathered by the tile-0 workgroups.
+// an 8-lane group owns 8 int16 columns accumulated in int32 (exact); PSQT
+// columns (P <= 8 int32 per row) are gathered by the tile-0 workgroups.
+// A tile is at most 64 MB, so row addresses are 32-bit offsets from the
+// tile's (wave-uniform) base.
+#ifndef SFT_I16_TILED_U
+#define SFT_I16_TILED_U 8
+#endif
+constexpr uint32_t kI16RowBytes = kTileCh * sizeof(i16x8);  // 128
+
+typedef short i16x2 __attribute__((ext_vector_type(2)));
+
+// acc[c] += w[c] over one row's 8 int16 columns.  v_dot2c_i32_i16 with the
+// weights (1, 0) and (0, 1) adds one sign-extended half of a packed pair into
+// an int32 (1·x is exact), two instructions per pair where widening costs an
+// extract per half plus the adds.
+__device__ __forceinline__ void add_pair_i16(i32x8 &acc, int j, i16x2 p) {
+  const i16x2 lo = {1, 0}, hi = {0, 1};
+  acc[2 * j] = __builtin_amdgcn_sdot2(p, lo, acc[2 * j], false);
+  acc[2 * j + 1] = __builtin_amdgcn_sdot2(p, hi, acc[2 * j + 1], false);
+}
+
+__device__ __forceinline__ void add_row_i16(i32x8 &acc, i16x8 w) {
+  add_pair_i16(acc, 0, __builtin_shufflevector(w, w, 0, 1));
+  add_pair_i16(acc, 1, __builtin_shufflevector(w, w, 2, 3));
+  add_pair_i16(acc, 2, __builtin_shufflevector(w, w, 4, 5));
+  add_pair_i16(acc, 3, __builtin_shufflevector(w, w, 6, 7));
+}
+
+__device__ __forceinline__ i16x8 i16_row(const char *tbase, uint32_t lane_off, int f) {
+  return *reinterpret_cast<const i16x8 *>(tbase + ((uint32_t)f * kI16RowBytes + lane_off));
+}
+
+// One position's rows of one tile: an unmasked main loop over the rows every
+// lane of the 8-lane group has (nmin), then a masked tail up to nmax.  MIXED
+// (block-uniform: the tile holds PSQT or padding lanes, see i16_relayout_kernel)
+// masks the padding lanes' loads, so that they fetch nothing, and adds the PSQT
+// lanes' four int32 columns as int32; in a pure int16 tile every lane loads.
+template <bool MIXED>
+__device__ __forceinline__ void i16_tile_rows(const int *mylist, int n, int nmin, int nmax, const char *tbase,
+                                              uint32_t lane_off, bool live, bool is_psqt, i32x8 &acc) {
+  constexpr int U = SFT_I16_TILED_U;
+  static_assert(U % 4 == 0, "rows are read from the LDS list four at a time");
+  auto add = [&](i16x8 w) {
+    if (MIXED && is_psqt) {
+      const i32x4 v = __builtin_bit_cast(i32x4, w);
+      acc[0] += v[0], acc[1] += v[1], acc[2] += v[2], acc[3] += v[3];
+    } else {
+      add_row_i16(acc, w);
+    }
+  };
+  int k = 0;
+  for (; k + U <= nmin; k += U) {
+    int fi[U];
+#pragma unroll
+    for (int u = 0; u < U; u += 4) {
+      const i32x4 f4 = read4(mylist, k + u);
+      fi[u] = f4[0], fi[u + 1] = f4[1], fi[u + 2] = f4[2], fi[u + 3] = f4[3];
+    }
+    i16x8 w[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      w[u] = (i16x8)0;
+      if (!MIXED || live) w[u] = i16_row(tbase, lane_off, fi[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) add(w[u]);
+  }
+  for (; k < nmax; k += 4) {
+    const i32x4 f4 = read4(mylist, k);
+    i16x8 w[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      w[u] = (i16x8)0;
+      if (k + u < n && (!MIXED || live)) w[u] = i16_row(tbase, lane_off, f4[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) add(w[u]);
+  }
+}
+
+// Lane chunk c = 8 * tile + t of the extended row: c < cols8 is int16 columns
+// 8c .. 8c+7 (plus bias, clamped into out), cols8 <= c < cols8 + pch is PSQT
+// columns 4j .. 4j+3 (j = c - cols8; into psqt_out, those < P), the rest is
+// padding.  The PSQT columns thus ride in the last tile(s), which the schedule
+// spreads over all XCDs, instead of loading every tile-0 workgroup.
 __global__ __launch_bounds__(kBlock) void fwd_i16_tiled_kernel(const int32_t *__restrict__ idx, int64_t B, int K,
                                                                int N, const i16x8 *__restrict__ Wt, int64_t cols8,
-                                                               const i16x8 *__restrict__ bias,
-                                                               const int32_t *__restrict__ psqt, int P,
+                                                               int pch, const i16x8 *__restrict__ bias, int P,
                                                                i16x8 *__restrict__ out, int32_t *__restrict__ psqt_out,
                                                                int clip_lo, int clip_hi, int wrap16, int kpad,
                                                                int ntiles, int nchunks) {
-  constexpr int U = 4;
   constexpr int PPW = kWave / kTileCh;
   static_assert(PPW <= kCompactRows, "compact_rows takes at most kCompactRows rows");
   extern __shared__ int smem[];
@@ -408,8 +513,11 @@ __global__ __launch_bounds__(kBlock) void fwd_i16_tiled_kernel(const int32_t *__
   const int g = lane / kTileCh, t = lane % kTileCh;
   const int64_t col = (int64_t)it.tile * kTileCh + t;
   const bool colok = col < cols8;
-  const bool do_psqt = psqt != nullptr && it.tile == 0 && t < P;
-  const i16x8 *wtile = Wt + (int64_t)it.tile * N * kTileCh + t;
+  const bool is_psqt = !colok && col < cols8 + pch;
+  const int pj = (int)(col - cols8) * 4;                     // first PSQT column of a PSQT lane
+  const bool mixed = (int64_t)(it.tile + 1) * kTileCh > cols8;  // block-uniform
+  const char *tbase = reinterpret_cast<const char *>(Wt + (int64_t)it.tile * N * kTileCh);
+  const uint32_t lane_off = (uint32_t)t * (uint32_t)sizeof(i16x8);
   const i32x8 b8 = colok ? Q16<i16x8>::widen(bias[col]) : (i32x8)0;
 
   for (int round = 0; round < kTiledRounds; ++round) {
@@ -420,33 +528,47 @@ __global__ __launch_bounds__(kBlock) void fwd_i16_tiled_kernel(const int32_t *__
     const int n = count[g];
     int nmin, nmax;
     group_minmax<kTileCh>(n, nmin, nmax);
-    (void)nmin;
     const int *mylist = list + g * kpad;
     i32x8 acc = b8;
-    int pacc = 0;
-    for (int k = 0; k < nmax; k += U) {
-      const i32x4 f4 = read4(mylist, k);
-      i16x8 w[U];
-      int pw[U];
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const bool v = k + u < n;
-        w[u] = (i16x8)0;
-        if (v && colok) w[u] = wtile[(int64_t)f4[u] * kTileCh];
-        pw[u] = 0;
-        if (v && do_psqt) pw[u] = psqt[(int64_t)f4[u] * P + t];
-      }
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        acc += Q16<i16x8>::widen(w[u]);
-        pacc += pw[u];
-      }
-    }
+    if (mixed)
+      i16_tile_rows<true>(mylist, n, nmin, nmax, tbase, lane_off, colok || is_psqt, is_psqt, acc);
+    else
+      i16_tile_rows<false>(mylist, n, nmin, nmax, tbase, lane_off, true, false, acc);
     if (pos < B) {
       if (colok) __builtin_nontemporal_store(Q16<i16x8>::finish(acc, clip_lo, clip_hi, wrap16), out + pos * cols8 + col);
-      if (do_psqt) psqt_out[pos * P + t] = pacc;
+      if (is_psqt) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (pj + e < P) psqt_out[pos * P + pj + e] = acc[e];
+      }
     }
     wave_lds_barrier();
+  }
+}
+
+// Extended int16 table in 64-column tiles: chunk c of row r (c < cols8: int16
+// columns 8c .. 8c+7 of weight; else PSQT columns 4j .. 4j+3 of psqt, j =
+// c - cols8, zero past P) goes to Wt[(t * N + r) * 8 + q], t = c / 8, q = c % 8.
+// total = N * (cols8 + pch) chunks < 2^31.
+__global__ __launch_bounds__(kBlock) void i16_relayout_kernel(const i16x8 *__restrict__ W, const int32_t *__restrict__ psqt,
+                                                              int P, int64_t N, int cols8, int pch,
+                                                              i16x8 *__restrict__ Wt) {
+  const int cw = cols8 + pch;
+  const int64_t total = N * cw;
+  for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < total; i += (int64_t)gridDim.x * kBlock) {
+    const int64_t r = i / cw;
+    const int c = (int)(i - r * cw);
+    i16x8 v;
+    if (c < cols8) {
+      v = W[r * cols8 + c];
+    } else {
+      const int j = 4 * (c - cols8);
+      i32x4 p;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) p[e] = j + e < P ? psqt[r * P + j + e] : 0;
+      v = __builtin_bit_cast(i16x8, p);
+    }
+    Wt[((int64_t)(c / kTileCh) * N + r) * kTileCh + c % kTileCh] = v;
   }
 }
 
@@ -620,6 +742,8 @@ static int pair_gather(const int32_t *idx0, const int32_t *idx1, int64_t B, int 
   const int kpad = round_up4(K);
   const size_t lds = index_lds_bytes(kTileCh, K);
   if (lds > kMaxIndexLds) return fail(SFT_EUNSUPPORTED, std::string(who) + ": max_active too large for the LDS index lists");
+  if (N * (int64_t)kTileRowBytes > (int64_t)UINT32_MAX)
+    return fail(SFT_EUNSUPPORTED, std::string(who) + ": more than 2^25 table rows");
   {
     ProfScope prof(kProfFwdFold, s);
     const int64_t total = N * map.cols4;
@@ -679,9 +803,12 @@ int fwd_transform_f32(const int32_t *idx0, const int32_t *idx1, int64_t B, int K
   return check_launch("sft_ft_fwd_transform_f32 (psqt)");
 }
 
-size_t fwd_i16_tiled_workspace(int64_t N, int L) {
+// PSQT chunks of 4 int32 columns appended to the L / 8 int16 chunks of a row.
+static int i16_psqt_chunks(int P) { return P > 0 ? (P + 3) / 4 : 0; }
+
+size_t fwd_i16_tiled_workspace(int64_t N, int L, int P) {
   if (L % 8 != 0) return 0;
-  const int64_t ntiles = ceil_div(L / 8, kTileCh);
+  const int64_t ntiles = ceil_div(L / 8 + i16_psqt_chunks(P), kTileCh);
   return (size_t)(ntiles * N * kTileCh) * 16;
 }
 
@@ -693,18 +820,21 @@ bool fwd_i16_tiled_supported(int64_t N, int L, int P, const void *W, const void 
 int fwd_i16_tiled(const int32_t *idx, int64_t B, int K, const int16_t *W, int64_t N, int L, const int16_t *bias,
                   const int32_t *psqt, int P, int16_t *out, int32_t *psqt_out, int lo, int hi, int wrap16, void *ws,
                   size_t ws_bytes, hipStream_t s) {
-  if (ws_bytes < fwd_i16_tiled_workspace(N, L) || ws == nullptr || (uintptr_t)ws % 256 != 0)
+  if (ws_bytes < fwd_i16_tiled_workspace(N, L, P) || ws == nullptr || (uintptr_t)ws % 256 != 0)
     return fail(SFT_EWORKSPACE, "sft_ft_fwd_i16_ex: workspace smaller than sft_ft_fwd_i16_workspace_size() "
                                 "or not 256-byte aligned");
-  const int64_t cols8 = L / 8;
-  const int ntiles = (int)ceil_div(cols8, kTileCh);
+  const int cols8 = L / 8;
+  const int pch = i16_psqt_chunks(P);
+  const int ntiles = (int)ceil_div(cols8 + pch, kTileCh);
   const int kpad = round_up4(K);
   const size_t lds = index_lds_bytes(kTileCh, K);
   if (lds > kMaxIndexLds) return fail(SFT_EUNSUPPORTED, "sft_ft_fwd_i16_ex: max_active too large for the LDS index lists");
   i16x8 *wt = static_cast<i16x8 *>(ws);
   {
     ProfScope prof(kProfFwdRelayout, s);
-    launch_tile_relayout(reinterpret_cast<const f32x4 *>(W), N, cols8, reinterpret_cast<f32x4 *>(wt), s);
+    const int64_t total = N * (cols8 + pch);
+    hipLaunchKernelGGL(i16_relayout_kernel, dim3((unsigned)std::min<int64_t>(ceil_div(total, kBlock), 1 << 16)),
+                       dim3(kBlock), 0, s, reinterpret_cast<const i16x8 *>(W), psqt, P, N, cols8, pch, wt);
   }
   int rc = check_launch("sft_ft_fwd_i16_ex (relayout)");
   if (rc != SFT_OK) return rc;
@@ -713,7 +843,7 @@ int fwd_i16_tiled(const int32_t *idx, int64_t B, int K, const int16_t *W, int64_
   {
     ProfScope prof(kProfFwdI16Tiled, s);
     hipLaunchKernelGGL(fwd_i16_tiled_kernel, dim3((unsigned)blocks), dim3(kBlock), lds, s, idx, B, K, (int)N, wt,
-                       cols8, reinterpret_cast<const i16x8 *>(bias), psqt, P, reinterpret_cast<i16x8 *>(out),
+                       (int64_t)cols8, pch, reinterpret_cast<const i16x8 *>(bias), P, reinterpret_cast<i16x8 *>(out),
                        psqt_out, lo, hi, wrap16, kpad, ntiles, nchunks);
   }
   return check_launch("sft_ft_fwd_i16_ex (tiled gather)");

@@ -27,7 +27,9 @@ def test_q16_fixture():
 @pytest.mark.parametrize("seed,B,N,K,L,P", [
     (1, 50, 300, 32, 1040, 8), (2, 77, 64, 7, 13, 3), (3, 129, 1000, 160, 256, 0),
     (4, 1000, 22528, 32, 128, 8), (5, 3, 10, 4, 2104, 8), (6, 40, 100, 32, 520, 64),
-    (7, 500, 2000, 32, 512, 8), (8, 300, 700, 13, 1040, 3)])
+    (7, 500, 2000, 32, 512, 8), (8, 300, 700, 13, 1040, 3),
+    # tiled without PSQT; PSQT columns 0-4 in a tile of their own (L / 8 % 8 == 0)
+    (9, 200, 500, 32, 1024, 0), (10, 150, 900, 20, 1024, 5)])
 @pytest.mark.parametrize("wrap16", [False, True])
 @pytest.mark.parametrize("rows", [False, True])
 def test_q16_matches_oracle(seed, B, N, K, L, P, wrap16, rows):
@@ -44,6 +46,27 @@ def test_q16_matches_oracle(seed, B, N, K, L, P, wrap16, rows):
         assert np.array_equal(host(out), ro)
         if P:
             assert np.array_equal(host(pout), rp)
+
+
+@pytest.mark.parametrize("wrap16", [False, True])
+@pytest.mark.parametrize("rows", [False, True])
+def test_q16_extreme_values(wrap16, rows):
+    """Weights drawn from the int16 extremes and their neighbours (sign
+    extension of 0x8000 / 0x7fff / 0xffff in either half of a packed pair),
+    PSQT weights near the int32 limit over K."""
+    announce(f"q16 extremes wrap16={wrap16} rows={rows}")
+    g = np.random.default_rng(11)
+    B, N, K, L, P = 300, 600, 32, 1040, 8
+    idx = workloads.make_indices(g, B, N, K, 0, K, sort=False)
+    pool = np.array([-32768, -32767, -1, 0, 1, 32766, 32767], dtype=np.int16)
+    Wq = pool[g.integers(0, len(pool), size=(N, L))]
+    bq = pool[g.integers(0, len(pool), size=L)]
+    lim = (2**31 - 1) // (K + 1)
+    ps = np.array([-lim, -1, 0, 1, lim], dtype=np.int32)[g.integers(0, 5, size=(N, P))]
+    for lo, hi in ((0, 127), (-32768, 32767)):
+        out, pout = quantized_ft_forward(dev(idx), dev(Wq), dev(bq), dev(ps), lo, hi, wrap16, rows)
+        ro, rp = ft_oracle.fwd_i16(idx, Wq, bq, ps, lo, hi, wrap16)
+        assert np.array_equal(host(out), ro) and np.array_equal(host(pout), rp)
 
 
 @pytest.mark.parametrize("scale", [127.0, 255.0])
