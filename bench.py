@@ -10,7 +10,7 @@ positions/s, the roofline of the dominant kernel (algorithmic bytes per launch
 over its average HIP-event duration), and a CPU baseline (the PyTorch-CPU
 restatement timed on a bounded sample of the same workload).
 
-  python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--workload 1]
+  python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--warmup-s 0.25] [--workload 1]
                   [--bwd sorted|atomic] [--cpu-seconds 12] [--no-cpu] [--no-graph]
   python bench.py --composed halfka|threats   (module surface, fused vs reference composition)
   python bench.py --transform halfka|threats  (FT + post-FT epilogue, fused vs reference ops)
@@ -78,6 +78,26 @@ def load_traffic(workload_name: str, kind: str):
     return d.get("traffic_bytes_per_launch")
 
 
+def warm_up(fn, n: int, min_s: float) -> int:
+    """Calls fn at least n times and until min_s seconds have passed with the GPU
+    busy (a synchronisation every few calls keeps the host clock on the GPU's
+    work).  MI355X raises its clocks over the first tens of milliseconds of
+    sustained load: a few short warm-up steps leave a short timed region at the
+    lower clock (the int16 step: 0.39 ms after 5 warm-up steps, 0.32 ms after
+    0.2 s).  Returns the number of calls."""
+    import torch
+
+    done = 0
+    t0 = time.perf_counter()
+    while done < n or time.perf_counter() - t0 < min_s:
+        fn()
+        done += 1
+        if done % 4 == 0:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
+    return done
+
+
 def attainable(dev) -> dict:
     """The measured HBM ceiling beside the 8 TB/s peak: a 1 GiB device-to-device
     copy, bytes read + written per second."""
@@ -141,7 +161,9 @@ def cpu_baseline(w, d, seconds: float) -> dict:
 
 def bench_q16(args, w, dev) -> int:
     """int16 inference forward of both perspectives (the quantized workload): one
-    step = two tiled int16 gathers (with their table re-layouts) + PSQT columns."""
+    step = one tiled int16 gather of both perspectives, PSQT columns included, from
+    the table the module packed when it was built (load time, as an engine lays out
+    its weights once); the pack's own time is reported beside the step."""
     import torch
 
     from sft_amd import _native, workloads
@@ -153,9 +175,7 @@ def bench_q16(args, w, dev) -> int:
     qft = QuantizedFeatureTransformer(*(torch.from_numpy(d[k]).to(dev) for k in ("Wq", "bq", "psqt")), 0, 127)
     iw = torch.from_numpy(d["idx_w"]).to(dev)
     ib = torch.from_numpy(d["idx_b"]).to(dev)
-    for _ in range(args.warmup):
-        qft(iw, ib)
-    torch.cuda.synchronize()
+    warm_up(lambda: qft(iw, ib), args.warmup, args.warmup_s)
     _native.prof_enable(True)
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
@@ -173,12 +193,20 @@ def bench_q16(args, w, dev) -> int:
         log(f"[bench]   {k:22s} {v['avg_ms']:8.4f} ms x {v['launches_per_step']:.0f}/step")
     gather = [k for k in prof if "i16" in k][0]
     g_avg = prof[gather][0] / prof[gather][1]
-    per_launch = step_bytes / 2
+    per_launch = step_bytes / (prof[gather][1] / args.steps)
     achieved = per_launch / (g_avg * 1e-3) / 1e9
+    p0 = torch.cuda.Event(enable_timing=True)
+    p1 = torch.cuda.Event(enable_timing=True)
+    p0.record()
+    for _ in range(5):
+        qft.repack()
+    p1.record()
+    torch.cuda.synchronize()
+    pack_ms = p0.elapsed_time(p1) / 5
     result = {
         "metric": "int16 FT forward positions/sec (both perspectives) @B=65536,L1=1040",
         "value": w.B / (ms * 1e-3), "unit": "positions/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
+        "warmup": args.warmup, "warmup_s": args.warmup_s, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "int16", "data": "synthetic",
         "config": {"workload": w.name, "feature_set": w.feature_set, "batch": w.B, "num_inputs": w.N,
                    "max_active": w.K, "active": [w.lo, w.hi], "output_size": w.L, "psqt": w.psqt,
@@ -188,6 +216,7 @@ def bench_q16(args, w, dev) -> int:
                      "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS, "traffic": load_traffic(w.name, gather),
                      "algorithmic_bytes_per_launch": per_launch, "avg_launch_ms": g_avg},
         "kernels": kern,
+        "pack_ms": pack_ms,
         "cpu_baseline": None,
     }
     print(json.dumps(result), flush=True)
@@ -236,9 +265,7 @@ def bench_composed(args, dev) -> int:
 
     def timed(fused: bool, prof: bool):
         ft.fused = fused
-        for _ in range(args.warmup):
-            step()
-        torch.cuda.synchronize()
+        warm_up(step, args.warmup, args.warmup_s)
         if prof:
             _native.prof_enable(True)
         e0 = torch.cuda.Event(enable_timing=True)
@@ -272,7 +299,7 @@ def bench_composed(args, dev) -> int:
     result = {
         "metric": "composed FT module fwd+bwd positions/sec @B=65536,L1=1040",
         "value": B / (ms * 1e-3), "unit": "positions/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
+        "warmup": args.warmup, "warmup_s": args.warmup_s, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "fp32", "data": "synthetic",
         "config": {"workload": f"composed_{args.composed}_b65536", "feature_set": name, "batch": B,
                    "num_inputs": N, "virtual_rows": vrows, "max_active": K, "active": [lo, hi],
@@ -338,9 +365,7 @@ def bench_transform(args, dev) -> int:
             l0, psqt = transform_inputs(ft, L1, us, iw, ib, k, fused=mode == "fused")
             torch.autograd.backward([l0, psqt], [g_l0, g_psqt])
 
-        for _ in range(args.warmup):
-            step()
-        torch.cuda.synchronize()
+        warm_up(step, args.warmup, args.warmup_s)
         if prof:
             _native.prof_enable(True)
         e0 = torch.cuda.Event(enable_timing=True)
@@ -377,7 +402,7 @@ def bench_transform(args, dev) -> int:
     result = {
         "metric": "FT + post-FT epilogue fwd+bwd positions/sec @B=65536,L1=1040",
         "value": B / (ms * 1e-3), "unit": "positions/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
+        "warmup": args.warmup, "warmup_s": args.warmup_s, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "fp32", "data": "synthetic",
         "config": {"workload": f"transform_{args.transform}_b65536", "feature_set": name, "batch": B,
                    "num_inputs": N, "virtual_rows": vrows, "max_active": K, "active": [lo, hi], "l1": L1,
@@ -434,10 +459,11 @@ def bench_optimizer(args, dev) -> int:
         p.sub_((pn / denom) * s[7])
 
     def timed(fn, prof):
-        for _ in range(args.warmup):
+        def one():
             for t in tensors:
                 fn(*t, scalars)
-        torch.cuda.synchronize()
+
+        warm_up(one, args.warmup, args.warmup_s)
         if prof:
             _native.prof_enable(True)
         e0 = torch.cuda.Event(enable_timing=True)
@@ -465,7 +491,7 @@ def bench_optimizer(args, dev) -> int:
     result = {
         "metric": "Ranger22 FT-parameter update, GB/s (HalfKAv2_hm^ weight + virtual + bias, L=1048)",
         "value": step_bytes / (ms * 1e-3) / 1e9, "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
+        "warmup": args.warmup, "warmup_s": args.warmup_s, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "fp32", "data": "synthetic",
         "config": {"workload": "ranger22_halfka_ft_params", "shapes": shapes, "elements": elems,
                    "parallelism": "single-gpu"},
@@ -500,9 +526,7 @@ def bench_encode(args, dev) -> int:
     boards_np, stm_np = positions.random_positions(B, seed=7)
     boards = torch.from_numpy(boards_np).to(dev)
     stm = torch.from_numpy(stm_np).to(dev)
-    for _ in range(args.warmup):
-        encode_batch(boards, stm, name)
-    torch.cuda.synchronize()
+    warm_up(lambda: encode_batch(boards, stm, name), args.warmup, args.warmup_s)
     _native.prof_enable(True)
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
@@ -542,7 +566,7 @@ def bench_encode(args, dev) -> int:
     result = {
         "metric": f"feature-index encode positions/sec ({name}, both perspectives) @B=65536",
         "value": B / (ms * 1e-3), "unit": "positions/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
+        "warmup": args.warmup, "warmup_s": args.warmup_s, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "int32", "data": "synthetic",
         "config": {"workload": f"encode_{args.encode}_b65536", "feature_set": name, "batch": B, "max_active": K,
                    "positions": "random armies (sft_amd.positions.random_positions, seed 7)",
@@ -570,9 +594,7 @@ def bench_export(args, dev) -> int:
     g = np.random.default_rng(11)
     w = np.clip(np.rint(g.standard_normal((22528, 1040)) * 40), -32768, 32767).astype(np.int16)
     t = torch.from_numpy(w).to(dev)
-    for _ in range(args.warmup):
-        _native.leb128_encode(t)
-    torch.cuda.synchronize()
+    warm_up(lambda: _native.leb128_encode(t), args.warmup, args.warmup_s)
     _native.prof_enable(True)
     t0 = time.perf_counter()
     for _ in range(args.steps):
@@ -597,7 +619,7 @@ def bench_export(args, dev) -> int:
                          f"{el:.1f} s"}
     result = {
         "metric": "signed LEB128 encode values/sec (HalfKAv2_hm FT weights 22528 x 1040 int16)",
-        "value": n / (kern * 1e-3), "unit": "values/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "value": n / (kern * 1e-3), "unit": "values/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "warmup_s": args.warmup_s,
         "ms_per_step": kern, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int16",
         "data": "synthetic", "config": {"workload": "leb128_halfka_export_weights", "values": n,
                                         "encoded_bytes": nbytes, "parallelism": "single-gpu"},
@@ -616,6 +638,8 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--warmup-s", type=float, default=0.25,
+                    help="warm-up also runs until this many seconds have passed (GPU clock ramp)")
     ap.add_argument("--workload", type=int, default=1)
     ap.add_argument("--bwd", choices=["sorted", "atomic"], default="sorted")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
@@ -694,10 +718,8 @@ def main() -> int:
         ob = SparseLinearFunction.apply(ib, W, b)
         torch.autograd.backward([ow, ob], [gw, gb])
 
-    log(f"[bench] warmup {args.warmup} steps")
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
+    nw = warm_up(step, args.warmup, args.warmup_s)
+    log(f"[bench] warmup {nw} steps (at least {args.warmup} and {args.warmup_s} s)")
 
     # Per-kernel durations: an eager pass with the library's launch events.
     _native.prof_enable(True)
@@ -729,9 +751,7 @@ def main() -> int:
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph):
             step()
-        for _ in range(args.warmup):
-            graph.replay()
-        torch.cuda.synchronize()
+        warm_up(graph.replay, args.warmup, args.warmup_s)
         t0 = time.perf_counter()
         e0.record()
         for _ in range(args.steps):
@@ -765,7 +785,7 @@ def main() -> int:
         "unit": "positions/s",
         "n_gpus": 1,
         "steps": args.steps,
-        "warmup": args.warmup,
+        "warmup": args.warmup, "warmup_s": args.warmup_s,
         "ms_per_step": ms,
         "higher_is_better": True,
         "scaling": "weak",

@@ -161,6 +161,46 @@ int sft_ft_fwd_i16_ex(const int32_t *idx, int64_t batch, int32_t max_active,
                       void *workspace, size_t workspace_bytes, uint32_t flags, void *stream);
 
 /*
+ * ---- int16 table packed once, forward of one or both perspectives ----
+ * No reference counterpart (the engine's int16 accumulator; the reference
+ * ships none).  For inference over a fixed exported table: the 64-column tiles
+ * with the PSQT columns appended, which sft_ft_fwd_i16_ex rebuilds in its
+ * workspace on every call, are built once by sft_ft_i16_pack and reused.
+ *
+ * Bytes of the packed table.  SFT_EUNSUPPORTED unless output_size % 8 == 0,
+ * output_size > 448 (at least 8 tiles of 64 columns), psqt_size <= 8 and
+ * num_inputs * 128 <= 64 MiB.
+ * Host-only computation.
+ */
+int sft_ft_i16_packed_size(int64_t num_inputs, int32_t output_size, int32_t psqt_size, size_t *bytes);
+
+/*
+ * Packs weight int16 [num_inputs, output_size] (16-byte aligned) and
+ * psqt_weight int32 [num_inputs, psqt_size] (NULL exactly when psqt_size == 0)
+ * into packed (256-byte aligned, packed_bytes >= sft_ft_i16_packed_size()).
+ * The packed table holds copies: repack after the weights change.
+ */
+int sft_ft_i16_pack(const int16_t *weight, int64_t num_inputs, int32_t output_size,
+                    const int32_t *psqt_weight, int32_t psqt_size, void *packed,
+                    size_t packed_bytes, void *stream);
+
+/*
+ * Forward from a packed table: for each given perspective p, out_p and
+ * psqt_out_p as sft_ft_fwd_i16 computes them from idx_p (bit for bit).  idx1
+ * NULL: one perspective (out1, psqt_out1 unused); otherwise both perspectives
+ * in one launch, sharing each tile while it is in L2.  num_inputs, output_size
+ * and psqt_size must be those the table was packed with; psqt_out_p are
+ * required when psqt_size > 0.  flags: SFT_Q16_WRAP16 or 0.  bias and outputs
+ * 16-byte aligned.
+ */
+int sft_ft_fwd_i16_packed(const int32_t *idx0, const int32_t *idx1, int64_t batch,
+                          int32_t max_active, const void *packed, size_t packed_bytes,
+                          int64_t num_inputs, int32_t output_size, const int16_t *bias,
+                          int32_t psqt_size, int16_t *out0, int16_t *out1, int32_t *psqt_out0,
+                          int32_t *psqt_out1, int32_t clip_lo, int32_t clip_hi, uint32_t flags,
+                          void *stream);
+
+/*
  * ---- Composed table, both perspectives in one call ----
  * The table is num_blocks (1..4) row blocks concatenated in order (the feature
  * sets of a composed transformer, FEAT/composed.py:49-50).  Block s has

@@ -25,6 +25,11 @@ bool fwd_i16_tiled_supported(int64_t N, int L, int P, const void *W, const void 
 int fwd_i16_tiled(const int32_t *idx, int64_t B, int K, const int16_t *W, int64_t N, int L, const int16_t *bias,
                   const int32_t *psqt, int P, int16_t *out, int32_t *psqt_out, int lo, int hi, int wrap16, void *ws,
                   size_t ws_bytes, hipStream_t s);
+int i16_pack(const int16_t *W, int64_t N, int L, const int32_t *psqt, int P, void *packed, size_t bytes,
+             hipStream_t s, const char *who);
+int fwd_i16_packed(const int32_t *idx0, const int32_t *idx1, int64_t B, int K, const void *packed, int64_t N, int L,
+                   const int16_t *bias, int P, int16_t *out0, int16_t *out1, int32_t *psqt_out0, int32_t *psqt_out1,
+                   int lo, int hi, int wrap16, hipStream_t s, const char *who);
 int bwd_f32(const int32_t *idx, int64_t B, int K, const float *grad, int64_t N, int L, float *dW, float *db,
             void *ws, size_t ws_bytes, uint32_t flags, hipStream_t s);
 size_t index_lds_bytes(int G, int K);
@@ -700,6 +705,63 @@ int sft_ft_fwd_i16_ex(const int32_t *idx, int64_t batch, int32_t max_active, con
                          clip_lo, clip_hi, wrap, workspace, workspace_bytes, (hipStream_t)stream);
   return fwd_i16(idx, batch, max_active, weight, num_inputs, output_size, bias, psqt_weight, P, out, psqt_out, clip_lo,
                  clip_hi, wrap, (hipStream_t)stream);
+}
+
+int sft_ft_i16_packed_size(int64_t num_inputs, int32_t output_size, int32_t psqt_size, size_t *bytes) {
+  clear_error();
+  std::string why;
+  if (!bytes) return fail(SFT_EINVAL, "sft_ft_i16_packed_size: null pointer");
+  if (bad_sizes(0, 1, num_inputs, output_size, why)) return fail(SFT_EINVAL, "sft_ft_i16_packed_size: " + why);
+  if (psqt_size < 0) return fail(SFT_EINVAL, "sft_ft_i16_packed_size: psqt_size must be >= 0");
+  if (!fwd_i16_tiled_supported(num_inputs, output_size, psqt_size, nullptr, nullptr, nullptr))
+    return fail(SFT_EUNSUPPORTED, "sft_ft_i16_packed_size: needs output_size % 8 == 0, at least 8 tiles of 64 "
+                                  "columns, psqt_size <= 8 and num_inputs * 128 <= 64 MiB");
+  *bytes = fwd_i16_tiled_workspace(num_inputs, output_size, psqt_size);
+  return SFT_OK;
+}
+
+int sft_ft_i16_pack(const int16_t *weight, int64_t num_inputs, int32_t output_size, const int32_t *psqt_weight,
+                    int32_t psqt_size, void *packed, size_t packed_bytes, void *stream) {
+  clear_error();
+  std::string why;
+  if (bad_sizes(0, 1, num_inputs, output_size, why)) return fail(SFT_EINVAL, "sft_ft_i16_pack: " + why);
+  if (!weight || !packed) return fail(SFT_EINVAL, "sft_ft_i16_pack: null pointer");
+  if ((psqt_weight == nullptr) != (psqt_size == 0))
+    return fail(SFT_EINVAL, "sft_ft_i16_pack: psqt_size must be 0 exactly when psqt_weight is NULL");
+  if (psqt_size < 0 || !fwd_i16_tiled_supported(num_inputs, output_size, psqt_size, weight, weight, weight))
+    return fail(SFT_EUNSUPPORTED, "sft_ft_i16_pack: shape outside the tiled path (see sft_ft_i16_packed_size) "
+                                  "or weight not 16-byte aligned");
+  return i16_pack(weight, num_inputs, output_size, psqt_weight, psqt_size, packed, packed_bytes, (hipStream_t)stream,
+                  "sft_ft_i16_pack");
+}
+
+int sft_ft_fwd_i16_packed(const int32_t *idx0, const int32_t *idx1, int64_t batch, int32_t max_active,
+                          const void *packed, size_t packed_bytes, int64_t num_inputs, int32_t output_size,
+                          const int16_t *bias,
+                          int32_t psqt_size, int16_t *out0, int16_t *out1, int32_t *psqt_out0, int32_t *psqt_out1,
+                          int32_t clip_lo, int32_t clip_hi, uint32_t flags, void *stream) {
+  clear_error();
+  std::string why;
+  const char *w = "sft_ft_fwd_i16_packed";
+  if (bad_sizes(batch, max_active, num_inputs, output_size, why)) return fail(SFT_EINVAL, std::string(w) + ": " + why);
+  if (max_active >= 65536) return fail(SFT_EINVAL, std::string(w) + ": max_active must be < 65536");
+  if (!packed || !bias) return fail(SFT_EINVAL, std::string(w) + ": null pointer");
+  if (batch > 0 && (!idx0 || !out0 || (idx1 && !out1)))
+    return fail(SFT_EINVAL, std::string(w) + ": null pointer");
+  if (psqt_size < 0 || (batch > 0 && psqt_size > 0 && (!psqt_out0 || (idx1 && !psqt_out1))))
+    return fail(SFT_EINVAL, std::string(w) + ": psqt outputs must be set when psqt_size > 0");
+  if (clip_lo > clip_hi || clip_lo < -32768 || clip_hi > 32767)
+    return fail(SFT_EINVAL, std::string(w) + ": need -32768 <= clip_lo <= clip_hi <= 32767");
+  if (flags & ~SFT_Q16_WRAP16) return fail(SFT_EINVAL, std::string(w) + ": unknown flags");
+  if ((uintptr_t)packed % 256 != 0 ||
+      !fwd_i16_tiled_supported(num_inputs, output_size, psqt_size, bias, out0, idx1 ? out1 : out0))
+    return fail(SFT_EUNSUPPORTED, std::string(w) + ": shape outside the tiled path, packed not 256-byte aligned, "
+                                                   "or bias / outputs not 16-byte aligned");
+  if (packed_bytes < fwd_i16_tiled_workspace(num_inputs, output_size, psqt_size))
+    return fail(SFT_EINVAL, std::string(w) + ": packed_bytes smaller than sft_ft_i16_packed_size() for these sizes");
+  return fwd_i16_packed(idx0, idx1, batch, max_active, packed, num_inputs, output_size, bias, psqt_size, out0, out1,
+                        psqt_size > 0 ? psqt_out0 : nullptr, psqt_size > 0 ? psqt_out1 : nullptr, clip_lo, clip_hi,
+                        (flags & SFT_Q16_WRAP16) ? 1 : 0, (hipStream_t)stream, w);
 }
 
 int sft_quantize_i16(const float *x, int64_t n, float scale, int16_t *out, void *stream) {

@@ -495,17 +495,29 @@ __device__ __forceinline__ void i16_tile_rows(const int *mylist, int n, int nmin
 // columns 4j .. 4j+3 (j = c - cols8; into psqt_out, those < P), the rest is
 // padding.  The PSQT columns thus ride in the last tile(s), which the schedule
 // spreads over all XCDs, instead of loading every tile-0 workgroup.
-__global__ __launch_bounds__(kBlock) void fwd_i16_tiled_kernel(const int32_t *__restrict__ idx, int64_t B, int K,
+// Two perspectives share a launch like the fp32 tiled gather: chunks
+// [0, nchunks_p) read idx0 into out0 / psqt_out0, chunks [nchunks_p, nchunks)
+// idx1 into out1 / psqt_out1; one perspective passes its arrays twice and
+// nchunks_p = nchunks.
+__global__ __launch_bounds__(kBlock) void fwd_i16_tiled_kernel(const int32_t *__restrict__ idx0,
+                                                               const int32_t *__restrict__ idx1, int64_t B, int K,
                                                                int N, const i16x8 *__restrict__ Wt, int64_t cols8,
                                                                int pch, const i16x8 *__restrict__ bias, int P,
-                                                               i16x8 *__restrict__ out, int32_t *__restrict__ psqt_out,
-                                                               int clip_lo, int clip_hi, int wrap16, int kpad,
-                                                               int ntiles, int nchunks) {
+                                                               i16x8 *__restrict__ out0, i16x8 *__restrict__ out1,
+                                                               int32_t *__restrict__ psqt_out0,
+                                                               int32_t *__restrict__ psqt_out1, int clip_lo,
+                                                               int clip_hi, int wrap16, int kpad, int ntiles,
+                                                               int nchunks, int nchunks_p) {
   constexpr int PPW = kWave / kTileCh;
   static_assert(PPW <= kCompactRows, "compact_rows takes at most kCompactRows rows");
   extern __shared__ int smem[];
-  const TileItem it = tile_sched_item(blockIdx.x, ntiles, nchunks);
+  TileItem it = tile_sched_item(blockIdx.x, ntiles, nchunks);
   if (it.tile >= ntiles) return;
+  const bool second = it.chunk >= nchunks_p;  // block-uniform
+  if (second) it.chunk -= nchunks_p;
+  const int32_t *__restrict__ idx = second ? idx1 : idx0;
+  i16x8 *__restrict__ out = second ? out1 : out0;
+  int32_t *__restrict__ psqt_out = second ? psqt_out1 : psqt_out0;
   const int wave = uniform(threadIdx.x / kWave);
   const int lane = threadIdx.x % kWave;
   int *list = smem + wave * PPW * kpad;
@@ -817,36 +829,59 @@ bool fwd_i16_tiled_supported(int64_t N, int L, int P, const void *W, const void 
          (uintptr_t)W % 16 == 0 && (uintptr_t)bias % 16 == 0 && (uintptr_t)out % 16 == 0;
 }
 
+int i16_pack(const int16_t *W, int64_t N, int L, const int32_t *psqt, int P, void *packed, size_t bytes,
+             hipStream_t s, const char *who) {
+  if (bytes < fwd_i16_tiled_workspace(N, L, P) || packed == nullptr || (uintptr_t)packed % 256 != 0)
+    return fail(SFT_EWORKSPACE, std::string(who) + ": buffer smaller than the packed table size or not 256-byte aligned");
+  const int cols8 = L / 8;
+  const int pch = i16_psqt_chunks(P);
+  {
+    ProfScope prof(kProfFwdRelayout, s);
+    const int64_t total = N * (cols8 + pch);
+    hipLaunchKernelGGL(i16_relayout_kernel, dim3((unsigned)std::min<int64_t>(ceil_div(total, kBlock), 1 << 16)),
+                       dim3(kBlock), 0, s, reinterpret_cast<const i16x8 *>(W), psqt, P, N, cols8, pch,
+                       static_cast<i16x8 *>(packed));
+  }
+  return check_launch((std::string(who) + " (pack)").c_str());
+}
+
+int fwd_i16_packed(const int32_t *idx0, const int32_t *idx1, int64_t B, int K, const void *packed, int64_t N, int L,
+                   const int16_t *bias, int P, int16_t *out0, int16_t *out1, int32_t *psqt_out0, int32_t *psqt_out1,
+                   int lo, int hi, int wrap16, hipStream_t s, const char *who) {
+  const int cols8 = L / 8;
+  const int pch = i16_psqt_chunks(P);
+  const int ntiles = (int)ceil_div(cols8 + pch, kTileCh);
+  const int kpad = round_up4(K);
+  const size_t lds = index_lds_bytes(kTileCh, K);
+  if (lds > kMaxIndexLds) return fail(SFT_EUNSUPPORTED, std::string(who) + ": max_active too large for the LDS index lists");
+  if (B == 0) return SFT_OK;
+  const int nchunks_p = (int)ceil_div(B, kTiledPosPerBlock);
+  const int persp = idx1 != nullptr ? 2 : 1;
+  const int64_t blocks = tile_sched_items_per_xcd(ntiles, persp * nchunks_p) * kXcds;
+  {
+    ProfScope prof(kProfFwdI16Tiled, s);
+    hipLaunchKernelGGL(fwd_i16_tiled_kernel, dim3((unsigned)blocks), dim3(kBlock), lds, s, idx0,
+                       persp == 2 ? idx1 : idx0, B, K, (int)N, static_cast<const i16x8 *>(packed), (int64_t)cols8,
+                       pch, reinterpret_cast<const i16x8 *>(bias), P, reinterpret_cast<i16x8 *>(out0),
+                       reinterpret_cast<i16x8 *>(persp == 2 ? out1 : out0), psqt_out0,
+                       persp == 2 ? psqt_out1 : psqt_out0, lo, hi, wrap16, kpad, ntiles, persp * nchunks_p,
+                       nchunks_p);
+  }
+  return check_launch((std::string(who) + " (tiled gather)").c_str());
+}
+
 int fwd_i16_tiled(const int32_t *idx, int64_t B, int K, const int16_t *W, int64_t N, int L, const int16_t *bias,
                   const int32_t *psqt, int P, int16_t *out, int32_t *psqt_out, int lo, int hi, int wrap16, void *ws,
                   size_t ws_bytes, hipStream_t s) {
   if (ws_bytes < fwd_i16_tiled_workspace(N, L, P) || ws == nullptr || (uintptr_t)ws % 256 != 0)
     return fail(SFT_EWORKSPACE, "sft_ft_fwd_i16_ex: workspace smaller than sft_ft_fwd_i16_workspace_size() "
                                 "or not 256-byte aligned");
-  const int cols8 = L / 8;
-  const int pch = i16_psqt_chunks(P);
-  const int ntiles = (int)ceil_div(cols8 + pch, kTileCh);
-  const int kpad = round_up4(K);
-  const size_t lds = index_lds_bytes(kTileCh, K);
-  if (lds > kMaxIndexLds) return fail(SFT_EUNSUPPORTED, "sft_ft_fwd_i16_ex: max_active too large for the LDS index lists");
-  i16x8 *wt = static_cast<i16x8 *>(ws);
-  {
-    ProfScope prof(kProfFwdRelayout, s);
-    const int64_t total = N * (cols8 + pch);
-    hipLaunchKernelGGL(i16_relayout_kernel, dim3((unsigned)std::min<int64_t>(ceil_div(total, kBlock), 1 << 16)),
-                       dim3(kBlock), 0, s, reinterpret_cast<const i16x8 *>(W), psqt, P, N, cols8, pch, wt);
-  }
-  int rc = check_launch("sft_ft_fwd_i16_ex (relayout)");
+  if (index_lds_bytes(kTileCh, K) > kMaxIndexLds)
+    return fail(SFT_EUNSUPPORTED, "sft_ft_fwd_i16_ex: max_active too large for the LDS index lists");
+  int rc = i16_pack(W, N, L, psqt, P, ws, ws_bytes, s, "sft_ft_fwd_i16_ex");
   if (rc != SFT_OK) return rc;
-  const int nchunks = (int)ceil_div(B, kTiledPosPerBlock);
-  const int64_t blocks = tile_sched_items_per_xcd(ntiles, nchunks) * kXcds;
-  {
-    ProfScope prof(kProfFwdI16Tiled, s);
-    hipLaunchKernelGGL(fwd_i16_tiled_kernel, dim3((unsigned)blocks), dim3(kBlock), lds, s, idx, B, K, (int)N, wt,
-                       (int64_t)cols8, pch, reinterpret_cast<const i16x8 *>(bias), P, reinterpret_cast<i16x8 *>(out),
-                       psqt_out, lo, hi, wrap16, kpad, ntiles, nchunks);
-  }
-  return check_launch("sft_ft_fwd_i16_ex (tiled gather)");
+  return fwd_i16_packed(idx, nullptr, B, K, ws, N, L, bias, P, out, nullptr, psqt_out, nullptr, lo, hi, wrap16, s,
+                        "sft_ft_fwd_i16_ex");
 }
 
 int fwd_i16(const int32_t *idx, int64_t B, int K, const int16_t *W, int64_t N, int L, const int16_t *bias,

@@ -60,6 +60,12 @@ SIGNATURES = {
     "sft_ft_fwd_i16_ex": (
         ctypes.c_int,
         [_vp, _i64, _i32, _vp, _i64, _i32, _vp, _vp, _i32, _vp, _vp, _i32, _i32, _vp, ctypes.c_size_t, _u32, _vp]),
+    "sft_ft_i16_packed_size": (ctypes.c_int, [_i64, _i32, _i32, ctypes.POINTER(ctypes.c_size_t)]),
+    "sft_ft_i16_pack": (ctypes.c_int, [_vp, _i64, _i32, _vp, _i32, _vp, ctypes.c_size_t, _vp]),
+    "sft_ft_fwd_i16_packed": (
+        ctypes.c_int,
+        [_vp, _vp, _i64, _i32, _vp, ctypes.c_size_t, _i64, _i32, _vp, _i32, _vp, _vp, _vp, _vp, _i32, _i32, _u32,
+         _vp]),
     "sft_ft_pair_workspace_size": (
         ctypes.c_int,
         [_i64, _i32, _i32, ctypes.POINTER(_i64), ctypes.POINTER(_i64), _i32, ctypes.POINTER(ctypes.c_size_t),
@@ -262,6 +268,67 @@ def ft_fwd_i16(idx: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor, out:
                                        _ptr(out), _ptr(psqt_out), clip_lo, clip_hi, ptr, nbytes, flags,
                                        _stream(idx.device)), "sft_ft_fwd_i16_ex")
     del ws
+
+
+def i16_packed_size(N: int, L: int, P: int) -> int | None:
+    """Bytes of the packed int16 table, or None when the shape is outside the tiled path."""
+    n = ctypes.c_size_t(0)
+    rc = lib().sft_ft_i16_packed_size(N, L, P, ctypes.byref(n))
+    if rc == SFT_EUNSUPPORTED:
+        return None
+    _check(rc, "sft_ft_i16_packed_size")
+    return int(n.value)
+
+
+def i16_pack(weight: torch.Tensor, psqt_weight: torch.Tensor | None = None) -> torch.Tensor | None:
+    """The int16 table (and PSQT columns) in the packed 64-column tiles, as a uint8
+    device tensor; None when the shape is outside the tiled path."""
+    _require(weight.dim() == 2 and weight.dtype == torch.int16, "weight must be int16 [N, L]")
+    N, L = weight.shape
+    P = 0
+    tensors = [weight]
+    if psqt_weight is not None:
+        _require(psqt_weight.dim() == 2 and psqt_weight.shape[0] == N and psqt_weight.dtype == torch.int32,
+                 "psqt_weight must be int32 [N, P]")
+        P = psqt_weight.shape[1]
+        tensors.append(psqt_weight)
+    _on_gpu(weight.device, *tensors)
+    nbytes = i16_packed_size(N, L, P)
+    if nbytes is None or weight.data_ptr() % 16 != 0:
+        return None
+    packed = torch.empty(nbytes, dtype=torch.uint8, device=weight.device)
+    with torch.cuda.device(weight.device):
+        _check(lib().sft_ft_i16_pack(_ptr(weight), N, L, _ptr(psqt_weight), P, _ptr(packed), nbytes,
+                                     _stream(weight.device)), "sft_ft_i16_pack")
+    return packed
+
+
+def ft_fwd_i16_packed(packed: torch.Tensor, N: int, L: int, P: int, bias: torch.Tensor, idx0: torch.Tensor,
+                      out0: torch.Tensor, psqt_out0: torch.Tensor | None, idx1: torch.Tensor | None = None,
+                      out1: torch.Tensor | None = None, psqt_out1: torch.Tensor | None = None,
+                      clip_lo: int = 0, clip_hi: int = 127, wrap16: bool = False) -> None:
+    """int16 forward of one (idx1 None) or both perspectives from a table packed by i16_pack."""
+    _require(packed.dtype == torch.uint8 and packed.dim() == 1, "packed must come from i16_pack")
+    _require(idx0.dim() == 2 and idx0.dtype == torch.int32, "idx0 must be int32 [B, K]")
+    B, K = idx0.shape
+    _require(bias.shape == (L,) and bias.dtype == torch.int16, "bias must be int16 [L]")
+    tensors = [packed, bias, idx0, out0]
+    for i, o, po in ((idx0, out0, psqt_out0), (idx1, out1, psqt_out1)):
+        if i is None:
+            continue
+        _require(i.shape == (B, K) and i.dtype == torch.int32, "idx must be int32 [B, K], same shape for both")
+        _require(o is not None and o.shape == (B, L) and o.dtype == torch.int16, "out must be int16 [B, L]")
+        tensors += [i, o]
+        if P:
+            _require(po is not None and po.shape == (B, P) and po.dtype == torch.int32,
+                     "psqt_out must be int32 [B, P]")
+            tensors.append(po)
+    _on_gpu(idx0.device, *tensors)
+    with torch.cuda.device(idx0.device):
+        _check(lib().sft_ft_fwd_i16_packed(_ptr(idx0), _ptr(idx1), B, K, _ptr(packed), packed.numel(), N, L,
+                                           _ptr(bias), P, _ptr(out0), _ptr(out1), _ptr(psqt_out0), _ptr(psqt_out1),
+                                           clip_lo, clip_hi, SFT_Q16_WRAP16 if wrap16 else SFT_Q16_ACC32,
+                                           _stream(idx0.device)), "sft_ft_fwd_i16_packed")
 
 
 # ---- composed table, both perspectives ----

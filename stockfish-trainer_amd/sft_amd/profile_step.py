@@ -22,7 +22,7 @@ if _PKG not in sys.path:
 import torch  # noqa: E402
 
 from sft_amd import _native, workloads  # noqa: E402
-from sft_amd.quantized import quantized_ft_forward  # noqa: E402
+from sft_amd.quantized import QuantizedFeatureTransformer  # noqa: E402
 from src.model.modules.feature_transformer import SparseLinearFunction  # noqa: E402
 from src.model.modules.feature_transformer import kernel as ftk  # noqa: E402
 
@@ -41,10 +41,12 @@ def main() -> int:
     print(f"[profile] {w.name} B={w.B} N={w.N} K={w.K} L={w.L}", flush=True)
     if w.quantized:
         d = workloads.make_q16_inputs(w)
-        idx = torch.from_numpy(d["idx_w"]).to(dev)
-        Wq, bq, ps = (torch.from_numpy(d[k]).to(dev) for k in ("Wq", "bq", "psqt"))
+        d["idx_b"] = workloads.make_indices(workloads.rng(w.wid, workloads.S_BLACK), w.B, w.N, w.K, w.lo, w.hi)
+        iw = torch.from_numpy(d["idx_w"]).to(dev)
+        ib = torch.from_numpy(d["idx_b"]).to(dev)
+        qft = QuantizedFeatureTransformer(*(torch.from_numpy(d[k]).to(dev) for k in ("Wq", "bq", "psqt")), 0, 127)
         for _ in range(args.steps + 1):
-            quantized_ft_forward(idx, Wq, bq, ps, 0, 127)
+            qft(iw, ib)
     else:
         d = workloads.make_fp32_inputs(w)
         iw = torch.from_numpy(d["idx_w"]).to(dev)

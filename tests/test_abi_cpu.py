@@ -91,6 +91,47 @@ def test_i16_rejects():
     assert lib.sft_ft_fwd_i16(*a) == -1 and "flags" in _native.last_error()
 
 
+def test_i16_packed_size_and_pack_checks():
+    lib = _native.lib()
+    n = ctypes.c_size_t(0)
+    # 1040 int16 columns = 130 chunks; 8 PSQT columns = 2 more chunks -> 17 tiles of N * 128 bytes
+    assert lib.sft_ft_i16_packed_size(22528, 1040, 8, ctypes.byref(n)) == 0
+    assert n.value == 17 * 22528 * 128
+    assert lib.sft_ft_i16_packed_size(22528, 1024, 0, ctypes.byref(n)) == 0 and n.value == 16 * 22528 * 128
+    assert lib.sft_ft_i16_packed_size(22528, 1024, 5, ctypes.byref(n)) == 0 and n.value == 17 * 22528 * 128
+    assert lib.sft_ft_i16_packed_size(22528, 256, 8, ctypes.byref(n)) == _native.SFT_EUNSUPPORTED  # 4 tiles
+    assert lib.sft_ft_i16_packed_size(22528, 1040, 9, ctypes.byref(n)) == _native.SFT_EUNSUPPORTED
+    assert lib.sft_ft_i16_packed_size(22528, 1040, 8, None) == -1
+    assert _native.i16_packed_size(22528, 1044, 8) is None
+    # psqt pointer and size must agree; nothing is launched
+    assert lib.sft_ft_i16_pack(P, 22528, 1040, None, 8, P, 1 << 30, None) == -1
+    assert "psqt_size" in _native.last_error()
+    assert lib.sft_ft_i16_pack(P, 22528, 1040, P, 8, P, 1000, None) == _native.SFT_EWORKSPACE
+
+
+def test_i16_packed_forward_rejects_before_launch():
+    lib = _native.lib()
+    need = 17 * 22528 * 128
+    ok = (P, P, 4, 32, P, need, 22528, 1040, P, 8, P, P, P, P, 0, 127, 0, None)
+
+    def call(**kw):
+        names = ["idx0", "idx1", "batch", "max_active", "packed", "packed_bytes", "num_inputs", "output_size",
+                 "bias", "psqt_size", "out0", "out1", "psqt_out0", "psqt_out1", "clip_lo", "clip_hi", "flags",
+                 "stream"]
+        a = dict(zip(names, ok))
+        a.update(kw)
+        return lib.sft_ft_fwd_i16_packed(*[a[k] for k in names])
+
+    assert call(packed_bytes=need - 1) == -1 and "packed_bytes" in _native.last_error()
+    assert call(flags=0x2) == -1 and "flags" in _native.last_error()
+    assert call(psqt_out1=None) == -1 and "psqt" in _native.last_error()
+    assert call(out1=None) == -1 and "null" in _native.last_error()
+    assert call(packed=ctypes.c_void_p(0x1010)) == _native.SFT_EUNSUPPORTED  # not 256-byte aligned
+    assert call(psqt_size=9) == _native.SFT_EUNSUPPORTED
+    assert call(clip_lo=10, clip_hi=5) == -1
+    assert call(batch=0, packed_bytes=need - 1) == -1  # sizes are checked even for an empty batch
+
+
 def test_quantize_rejects():
     lib = _native.lib()
     assert lib.sft_quantize_i16(P, -1, 1.0, P, None) == -1

@@ -69,6 +69,55 @@ def test_q16_extreme_values(wrap16, rows):
         assert np.array_equal(host(out), ro) and np.array_equal(host(pout), rp)
 
 
+@pytest.mark.parametrize("seed,B,N,K,L,P", [
+    (21, 300, 1000, 32, 1040, 8), (22, 77, 500, 13, 1024, 0), (23, 129, 800, 20, 2104, 5), (24, 1, 64, 4, 512, 3),
+    (25, 1000, 22528, 32, 1040, 8)])
+@pytest.mark.parametrize("wrap16", [False, True])
+def test_packed_table_matches_oracle(seed, B, N, K, L, P, wrap16):
+    """sft_ft_i16_pack + sft_ft_fwd_i16_packed, both perspectives in one launch and
+    one perspective alone, against the oracle."""
+    announce(f"q16 packed seed={seed} B={B} N={N} K={K} L={L} P={P} wrap16={wrap16}")
+    g = np.random.default_rng(seed)
+    i0 = workloads.make_indices(g, B, N, K, 0, K, sort=False)
+    i1 = workloads.make_indices(g, B, N, K, 0, K, sort=False)
+    Wq = g.integers(-32768, 32768, size=(N, L)).astype(np.int16)
+    bq = g.integers(-3000, 3000, size=L).astype(np.int16)
+    ps = g.integers(-10**6, 10**6, size=(N, P)).astype(np.int32) if P else None
+    packed = _native.i16_pack(dev(Wq), None if ps is None else dev(ps))
+    assert packed is not None
+    for lo, hi in ((0, 127), (-32768, 32767)):
+        o = [torch.empty(B, L, dtype=torch.int16, device=DEV) for _ in range(3)]
+        po = [torch.empty(B, P, dtype=torch.int32, device=DEV) if P else None for _ in range(3)]
+        _native.ft_fwd_i16_packed(packed, N, L, P, dev(bq), dev(i0), o[0], po[0], dev(i1), o[1], po[1], lo, hi, wrap16)
+        _native.ft_fwd_i16_packed(packed, N, L, P, dev(bq), dev(i1), o[2], po[2], clip_lo=lo, clip_hi=hi,
+                                  wrap16=wrap16)
+        for j, idx in ((0, i0), (1, i1), (2, i1)):
+            ro, rp = ft_oracle.fwd_i16(idx, Wq, bq, ps, lo, hi, wrap16)
+            assert np.array_equal(host(o[j]), ro), j
+            if P:
+                assert np.array_equal(host(po[j]), rp), j
+
+
+def test_quantized_module_repacks_after_in_place_update():
+    announce("q16 module repack")
+    g = np.random.default_rng(31)
+    B, N, K, L, P = 200, 700, 32, 1040, 8
+    i0 = workloads.make_indices(g, B, N, K, 0, K, sort=False)
+    i1 = workloads.make_indices(g, B, N, K, 0, K, sort=False)
+    Wq = g.integers(-3000, 3000, size=(N, L)).astype(np.int16)
+    bq = g.integers(-3000, 3000, size=L).astype(np.int16)
+    ps = g.integers(-10**5, 10**5, size=(N, P)).astype(np.int32)
+    qft = QuantizedFeatureTransformer(dev(Wq), dev(bq), dev(ps), -32768, 32767)
+    assert qft.packed is not None
+    qft(dev(i0), dev(i1))
+    qft.weight_q.add_(7)  # in place through torch: the version counter moves
+    qft.psqt_q.mul_(-1)
+    (ow, pw), (ob, pb) = qft(dev(i0), dev(i1))
+    for idx, o, p in ((i0, ow, pw), (i1, ob, pb)):
+        ro, rp = ft_oracle.fwd_i16(idx, Wq + np.int16(7), bq, -ps, -32768, 32767, False)
+        assert np.array_equal(host(o), ro) and np.array_equal(host(p), rp)
+
+
 @pytest.mark.parametrize("scale", [127.0, 255.0])
 def test_full_workload_q16(scale):
     w = workloads.WORKLOADS[4]
