@@ -410,8 +410,9 @@ __global__ __launch_bounds__(kBlock) void psqt_out_kernel(const f32x4 *__restric
 // ----------------------------------------------------- tiled int16 gather ----
 // Same schedule as the fp32 tiled gather over an int16 table re-laid out in
 // 64-column tiles (128 B per row; 2.9 MB per tile at N = 22 528).  Lane t of
-// an 8-lane group owns 8 int16 columns accumulated in int32 (exact); PSQT
-// columns (P <= 8 int32 per row) are gathered by the tile-0 workgroups.
+// an 8-lane group owns 8 int16 columns accumulated in int32 (exact); the PSQT
+// columns (P <= 8 int32 per row) are appended to every packed row as extra
+// 16-byte chunks and summed by the lanes that hold them (i16_relayout_kernel).
 // A tile is at most 64 MB, so row addresses are 32-bit offsets from the
 // tile's (wave-uniform) base.
 #ifndef SFT_I16_TILED_U
