@@ -356,8 +356,12 @@ __global__ __launch_bounds__(kBlock) void gather_rows_kernel(const int32_t *__re
 // (FT/kernel.py:122, 178-181), bit for bit.  A lane group of 8 lanes x 16 B
 // owns one feature's tile row; tiles go to XCDs whole (tile_sched_item), so an
 // XCD reads one tile-half of Gt at a time: 32768 x 128 B = 4 MB, its L2.
+// The weight-grad tile rows are written once per launch and read back, if at
+// all, by the next launch: non-temporal stores keep them from evicting the
+// grad tile the XCD is gathering from (220 -> 215 us per launch, workload 1).
+// Non-temporal loads of the values read back made the gather slower.
 #ifndef SFT_BWD_NT_STORE
-#define SFT_BWD_NT_STORE 0
+#define SFT_BWD_NT_STORE 1
 #endif
 constexpr int kBwdTileCh = 8;  // float4 chunks per 32-column tile row
 // Grad tile width of the plain (single-perspective) tiled backward, in 16-byte chunks.
@@ -536,18 +540,25 @@ __global__ __launch_bounds__(kBlock) void bwd_tiled_gather_kernel(const int32_t 
   else
     bwd_tile_sum<false, TCH>(sorted_pos + s0, n, nmin, nmax, t, colok, gcol, acc);
   if (!mine) return;
+#if SFT_BWD_NT_STORE
+  if (dst_mode == kDstTmp) {
+    __builtin_nontemporal_store(acc, tp);
+  } else if (dst_mode == kDstOutPlus) {
+    const f32x4 prev = __builtin_nontemporal_load(d);
+    __builtin_nontemporal_store(prev + acc, d);
+  } else if (!skip_untouched || n > 0) {
+    __builtin_nontemporal_store(acc, d);
+  }
+#else
   if (dst_mode == kDstTmp) {
     *tp = acc;
   } else if (dst_mode == kDstOutPlus) {
     const f32x4 prev = *d;
     *d = prev + acc;
   } else if (!skip_untouched || n > 0) {
-#if SFT_BWD_NT_STORE
-    __builtin_nontemporal_store(acc, d);
-#else
     *d = acc;
-#endif
   }
+#endif
 }
 
 // dV[j, :] = sum over i < reps of dWb[i * period + j, :], i ascending (the
