@@ -357,12 +357,24 @@ __global__ __launch_bounds__(kBlock) void gather_rows_kernel(const int32_t *__re
 // owns one feature's tile row; tiles go to XCDs whole (tile_sched_item), so an
 // XCD reads one tile-half of Gt at a time: 32768 x 128 B = 4 MB, its L2.
 // The weight-grad tile rows are written once per launch and read back, if at
-// all, by the next launch: non-temporal stores keep them from evicting the
-// grad tile the XCD is gathering from (220 -> 215 us per launch, workload 1).
+// all, by the next launch.  When a tile-half of the grad tiles takes half of an
+// XCD's L2 or more, non-temporal stores keep them from evicting it (220 -> 215
+// us per launch at B = 65536); with smaller batches the grad tile fits anyway
+// and the read-back is cheaper from the cache (B = 16384: 90 vs 99 us), so the
+// host picks per launch (kNtStoreTileBytes; a template parameter, as the
+// compiler merges a runtime choice between the two stores into a plain one).
 // Non-temporal loads of the values read back made the gather slower.
-#ifndef SFT_BWD_NT_STORE
-#define SFT_BWD_NT_STORE 1
-#endif
+constexpr int64_t kNtStoreTileBytes = 2 << 20;
+template <bool NT>
+__device__ __forceinline__ void store_row(f32x4 *p, f32x4 v) {
+  if constexpr (NT) __builtin_nontemporal_store(v, p);
+  else *p = v;
+}
+template <bool NT>
+__device__ __forceinline__ f32x4 load_row(const f32x4 *p) {
+  if constexpr (NT) return __builtin_nontemporal_load(p);
+  else return *p;
+}
 constexpr int kBwdTileCh = 8;  // float4 chunks per 32-column tile row
 // Grad tile width of the plain (single-perspective) tiled backward, in 16-byte chunks.
 #ifndef SFT_BWD_TCH
@@ -449,7 +461,7 @@ __device__ __forceinline__ void bwd_tile_sum(const int32_t *list, int n, int nmi
 // chunk's listed long segments j, j + nlong, ... for this tile with the
 // whole workgroup (long_segment_sum_wg), while the tile is in the XCD's L2;
 // the feature blocks follow.
-template <int TCH>
+template <int TCH, bool NT>
 __global__ __launch_bounds__(kBlock) void bwd_tiled_gather_kernel(const int32_t *__restrict__ seg,
                                                                   const int32_t *__restrict__ sorted_pos, int64_t N,
                                                                   const f32x4 *__restrict__ gt, int64_t B,
@@ -540,25 +552,14 @@ __global__ __launch_bounds__(kBlock) void bwd_tiled_gather_kernel(const int32_t 
   else
     bwd_tile_sum<false, TCH>(sorted_pos + s0, n, nmin, nmax, t, colok, gcol, acc);
   if (!mine) return;
-#if SFT_BWD_NT_STORE
   if (dst_mode == kDstTmp) {
-    __builtin_nontemporal_store(acc, tp);
+    store_row<NT>(tp, acc);
   } else if (dst_mode == kDstOutPlus) {
-    const f32x4 prev = __builtin_nontemporal_load(d);
-    __builtin_nontemporal_store(prev + acc, d);
+    const f32x4 prev = load_row<NT>(d);
+    store_row<NT>(d, prev + acc);
   } else if (!skip_untouched || n > 0) {
-    __builtin_nontemporal_store(acc, d);
+    store_row<NT>(d, acc);
   }
-#else
-  if (dst_mode == kDstTmp) {
-    *tp = acc;
-  } else if (dst_mode == kDstOutPlus) {
-    const f32x4 prev = *d;
-    *d = prev + acc;
-  } else if (!skip_untouched || n > 0) {
-    *d = acc;
-  }
-#endif
 }
 
 // dV[j, :] = sum over i < reps of dWb[i * period + j, :], i ascending (the
@@ -1075,9 +1076,11 @@ int bwd_f32(const int32_t *idx, int64_t B, int K, const float *grad, int64_t N, 
     dst.p[0] = reinterpret_cast<f32x4 *>(dW);
     for (int h = 0; h < nc; ++h) {
       ProfScope prof(kProfBwdTiled, s);
-      hipLaunchKernelGGL(bwd_tiled_gather_kernel<TCH>, dim3((unsigned)blocks), dim3(kBlock), 0, s,
-                         seg + (int64_t)h * N, pos, N, gt, B, map, dst, (f32x4 *)nullptr, h == 0 ? kSrcZero : kSrcDst,
-                         kDstOut, ntiles, ngroups, sb.list + h * N, sb.count + h, nlong);
+      const bool nt = half_rows(B) * TCH * 16 >= kNtStoreTileBytes;
+      hipLaunchKernelGGL((nt ? bwd_tiled_gather_kernel<TCH, true> : bwd_tiled_gather_kernel<TCH, false>),
+                         dim3((unsigned)blocks), dim3(kBlock), 0, s, seg + (int64_t)h * N, pos, N, gt, B, map, dst,
+                         (f32x4 *)nullptr, h == 0 ? kSrcZero : kSrcDst, kDstOut, ntiles, ngroups, sb.list + h * N,
+                         sb.count + h, nlong);
       if ((rc = check_launch("tiled feature gather")) != SFT_OK) return rc;
     }
     return SFT_OK;
@@ -1175,9 +1178,11 @@ static int pair_gather_perspective(int p, const SortedSlots &ss, int64_t B, int6
       dst_mode = h == nc - 1 ? kDstOutPlus : kDstTmp;
     }
     ProfScope prof(kProfBwdTiled, s);
-    hipLaunchKernelGGL(bwd_tiled_gather_kernel<kBwdTileCh>, dim3((unsigned)blocks), dim3(kBlock), 0, s,
-                       ss.sb.seg + (int64_t)h * N, ss.pos, N, gt, B, map, dst, tmp, src_mode, dst_mode, ntiles,
-                       ngroups, ss.sb.list + h * N, ss.sb.count + h, kLongSlots);
+    const bool nt = half_rows(B) * kBwdTileCh * 16 >= kNtStoreTileBytes;
+    hipLaunchKernelGGL((nt ? bwd_tiled_gather_kernel<kBwdTileCh, true> : bwd_tiled_gather_kernel<kBwdTileCh, false>),
+                       dim3((unsigned)blocks), dim3(kBlock), 0, s, ss.sb.seg + (int64_t)h * N, ss.pos, N, gt, B, map,
+                       dst, tmp, src_mode, dst_mode, ntiles, ngroups, ss.sb.list + h * N, ss.sb.count + h,
+                       kLongSlots);
     const int rc = check_launch("tiled feature gather");
     if (rc != SFT_OK) return rc;
   }
