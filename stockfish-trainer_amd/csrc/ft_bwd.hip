@@ -389,7 +389,7 @@ constexpr int bwd_feat_per_block() {
 template <int TCH>
 constexpr bool kLongPath = TCH == 8;
 #ifndef SFT_BWD_LONG_SLOTS
-#define SFT_BWD_LONG_SLOTS 128
+#define SFT_BWD_LONG_SLOTS 256
 #endif
 constexpr int kLongSlots = SFT_BWD_LONG_SLOTS;  // long-segment workgroups per tile
 #ifndef SFT_BWD_ROW_LONG_BLOCKS

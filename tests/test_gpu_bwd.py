@@ -91,6 +91,20 @@ def test_sorted_bwd_skewed_segments(seed, B, N, K, L, hot, p_hot, overwrite, row
     assert np.array_equal(dW, rW)
 
 
+@pytest.mark.parametrize("N", [2500, 1500])
+def test_sorted_bwd_every_segment_long(N):
+    """Every feature long (~450 and ~750 slots per position chunk): thousands
+    of long segments per chunk, many per long-segment slot."""
+    announce(f"bwd every segment long N={N}")
+    g = np.random.default_rng(41)
+    B, K, L = 40000, 64, 256
+    idx = workloads.make_indices(g, B, N, K, 48, 64, sort=False)
+    G = g.standard_normal((B, L)).astype(np.float32)
+    dW, _ = run_bwd(idx, G, N, _native.SFT_BWD_OVERWRITE)
+    rW, _ = ft_oracle.bwd_f32(idx, G, N)
+    assert np.array_equal(dW, rW)
+
+
 @pytest.mark.parametrize("L,rows", [(1048, False), (136, True)])
 def test_sorted_bwd_long_segments_with_repeated_slots(L, rows):
     """A feature repeated within rows: its long segment holds each such
