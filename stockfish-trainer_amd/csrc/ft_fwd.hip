@@ -710,8 +710,16 @@ size_t fwd_tiled_workspace(int64_t N, int L) {
 #ifndef SFT_FWD_TILE_MAX_BYTES
 #define SFT_FWD_TILE_MAX_BYTES (64ll << 20)
 #endif
+// The fp32 forward tiles from 4 column tiles up (L > 96): at L = 136 (5 tiles,
+// the leftover groups of XCDs sharing each) the tiled gather and its re-layout
+// take 86 us against 95 us for the row gather.  The backward keeps kMinTiles:
+// its tiled path needs the grad tiles of the bias pass, which cost more than
+// they save at that width.
+#ifndef SFT_FWD_MIN_TILES
+#define SFT_FWD_MIN_TILES 4
+#endif
 bool fwd_tiled_supported(int64_t N, int L, const void *W, const void *bias, const void *out) {
-  return L % 4 == 0 && ceil_div(L, kTileF) >= kMinTiles && N * kTileF * 4 <= (int64_t)(SFT_FWD_TILE_MAX_BYTES) &&
+  return L % 4 == 0 && ceil_div(L, kTileF) >= SFT_FWD_MIN_TILES && N * kTileF * 4 <= (int64_t)(SFT_FWD_TILE_MAX_BYTES) &&
          (uintptr_t)W % 16 == 0 && (uintptr_t)bias % 16 == 0 && (uintptr_t)out % 16 == 0;
 }
 
