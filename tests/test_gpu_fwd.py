@@ -27,6 +27,9 @@ SHAPES = [
     (12, 77, 900, 13, 1040, 0, 13, False),    # K = 13: four rows per ballot
     (13, 700, 40000, 32, 1048, 16, 32, True),  # 32-column tile > 4 MB: 16-column tiles
     (14, 300, 85296, 160, 1048, 32, 160, False),  # threat-sized table, 16-column tiles
+    (15, 500, 3000, 32, 100, 0, 32, False),   # 4 tiles, the last holding one 16-byte chunk
+    (16, 400, 2500, 24, 228, 8, 24, True),    # 8 tiles, the last holding one chunk
+    (17, 300, 1200, 32, 96, 0, 32, False),    # 3 tiles: row gather
 ]
 
 
