@@ -167,7 +167,7 @@ def bench_q16(args, w, dev) -> int:
     import torch
 
     from sft_amd import _native, workloads
-    from sft_amd.quantized import QuantizedFeatureTransformer
+    from sft_amd.quantized import QuantizedFeatureTransformer, quantized_ft_forward
 
     log(f"[bench] generating {w.name}: B={w.B} N={w.N} K={w.K} active U[{w.lo},{w.hi}] L={w.L} int16")
     d = workloads.make_q16_inputs(w)
@@ -203,6 +203,20 @@ def bench_q16(args, w, dev) -> int:
     p1.record()
     torch.cuda.synchronize()
     pack_ms = p0.elapsed_time(p1) / 5
+
+    # The same forward without the kept pack: sft_ft_fwd_i16_ex per perspective,
+    # each call re-laying the table out in its workspace.
+    def per_call():
+        for i in (iw, ib):
+            quantized_ft_forward(i, qft.weight_q, qft.bias_q, qft.psqt_q, 0, 127)
+
+    warm_up(per_call, args.warmup, args.warmup_s)
+    p0.record()
+    for _ in range(args.steps):
+        per_call()
+    p1.record()
+    torch.cuda.synchronize()
+    per_call_ms = p0.elapsed_time(p1) / args.steps
     result = {
         "metric": "int16 FT forward positions/sec (both perspectives) @B=65536,L1=1040",
         "value": w.B / (ms * 1e-3), "unit": "positions/s", "n_gpus": 1, "steps": args.steps,
@@ -217,6 +231,7 @@ def bench_q16(args, w, dev) -> int:
                      "algorithmic_bytes_per_launch": per_launch, "avg_launch_ms": g_avg},
         "kernels": kern,
         "pack_ms": pack_ms,
+        "per_call_pack_ms_per_step": per_call_ms,
         "cpu_baseline": None,
     }
     print(json.dumps(result), flush=True)
