@@ -344,6 +344,8 @@ static int check_pair_shape(const char *who, int64_t batch, int32_t max_active, 
     return fail(SFT_EUNSUPPORTED, w + ": table too large for the tiled composed path");
   if (index_lds_bytes(8, max_active) > kMaxIndexLds)
     return fail(SFT_EUNSUPPORTED, w + ": max_active too large for the LDS index lists");
+  if (batch * 128 > (int64_t)UINT32_MAX)  // grad tile rows are 32-bit offsets
+    return fail(SFT_EUNSUPPORTED, w + ": batch above 2^25 for the tiled composed path");
   *N = n;
   return SFT_OK;
 }

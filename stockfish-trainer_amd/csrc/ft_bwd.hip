@@ -407,10 +407,15 @@ constexpr int kBwdPosLds = SFT_BWD_POS_LDS;  // staged positions per workgroup
 
 // Sums one lane group's positions from `list` (LDS or global) into acc.  A
 // lane group has TCH lanes (one 16-byte chunk of the tile row each) and keeps
-// TCH row loads in flight.
+// TCH row loads in flight.  Rows are 32-bit byte offsets from the grad tile's
+// wave-uniform base (a tile is B x 16 TCH bytes, B < 2^31 / K).
 template <bool FROM_LDS, int TCH>
 __device__ __forceinline__ void bwd_tile_sum(const int32_t *list, int n, int nmin, int nmax, int t, bool colok,
-                                             const f32x4 *__restrict__ gcol, f32x4 &acc) {
+                                             const char *__restrict__ gtile, f32x4 &acc) {
+  const uint32_t lane_off = (uint32_t)t * (uint32_t)sizeof(f32x4);
+  auto row = [&](int b) {
+    return *reinterpret_cast<const f32x4 *>(gtile + ((uint32_t)b * (uint32_t)(TCH * sizeof(f32x4)) + lane_off));
+  };
   constexpr int U = TCH;  // one position per lane of the group when read from global memory
   int k = 0;
   for (; k + U <= nmin; k += U) {
@@ -425,7 +430,7 @@ __device__ __forceinline__ void bwd_tile_sum(const int32_t *list, int n, int nmi
     }
     f32x4 w[U];
 #pragma unroll
-    for (int u = 0; u < U; ++u) w[u] = colok ? gcol[(int64_t)b[u] * TCH] : f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int u = 0; u < U; ++u) w[u] = colok ? row(b[u]) : f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int u = 0; u < U; ++u) acc += w[u];
   }
@@ -443,7 +448,7 @@ __device__ __forceinline__ void bwd_tile_sum(const int32_t *list, int n, int nmi
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       w[u] = f32x4{0.f, 0.f, 0.f, 0.f};
-      if (k + u < n && colok) w[u] = gcol[(int64_t)b[u] * TCH];
+      if (k + u < n && colok) w[u] = row(b[u]);
     }
 #pragma unroll
     for (int u = 0; u < U; ++u)
@@ -537,7 +542,7 @@ __global__ __launch_bounds__(kBlock) void bwd_tiled_gather_kernel(const int32_t 
   if (skip_untouched && !wave_has_work) return;  // nothing to change anywhere in the wave
   int nmin, nmax;
   group_minmax<TCH>(n, nmin, nmax);
-  const f32x4 *gcol = gt + (int64_t)it.tile * B * TCH + t;
+  const char *gtile = reinterpret_cast<const char *>(gt + (int64_t)it.tile * B * TCH);
   const int blk = block_of(f, dst.n, dst.start);
   f32x4 *d = pick(dst.p, blk) + (f - pick(dst.start, blk)) * cols4 + col4;
   f32x4 *tp = tmp + f * cols4 + col4;
@@ -548,9 +553,9 @@ __global__ __launch_bounds__(kBlock) void bwd_tiled_gather_kernel(const int32_t 
     else if (src_mode == kSrcTmp) acc = *tp;
   }
   if (staged)
-    bwd_tile_sum<true, TCH>(spos + (s0 - r0), n, nmin, nmax, t, colok, gcol, acc);
+    bwd_tile_sum<true, TCH>(spos + (s0 - r0), n, nmin, nmax, t, colok, gtile, acc);
   else
-    bwd_tile_sum<false, TCH>(sorted_pos + s0, n, nmin, nmax, t, colok, gcol, acc);
+    bwd_tile_sum<false, TCH>(sorted_pos + s0, n, nmin, nmax, t, colok, gtile, acc);
   if (!mine) return;
   if (dst_mode == kDstTmp) {
     store_row<NT>(tp, acc);
@@ -867,9 +872,9 @@ int bias_parts(int64_t B) {
   return (int)std::max<int64_t>(1, std::min<int64_t>(kBiasMaxParts, ceil_div(B, kBiasRowsPerBlock)));
 }
 
-bool tiled_shape(int L, uint32_t flags) {
+bool tiled_shape(int64_t B, int L, uint32_t flags) {
   return !(flags & (SFT_BWD_ATOMIC | SFT_BWD_ROWS)) && (flags & SFT_BWD_OVERWRITE) && L % 4 == 0 &&
-         ceil_div(L, 32) >= kMinTiles;
+         ceil_div(L, 32) >= kMinTiles && B * 16 * SFT_BWD_TCH <= (int64_t)UINT32_MAX;  // 32-bit grad row offsets
 }
 
 // Position chunks of the tiled gather (one launch each).
@@ -878,7 +883,7 @@ bool tiled_shape(int L, uint32_t flags) {
 #endif
 constexpr int kBwdHalves = SFT_BWD_CHUNKS;
 int sort_chunks(int64_t B, int L, uint32_t flags) {
-  return tiled_shape(L, flags) && B >= kBwdHalves ? kBwdHalves : 1;
+  return tiled_shape(B, L, flags) && B >= kBwdHalves ? kBwdHalves : 1;
 }
 int64_t half_rows(int64_t B) { return ceil_div(B, kBwdHalves); }
 
@@ -986,7 +991,7 @@ int bwd_f32(const int32_t *idx, int64_t B, int K, const float *grad, int64_t N, 
 
   // The tiled weight-grad gather reads the grad in column tiles; the bias pass
   // writes that layout while it streams the grad.
-  const bool tiled = !(flags & SFT_BWD_ATOMIC) && M > 0 && tiled_shape(L, flags) && (uintptr_t)grad % 16 == 0 &&
+  const bool tiled = !(flags & SFT_BWD_ATOMIC) && M > 0 && tiled_shape(B, L, flags) && (uintptr_t)grad % 16 == 0 &&
                      (uintptr_t)dW % 16 == 0 && (uintptr_t)db % 16 == 0;
   f32x4 *gt = tiled ? reinterpret_cast<f32x4 *>(w + lay.gt) : nullptr;
 
