@@ -176,7 +176,6 @@ def bench_q16(args, w, dev) -> int:
     iw = torch.from_numpy(d["idx_w"]).to(dev)
     ib = torch.from_numpy(d["idx_b"]).to(dev)
     warm_up(lambda: qft(iw, ib), args.warmup, args.warmup_s)
-    _native.prof_enable(True)
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
     e0.record()
@@ -185,6 +184,10 @@ def bench_q16(args, w, dev) -> int:
     e1.record()
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / args.steps
+    _native.prof_enable(True)  # per-kernel durations from a separate pass with the launch events
+    for _ in range(args.steps):
+        qft(iw, ib)
+    torch.cuda.synchronize()
     prof = _native.prof_collect()
     _native.prof_enable(False)
     step_bytes = sum(workloads.q16_fwd_bytes(i, w.N, w.L, w.psqt) for i in (d["idx_w"], d["idx_b"]))
@@ -281,8 +284,6 @@ def bench_composed(args, dev) -> int:
     def timed(fused: bool, prof: bool):
         ft.fused = fused
         warm_up(step, args.warmup, args.warmup_s)
-        if prof:
-            _native.prof_enable(True)
         e0 = torch.cuda.Event(enable_timing=True)
         e1 = torch.cuda.Event(enable_timing=True)
         e0.record()
@@ -290,8 +291,14 @@ def bench_composed(args, dev) -> int:
             step()
         e1.record()
         torch.cuda.synchronize()
-        out = _native.prof_collect() if prof else None
-        _native.prof_enable(False)
+        out = None
+        if prof:  # per-kernel durations from a separate pass with the launch events
+            _native.prof_enable(True)
+            for _ in range(args.steps):
+                step()
+            torch.cuda.synchronize()
+            out = _native.prof_collect()
+            _native.prof_enable(False)
         return e0.elapsed_time(e1) / args.steps, out
 
     ref_ms, _ = timed(False, False)
@@ -381,8 +388,6 @@ def bench_transform(args, dev) -> int:
             torch.autograd.backward([l0, psqt], [g_l0, g_psqt])
 
         warm_up(step, args.warmup, args.warmup_s)
-        if prof:
-            _native.prof_enable(True)
         e0 = torch.cuda.Event(enable_timing=True)
         e1 = torch.cuda.Event(enable_timing=True)
         e0.record()
@@ -390,8 +395,14 @@ def bench_transform(args, dev) -> int:
             step()
         e1.record()
         torch.cuda.synchronize()
-        out = _native.prof_collect() if prof else None
-        _native.prof_enable(False)
+        out = None
+        if prof:  # per-kernel durations from a separate pass with the launch events
+            _native.prof_enable(True)
+            for _ in range(args.steps):
+                step()
+            torch.cuda.synchronize()
+            out = _native.prof_collect()
+            _native.prof_enable(False)
         return e0.elapsed_time(e1) / args.steps, out
 
     ref_ms, _ = run("reference", False)
@@ -479,18 +490,21 @@ def bench_optimizer(args, dev) -> int:
                 fn(*t, scalars)
 
         warm_up(one, args.warmup, args.warmup_s)
-        if prof:
-            _native.prof_enable(True)
         e0 = torch.cuda.Event(enable_timing=True)
         e1 = torch.cuda.Event(enable_timing=True)
         e0.record()
         for _ in range(args.steps):
-            for t in tensors:
-                fn(*t, scalars)
+            one()
         e1.record()
         torch.cuda.synchronize()
-        out = _native.prof_collect() if prof else None
-        _native.prof_enable(False)
+        out = None
+        if prof:  # per-kernel durations from a separate pass with the launch events
+            _native.prof_enable(True)
+            for _ in range(args.steps):
+                one()
+            torch.cuda.synchronize()
+            out = _native.prof_collect()
+            _native.prof_enable(False)
         return e0.elapsed_time(e1) / args.steps, out
 
     ref_ms, _ = timed(reference, False)
@@ -542,7 +556,6 @@ def bench_encode(args, dev) -> int:
     boards = torch.from_numpy(boards_np).to(dev)
     stm = torch.from_numpy(stm_np).to(dev)
     warm_up(lambda: encode_batch(boards, stm, name), args.warmup, args.warmup_s)
-    _native.prof_enable(True)
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
     e0.record()
@@ -551,6 +564,10 @@ def bench_encode(args, dev) -> int:
     e1.record()
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / args.steps
+    _native.prof_enable(True)  # kernel durations from a separate pass with the launch events
+    for _ in range(args.steps):
+        out = encode_batch(boards, stm, name)
+    torch.cuda.synchronize()
     tot, cnt = _native.prof_collect()["encode_features"]
     _native.prof_enable(False)
     comps, K = parse_feature_set(name)
@@ -736,8 +753,8 @@ def main() -> int:
     nw = warm_up(step, args.warmup, args.warmup_s)
     log(f"[bench] warmup {nw} steps (at least {args.warmup} and {args.warmup_s} s)")
 
-    # Per-kernel durations: an eager pass with the library's launch events.
-    _native.prof_enable(True)
+    # The eager step, then per-kernel durations from a second eager pass with the
+    # library's launch events (which add ~0.1 ms per step of their own).
     torch.cuda.synchronize()
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
@@ -749,9 +766,13 @@ def main() -> int:
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     eager_ms = e0.elapsed_time(e1) / args.steps
+    log(f"[bench] eager {args.steps} steps: {eager_ms:.3f} ms/step (wall {wall * 1e3 / args.steps:.3f} ms/step)")
+    _native.prof_enable(True)
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
     prof = _native.prof_collect()
     _native.prof_enable(False)
-    log(f"[bench] eager {args.steps} steps: {eager_ms:.3f} ms/step (wall {wall * 1e3 / args.steps:.3f} ms/step)")
     ms = eager_ms
     if args.graph:
         # The whole step (both forwards, autograd backward, the grad sum) as one
