@@ -730,7 +730,7 @@ int sft_ft_i16_pack(const int16_t *weight, int64_t num_inputs, int32_t output_si
   if (!weight || !packed) return fail(SFT_EINVAL, "sft_ft_i16_pack: null pointer");
   if ((psqt_weight == nullptr) != (psqt_size == 0))
     return fail(SFT_EINVAL, "sft_ft_i16_pack: psqt_size must be 0 exactly when psqt_weight is NULL");
-  if (psqt_size < 0 || !fwd_i16_tiled_supported(num_inputs, output_size, psqt_size, weight, weight, weight))
+  if (psqt_size < 0 || !fwd_i16_tiled_supported(num_inputs, output_size, psqt_size, weight, nullptr, nullptr))
     return fail(SFT_EUNSUPPORTED, "sft_ft_i16_pack: shape outside the tiled path (see sft_ft_i16_packed_size) "
                                   "or weight not 16-byte aligned");
   return i16_pack(weight, num_inputs, output_size, psqt_weight, psqt_size, packed, packed_bytes, (hipStream_t)stream,
