@@ -34,8 +34,17 @@ int slot_sort(const int32_t *idx, int64_t M, int K, int64_t N, int chunk_rows, i
 
 namespace {
 
-constexpr int kBiasRowsPerBlock = 128;
-constexpr int kBiasMaxParts = 512;
+// Row blocks of the bias pass: up to 512 (B = 65536: 128 rows each; 1024 blocks
+// of 64 made the pass slower beside the sort, 120 -> 126 us), and at least 64
+// rows each (B = 16384: 256 blocks instead of 128, 56 -> 39 us).
+#ifndef SFT_BIAS_ROWS
+#define SFT_BIAS_ROWS 64
+#endif
+#ifndef SFT_BIAS_PARTS
+#define SFT_BIAS_PARTS 512
+#endif
+constexpr int kBiasRowsPerBlock = SFT_BIAS_ROWS;
+constexpr int kBiasMaxParts = SFT_BIAS_PARTS;
 
 // ------------------------------------------------------- long segments ----
 // On real data a few features are active in a large share of the positions
