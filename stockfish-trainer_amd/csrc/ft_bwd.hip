@@ -891,8 +891,14 @@ bool tiled_shape(int64_t B, int L, uint32_t flags) {
 #define SFT_BWD_CHUNKS 2
 #endif
 constexpr int kBwdHalves = SFT_BWD_CHUNKS;
+// A batch whose whole grad tile fits half an XCD's L2 is gathered in one
+// position chunk: no partial weight grads to store and reload.
+#ifndef SFT_BWD_ONE_CHUNK_BYTES
+#define SFT_BWD_ONE_CHUNK_BYTES (2 << 20)
+#endif
 int sort_chunks(int64_t B, int L, uint32_t flags) {
-  return tiled_shape(B, L, flags) && B >= kBwdHalves ? kBwdHalves : 1;
+  if (!tiled_shape(B, L, flags) || B < kBwdHalves) return 1;
+  return B * 16 * SFT_BWD_TCH <= (int64_t)(SFT_BWD_ONE_CHUNK_BYTES) ? 1 : kBwdHalves;
 }
 int64_t half_rows(int64_t B) { return ceil_div(B, kBwdHalves); }
 
@@ -913,7 +919,7 @@ int make_layout(int64_t B, int K, int64_t N, int L, uint32_t flags, BwdLayout &l
     lay.seg = off;
     off = align256(off + seg_region_bytes(nc, N));
     lay.gt = off;
-    if (nc > 1) {
+    if (tiled_shape(B, L, flags)) {  // the grad tiles the bias pass writes, whatever the chunk count
       const int64_t ntiles = ceil_div(L / 4, SFT_BWD_TCH);
       off = align256(off + (size_t)(ntiles * B * SFT_BWD_TCH) * 16);
     }
@@ -1090,7 +1096,7 @@ int bwd_f32(const int32_t *idx, int64_t B, int K, const float *grad, int64_t N, 
     dst.p[0] = reinterpret_cast<f32x4 *>(dW);
     for (int h = 0; h < nc; ++h) {
       ProfScope prof(kProfBwdTiled, s);
-      const bool nt = half_rows(B) * TCH * 16 >= kNtStoreTileBytes;
+      const bool nt = (nc > 1 ? half_rows(B) : B) * TCH * 16 >= kNtStoreTileBytes;
       hipLaunchKernelGGL((nt ? bwd_tiled_gather_kernel<TCH, true> : bwd_tiled_gather_kernel<TCH, false>),
                          dim3((unsigned)blocks), dim3(kBlock), 0, s, seg + (int64_t)h * N, pos, N, gt, B, map, dst,
                          (f32x4 *)nullptr, h == 0 ? kSrcZero : kSrcDst, kDstOut, ntiles, ngroups, sb.list + h * N,
@@ -1192,7 +1198,7 @@ static int pair_gather_perspective(int p, const SortedSlots &ss, int64_t B, int6
       dst_mode = h == nc - 1 ? kDstOutPlus : kDstTmp;
     }
     ProfScope prof(kProfBwdTiled, s);
-    const bool nt = half_rows(B) * kBwdTileCh * 16 >= kNtStoreTileBytes;
+    const bool nt = (nc > 1 ? half_rows(B) : B) * kBwdTileCh * 16 >= kNtStoreTileBytes;
     hipLaunchKernelGGL((nt ? bwd_tiled_gather_kernel<kBwdTileCh, true> : bwd_tiled_gather_kernel<kBwdTileCh, false>),
                        dim3((unsigned)blocks), dim3(kBlock), 0, s, ss.sb.seg + (int64_t)h * N, ss.pos, N, gt, B, map,
                        dst, tmp, src_mode, dst_mode, ntiles, ngroups, ss.sb.list + h * N, ss.sb.count + h,
