@@ -132,11 +132,11 @@ def test_i16_packed_forward_rejects_before_launch():
     assert call(batch=0, packed_bytes=need - 1) == -1  # sizes are checked even for an empty batch
 
 
-@pytest.mark.parametrize("B", [1, 2, 9000, 16384, 16385, 65536])
+@pytest.mark.parametrize("B", [1, 2, 9000, 16384, 32768, 32769, 65536])
 def test_bwd_workspace_holds_the_grad_tiles(B):
     """The tiled backward's bias pass writes ceil(L/32) x B x 128 bytes of grad
     tiles into the workspace whatever the number of position chunks (one for
-    batches whose tile fits 2 MB, two above)."""
+    batches whose tile fits 4 MB, two above)."""
     n = ctypes.c_size_t(0)
     L, N, K = 1048, 23232, 32
     assert _native.lib().sft_ft_bwd_f32_workspace_size(B, K, N, L, _native.SFT_BWD_OVERWRITE, ctypes.byref(n)) == 0

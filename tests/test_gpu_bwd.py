@@ -72,8 +72,8 @@ def skewed_indices(g, B, N, K, hot, p_hot):
 
 
 @pytest.mark.parametrize("seed,B,N,K,L,hot,p_hot", [
-    (21, 20000, 3000, 32, 1048, 12, 0.35),  # tiled: long segments in both position chunks
-    (24, 9000, 3000, 32, 1048, 12, 0.35),   # tiled, one position chunk (B x 128 B <= 2 MB)
+    (21, 40000, 3000, 32, 1048, 12, 0.35),  # tiled: long segments in both position chunks
+    (24, 9000, 3000, 32, 1048, 12, 0.35),   # tiled, one position chunk (B x 128 B <= 4 MB)
     (22, 5000, 400, 24, 136, 40, 0.2),      # narrow rows (row gather)
     (23, 1200, 50, 16, 520, 6, 0.9),        # segments just above and below the long threshold
 ])
