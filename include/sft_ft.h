@@ -161,6 +161,25 @@ int sft_ft_fwd_i16_ex(const int32_t *idx, int64_t batch, int32_t max_active,
                       void *workspace, size_t workspace_bytes, uint32_t flags, void *stream);
 
 /*
+ * int16 forward that allocates nothing and takes no workspace.  No reference
+ * counterpart: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, serving loops, harnesses that forbid hipMalloc).
+ * Same arguments, flags and results, bit for bit, as sft_ft_fwd_i16_ex with a
+ * workspace of sft_ft_fwd_i16_workspace_size() bytes.  The packed tiles go to
+ * a static device array of SFT_NOALLOC_SCRATCH_BYTES that each GPU holds until
+ * the process ends; a tiled shape whose packed table is larger returns
+ * SFT_EWORKSPACE and launches nothing (shapes outside the tiled path run the
+ * row gather, which needs no scratch).  All calls on one GPU share its array:
+ * calls that overlap on one GPU (other threads or streams) race; serialise them.
+ */
+#define SFT_NOALLOC_SCRATCH_BYTES (64u << 20)
+int sft_ft_fwd_i16_noalloc(const int32_t *idx, int64_t batch, int32_t max_active,
+                           const int16_t *weight, int64_t num_inputs, int32_t output_size,
+                           const int16_t *bias, const int32_t *psqt_weight, int32_t psqt_size,
+                           int16_t *out, int32_t *psqt_out, int32_t clip_lo, int32_t clip_hi,
+                           uint32_t flags, void *stream);
+
+/*
  * ---- int16 table packed once, forward of one or both perspectives ----
  * No reference counterpart (the engine's int16 accumulator; the reference
  * ships none).  For inference over a fixed exported table: the 64-column tiles

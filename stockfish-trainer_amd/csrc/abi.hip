@@ -250,6 +250,27 @@ bool bad_sizes(int64_t B, int32_t K, int64_t N, int32_t L, std::string &why) {
 
 }  // namespace
 
+namespace sft {
+// Host-side validation shared by the int16 forward entry points.
+int check_i16_args(const char *who, const int32_t *idx, int64_t batch, int32_t max_active, const int16_t *weight,
+                   int64_t num_inputs, int32_t output_size, const int16_t *bias, const int32_t *psqt_weight,
+                   int32_t psqt_size, int16_t *out, int32_t *psqt_out, int32_t clip_lo, int32_t clip_hi,
+                   uint32_t flags) {
+  std::string why;
+  const std::string w(who);
+  if (bad_sizes(batch, max_active, num_inputs, output_size, why)) return fail(SFT_EINVAL, w + ": " + why);
+  if (max_active >= 65536) return fail(SFT_EINVAL, w + ": max_active must be < 65536");
+  if (!weight || !bias || (batch > 0 && (!idx || !out))) return fail(SFT_EINVAL, w + ": null pointer");
+  if ((psqt_weight == nullptr) != (psqt_out == nullptr))
+    return fail(SFT_EINVAL, w + ": psqt_weight and psqt_out must both be set or both be NULL");
+  if (psqt_weight && (psqt_size <= 0 || psqt_size > kWave)) return fail(SFT_EINVAL, w + ": psqt_size must be in [1, 64]");
+  if (clip_lo > clip_hi || clip_lo < -32768 || clip_hi > 32767)
+    return fail(SFT_EINVAL, w + ": need -32768 <= clip_lo <= clip_hi <= 32767");
+  if (flags & ~(SFT_Q16_WRAP16 | SFT_Q16_ROWS)) return fail(SFT_EINVAL, w + ": unknown flags");
+  return SFT_OK;
+}
+}  // namespace sft
+
 extern "C" {
 
 int sft_abi_version(void) { return SFT_ABI_VERSION; }
@@ -644,23 +665,6 @@ int sft_leb128_encode(const void *values, int32_t elem_bytes, int64_t n, uint8_t
   return leb128_encode(values, elem_bytes, n, out, out_len, workspace, (hipStream_t)stream);
 }
 
-static int check_i16_args(const char *who, const int32_t *idx, int64_t batch, int32_t max_active,
-                          const int16_t *weight, int64_t num_inputs, int32_t output_size, const int16_t *bias,
-                          const int32_t *psqt_weight, int32_t psqt_size, int16_t *out, int32_t *psqt_out,
-                          int32_t clip_lo, int32_t clip_hi, uint32_t flags) {
-  std::string why;
-  const std::string w(who);
-  if (bad_sizes(batch, max_active, num_inputs, output_size, why)) return fail(SFT_EINVAL, w + ": " + why);
-  if (max_active >= 65536) return fail(SFT_EINVAL, w + ": max_active must be < 65536");
-  if (!weight || !bias || (batch > 0 && (!idx || !out))) return fail(SFT_EINVAL, w + ": null pointer");
-  if ((psqt_weight == nullptr) != (psqt_out == nullptr))
-    return fail(SFT_EINVAL, w + ": psqt_weight and psqt_out must both be set or both be NULL");
-  if (psqt_weight && (psqt_size <= 0 || psqt_size > kWave)) return fail(SFT_EINVAL, w + ": psqt_size must be in [1, 64]");
-  if (clip_lo > clip_hi || clip_lo < -32768 || clip_hi > 32767)
-    return fail(SFT_EINVAL, w + ": need -32768 <= clip_lo <= clip_hi <= 32767");
-  if (flags & ~(SFT_Q16_WRAP16 | SFT_Q16_ROWS)) return fail(SFT_EINVAL, w + ": unknown flags");
-  return SFT_OK;
-}
 
 int sft_ft_fwd_i16(const int32_t *idx, int64_t batch, int32_t max_active, const int16_t *weight, int64_t num_inputs,
                    int32_t output_size, const int16_t *bias, const int32_t *psqt_weight, int32_t psqt_size,

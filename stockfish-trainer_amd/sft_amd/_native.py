@@ -60,6 +60,9 @@ SIGNATURES = {
     "sft_ft_fwd_i16_ex": (
         ctypes.c_int,
         [_vp, _i64, _i32, _vp, _i64, _i32, _vp, _vp, _i32, _vp, _vp, _i32, _i32, _vp, ctypes.c_size_t, _u32, _vp]),
+    "sft_ft_fwd_i16_noalloc": (
+        ctypes.c_int,
+        [_vp, _i64, _i32, _vp, _i64, _i32, _vp, _vp, _i32, _vp, _vp, _i32, _i32, _u32, _vp]),
     "sft_ft_i16_packed_size": (ctypes.c_int, [_i64, _i32, _i32, ctypes.POINTER(ctypes.c_size_t)]),
     "sft_ft_i16_pack": (ctypes.c_int, [_vp, _i64, _i32, _vp, _i32, _vp, ctypes.c_size_t, _vp]),
     "sft_ft_fwd_i16_packed": (
@@ -268,6 +271,34 @@ def ft_fwd_i16(idx: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor, out:
                                        _ptr(out), _ptr(psqt_out), clip_lo, clip_hi, ptr, nbytes, flags,
                                        _stream(idx.device)), "sft_ft_fwd_i16_ex")
     del ws
+
+
+def ft_fwd_i16_noalloc(idx: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor, out: torch.Tensor,
+                       psqt_weight: torch.Tensor | None = None, psqt_out: torch.Tensor | None = None,
+                       clip_lo: int = 0, clip_hi: int = 127, wrap16: bool = False, rows: bool = False) -> None:
+    """ft_fwd_i16 through sft_ft_fwd_i16_noalloc: no workspace, nothing allocated by
+    the library; the packed tiles go to its static per-GPU scratch array."""
+    _require(idx.dim() == 2 and idx.dtype == torch.int32, "idx must be int32 [B, K]")
+    _require(weight.dim() == 2 and weight.dtype == torch.int16, "weight must be int16 [N, L]")
+    B, K = idx.shape
+    N, L = weight.shape
+    _require(bias.shape == (L,) and bias.dtype == torch.int16, "bias must be int16 [L]")
+    _require(out.shape == (B, L) and out.dtype == torch.int16, "out must be int16 [B, L]")
+    tensors = [idx, weight, bias, out]
+    P = 0
+    if psqt_weight is not None or psqt_out is not None:
+        _require(psqt_weight is not None and psqt_out is not None, "psqt_weight and psqt_out go together")
+        _require(psqt_weight.dim() == 2 and psqt_weight.shape[0] == N and psqt_weight.dtype == torch.int32,
+                 "psqt_weight must be int32 [N, P]")
+        P = psqt_weight.shape[1]
+        _require(psqt_out.shape == (B, P) and psqt_out.dtype == torch.int32, "psqt_out must be int32 [B, P]")
+        tensors += [psqt_weight, psqt_out]
+    _on_gpu(idx.device, *tensors)
+    flags = (SFT_Q16_WRAP16 if wrap16 else SFT_Q16_ACC32) | (SFT_Q16_ROWS if rows else 0)
+    with torch.cuda.device(idx.device):
+        _check(lib().sft_ft_fwd_i16_noalloc(_ptr(idx), B, K, _ptr(weight), N, L, _ptr(bias), _ptr(psqt_weight), P,
+                                            _ptr(out), _ptr(psqt_out), clip_lo, clip_hi, flags,
+                                            _stream(idx.device)), "sft_ft_fwd_i16_noalloc")
 
 
 def i16_packed_size(N: int, L: int, P: int) -> int | None:

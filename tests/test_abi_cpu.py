@@ -91,6 +91,28 @@ def test_i16_rejects():
     assert lib.sft_ft_fwd_i16(*a) == -1 and "flags" in _native.last_error()
 
 
+def test_i16_noalloc_rejects_before_launch():
+    """sft_ft_fwd_i16_noalloc validates like sft_ft_fwd_i16 and refuses a tiled
+    shape whose packed table exceeds its static scratch, before any HIP call."""
+    lib = _native.lib()
+    m = re.search(r"#define SFT_NOALLOC_SCRATCH_BYTES \((\d+)u << (\d+)\)", open(HEADER).read())
+    limit = int(m.group(1)) << int(m.group(2))
+    base = [P, 4, 32, P, 22528, 1040, P, P, 8, P, P, 0, 127, 0, None]
+    a = list(base); a[10] = None  # psqt weight without output
+    assert lib.sft_ft_fwd_i16_noalloc(*a) == -1 and "psqt" in _native.last_error()
+    a = list(base); a[11], a[12] = 5, 4
+    assert lib.sft_ft_fwd_i16_noalloc(*a) == -1 and "clip" in _native.last_error()
+    a = list(base); a[13] = 4
+    assert lib.sft_ft_fwd_i16_noalloc(*a) == -1 and "flags" in _native.last_error()
+    # 500 000 rows x 17 tiles x 128 B = 1.09 GB of packed table (rows x 128 B = 64 MB still tiles)
+    a = list(base); a[4] = 500_000
+    assert 17 * 500_000 * 128 > limit
+    assert lib.sft_ft_fwd_i16_noalloc(*a) == _native.SFT_EWORKSPACE
+    err = _native.last_error()
+    assert "sft_ft_fwd_i16_noalloc" in err and str(limit) in err and str(17 * 500_000 * 128) in err
+    assert 17 * 22528 * 128 <= limit  # the exported HalfKAv2_hm table (1040 + 8 PSQT columns) fits
+
+
 def test_i16_packed_size_and_pack_checks():
     lib = _native.lib()
     n = ctypes.c_size_t(0)
