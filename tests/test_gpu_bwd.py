@@ -21,8 +21,8 @@ SHAPES = [
     (7, 64, 50, 5, 2100, 0, 5, False),
     (8, 3000, 23232, 32, 136, 16, 32, True),
     (9, 333, 4000, 48, 520, 0, 48, False),
-    (10, 20000, 700, 32, 256, 0, 32, True),  # several position chunks, long segments
-    (11, 17000, 5, 3, 1040, 0, 3, False),    # three features: every segment spans all chunks
+    (10, 40000, 700, 32, 256, 0, 32, True),  # two position chunks (B x 128 B > 4 MB), long segments
+    (11, 34000, 5, 3, 1040, 0, 3, False),    # five features: every segment crosses the chunk boundary
 ]
 
 

@@ -47,8 +47,17 @@ SHAPES = [
     (3, 1000, 32, 1048, 16, 32, [(2000, 0)]),           # no virtual rows
     (4, 257, 24, 260, 0, 24, [(960, 32), (500, 0), (64, 16), (100, 0)]),  # four blocks, partial last tile
     (5, 2048, 160, 1048, 32, 160, [(6072, 0), (3072, 768)]),  # threats-shaped composition
-    (6, 6000, 32, 520, 16, 32, [(40, 8), (24, 0)]),  # 64 rows: long segments in both position chunks
+    (6, 6000, 32, 520, 16, 32, [(40, 8), (24, 0)]),  # 64 rows, one position chunk: every segment long
+    (7, 40000, 32, 520, 16, 32, [(40, 8), (24, 0)]),  # two position chunks: long segments in both
+    (8, 40000, 32, 520, 16, 32, [(3072, 96), (700, 0)]),  # two chunks, Zipf-skewed: hot and short segments
 ]
+ZIPF = {8: 1.0}  # seeds whose rows draw features with skewed frequencies
+
+
+def _indices(g, seed, B, N, K, lo, hi, sort):
+    if seed in ZIPF:
+        return workloads.make_zipf_indices(g, B, N, K, lo, hi, ZIPF[seed], sort=sort)
+    return workloads.make_indices(g, B, N, K, lo, hi, sort=sort)
 
 
 @pytest.mark.parametrize("seed,B,K,L,lo,hi,spec", SHAPES)
@@ -56,8 +65,8 @@ def test_pair_matches_composed_oracle(seed, B, K, L, lo, hi, spec):
     announce(f"pair seed={seed} B={B} K={K} L={L} blocks={spec}")
     g = np.random.default_rng(seed)
     N = sum(r for r, _ in spec)
-    idx0 = workloads.make_indices(g, B, N, K, lo, hi)
-    idx1 = workloads.make_indices(g, B, N, K, lo, hi, sort=True)
+    idx0 = _indices(g, seed, B, N, K, lo, hi, sort=False)
+    idx1 = _indices(g, seed, B, N, K, lo, hi, sort=True)
     if B > 3:
         idx0[1, 0] = -1
         idx1[2, :] = -1

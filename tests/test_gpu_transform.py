@@ -27,8 +27,17 @@ SHAPES = [
     (3, 1000, 32, 1040, 8, 16, 32, [(2000, 0)]),                          # half of L1 = 130 chunks
     (4, 257, 24, 248, 12, 0, 24, [(960, 32), (500, 0), (64, 16), (100, 0)]),  # partial paired and PSQT tiles
     (5, 2048, 160, 1040, 8, 32, 160, [(6072, 0), (3072, 768)]),
-    (6, 6000, 32, 512, 8, 16, 32, [(40, 8), (24, 0)]),  # 64 rows: long segments
+    (6, 6000, 32, 512, 8, 16, 32, [(40, 8), (24, 0)]),  # 64 rows, one position chunk: every segment long
+    (7, 40000, 32, 512, 8, 16, 32, [(40, 8), (24, 0)]),  # two position chunks: long segments in both
+    (8, 40000, 32, 512, 8, 16, 32, [(3072, 96), (700, 0)]),  # two chunks, Zipf-skewed: hot and short segments
 ]
+ZIPF = {8: 1.0}  # seeds whose rows draw features with skewed frequencies
+
+
+def _indices(g, seed, B, N, K, lo, hi, sort):
+    if seed in ZIPF:
+        return workloads.make_zipf_indices(g, B, N, K, lo, hi, ZIPF[seed], sort=sort)
+    return workloads.make_indices(g, B, N, K, lo, hi, sort=sort)
 
 
 @pytest.mark.parametrize("seed,B,K,L1,P,lo,hi,spec", SHAPES)
@@ -37,8 +46,8 @@ def test_transform_matches_oracles(seed, B, K, L1, P, lo, hi, spec):
     g = np.random.default_rng(seed)
     L = L1 + P
     N = sum(r for r, _ in spec)
-    idx0 = workloads.make_indices(g, B, N, K, lo, hi)
-    idx1 = workloads.make_indices(g, B, N, K, lo, hi, sort=True)
+    idx0 = _indices(g, seed, B, N, K, lo, hi, sort=False)
+    idx1 = _indices(g, seed, B, N, K, lo, hi, sort=True)
     # weights around the clamp window so that every branch of the epilogue occurs
     blocks = [((g.standard_normal((R, L)) * 0.1).astype(np.float32),
                (g.standard_normal((V, L)) * 0.05).astype(np.float32) if V else None) for R, V in spec]
