@@ -6,12 +6,23 @@ SparseLinearFunction (two applies sharing W and b, autograd summing the two
 dense weight grads), on inputs already resident in HBM, timed as replays of
 the step captured in a HIP graph (--no-graph: launched eagerly; the per-kernel
 durations always come from an eager pass).  Prints one JSON line:
-positions/s, the roofline of the dominant kernel (algorithmic bytes per launch
-over its average HIP-event duration), and a CPU baseline (the PyTorch-CPU
-restatement timed on a bounded sample of the same workload).
+positions/s of the headline workload (1: B=65536, L=1048), the roofline of its
+dominant kernel, a CPU baseline (the PyTorch-CPU restatement timed on a bounded
+sample of the same workload) and, under "configs", the same measurements for
+every workload 0-4.
+
+Rooflines: a gather kernel's algorithmic bytes per launch (the rows it
+requests) over its average HIP-event duration, against the L2's peak (every
+requested byte passes the L2) and the measured ceiling of L2-served row
+gathers (sft_probe_l2_gather); a streaming kernel's against HBM's 8 TB/s.  The
+memory-side bytes the counters report (two rocprofv3 passes run in child
+processes before this process touches the GPU, or the committed summary) give
+each kernel's HBM view, and the step's compulsory bytes (what it cannot avoid
+moving) its HBM fraction.
 
   python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--warmup-s 0.25] [--workload 1]
                   [--bwd sorted|atomic] [--cpu-seconds 12] [--no-cpu] [--no-graph]
+                  [--no-configs] [--traffic live|profile|off]
   python bench.py --composed halfka|threats   (module surface, fused vs reference composition)
   python bench.py --transform halfka|threats  (FT + post-FT epilogue, fused vs reference ops)
   python bench.py --optimizer                 (fused Ranger22 update of the FT parameters)
@@ -68,14 +79,95 @@ def kernel_step_bytes(kind: str, w, idx_pair) -> float | None:
     return None
 
 
-def load_traffic(workload_name: str, kind: str):
-    """HBM bytes per launch from the committed rocprofv3 PMC summary, if any."""
-    path = os.path.join(ROOT, "profiles", f"traffic_{kind}_{workload_name}.json")
+# What the L2 can deliver to the CUs: 8 XCDs x 16 L2 channels x 128 B per clock at
+# the 2.4 GHz peak engine clock (the CDNA L2 width; MI355X has 4 MB of L2 per XCD).
+L2_PEAK_GBS = 8 * 16 * 128 * 2.4
+
+# Kernels that fetch rows at random from a table or grad tile: every byte they
+# request passes the L2, whether it hits there or comes from MALL or HBM.
+GATHER_KINDS = {"fwd_f32_gather", "fwd_f32_tiled_gather", "bwd_feature_gather", "bwd_tiled_gather",
+                "fwd_i16_gather", "fwd_i16_tiled_gather", "bwd_atomic_scatter"}
+
+
+def roofline(kind: str, bytes_per_launch: float, avg_ms: float, traffic: float | None = None,
+             traffic_source: str | None = None, l2_attainable: float | None = None) -> dict:
+    """A kernel against the bound that limits it.
+
+    Gathers are priced against the L2's peak (their algorithmic bytes are the rows
+    they request, nearly all of which the tiled design serves from L2), with the
+    measured ceiling of L2-served row gathers beside it; kernels that stream each
+    byte through HBM once (re-layouts, bias sums) against HBM's peak.  `traffic`
+    is the memory-side bytes per launch the counters report (MALL hits included):
+    the `hbm` entry prices that against 8 TB/s, so every fraction is at most 1.
+    """
+    achieved = bytes_per_launch / (avg_ms * 1e-3) / 1e9
+    gather = kind in GATHER_KINDS
+    peak = L2_PEAK_GBS if gather else HBM_PEAK_GBS
+    r = {"kernel": kind, "bound": "l2" if gather else "hbm", "achieved": achieved, "peak": peak, "unit": "GB/s",
+         "frac": achieved / peak, "traffic": traffic}
+    if gather and l2_attainable:
+        r["attainable"] = l2_attainable
+        r["frac_of_attainable"] = achieved / l2_attainable
+    if traffic:
+        hbm = traffic / (avg_ms * 1e-3) / 1e9
+        r["hbm"] = {"achieved": hbm, "peak": HBM_PEAK_GBS, "frac": hbm / HBM_PEAK_GBS, "source": traffic_source}
+    r["algorithmic_bytes_per_launch"] = bytes_per_launch
+    r["avg_launch_ms"] = avg_ms
+    return r
+
+
+def committed_traffic(name: str) -> dict | None:
+    """Per-kind memory-side bytes per step of a workload from its committed counter summary."""
+    path = os.path.join(ROOT, "profiles", f"traffic_{name}.json")
     if not os.path.exists(path):
         return None
     with open(path) as f:
         d = json.load(f)
-    return d.get("traffic_bytes_per_launch")
+    d["source"] = os.path.relpath(path, ROOT)
+    return d
+
+
+def live_traffic(wid: int, log_fn) -> dict | None:
+    """Both counter passes over the workload, run before this process touches the GPU."""
+    import tempfile
+
+    from sft_amd import traffic as tr
+
+    tmp = tempfile.mkdtemp(prefix="sft_pmc_", dir="/tmp")
+    try:
+        t = tr.measure(wid, tmp, log=log_fn)
+    except Exception as e:  # noqa: BLE001 - a failed counter pass leaves traffic unmeasured, not the bench
+        log_fn(f"[bench] live counter passes failed: {e}")
+        return None
+    finally:
+        import shutil
+
+        shutil.rmtree(tmp, ignore_errors=True)
+    t["source"] = "live: " + "; ".join(t["commands"])
+    return t
+
+
+def l2_gather_ceiling(dev, warmup_s: float) -> dict:
+    """Measured ceiling of L2-served 128-byte row gathers: sft_probe_l2_gather over
+    a 2 MB table (every XCD's L2 holds it), 8192 workgroups x 32 lane groups x 256
+    rows per launch, timed with the library's launch events after a warm-up."""
+    import torch
+
+    from sft_amd import _native
+
+    table = torch.randn(1 << 14, 32, device=dev)
+    blocks, rounds = 8192, 32
+    out = torch.empty(blocks * 1024, device=dev)
+    warm_up(lambda: _native.probe_l2_gather(table, rounds, blocks, out), 3, warmup_s)
+    _native.prof_enable(True)
+    for _ in range(10):
+        nbytes = _native.probe_l2_gather(table, rounds, blocks, out)
+    torch.cuda.synchronize()
+    tot, cnt = _native.prof_collect()["probe_l2_gather"]
+    _native.prof_enable(False)
+    avg = tot / cnt
+    return {"gbs": nbytes / (avg * 1e-3) / 1e9, "kernel": "probe_l2_gather", "table_bytes": table.numel() * 4,
+            "bytes_per_launch": nbytes, "avg_launch_ms": avg}
 
 
 def warm_up(fn, n: int, min_s: float) -> int:
@@ -159,7 +251,7 @@ def cpu_baseline(w, d, seconds: float) -> dict:
     }
 
 
-def bench_q16(args, w, dev) -> int:
+def run_q16(args, w, dev, l2_attainable=None, traffic=None) -> dict:
     """int16 inference forward of both perspectives (the quantized workload): one
     step = one tiled int16 gather of both perspectives, PSQT columns included, from
     the table the module packed when it was built (load time, as an engine lays out
@@ -196,8 +288,11 @@ def bench_q16(args, w, dev) -> int:
         log(f"[bench]   {k:22s} {v['avg_ms']:8.4f} ms x {v['launches_per_step']:.0f}/step")
     gather = [k for k in prof if "i16" in k][0]
     g_avg = prof[gather][0] / prof[gather][1]
-    per_launch = step_bytes / (prof[gather][1] / args.steps)
-    achieved = per_launch / (g_avg * 1e-3) / 1e9
+    launches = prof[gather][1] / args.steps
+    per_launch = step_bytes / launches
+    t_launch = None
+    if traffic and gather in traffic["kind_step_bytes"]:
+        t_launch = traffic["kind_step_bytes"][gather] / launches
     p0 = torch.cuda.Event(enable_timing=True)
     p1 = torch.cuda.Event(enable_timing=True)
     p0.record()
@@ -220,21 +315,33 @@ def bench_q16(args, w, dev) -> int:
     p1.record()
     torch.cuda.synchronize()
     per_call_ms = p0.elapsed_time(p1) / args.steps
+    compulsory = workloads.q16_compulsory_bytes(w.B, w.K, w.N, w.L, w.psqt)
+    return {
+        "workload": w.name, "dtype": "int16", "feature_set": w.feature_set, "batch": w.B, "num_inputs": w.N,
+        "max_active": w.K, "active": [w.lo, w.hi], "output_size": w.L, "psqt": w.psqt, "quant_scale": 127,
+        "clip": [0, 127], "step": "int16 forward of both perspectives from the packed table",
+        "ms_per_step": ms, "positions_per_s": w.B / (ms * 1e-3), "step_bytes": step_bytes,
+        "step_gbs": step_bytes / (ms * 1e-3) / 1e9,
+        "step_compulsory_bytes": compulsory,
+        "step_compulsory_frac_of_hbm_peak": compulsory / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+        "roofline": roofline(gather, per_launch, g_avg, t_launch, traffic["source"] if t_launch else None,
+                             l2_attainable),
+        "kernels": kern, "pack_ms": pack_ms, "per_call_pack_ms_per_step": per_call_ms,
+    }
+
+
+def bench_q16(args, w, dev) -> int:
+    c = run_q16(args, w, dev, traffic=committed_traffic(w.name))
     result = {
         "metric": "int16 FT forward positions/sec (both perspectives) @B=65536,L1=1040",
-        "value": w.B / (ms * 1e-3), "unit": "positions/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "warmup_s": args.warmup_s, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "int16", "data": "synthetic",
+        "value": c["positions_per_s"], "unit": "positions/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "warmup_s": args.warmup_s, "ms_per_step": c["ms_per_step"], "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "int16", "data": "synthetic",
         "config": {"workload": w.name, "feature_set": w.feature_set, "batch": w.B, "num_inputs": w.N,
                    "max_active": w.K, "active": [w.lo, w.hi], "output_size": w.L, "psqt": w.psqt,
                    "quant_scale": 127, "clip": [0, 127], "parallelism": "single-gpu"},
-        "step_bytes": step_bytes,
-        "roofline": {"kernel": gather, "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS, "traffic": load_traffic(w.name, gather),
-                     "algorithmic_bytes_per_launch": per_launch, "avg_launch_ms": g_avg},
-        "kernels": kern,
-        "pack_ms": pack_ms,
-        "per_call_pack_ms_per_step": per_call_ms,
+        **{k: c[k] for k in ("step_bytes", "step_gbs", "step_compulsory_bytes", "step_compulsory_frac_of_hbm_peak",
+                             "roofline", "kernels", "pack_ms", "per_call_pack_ms_per_step")},
         "cpu_baseline": None,
     }
     print(json.dumps(result), flush=True)
@@ -316,7 +423,6 @@ def bench_composed(args, dev) -> int:
     dom = max(prof, key=lambda k: prof[k][0])
     dom_avg = prof[dom][0] / prof[dom][1]
     dom_bytes = kern[dom]["bytes_per_launch"]
-    achieved = dom_bytes / (dom_avg * 1e-3) / 1e9
     step_bytes = workloads.step_bytes(idx[0], idx[1], N, L)
     result = {
         "metric": "composed FT module fwd+bwd positions/sec @B=65536,L1=1040",
@@ -330,9 +436,7 @@ def bench_composed(args, dev) -> int:
         "speedup_vs_reference_composition": ref_ms / ms,
         "step_bytes": step_bytes,
         "step_gbs": step_bytes / (ms * 1e-3) / 1e9,
-        "roofline": {"kernel": dom, "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": None,
-                     "algorithmic_bytes_per_launch": dom_bytes, "avg_launch_ms": dom_avg},
+        "roofline": roofline(dom, dom_bytes, dom_avg),
         "kernels": kern,
         "cpu_baseline": None,
     }
@@ -424,7 +528,6 @@ def bench_transform(args, dev) -> int:
     dom = max(prof, key=lambda kk: prof[kk][0])
     dom_avg = prof[dom][0] / prof[dom][1]
     dom_bytes = kern[dom]["bytes_per_launch"]
-    achieved = dom_bytes / (dom_avg * 1e-3) / 1e9
     result = {
         "metric": "FT + post-FT epilogue fwd+bwd positions/sec @B=65536,L1=1040",
         "value": B / (ms * 1e-3), "unit": "positions/s", "n_gpus": 1, "steps": args.steps,
@@ -436,9 +539,7 @@ def bench_transform(args, dev) -> int:
         "reference_ops_over_reference_composition": {"ms_per_step": ref_ms, "value": B / (ref_ms * 1e-3)},
         "reference_ops_over_composed_op": {"ms_per_step": f1_ms, "value": B / (f1_ms * 1e-3)},
         "speedup_vs_reference": ref_ms / ms,
-        "roofline": {"kernel": dom, "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": None,
-                     "algorithmic_bytes_per_launch": dom_bytes, "avg_launch_ms": dom_avg},
+        "roofline": roofline(dom, dom_bytes, dom_avg),
         "kernels": kern,
         "cpu_baseline": None,
     }
@@ -687,6 +788,11 @@ def main() -> int:
     ap.add_argument("--encode", choices=["halfka", "threats"], default=None,
                     help="time the GPU feature-index encoder instead")
     ap.add_argument("--export", action="store_true", help="time the GPU LEB128 encoder of the .nnue export instead")
+    ap.add_argument("--configs", action=argparse.BooleanOptionalAction, default=True,
+                    help="also time every workload (0-4) and list them under 'configs' (default on)")
+    ap.add_argument("--traffic", choices=["live", "profile", "off"], default="live",
+                    help="memory-side bytes per kernel: two rocprofv3 counter passes before the timing (live), "
+                         "the committed profiles/traffic_<workload>.json (profile), or none")
     ap.add_argument("--zipf", type=float, default=None, metavar="ALPHA",
                     help="skewed feature frequencies (probability ~ 1 / (rank + 10)^ALPHA) instead of uniform ones; "
                          "a robustness run, not the headline")
@@ -697,14 +803,18 @@ def main() -> int:
               "(this build runs the FT on a single MI355X).", file=sys.stderr)
         return 2
 
-    import numpy as np
     import torch
 
     from sft_amd import _native, workloads
-    from src.model.modules.feature_transformer import SparseLinearFunction
-    from src.model.modules.feature_transformer import kernel as ftk
 
     w = workloads.WORKLOADS[args.workload]
+    special = args.composed or args.transform or args.optimizer or args.encode or args.export
+    # The counter passes run in child processes before this one touches the GPU.
+    traffic = None
+    if not special and args.zipf is None and args.traffic == "live":
+        traffic = live_traffic(w.wid, log)
+    if traffic is None and not special and args.zipf is None and args.traffic != "off":
+        traffic = committed_traffic(w.name)
     dev = torch.device("cuda:0")
     _native.lib()  # fail loudly if the library is missing
     if args.composed:
@@ -719,14 +829,94 @@ def main() -> int:
         return bench_export(args, dev)
     if w.quantized:
         return bench_q16(args, w, dev)
+
+    l2 = l2_gather_ceiling(dev, args.warmup_s)
+    log(f"[bench] L2-served 128-byte row gathers (probe): {l2['gbs']:.0f} GB/s; L2 peak {L2_PEAK_GBS:.0f} GB/s")
+    head, d = run_fp32(args, w, dev, zipf=args.zipf, traffic=traffic, l2_attainable=l2["gbs"], graph=args.graph,
+                       hashes=True)
+    ms = head["ms_per_step"]
+    result = {
+        "metric": METRIC,
+        "value": w.B / (ms * 1e-3),
+        "unit": "positions/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup, "warmup_s": args.warmup_s,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic" if args.zipf is None else f"synthetic, Zipf-like feature frequencies (alpha {args.zipf})",
+        "config": {
+            "workload": w.name, "feature_set": w.feature_set, "batch": w.B, "num_inputs": w.N,
+            "max_active": w.K, "active": [w.lo, w.hi], "output_size": w.L, "bwd": args.bwd,
+            "feature_freq": "uniform" if args.zipf is None else f"1/(rank+10)^{args.zipf}",
+            "launch": "hip_graph" if args.graph else "eager",
+            "parallelism": "single-gpu",
+            "input_sha256": head.pop("input_sha256"),
+        },
+        "eager_ms_per_step": head["eager_ms_per_step"],
+        "step_bytes": head["step_bytes"],
+        "step_gbs": head["step_gbs"],
+        "step_compulsory_bytes": head["step_compulsory_bytes"],
+        "step_compulsory_frac_of_hbm_peak": head["step_compulsory_frac_of_hbm_peak"],
+        "step_traffic_bytes": head.get("step_traffic_bytes"),
+        "step_traffic_frac_of_hbm_peak": head.get("step_traffic_frac_of_hbm_peak"),
+        "roofline": head["roofline"],
+        "l2_gather_ceiling": l2,
+        "kernels": head["kernels"],
+    }
+    result["attainable"] = attainable(dev)
+    log(f"[bench] attainable: 1 GiB device copy {result['attainable']['copy_gbs']:.0f} GB/s")
+    if not args.no_cpu:
+        log(f"[bench] cpu baseline ({args.cpu_seconds:.0f} s budget)")
+        result["cpu_baseline"] = cpu_baseline(w, d, args.cpu_seconds)
+        result["gpu_over_cpu"] = result["value"] / result["cpu_baseline"]["value"]
+    else:
+        result["cpu_baseline"] = None
+    del d
+    if args.configs and args.zipf is None:
+        configs = []
+        for wid in sorted(workloads.WORKLOADS):
+            cw = workloads.WORKLOADS[wid]
+            if wid == w.wid:
+                entry = dict(head, workload=cw.name, dtype="fp32")
+            elif cw.quantized:
+                entry = run_q16(args, cw, dev, l2_attainable=l2["gbs"], traffic=committed_traffic(cw.name))
+            else:
+                entry, _ = run_fp32(args, cw, dev, traffic=committed_traffic(cw.name), l2_attainable=l2["gbs"],
+                                    graph=args.graph)
+                entry = dict(entry, workload=cw.name, dtype="fp32")
+            entry.pop("kernels", None)
+            configs.append(entry)
+            r = entry["roofline"]
+            log(f"[bench] config {wid} {cw.name}: {entry['ms_per_step']:.3f} ms/step, "
+                f"{entry['positions_per_s'] / 1e6:.1f} M positions/s; {r['kernel']} {r['bound']} frac {r['frac']:.2f}"
+                + (f", hbm frac {r['hbm']['frac']:.2f}" if r.get("hbm") else ""))
+            torch.cuda.empty_cache()
+        result["configs"] = configs
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+def run_fp32(args, w, dev, zipf=None, traffic=None, l2_attainable=None, graph=True, hashes=False):
+    """Times the fp32 step of one workload (both perspectives through
+    SparseLinearFunction, fwd + bwd); returns its measurements and the inputs."""
+    import torch
+
+    from sft_amd import _native, workloads
+    from src.model.modules.feature_transformer import SparseLinearFunction
+    from src.model.modules.feature_transformer import kernel as ftk
+
     log(f"[bench] generating {w.name}: B={w.B} N={w.N} K={w.K} active U[{w.lo},{w.hi}] L={w.L}")
     d = workloads.make_fp32_inputs(w)
-    if args.zipf is not None:
-        log(f"[bench] Zipf-like feature frequencies, alpha={args.zipf}")
+    if zipf is not None:
+        log(f"[bench] Zipf-like feature frequencies, alpha={zipf}")
         d["idx_w"] = workloads.make_zipf_indices(workloads.rng(w.wid, workloads.S_WHITE), w.B, w.N, w.K, w.lo, w.hi,
-                                                 args.zipf)
+                                                 zipf)
         d["idx_b"] = workloads.make_zipf_indices(workloads.rng(w.wid, workloads.S_BLACK), w.B, w.N, w.K, w.lo, w.hi,
-                                                 args.zipf)
+                                                 zipf)
     iw = torch.from_numpy(d["idx_w"]).to(dev)
     ib = torch.from_numpy(d["idx_b"]).to(dev)
     W = torch.from_numpy(d["W"]).to(dev).requires_grad_(True)
@@ -734,6 +924,7 @@ def main() -> int:
     gw = torch.from_numpy(d["g_w"]).to(dev)
     gb = torch.from_numpy(d["g_b"]).to(dev)
 
+    restore = None
     if args.bwd == "atomic":
         orig = ftk._BackwardKernel.__call__
 
@@ -742,6 +933,7 @@ def main() -> int:
             return orig(self, *a, **k)
 
         ftk._BackwardKernel.__call__ = atomic_call
+        restore = orig
 
     def step():
         W.grad = None
@@ -774,7 +966,7 @@ def main() -> int:
     prof = _native.prof_collect()
     _native.prof_enable(False)
     ms = eager_ms
-    if args.graph:
+    if graph:
         # The whole step (both forwards, autograd backward, the grad sum) as one
         # HIP graph: the library makes no host synchronisation inside its calls.
         side = torch.cuda.Stream()
@@ -784,85 +976,58 @@ def main() -> int:
                 step()
         torch.cuda.current_stream().wait_stream(side)
         torch.cuda.synchronize()
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
             step()
-        warm_up(graph.replay, args.warmup, args.warmup_s)
+        warm_up(g.replay, args.warmup, args.warmup_s)
         t0 = time.perf_counter()
         e0.record()
         for _ in range(args.steps):
-            graph.replay()
+            g.replay()
         e1.record()
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
         ms = e0.elapsed_time(e1) / args.steps
         log(f"[bench] graph {args.steps} replays: {ms:.3f} ms/step (wall {wall * 1e3 / args.steps:.3f} ms/step)")
+        del g
+    if restore is not None:
+        ftk._BackwardKernel.__call__ = restore
 
     step_bytes = workloads.step_bytes(d["idx_w"], d["idx_b"], w.N, w.L)
+    kt = traffic["kind_step_bytes"] if traffic else {}
     kern = {}
     for kind, (tot, cnt) in prof.items():
         avg = tot / cnt
+        lps = cnt / args.steps
         sb = kernel_step_bytes(kind, w, (d["idx_w"], d["idx_b"]))
-        per_launch = sb / (cnt / args.steps) if sb else None
-        kern[kind] = {"avg_ms": avg, "launches_per_step": cnt / args.steps,
-                      "bytes_per_launch": per_launch,
-                      "gbs": (per_launch / (avg * 1e-3) / 1e9) if per_launch else None}
-        log(f"[bench]   {kind:22s} {avg:8.4f} ms x {cnt / args.steps:.0f}/step"
-            + (f"  {kern[kind]['gbs']:8.1f} GB/s algorithmic" if per_launch else ""))
+        per_launch = sb / lps if sb else None
+        kern[kind] = {"avg_ms": avg, "launches_per_step": lps, "bytes_per_launch": per_launch,
+                      "gbs": (per_launch / (avg * 1e-3) / 1e9) if per_launch else None,
+                      "traffic_per_launch": kt[kind] / lps if kind in kt else None}
+        log(f"[bench]   {kind:22s} {avg:8.4f} ms x {lps:.0f}/step"
+            + (f"  {kern[kind]['gbs']:8.1f} GB/s algorithmic" if per_launch else "")
+            + (f"  {kern[kind]['traffic_per_launch'] / 1e6:7.1f} MB traffic" if kind in kt else ""))
     dom = max(prof, key=lambda k: prof[k][0])
-    dom_avg = prof[dom][0] / prof[dom][1]
-    dom_bytes = kern[dom]["bytes_per_launch"]
-    achieved = dom_bytes / (dom_avg * 1e-3) / 1e9
-    traffic = load_traffic(w.name, dom) if args.zipf is None else None
-
-    result = {
-        "metric": METRIC,
-        "value": w.B / (ms * 1e-3),
-        "unit": "positions/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup, "warmup_s": args.warmup_s,
-        "ms_per_step": ms,
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "fp32",
-        "data": "synthetic" if args.zipf is None else f"synthetic, Zipf-like feature frequencies (alpha {args.zipf})",
-        "config": {
-            "workload": w.name, "feature_set": w.feature_set, "batch": w.B, "num_inputs": w.N,
-            "max_active": w.K, "active": [w.lo, w.hi], "output_size": w.L, "bwd": args.bwd,
-            "feature_freq": "uniform" if args.zipf is None else f"1/(rank+10)^{args.zipf}",
-            "launch": "hip_graph" if args.graph else "eager",
-            "parallelism": "single-gpu",
-            "input_sha256": {k: workloads.sha256(v) for k, v in d.items()},
-        },
-        "eager_ms_per_step": eager_ms,
-        "step_bytes": step_bytes,
-        "step_gbs": step_bytes / (ms * 1e-3) / 1e9,
-        "step_frac_of_hbm_peak": step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
-        "roofline": {
-            "kernel": dom,
-            "bound": "hbm",
-            "achieved": achieved,
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": achieved / HBM_PEAK_GBS,
-            "traffic": traffic,
-            "algorithmic_bytes_per_launch": dom_bytes,
-            "avg_launch_ms": dom_avg,
-        },
+    dk = kern[dom]
+    compulsory = workloads.step_compulsory_bytes(w.B, w.K, w.N, w.L)
+    out = {
+        "feature_set": w.feature_set, "batch": w.B, "num_inputs": w.N, "max_active": w.K, "active": [w.lo, w.hi],
+        "output_size": w.L, "step": "fwd + bwd of both perspectives through SparseLinearFunction",
+        "ms_per_step": ms, "eager_ms_per_step": eager_ms, "positions_per_s": w.B / (ms * 1e-3),
+        "step_bytes": step_bytes, "step_gbs": step_bytes / (ms * 1e-3) / 1e9,
+        "step_compulsory_bytes": compulsory,
+        "step_compulsory_frac_of_hbm_peak": compulsory / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+        "roofline": roofline(dom, dk["bytes_per_launch"], dk["avg_ms"], dk["traffic_per_launch"],
+                             traffic["source"] if traffic else None, l2_attainable),
         "kernels": kern,
     }
-    result["attainable"] = attainable(dev)
-    log(f"[bench] attainable: 1 GiB device copy {result['attainable']['copy_gbs']:.0f} GB/s")
-    if not args.no_cpu:
-        log(f"[bench] cpu baseline ({args.cpu_seconds:.0f} s budget)")
-        result["cpu_baseline"] = cpu_baseline(w, d, args.cpu_seconds)
-        result["gpu_over_cpu"] = result["value"] / result["cpu_baseline"]["value"]
-    else:
-        result["cpu_baseline"] = None
-    print(json.dumps(result), flush=True)
-    return 0
+    if traffic:
+        out["step_traffic_bytes"] = traffic["step_bytes"]
+        out["step_traffic_frac_of_hbm_peak"] = traffic["step_bytes"] / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS
+        out["traffic_source"] = traffic["source"]
+    if hashes:
+        out["input_sha256"] = {k: workloads.sha256(v) for k, v in d.items()}
+    return out, d
 
 
 if __name__ == "__main__":

@@ -396,6 +396,19 @@ int sft_leb128_encode(const void *values, int32_t elem_bytes, int64_t n, uint8_t
 int sft_quantize_i16(const float *x, int64_t n, float scale, int16_t *out, void *stream);
 
 /*
+ * Measurement helper (no reference counterpart): one dispatch of `blocks`
+ * 256-thread workgroups whose 8-lane groups each gather 8 * rounds 128-byte rows
+ * of table (table_rows x 128 bytes, table_rows a power of two <= 2^24, 16-byte
+ * aligned) at pseudo-random row numbers, writing one 16-byte sum per thread to
+ * out (out_bytes >= blocks * 4096).  Bytes gathered = blocks * 32 * 8 * rounds
+ * * 128.  With a table that fits one XCD's L2 it measures the attainable rate of
+ * the L2-served row gathers the tiled FT kernels make (timed as
+ * "probe_l2_gather" by sft_prof_*).
+ */
+int sft_probe_l2_gather(const float *table, int64_t table_rows, int32_t rounds, int32_t blocks,
+                        float *out, size_t out_bytes, void *stream);
+
+/*
  * Kernel timing over a measured region (no reference counterpart).  While
  * enabled, every launch made by the entry points above is bracketed by a pair
  * of HIP events on its stream.  sft_prof_collect() waits for the recorded

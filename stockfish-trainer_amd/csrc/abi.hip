@@ -45,6 +45,7 @@ int ranger_update_f32(float *p, const float *grad, float *variance_ma, float *gm
                       int64_t rows, int64_t cols, const float *scalars, hipStream_t s);
 size_t leb128_workspace(int64_t n);
 int leb128_encode(const void *values, int elem, int64_t n, uint8_t *out, int64_t *out_len, void *ws, hipStream_t s);
+int probe_l2_gather(const float *table, int64_t table_rows, int rounds, int blocks, float *out, hipStream_t s);
 int encode_features(const uint8_t *boards, const uint8_t *stm, int64_t B, const int32_t *comps, int ncomp,
                     int32_t *white, int32_t *black, int K, float *us, int64_t *psqt, int64_t *ls, int32_t *count_w,
                     int32_t *count_b, hipStream_t s);
@@ -144,6 +145,13 @@ int join_side(hipStream_t s) {
   return rc != SFT_OK ? rc : wait_side(s, 0);
 }
 
+SideJoinGuard::~SideJoinGuard() {
+  if (!armed_) return;
+  const std::string keep = t_error;
+  (void)join_side(s_);
+  t_error = keep;
+}
+
 Mapping choose_mapping(int64_t chunks, int min_group) {
   // Largest lane group whose single-slab lane use is >= 75%; otherwise the
   // single-slab mapping with the best lane use; rows too wide for one slab
@@ -210,6 +218,7 @@ const char *const kKindNames[] = {
     "bwd_bias_final",   "bwd_atomic_scatter", "bwd_zero_fill",      "fwd_i16_gather",     "quantize_i16",
     "fwd_tile_relayout", "fwd_f32_tiled_gather", "bwd_tiled_gather", "fwd_i16_tiled_gather",
     "fwd_fold_relayout", "bwd_virtual_reduce", "bwd_epilogue", "ranger22_update", "encode_features", "leb128_encode",
+    "probe_l2_gather",
 };
 static_assert(sizeof(kKindNames) / sizeof(kKindNames[0]) == kProfNumKinds, "one name per profiling kind");
 }  // namespace
@@ -814,6 +823,22 @@ int sft_prof_collect(double *total_ms, int64_t *launches, int n_kinds) {
   }
   drop_pending_locked();
   return rc;
+}
+
+int sft_probe_l2_gather(const float *table, int64_t table_rows, int32_t rounds, int32_t blocks, float *out,
+                        size_t out_bytes, void *stream) {
+  clear_error();
+  const char *w = "sft_probe_l2_gather";
+  if (!table || !out) return fail(SFT_EINVAL, std::string(w) + ": null pointer");
+  if (table_rows < 1 || table_rows > (1 << 24) || (table_rows & (table_rows - 1)) != 0)
+    return fail(SFT_EINVAL, std::string(w) + ": table_rows must be a power of two in [1, 2^24]");
+  if (rounds < 1 || blocks < 1 || blocks > (1 << 20))
+    return fail(SFT_EINVAL, std::string(w) + ": need rounds >= 1 and 1 <= blocks <= 2^20");
+  if (out_bytes < (size_t)blocks * kBlock * 16)
+    return fail(SFT_EINVAL, std::string(w) + ": out smaller than blocks * 256 * 16 bytes");
+  if ((uintptr_t)table % 16 != 0 || (uintptr_t)out % 16 != 0)
+    return fail(SFT_EINVAL, std::string(w) + ": table and out must be 16-byte aligned");
+  return probe_l2_gather(table, table_rows, rounds, blocks, out, (hipStream_t)stream);
 }
 
 }  // extern "C"

@@ -39,6 +39,22 @@ int fork_side(hipStream_t s, hipStream_t *side);
 int mark_side(int slot);
 int wait_side(hipStream_t s, int slot);
 int join_side(hipStream_t s);
+// Joins the side stream into s when it goes out of scope unless release()d, so
+// an error return after fork_side never leaves side-stream work unordered with
+// s (a graph capture stays joined; freed workspace is not reused early).  It
+// keeps the error message of the failure that caused the early return.
+class SideJoinGuard {
+ public:
+  explicit SideJoinGuard(hipStream_t s) : s_(s) {}
+  ~SideJoinGuard();
+  void release() { armed_ = false; }
+  SideJoinGuard(const SideJoinGuard &) = delete;
+  SideJoinGuard &operator=(const SideJoinGuard &) = delete;
+
+ private:
+  hipStream_t s_;
+  bool armed_ = true;
+};
 
 // ---- kernel timing hooks (active only between sft_prof_enable(1) and (0)) ----
 enum ProfKind : int {
@@ -62,6 +78,7 @@ enum ProfKind : int {
   kProfOptim,
   kProfEncode,
   kProfLeb128,
+  kProfProbeL2Gather,
   kProfNumKinds
 };
 struct ProfScope {

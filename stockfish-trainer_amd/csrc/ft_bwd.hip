@@ -18,6 +18,7 @@
 // Bias grad (FT/kernel.py:269): per-block column partial sums, then a fixed-
 // order reduction of the partials; deterministic.
 #include <algorithm>
+#include <optional>
 #include <type_traits>
 
 #include "common.h"
@@ -1021,9 +1022,11 @@ int bwd_f32(const int32_t *idx, int64_t B, int K, const float *grad, int64_t N, 
   unsigned *keys = nullptr, *totals = nullptr;
   int32_t *pos = nullptr;
   int ntot = 0;
+  std::optional<SideJoinGuard> side_join;  // joins the side stream on every early return
   if (sorted) {
     hipStream_t side;
     if ((rc = fork_side(s, &side)) != SFT_OK) return rc;
+    side_join.emplace(s);
     {
       ProfScope prof(kProfBwdSort, side);
       if ((rc = slot_sort(idx, M, K, N, (int)(nc > 1 ? half_rows(B) : B), nc, w + lay.sort, &keys, &pos, &totals,
@@ -1043,7 +1046,10 @@ int bwd_f32(const int32_t *idx, int64_t B, int K, const float *grad, int64_t N, 
                                 s)) != SFT_OK)
       return rc;
   }
-  if (sorted && (rc = join_side(s)) != SFT_OK) return rc;
+  if (sorted) {
+    if ((rc = join_side(s)) != SFT_OK) return rc;
+    side_join->release();
+  }
 
   if (flags & SFT_BWD_ATOMIC) {
     if (overwrite) {
@@ -1220,12 +1226,14 @@ static int pair_sort_both(const int32_t *idx0, const int32_t *idx1, int64_t B, i
   hipStream_t side;
   int rc = fork_side(s, &side);
   if (rc != SFT_OK) return rc;
+  SideJoinGuard side_join(s);
   for (int p = 0; p < 2; ++p) {
     if ((rc = pair_sort_perspective(p == 0 ? idx0 : idx1, B, K, N, nc, w + sort_off[p],
                                     reinterpret_cast<int32_t *>(w + seg_off[p]), ss[p], side)) != SFT_OK)
       return rc;
     if ((rc = mark_side(p)) != SFT_OK) return rc;
   }
+  side_join.release();  // the caller waits for each mark before that perspective's gathers
   return SFT_OK;
 }
 
@@ -1260,6 +1268,7 @@ int bwd_pair_f32(const int32_t *idx0, const int32_t *idx1, int64_t B, int K, con
   SortedSlots ss[2];
   int rc = pair_sort_both(idx0, idx1, B, K, N, lay.nc, w, lay.sort, lay.seg, ss, s);
   if (rc != SFT_OK) return rc;
+  SideJoinGuard side_join(s);  // until both marks are waited for
   // Both bias passes (which also write each perspective's grad tiles) run while
   // the side stream sorts, so that no sort overlaps a gather.
   for (int p = 0; p < 2; ++p) {
@@ -1272,6 +1281,7 @@ int bwd_pair_f32(const int32_t *idx0, const int32_t *idx1, int64_t B, int K, con
     if ((rc = wait_side(s, p)) != SFT_OK) return rc;
     if ((rc = pair_gather_perspective(p, ss[p], B, N, map, gt[p], dst, tmp, lay.nc, s)) != SFT_OK) return rc;
   }
+  side_join.release();
   if ((rc = launch_bias_final(partial, 2 * lay.nparts, L, db, 1, true, s)) != SFT_OK) return rc;
   return virtual_reduce(vgrad_src, vgrad, vperiod, vreps, nvirt, L / 4, s);
 }
@@ -1343,6 +1353,7 @@ int bwd_transform_f32(const int32_t *idx0, const int32_t *idx1, int64_t B, int K
   SortedSlots ss[2];  // sorted on the side stream while the epilogue runs
   int rc = pair_sort_both(idx0, idx1, B, K, N, lay.nc, w, lay.sort, lay.seg, ss, s);
   if (rc != SFT_OK) return rc;
+  SideJoinGuard side_join(s);  // until both marks are waited for
   {
     ProfScope prof(kProfBwdEpilogue, s);
     hipLaunchKernelGGL(bwd_epilogue_kernel, dim3((unsigned)lay.nparts), dim3(kBlock), 0, s, e, map, B,
@@ -1358,6 +1369,7 @@ int bwd_transform_f32(const int32_t *idx0, const int32_t *idx1, int64_t B, int K
     if ((rc = pair_gather_perspective(p, ss[p], B, N, map, p == 0 ? gt0 : gt1, dst, tmp, lay.nc, s)) != SFT_OK)
       return rc;
   }
+  side_join.release();
   return virtual_reduce(vgrad_src, vgrad, vperiod, vreps, nvirt, L / 4, s);
 }
 

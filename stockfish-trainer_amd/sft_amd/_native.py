@@ -99,6 +99,7 @@ SIGNATURES = {
     "sft_leb128_workspace_size": (ctypes.c_int, [_i64, ctypes.POINTER(ctypes.c_size_t)]),
     "sft_leb128_encode": (ctypes.c_int, [_vp, _i32, _i64, _vp, ctypes.c_size_t, _vp, _vp, ctypes.c_size_t, _vp]),
     "sft_quantize_i16": (ctypes.c_int, [_vp, _i64, ctypes.c_float, _vp, _vp]),
+    "sft_probe_l2_gather": (ctypes.c_int, [_vp, _i64, _i32, _i32, _vp, ctypes.c_size_t, _vp]),
     "sft_prof_enable": (ctypes.c_int, [ctypes.c_int]),
     "sft_prof_num_kinds": (ctypes.c_int, []),
     "sft_prof_kind_name": (ctypes.c_char_p, [ctypes.c_int]),
@@ -586,6 +587,19 @@ def quantize_i16(x: torch.Tensor, scale: float) -> torch.Tensor:
 
 
 # ---- per-launch kernel timing ----
+def probe_l2_gather(table: torch.Tensor, rounds: int, blocks: int, out: torch.Tensor) -> int:
+    """One dispatch of the L2 row-gather probe over `table` (float32 [rows, 32],
+    rows a power of two); returns the bytes it gathers."""
+    _require(table.dim() == 2 and table.shape[1] == 32 and table.dtype == torch.float32,
+             "table must be float32 [rows, 32]")
+    _require(out.dtype == torch.float32 and out.numel() >= blocks * 256 * 4, "out must hold blocks * 1024 floats")
+    _on_gpu(table.device, table, out)
+    with torch.cuda.device(table.device):
+        _check(lib().sft_probe_l2_gather(_ptr(table), table.shape[0], rounds, blocks, _ptr(out), out.numel() * 4,
+                                         _stream(table.device)), "sft_probe_l2_gather")
+    return blocks * 32 * 8 * rounds * 128
+
+
 def prof_enable(on: bool) -> None:
     _check(lib().sft_prof_enable(1 if on else 0), "sft_prof_enable")
 

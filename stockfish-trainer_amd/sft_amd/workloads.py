@@ -195,6 +195,22 @@ def step_bytes(idx_w: np.ndarray, idx_b: np.ndarray, N: int, L: int) -> int:
     return total + 4 * N * L
 
 
+def step_compulsory_bytes(B: int, K: int, N: int, L: int) -> int:
+    """Bytes an fp32 fwd+bwd step of both perspectives through SparseLinearFunction
+    cannot avoid moving to or from HBM: both index tensors and the table read
+    once, both outputs written, both upstream grads read once, each
+    perspective's dense weight grad written and autograd's sum of the two (two
+    read, one written).  The bias and its grad are negligible."""
+    return 2 * 4 * B * K + 4 * N * L + 2 * 4 * B * L + 2 * 4 * B * L + 2 * 4 * N * L + 3 * 4 * N * L
+
+
+def q16_compulsory_bytes(B: int, K: int, N: int, L: int, psqt: int = 0) -> int:
+    """Bytes the int16 forward of both perspectives cannot avoid: both index
+    tensors and the table (with its PSQT columns) read once, both int16 outputs
+    and PSQT outputs written."""
+    return 2 * 4 * B * K + N * (2 * L + 4 * psqt) + 2 * (2 * B * L + 4 * B * psqt)
+
+
 def fwd_kernel_bytes(idx: np.ndarray, N: int, L: int) -> int:
     """One fp32 forward launch (one perspective): index rows, gathered rows, output rows."""
     K = idx.shape[1]
