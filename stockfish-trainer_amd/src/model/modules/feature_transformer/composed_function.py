@@ -21,21 +21,8 @@ from torch import autograd
 
 from sft_amd import _native
 
-
-def split_tables(tables, virtual_rows):
-    """Flat (w_0, [v_0], w_1, [v_1], ...) -> ([w_s], [v_s or None])."""
-    weights, virtuals = [], []
-    i = 0
-    for vr in virtual_rows:
-        weights.append(tables[i])
-        i += 1
-        if vr > 0:
-            virtuals.append(tables[i])
-            i += 1
-        else:
-            virtuals.append(None)
-    assert i == len(tables)
-    return weights, virtuals
+from . import ops  # noqa: F401  (registers torch.ops.sft.*)
+from .ops import split_tables  # noqa: F401  (re-exported)
 
 
 class ComposedSparseLinearFunction(autograd.Function):
@@ -46,7 +33,6 @@ class ComposedSparseLinearFunction(autograd.Function):
 
     @staticmethod
     def forward(ctx, feature_indices_0, feature_indices_1, bias, virtual_rows, *tables):
-        weights, virtuals = split_tables(tables, virtual_rows)
         for idx in (feature_indices_0, feature_indices_1):
             assert len(idx.shape) == 2
             assert idx.dtype == torch.int32
@@ -64,36 +50,32 @@ class ComposedSparseLinearFunction(autograd.Function):
             assert t.is_cuda and t.device == feature_indices_0.device
             assert t.is_contiguous()
 
-        device = feature_indices_0.device
-        batch_size = feature_indices_0.shape[0]
-        output_size = bias.shape[0]
-        out0 = torch.empty(batch_size, output_size, dtype=torch.float32, device=device)
-        out1 = torch.empty(batch_size, output_size, dtype=torch.float32, device=device)
-        _native.ft_fwd_pair_f32(feature_indices_0, feature_indices_1, weights, virtuals, bias, out0, out1)
-
+        out0, out1 = torch.ops.sft.composed_fwd(feature_indices_0, feature_indices_1, bias, list(virtual_rows),
+                                                list(tables))
         ctx.save_for_backward(feature_indices_0, feature_indices_1)
         ctx.virtual_rows = tuple(virtual_rows)
-        ctx.table_shapes = [t.shape for t in tables]
+        ctx.table_rows = [t.shape[0] for t in tables]
         return out0, out1
 
     @staticmethod
     def backward(ctx, grad_0, grad_1):
         assert not ctx.needs_input_grad[0] and not ctx.needs_input_grad[1]
         idx0, idx1 = ctx.saved_tensors
-        device = idx0.device
-        grad_0 = grad_0.contiguous()
-        grad_1 = grad_1.contiguous()
-        # Every output is overwritten by the library: no zero-fill.
-        grads = [torch.empty(shape, dtype=torch.float32, device=device) for shape in ctx.table_shapes]
-        bias_grad = torch.empty(grad_0.shape[1], dtype=torch.float32, device=device)
-        weight_grads, virtual_grads = split_tables(grads, ctx.virtual_rows)
-        _native.ft_bwd_pair_f32(idx0, idx1, grad_0, grad_1, weight_grads, virtual_grads, bias_grad)
-        return (None, None, bias_grad, None, *grads)
+        # Every grad is overwritten by the library: no zero-fill.
+        res = torch.ops.sft.composed_bwd(idx0, idx1, grad_0.contiguous(), grad_1.contiguous(),
+                                         list(ctx.virtual_rows), list(ctx.table_rows))
+        return (None, None, res[-1], None, *res[:-1])
+
+
+@torch.compiler.assume_constant_result
+def _pair_shape_supported(batch_size: int, max_active: int, rows: tuple, vrows: tuple, output_size: int) -> bool:
+    # a host-only library query: a constant for torch.compile, not a graph break
+    return _native.pair_workspace_bytes(batch_size, max_active, list(rows), list(vrows), output_size) is not None
 
 
 def composed_pair_supported(batch_size: int, max_active: int, blocks, output_size: int) -> bool:
     """Whether the library runs this composed shape fused (else the caller
     composes the table and runs SparseLinearFunction twice)."""
-    rows = [w.shape[0] for w, _ in blocks]
-    vrows = [0 if v is None else v.shape[0] for _, v in blocks]
-    return _native.pair_workspace_bytes(batch_size, max_active, rows, vrows, output_size) is not None
+    rows = tuple(w.shape[0] for w, _ in blocks)
+    vrows = tuple(0 if v is None else v.shape[0] for _, v in blocks)
+    return _pair_shape_supported(batch_size, max_active, rows, vrows, output_size)

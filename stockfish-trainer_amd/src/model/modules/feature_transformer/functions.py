@@ -1,14 +1,16 @@
 """SparseLinearFunction: the FT's autograd op (reference
 src/model/modules/feature_transformer/functions.py:10-72), same inputs, asserts,
-outputs and gradients, running the gfx950 kernels of libsft_ft.so."""
+outputs and gradients, running the gfx950 kernels of libsft_ft.so.
+
+The kernels are reached through the custom ops sft::sparse_linear_fwd / _bwd
+(ops.py), which run the factories' callables (kernel.py); as opaque ops with
+fake implementations they let torch.compile trace this function without the
+graph break the reference's compiler-disabled factories cause."""
 
 import torch
 from torch import autograd
 
-from .kernel import (
-    make_sparse_input_linear_forward_kernel,
-    make_sparse_input_linear_backward_kernel,
-)
+from . import ops  # noqa: F401  (registers torch.ops.sft.*)
 
 
 class SparseLinearFunction(autograd.Function):
@@ -31,25 +33,9 @@ class SparseLinearFunction(autograd.Function):
         assert weight.is_contiguous()
         assert bias.is_contiguous()
 
-        device = feature_indices.device
-        batch_size = feature_indices.shape[0]
-        max_active_features = feature_indices.shape[1]
-        output_size = weight.shape[1]
-
-        output = torch.empty(
-            batch_size,
-            output_size,
-            dtype=torch.float32,
-            device=device,
-            requires_grad=True,
-        )
-
-        kernel = make_sparse_input_linear_forward_kernel(
-            max_active_features, output_size
-        )
-        kernel(feature_indices, weight, bias, output)
-
-        return output
+        # make_sparse_input_linear_forward_kernel(K, L)(idx, W, b, out) on a new
+        # [B, L] output, as one opaque op
+        return torch.ops.sft.sparse_linear_fwd(feature_indices, weight, bias)
 
     @staticmethod
     def backward(ctx, grad_output):
@@ -59,20 +45,9 @@ class SparseLinearFunction(autograd.Function):
 
         feature_indices, weight, _bias = ctx.saved_tensors
 
-        device = feature_indices.device
-        max_active_features = feature_indices.shape[1]
-        output_size = weight.shape[1]
-
-        # The kernel writes every row (absent features get 0), so the grads
-        # need no zero-fill; the values equal zero-init + accumulate exactly.
-        weight_grad = torch.empty(
-            weight.shape[0], weight.shape[1], dtype=torch.float32, device=device
-        )
-        bias_grad = torch.empty(output_size, dtype=torch.float32, device=device)
-
-        kernel = make_sparse_input_linear_backward_kernel(
-            max_active_features, output_size
-        )
-        kernel(feature_indices, weight_grad, bias_grad, grad_output, accumulate=False)
+        # The backward kernel in overwrite mode writes every row (absent features
+        # get 0), so the grads need no zero-fill; the values equal zero-init +
+        # accumulate exactly.
+        weight_grad, bias_grad = torch.ops.sft.sparse_linear_bwd(feature_indices, grad_output, weight.shape[0])
 
         return None, weight_grad, bias_grad

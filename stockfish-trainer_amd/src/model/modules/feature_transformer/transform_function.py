@@ -20,7 +20,7 @@ from torch import autograd
 
 from sft_amd import _native
 
-from .composed_function import split_tables
+from . import ops  # noqa: F401  (registers torch.ops.sft.*)
 
 
 class TransformedFeatureFunction(autograd.Function):
@@ -28,7 +28,6 @@ class TransformedFeatureFunction(autograd.Function):
 
     @staticmethod
     def forward(ctx, us, feature_indices_0, feature_indices_1, psqt_indices, bias, l1, virtual_rows, *tables):
-        weights, virtuals = split_tables(tables, virtual_rows)
         for idx in (feature_indices_0, feature_indices_1):
             assert len(idx.shape) == 2
             assert idx.dtype == torch.int32
@@ -38,40 +37,37 @@ class TransformedFeatureFunction(autograd.Function):
         assert bias.dtype == torch.float32 and bias.is_contiguous() and bias.is_cuda
         for t in tables:
             assert t.dtype == torch.float32 and t.is_contiguous() and t.is_cuda
-        batch_size = feature_indices_0.shape[0]
-        device = feature_indices_0.device
         us_flat = us.reshape(-1).to(torch.float32).contiguous()
         psqt_flat = psqt_indices.reshape(-1).to(torch.int64).contiguous()
-        l0 = torch.empty(batch_size, l1, dtype=torch.float32, device=device)
-        psqt = torch.empty(batch_size, 1, dtype=torch.float32, device=device)
-        saved = _native.ft_fwd_transform_f32(feature_indices_0, feature_indices_1, weights, virtuals, bias, us_flat,
-                                             psqt_flat, l1, l0, psqt)
-        ctx.save_for_backward(feature_indices_0, feature_indices_1, us_flat, psqt_flat)
-        ctx.saved_buffer = saved
+        l0, psqt, saved = torch.ops.sft.transform_fwd(feature_indices_0, feature_indices_1, bias, us_flat, psqt_flat,
+                                                      l1, list(virtual_rows), list(tables))
+        # the pre-activations kept for the backward (an opaque uint8 buffer)
+        ctx.save_for_backward(feature_indices_0, feature_indices_1, us_flat, psqt_flat, saved)
         ctx.l1 = l1
         ctx.virtual_rows = tuple(virtual_rows)
-        ctx.table_shapes = [t.shape for t in tables]
+        ctx.table_rows = [t.shape[0] for t in tables]
         ctx.output_size = bias.shape[0]
         return l0, psqt
 
     @staticmethod
     def backward(ctx, grad_l0, grad_psqt):
-        idx0, idx1, us_flat, psqt_flat = ctx.saved_tensors
-        device = idx0.device
-        grad_l0 = grad_l0.contiguous()
-        grad_psqt = grad_psqt.reshape(-1).contiguous()
-        grads = [torch.empty(shape, dtype=torch.float32, device=device) for shape in ctx.table_shapes]
-        bias_grad = torch.empty(ctx.output_size, dtype=torch.float32, device=device)
-        weight_grads, virtual_grads = split_tables(grads, ctx.virtual_rows)
-        _native.ft_bwd_transform_f32(idx0, idx1, grad_l0, grad_psqt, us_flat, psqt_flat, ctx.saved_buffer, ctx.l1,
-                                     weight_grads, virtual_grads, bias_grad)
-        ctx.saved_buffer = None
-        return (None, None, None, None, bias_grad, None, None, *grads)
+        idx0, idx1, us_flat, psqt_flat, saved = ctx.saved_tensors
+        res = torch.ops.sft.transform_bwd(idx0, idx1, grad_l0.contiguous(), grad_psqt.reshape(-1).contiguous(),
+                                          us_flat, psqt_flat, saved, ctx.l1, ctx.output_size,
+                                          list(ctx.virtual_rows), list(ctx.table_rows))
+        return (None, None, None, None, res[-1], None, None, *res[:-1])
+
+
+@torch.compiler.assume_constant_result
+def _transform_shape_supported(batch_size: int, max_active: int, rows: tuple, vrows: tuple, output_size: int,
+                               l1: int) -> bool:
+    # a host-only library query: a constant for torch.compile, not a graph break
+    return _native.transform_workspace_bytes(batch_size, max_active, list(rows), list(vrows), output_size,
+                                             l1) is not None
 
 
 def transform_supported(input_module, batch_size: int, max_active: int, l1: int) -> bool:
     blocks = [f.table_blocks() for f in input_module.features]
-    rows = [w.shape[0] for w, _ in blocks]
-    vrows = [0 if v is None else v.shape[0] for _, v in blocks]
-    return _native.transform_workspace_bytes(batch_size, max_active, rows, vrows, input_module.num_outputs,
-                                             l1) is not None
+    rows = tuple(w.shape[0] for w, _ in blocks)
+    vrows = tuple(0 if v is None else v.shape[0] for _, v in blocks)
+    return _transform_shape_supported(batch_size, max_active, rows, vrows, input_module.num_outputs, l1)

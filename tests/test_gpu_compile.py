@@ -1,0 +1,132 @@
+"""torch.compile over the FT surface: the library calls are custom ops with fake
+implementations, so Dynamo traces SparseLinearFunction, the fused composed
+module and the fused transform without a graph break (the reference breaks the
+graph at its compiler-disabled factories, FT/kernel.py:301,315), and the
+compiled functions give outputs and grads bit-identical to eager."""
+
+import numpy as np
+import pytest
+import torch
+
+from gpu_helpers import DEV, announce, dev
+from sft_amd import workloads
+from src.model.modules.feature_transformer import SparseLinearFunction
+from src.model.modules.features import get_feature_cls
+from src.model.transform_inputs import transform_inputs
+
+pytestmark = pytest.mark.gpu
+
+BACKEND = "aot_eager"  # Dynamo + AOTAutograd over fake tensors; the FT ops stay opaque
+
+
+def _no_breaks(fn, *args):
+    torch._dynamo.reset()
+    ex = torch._dynamo.explain(fn)(*args)
+    assert ex.graph_break_count == 0, ex.break_reasons
+    assert ex.graph_count == 1
+
+
+def test_sparse_linear_compiles_without_graph_break():
+    announce("compile SparseLinearFunction")
+    g = np.random.default_rng(5)
+    B, N, K, L = 3000, 4000, 32, 1048
+    iw = dev(workloads.make_indices(g, B, N, K, 16, 32, sort=False))
+    ib = dev(workloads.make_indices(g, B, N, K, 16, 32, sort=False))
+    W0 = torch.from_numpy((g.standard_normal((N, L)) * 0.01).astype(np.float32)).to(DEV)
+    b0 = torch.from_numpy(g.uniform(-0.1, 0.1, L).astype(np.float32)).to(DEV)
+    gw = torch.randn(B, L, device=DEV)
+    gb = torch.randn(B, L, device=DEV)
+
+    def step(iw, ib, W, b):
+        return SparseLinearFunction.apply(iw, W, b), SparseLinearFunction.apply(ib, W, b)
+
+    _no_breaks(step, iw, ib, W0.clone().requires_grad_(True), b0.clone().requires_grad_(True))
+
+    def run(fn):
+        W = W0.clone().requires_grad_(True)
+        b = b0.clone().requires_grad_(True)
+        ow, ob = fn(iw, ib, W, b)
+        torch.autograd.backward([ow, ob], [gw, gb])
+        torch.cuda.synchronize()
+        return ow.detach(), ob.detach(), W.grad, b.grad
+
+    torch._dynamo.reset()
+    compiled = torch.compile(step, backend=BACKEND, fullgraph=True)
+    ref = run(step)
+    for _ in range(2):  # the second call runs the cached graph
+        got = run(compiled)
+        for a, r in zip(got, ref):
+            assert torch.equal(a, r)
+
+
+@pytest.mark.parametrize("name,B,L", [("HalfKAv2_hm^", 4096, 1048), ("Full_Threats+HalfKAv2_hm^", 1500, 520)])
+def test_composed_module_compiles_without_graph_break(name, B, L):
+    announce(f"compile composed module {name} B={B} L={L}")
+    torch.manual_seed(4)
+    ft = get_feature_cls(name)(L).to(DEV)
+    for f in ft.features:
+        if hasattr(f, "virtual_weight"):
+            with torch.no_grad():
+                f.virtual_weight.normal_(0, 0.01)
+    g = np.random.default_rng(B)
+    K, lo = ft.MAX_ACTIVE_FEATURES, (16 if ft.MAX_ACTIVE_FEATURES == 32 else 32)
+    iw = dev(workloads.make_indices(g, B, ft.NUM_INPUTS, K, lo, K, sort=False))
+    ib = dev(workloads.make_indices(g, B, ft.NUM_INPUTS, K, lo, K, sort=False))
+    gw = torch.randn(B, L, device=DEV)
+    gb = torch.randn(B, L, device=DEV)
+    _no_breaks(ft, iw, ib)
+
+    def run(fn):
+        for p in ft.parameters():
+            p.grad = None
+        ow, ob = fn(iw, ib)
+        torch.autograd.backward([ow, ob], [gw, gb])
+        torch.cuda.synchronize()
+        return [ow.detach(), ob.detach()] + [p.grad.clone() for p in ft.parameters()]
+
+    torch._dynamo.reset()
+    compiled = torch.compile(ft, backend=BACKEND, fullgraph=True)
+    ref = run(ft)
+    got = run(compiled)
+    for a, r in zip(got, ref):
+        assert torch.equal(a, r)
+
+
+def test_fused_transform_compiles_without_graph_break():
+    announce("compile fused transform")
+    torch.manual_seed(6)
+    L1, P, B = 1040, 8, 2048
+    ft = get_feature_cls("HalfKAv2_hm^")(L1 + P).to(DEV)
+    with torch.no_grad():
+        for f in ft.features:
+            f.weight.normal_(0, 0.05)
+            f.virtual_weight.normal_(0, 0.02)
+        ft.bias.uniform_(0.0, 0.6)
+    g = np.random.default_rng(9)
+    K = ft.MAX_ACTIVE_FEATURES
+    iw = dev(workloads.make_indices(g, B, ft.NUM_INPUTS, K, 16, K, sort=False))
+    ib = dev(workloads.make_indices(g, B, ft.NUM_INPUTS, K, 16, K, sort=False))
+    us = dev(g.integers(0, 2, (B, 1)).astype(np.float32))
+    k = dev(g.integers(0, P, B).astype(np.int64))
+    g_l0 = torch.randn(B, L1, device=DEV)
+    g_psqt = torch.randn(B, 1, device=DEV)
+
+    def step(us, iw, ib, k):
+        return transform_inputs(ft, L1, us, iw, ib, k)
+
+    _no_breaks(step, us, iw, ib, k)
+
+    def run(fn):
+        for p in ft.parameters():
+            p.grad = None
+        l0, psqt = fn(us, iw, ib, k)
+        torch.autograd.backward([l0, psqt], [g_l0, g_psqt])
+        torch.cuda.synchronize()
+        return [l0.detach(), psqt.detach()] + [p.grad.clone() for p in ft.parameters()]
+
+    torch._dynamo.reset()
+    compiled = torch.compile(step, backend=BACKEND, fullgraph=True)
+    ref = run(step)
+    got = run(compiled)
+    for a, r in zip(got, ref):
+        assert torch.equal(a, r)
