@@ -6,6 +6,7 @@
 #include <cstdint>
 #include <string>
 
+#include "index_math.h"
 #include "sft_ft.h"
 
 namespace sft {
@@ -189,43 +190,10 @@ __device__ __forceinline__ void compact_rows(const int32_t *__restrict__ idx, in
   }
 }
 
-// ---- XCD-aware tile schedule ----
-// MI355X runs a dispatch's workgroups round-robin over its 8 XCDs (workgroup i
-// on XCD i % 8), and each XCD has its own 4 MB L2.  Tiled kernels give every
-// XCD whole column tiles: workgroup i serves the (i / 8)-th item of XCD i % 8,
-// where XCD x owns tiles x, x + 8, ... (all chunks of one tile, then the next).
-// The rem = ntiles % 8 tiles left after the last full round each go to a
-// group of 8 / rem (rounded down or up) XCDs -- XCD x to leftover tile
-// x * rem / 8 -- whose members take its chunks in turn, so an XCD still reads
-// one tile.  Any other placement only costs locality, never results.
-constexpr int kXcds = 8;
 #ifndef SFT_MIN_TILES
 #define SFT_MIN_TILES 8
 #endif
 constexpr int kMinTiles = SFT_MIN_TILES;  // fewest column tiles for which the tiled kernels are used
-struct TileItem {
-  int tile, chunk;
-};
-__host__ __device__ inline int64_t tile_sched_items_per_xcd(int ntiles, int nchunks) {
-  const int full = ntiles / kXcds, rem = ntiles % kXcds;
-  if (rem == 0) return (int64_t)full * nchunks;
-  const int gmin = kXcds / rem;  // smallest group
-  return (int64_t)full * nchunks + ((int64_t)nchunks + gmin - 1) / gmin;
-}
-__device__ __forceinline__ TileItem tile_sched_item(int64_t bid, int ntiles, int nchunks) {
-  const int xcd = (int)(bid % kXcds);
-  const int64_t j = bid / kXcds;
-  const int full = ntiles / kXcds, rem = ntiles % kXcds;
-  const int64_t fj = (int64_t)full * nchunks;
-  if (j < fj) return TileItem{xcd + kXcds * (int)(j / nchunks), (int)(j % nchunks)};
-  if (rem == 0) return TileItem{ntiles, 0};  // no work
-  const int t = xcd * rem / kXcds;                              // leftover tile of this XCD's group
-  const int x0 = (t * kXcds + rem - 1) / rem;                   // first XCD of the group
-  const int gs = ((t + 1) * kXcds + rem - 1) / rem - x0;        // group size
-  const int64_t c = (xcd - x0) + (j - fj) * gs;
-  if (c >= nchunks) return TileItem{ntiles, 0};  // no work
-  return TileItem{kXcds * full + t, (int)c};
-}
 
 // ---- composed tables ----
 // A composed feature transformer's table is the concatenation of up to
@@ -246,57 +214,6 @@ struct RowDst {
   int64_t start[kMaxBlocks + 1];
   f32x4 *p[kMaxBlocks];
 };
-// ---- column maps of the 32-column tiles ----
-// Tile t, lane q (one 16-byte chunk of 4 columns) of a tile row holds chunk
-// tile_col(m, t, q) of the row-major table (-1: padding).
-//   plain  (half4 == 0): chunks 8t .. 8t+7.
-//   paired (half4 > 0):  for t < t1, chunks 4t .. 4t+3 of the first half
-//     (lanes 0-3) and the same chunks of the second half (lanes 4-7), where a
-//     half is half4 chunks; tiles t >= t1 hold the chunks after both halves
-//     (the PSQT columns), 8 per tile.  Columns j and j + L1/2 of a row, which
-//     the post-FT epilogue multiplies together, then sit in lanes q and q ^ 4.
-struct ColMap {
-  int half4;  // chunks per half (0: plain map)
-  int t1;     // paired tiles
-  int cols4;  // chunks per row
-  int tch;    // plain map: chunks per tile row (8: 32 columns, 4: 16 columns)
-};
-__host__ __device__ inline int tile_col(const ColMap &m, int t, int q) {
-  if (m.half4 == 0) {
-    const int c = m.tch * t + q;
-    return (q < m.tch && c < m.cols4) ? c : -1;
-  }
-  if (t < m.t1) {
-    const int j = 4 * t + (q & 3);
-    return j < m.half4 ? j + (q >> 2) * m.half4 : -1;
-  }
-  const int c = 2 * m.half4 + 8 * (t - m.t1) + q;
-  return c < m.cols4 ? c : -1;
-}
-// Inverse: tile and lane of chunk c.
-__host__ __device__ inline void tile_of_col(const ColMap &m, int c, int &t, int &q) {
-  if (m.half4 == 0) {
-    t = c / m.tch;
-    q = c % m.tch;
-  } else if (c < 2 * m.half4) {
-    const int h = c >= m.half4 ? 1 : 0;
-    const int j = c - h * m.half4;
-    t = j >> 2;
-    q = (j & 3) + 4 * h;
-  } else {
-    const int k = c - 2 * m.half4;
-    t = m.t1 + (k >> 3);
-    q = k & 7;
-  }
-}
-__host__ __device__ inline ColMap plain_map(int cols4, int tch = 8) { return ColMap{0, 0, cols4, tch}; }
-inline ColMap paired_map(int cols4, int half4) {
-  return ColMap{half4, (half4 + 3) / 4, cols4, 8};
-}
-__host__ __device__ inline int map_tiles(const ColMap &m) {
-  return m.half4 == 0 ? (m.cols4 + m.tch - 1) / m.tch : m.t1 + (m.cols4 - 2 * m.half4 + 7) / 8;
-}
-
 // a[s] for a run-time s without indexing the kernel-argument array (selects).
 template <typename T, int M>
 __device__ __forceinline__ T pick(const T (&a)[M], int s) {
@@ -311,8 +228,5 @@ __device__ __forceinline__ int block_of(int64_t r, int n, const int64_t *start) 
   for (int j = 1; j < kMaxBlocks; ++j) s += (j < n && r >= start[j]) ? 1 : 0;
   return s;
 }
-
-__host__ __device__ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
-__host__ __device__ inline int round_up4(int v) { return (v + 3) & ~3; }
 
 }  // namespace sft

@@ -55,16 +55,15 @@ constexpr int kBiasMaxParts = SFT_BIAS_PARTS;
 // skipped by the per-feature lane groups.  Whether segment [s0, s1) of the
 // sorted slots is long depends on its bounds alone, so both sides agree: it
 // is long when it contains two consecutive multiples of kLongSeg ("samples")
-// of the sorted slot index.  Every segment of more than 2 kLongSeg slots is
-// long, none of fewer than kLongSeg + 2.  seg_offsets_kernel lists them (per
+// of the sorted slot index.  Every segment of 2 kLongSeg slots or more is
+// long, none of kLongSeg slots or fewer.  seg_offsets_kernel lists them (per
 // position chunk) as it finds them at their first sample m:
 // keys[m + kLongSeg] == keys[m] != keys[m - kLongSeg].
 #ifndef SFT_BWD_LONG_SEG
 #define SFT_BWD_LONG_SEG 128
 #endif
 constexpr int kLongSeg = SFT_BWD_LONG_SEG;
-__host__ __device__ inline int64_t long_first_sample(int64_t s0) { return (s0 + kLongSeg - 1) / kLongSeg * kLongSeg; }
-__host__ __device__ inline bool long_segment(int64_t s0, int64_t s1) { return long_first_sample(s0) + kLongSeg < s1; }
+__host__ __device__ inline bool long_segment(int64_t s0, int64_t s1) { return sft::long_segment(s0, s1, kLongSeg); }
 
 // Segment starts and the lists of long segments of one sort: seg[0 .. nc N]
 // (nc position chunks of nfeat features), then per chunk c a list of its long
@@ -107,8 +106,7 @@ __global__ __launch_bounds__(kBlock) void seg_offsets_kernel(const unsigned *__r
     const int64_t prev = i > 0 ? (int64_t)keys[i - 1] : -1;
     const int64_t hi = cur < N ? cur : N;
     for (int64_t f = prev + 1; f <= hi; ++f) seg_start[f] = (int32_t)i;
-    if (i % kLongSeg == 0 && i + kLongSeg < M && (int64_t)keys[i + kLongSeg] == cur &&
-        (i < kLongSeg || (int64_t)keys[i - kLongSeg] != cur)) {
+    if (long_listed_at(keys, M, i, kLongSeg)) {
       const int64_t c = cur / nfeat;
       const int at = atomicAdd(long_count + c, 1);
       long_list[c * nfeat + at] = (int32_t)(cur - c * nfeat);

@@ -32,25 +32,7 @@ constexpr int64_t kBigSort = 4 << 20;
 constexpr int kSortTile = kBlock * kSortItems;  // the smaller tile: sizes the count buffer
 constexpr int kMaxRadix = 512;
 
-// n / d for 32-bit n by a divisor fixed at launch: multiply-high by a magic
-// number (Granlund & Montgomery 1994, round-up variant): with l = ceil(log2 d)
-// and m = floor(2^32 (2^l - d) / d) + 1, n / d = (t + ((n - t) >> 1)) >> (l - 1)
-// where t = mulhi(m, n), for d >= 2.
-struct FastDiv {
-  uint32_t d, mul, shift;
-  FastDiv() = default;
-  __host__ explicit FastDiv(uint32_t div) : d(div), mul(0), shift(0) {
-    uint32_t l = 0;
-    while (((uint64_t)1 << l) < div) ++l;
-    shift = l;
-    mul = (uint32_t)((((uint64_t)1 << 32) * (((uint64_t)1 << l) - div)) / div + 1);
-  }
-  __device__ __forceinline__ uint32_t operator()(uint32_t n) const {
-    if (d == 1) return n;
-    const uint32_t t = __umulhi(mul, n);
-    return (t + ((n - t) >> 1)) >> (shift - 1);
-  }
-};
+// FastDiv (index_math.h): n / d by a divisor fixed at launch.
 
 // Key of slot s (s < 2^31): chunk(b) * N + feature for an active slot, the
 // sentinel (>= every real key) for an inactive one; the value is b = s / K.
