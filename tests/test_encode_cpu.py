@@ -128,3 +128,38 @@ def test_threat_rows_are_unique_and_in_range():
             assert len(set(row.tolist())) == len(row)
             assert ((row >= 0) & (row < 85296)).all()
             assert (out[key][b, out[cnt][b]:] == -1).all()
+
+
+def _rows_and_pushes(boards, stm):
+    from threat_order import threat_row
+
+    out = fo.encode(boards, stm, ["Full_Threats"])
+    rows = []
+    for b in range(boards.shape[0]):
+        for persp, key, cnt in ((0, "white", "count_w"), (1, "black", "count_b")):
+            n = min(int(out[cnt][b]), 128)
+            rows.append((b, persp, out[key][b, :n].tolist(), threat_row(boards[b], persp)))
+    return rows
+
+
+def test_threat_row_order_follows_the_reference_loops():
+    """The oracle's (and so the GPU encoder's) Full_Threats rows list the
+    threats in the order of the reference's loops, restated independently in
+    tests/threat_order.py; two planted ordering mistakes must change rows."""
+    from threat_order import threat_row
+
+    boards, stm = positions.random_positions(400, seed=5)
+    fens = ["4k3/8/3p4/3P4/8/8/8/4K3 w - - 0 1",          # white pawn pushes onto a black pawn
+            "4k3/8/8/2pp4/2PP4/8/8/4K3 b - - 0 1",
+            "4k3/3p4/3p4/8/8/3P4/3P4/4K3 w - - 0 1",      # pawns blocked by their own pawns
+            positions.STARTPOS]
+    fb = [positions.board_from_fen(f) for f in fens]
+    boards = np.concatenate([boards, np.stack([b for b, _ in fb])])
+    stm = np.concatenate([stm, np.array([s for _, s in fb], np.uint8)])
+    rows = _rows_and_pushes(boards, stm)
+    for b, persp, got, want in rows:
+        assert got == want, (b, persp)
+    # the restatement is order-sensitive: both planted mistakes disagree somewhere
+    swapped = sum(threat_row(boards[b], p, swap_colors=True) != got for b, p, got, _ in rows)
+    pushes_first = sum(threat_row(boards[b], p, push_first=True) != got for b, p, got, _ in rows)
+    assert swapped > 100 and pushes_first > 0, (swapped, pushes_first)

@@ -51,3 +51,20 @@ def test_encode_random(name, B, seed):
     announce(f"encode random {name} B={B}")
     boards, stm = positions.random_positions(B, seed=seed)
     _check(boards, stm, name)
+
+
+def test_encode_threat_order_matches_the_reference_loops():
+    """The GPU encoder's Full_Threats rows against the loop-order restatement
+    (tests/threat_order.py), independently of the oracle's own walk."""
+    from threat_order import threat_row
+
+    announce("encode threat order")
+    boards, stm = positions.random_positions(300, seed=6)
+    got = encode_batch(torch.from_numpy(boards).to(DEV), torch.from_numpy(stm).to(DEV), "Full_Threats",
+                       with_counts=True)
+    torch.cuda.synchronize()
+    for key, cnt, persp in (("white", "white_count", 0), ("black", "black_count", 1)):
+        rows, counts = host(got[key]), host(got[cnt])
+        for b in range(boards.shape[0]):
+            n = min(int(counts[b]), 128)
+            assert rows[b, :n].tolist() == threat_row(boards[b], persp), (key, b)
