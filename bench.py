@@ -28,6 +28,7 @@ moving) its HBM fraction.
   python bench.py --optimizer                 (fused Ranger22 update of the FT parameters)
   python bench.py --encode halfka|threats     (GPU feature-index encoder)
   python bench.py --export                    (GPU LEB128 of the .nnue FT weights)
+  python bench.py --pipeline                  (host data pipeline + copy + GPU feature encode)
 """
 
 from __future__ import annotations
@@ -766,6 +767,70 @@ def bench_export(args, dev) -> int:
     return 0
 
 
+def bench_pipeline(args, dev) -> int:
+    """Host data pipeline -> GPU: entries read from a file of 1 048 576 decoded
+    training entries (16 copies of 65 536 random positions), skip filter off,
+    per-reader shuffle buffers of 16 384, batches of 65 536 in pinned slabs,
+    copied to the GPU and encoded there (Full_Threats+HalfKAv2_hm).  Reports the
+    host stream alone and the stream with the copy and the GPU encode."""
+    import tempfile
+
+    import numpy as np
+    import torch
+
+    from sft_amd import pipeline as pl
+    from sft_amd import positions
+
+    B, copies = 65536, 16
+    boards, stm = positions.random_positions(B, seed=13)
+    e = pl.make_entries(boards, stm, score=np.arange(B) % 2000 - 1000, result=np.arange(B) % 3 - 1, ply=60)
+    tmp = tempfile.mkdtemp(prefix="sft_pipe_", dir="/tmp")
+    path = os.path.join(tmp, "entries.sftpos")
+    pl.write_entries(path, np.concatenate([e] * copies), entries_per_chunk=16384)
+    n = B * copies
+    try:
+        threads = max(1, min(len(os.sched_getaffinity(0)), int(os.environ.get("OMP_NUM_THREADS", "64"))) - 2)
+    except OSError:
+        threads = 4
+
+    def run(to_gpu: bool):
+        stream = pl.BatchStream([path], B, reader_threads=threads, shuffle_buffer_entries=16384, seed=1,
+                                pin_memory=to_gpu, slab_count=4)
+        t0 = time.perf_counter()
+        got = 0
+        for batch in stream:
+            if to_gpu:
+                batch.to_device(dev, "Full_Threats+HalfKAv2_hm")
+            got += batch.size
+            batch.release()
+        if to_gpu:
+            torch.cuda.synchronize()
+        el = time.perf_counter() - t0
+        stream.close()
+        assert got == n
+        return n / el
+
+    host_rate = run(False)
+    run(True)  # warm-up of the encode path
+    gpu_rate = run(True)
+    import shutil
+
+    shutil.rmtree(tmp, ignore_errors=True)
+    log(f"[bench] pipeline: host stream {host_rate / 1e6:.2f} M entries/s, with GPU encode {gpu_rate / 1e6:.2f} M/s "
+        f"({threads} reader threads)")
+    result = {
+        "metric": "training entries/sec through the host pipeline + GPU feature encode (Full_Threats+HalfKAv2_hm)",
+        "value": gpu_rate, "unit": "entries/s", "n_gpus": 1, "steps": 1, "warmup": 1, "ms_per_step": B / gpu_rate * 1e3,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int32", "data": "synthetic",
+        "config": {"workload": "pipeline_threats_b65536", "entries": n, "batch": B, "reader_threads": threads,
+                   "shuffle_buffer_entries": 16384, "skip_filter": "off", "parallelism": "single-gpu"},
+        "host_stream_entries_per_s": host_rate,
+        "cpu_baseline": None,
+    }
+    print(json.dumps(result), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -788,6 +853,8 @@ def main() -> int:
     ap.add_argument("--encode", choices=["halfka", "threats"], default=None,
                     help="time the GPU feature-index encoder instead")
     ap.add_argument("--export", action="store_true", help="time the GPU LEB128 encoder of the .nnue export instead")
+    ap.add_argument("--pipeline", action="store_true",
+                    help="time the host data pipeline with the copy to the GPU and the GPU encode instead")
     ap.add_argument("--configs", action=argparse.BooleanOptionalAction, default=True,
                     help="also time every workload (0-4) and list them under 'configs' (default on)")
     ap.add_argument("--traffic", choices=["live", "profile", "off"], default="live",
@@ -808,7 +875,7 @@ def main() -> int:
     from sft_amd import _native, workloads
 
     w = workloads.WORKLOADS[args.workload]
-    special = args.composed or args.transform or args.optimizer or args.encode or args.export
+    special = args.composed or args.transform or args.optimizer or args.encode or args.export or args.pipeline
     # The counter passes run in child processes before this one touches the GPU.
     traffic = None
     if not special and args.zipf is None and args.traffic == "live":
@@ -827,6 +894,8 @@ def main() -> int:
         return bench_encode(args, dev)
     if args.export:
         return bench_export(args, dev)
+    if args.pipeline:
+        return bench_pipeline(args, dev)
     if w.quantized:
         return bench_q16(args, w, dev)
 
