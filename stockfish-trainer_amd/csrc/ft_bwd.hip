@@ -18,8 +18,11 @@
 // Bias grad (FT/kernel.py:269): per-block column partial sums, then a fixed-
 // order reduction of the partials; deterministic.
 #include <algorithm>
+#include <mutex>
 #include <optional>
 #include <type_traits>
+#include <utility>
+#include <vector>
 
 #include "common.h"
 
@@ -184,6 +187,7 @@ __device__ __forceinline__ void long_store(const LongEnds &e, int dst_mode, floa
 // next batch's loads in flight meanwhile) and lanes 0-31 of wave 0 add them in
 // order: acc = start value, acc += row for the positions ascending -- the
 // gather's own sequence, so a feature's result does not depend on the path.
+// Threads kBlock and above of a larger workgroup take part in the barriers only.
 constexpr int kWgLongRows = 128;  // 128 x 128 B = 16 KB of LDS
 __device__ __forceinline__ void long_segment_sum_wg(const int32_t *__restrict__ sorted_pos, int64_t f, int s0, int n,
                                                     int cb, const LongRows &rows, const ColMap &map,
@@ -191,6 +195,7 @@ __device__ __forceinline__ void long_segment_sum_wg(const int32_t *__restrict__ 
                                                     int dst_mode, f32x4 *buf) {
   constexpr int kRowsPerPass = kBlock / 8;
   constexpr int kPass = kWgLongRows / kRowsPerPass;
+  const bool stager = threadIdx.x < kBlock;
   const LongEnds ends = long_ends(f, cb, (int)threadIdx.x, map, dst, tmp);
   float acc = long_start(ends, src_mode);
   const int q = threadIdx.x & 7, r0 = threadIdx.x >> 3;  // staging: chunk q of rows r0 + 32 u
@@ -203,7 +208,7 @@ __device__ __forceinline__ void long_segment_sum_wg(const int32_t *__restrict__ 
 #pragma unroll
     for (int u = 0; u < kPass; ++u) {
       const int r = b * kWgLongRows + r0 + kRowsPerPass * u;
-      p[u] = r < n ? sorted_pos[s0 + r] : -1;
+      p[u] = (stager && r < n) ? sorted_pos[s0 + r] : -1;
     }
   };
   auto load_rows = [&]() {
@@ -212,6 +217,7 @@ __device__ __forceinline__ void long_segment_sum_wg(const int32_t *__restrict__ 
       v[u] = (p[u] >= 0 && qok) ? src[(int64_t)p[u] * rows.pos_stride] : f32x4{0.f, 0.f, 0.f, 0.f};
   };
   auto stage = [&]() {
+    if (!stager) return;
 #pragma unroll
     for (int u = 0; u < kPass; ++u) buf[(r0 + kRowsPerPass * u) * 8 + q] = v[u];
   };
@@ -383,19 +389,11 @@ __device__ __forceinline__ f32x4 load_row(const f32x4 *p) {
   if constexpr (NT) return __builtin_nontemporal_load(p);
   else return *p;
 }
-constexpr int kBwdTileCh = 8;  // float4 chunks per 32-column tile row
-// Grad tile width of the plain (single-perspective) tiled backward, in 16-byte chunks.
-#ifndef SFT_BWD_TCH
-#define SFT_BWD_TCH 8
-#endif
-template <int TCH>
-constexpr int bwd_feat_per_block() {
-  return kWavesPerBlock * (kWave / TCH);
-}
+constexpr int kBwdTileCh = 8;  // float4 chunks per 32-column tile row (grad tiles and weight-grad blocks)
+// Features per workgroup of the tiled gather: one per 8-lane group.
+constexpr int bwd_feat_per_block() { return kWavesPerBlock * (kWave / kBwdTileCh); }
 // Long segments are summed in 32-column blocks by the tiled gather's
 // long-segment slots.
-template <int TCH>
-constexpr bool kLongPath = TCH == 8;
 #ifndef SFT_BWD_LONG_SLOTS
 #define SFT_BWD_LONG_SLOTS 256
 #endif
@@ -405,9 +403,6 @@ constexpr int kLongSlots = SFT_BWD_LONG_SLOTS;  // long-segment workgroups per t
 #endif
 constexpr int kRowLongBlocks = SFT_BWD_ROW_LONG_BLOCKS;  // long-segment workgroups of the row gather
 
-#ifndef SFT_BWD_BALANCE
-#define SFT_BWD_BALANCE 1
-#endif
 #ifndef SFT_BWD_POS_LDS
 #define SFT_BWD_POS_LDS 4096
 #endif
@@ -416,9 +411,12 @@ constexpr int kBwdPosLds = SFT_BWD_POS_LDS;  // staged positions per workgroup
 // Sums one lane group's positions from `list` (LDS or global) into acc.  A
 // lane group has TCH lanes (one 16-byte chunk of the tile row each) and keeps
 // TCH row loads in flight.  Rows are 32-bit byte offsets from the grad tile's
-// wave-uniform base (a tile is B x 16 TCH bytes, B < 2^31 / K).
+// wave-uniform base (a tile is B x 16 TCH bytes, B < 2^31 / K).  Every lane
+// loads, padding lanes of the last tile included (a tile holds all TCH chunks
+// of each row; the caller does not store a padding lane's sum), so the loads
+// carry no execution masks.
 template <bool FROM_LDS, int TCH>
-__device__ __forceinline__ void bwd_tile_sum(const int32_t *list, int n, int nmin, int nmax, int t, bool colok,
+__device__ __forceinline__ void bwd_tile_sum(const int32_t *list, int n, int nmin, int nmax, int t,
                                              const char *__restrict__ gtile, f32x4 &acc) {
   const uint32_t lane_off = (uint32_t)t * (uint32_t)sizeof(f32x4);
   auto row = [&](int b) {
@@ -438,7 +436,7 @@ __device__ __forceinline__ void bwd_tile_sum(const int32_t *list, int n, int nmi
     }
     f32x4 w[U];
 #pragma unroll
-    for (int u = 0; u < U; ++u) w[u] = colok ? row(b[u]) : f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int u = 0; u < U; ++u) w[u] = row(b[u]);
 #pragma unroll
     for (int u = 0; u < U; ++u) acc += w[u];
   }
@@ -456,7 +454,7 @@ __device__ __forceinline__ void bwd_tile_sum(const int32_t *list, int n, int nmi
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       w[u] = f32x4{0.f, 0.f, 0.f, 0.f};
-      if (k + u < n && colok) w[u] = row(b[u]);
+      if (k + u < n) w[u] = row(b[u]);
     }
 #pragma unroll
     for (int u = 0; u < U; ++u)
@@ -465,16 +463,46 @@ __device__ __forceinline__ void bwd_tile_sum(const int32_t *list, int n, int nmi
 }
 
 // The 32 features of a workgroup are consecutive, so their position lists
-// form one contiguous range of the sorted array; it is copied to LDS with
-// coalesced loads and read from there, which keeps the position reads off the
-// in-order vector-memory counter the row loads wait on.  Ranges longer than
-// kBwdPosLds entries read their positions from global memory instead.
+// form one contiguous range of the sorted array; it is copied to LDS and read
+// from there, which keeps the position reads off the in-order vector-memory
+// counter the row loads wait on.  Ranges longer than kBwdPosLds entries read
+// their positions from global memory instead.
+//
+// In front of the gather a workgroup makes two rounds of global loads, each
+// issued whole before anything waits on it: (1) the segment bounds; (2) the
+// positions (8 loads per thread in flight) together with the rows the sums
+// start from and, for kDstOutPlus, the rows they add onto -- thread i loads
+// chunk i % 8 of feature i / 8 into LDS.  Meanwhile wave 0 ranks the 32
+// features by segment length with cross-lane reads.  One barrier, then each
+// lane group sums one feature.  (Staging one position per thread per round
+// trip, reading the segment bounds again after the ranking barrier and loading
+// the start row after it made a chain of about ten dependent round trips that
+// took half of a launch at B = 65536.)
 //
 // Each tile's items start with nlong long-segment slots: slot j sums the
 // chunk's listed long segments j, j + nlong, ... for this tile with the
 // whole workgroup (long_segment_sum_wg), while the tile is in the XCD's L2;
 // the feature blocks follow.
-template <int TCH, bool NT>
+//
+// Dynamic LDS: positions (kBwdPosLds ints) | start rows | plus rows (256
+// chunks each, present when used); at least the long-segment row buffer.
+constexpr int kBwdFeat = bwd_feat_per_block();  // 32
+struct GatherLds {
+  int start, plus, bytes;  // byte offsets (-1: absent) and size
+};
+__host__ __device__ inline GatherLds gather_lds(int src_mode, int dst_mode) {
+  GatherLds l;
+  int off = kBwdPosLds * 4;
+  l.start = src_mode != kSrcZero ? off : -1;
+  off += src_mode != kSrcZero ? kBlock * 16 : 0;
+  l.plus = dst_mode == kDstOutPlus ? off : -1;
+  off += dst_mode == kDstOutPlus ? kBlock * 16 : 0;
+  const int long_buf = kWgLongRows * 8 * (int)sizeof(f32x4);
+  l.bytes = off > long_buf ? off : long_buf;
+  return l;
+}
+
+template <bool NT>
 __global__ __launch_bounds__(kBlock) void bwd_tiled_gather_kernel(const int32_t *__restrict__ seg,
                                                                   const int32_t *__restrict__ sorted_pos, int64_t N,
                                                                   const f32x4 *__restrict__ gt, int64_t B,
@@ -482,97 +510,144 @@ __global__ __launch_bounds__(kBlock) void bwd_tiled_gather_kernel(const int32_t 
                                                                   int src_mode, int dst_mode, int ntiles, int ngroups,
                                                                   const int32_t *__restrict__ long_list,
                                                                   const int *__restrict__ long_count, int nlong) {
-  __shared__ __align__(16) int spos[kBwdPosLds];
-  constexpr int FPB = bwd_feat_per_block<TCH>();
-  __shared__ int s_len[FPB], s_perm[FPB];
+  constexpr int TCH = kBwdTileCh;
+  extern __shared__ __align__(16) char gsm[];
+  __shared__ int s_seg[kBwdFeat + 1], s_perm[kBwdFeat];
   const TileItem it = tile_sched_item(blockIdx.x, ntiles, ngroups + nlong);
   if (it.tile >= ntiles) return;  // whole block: uniform
   if (it.chunk < nlong) {         // whole block: uniform
-    static_assert(kWgLongRows * 8 * sizeof(f32x4) <= sizeof(spos), "long-segment batch must fit the LDS list");
     const int cnt = *long_count;
     for (int e = it.chunk; e < cnt; e += nlong) {
       const int64_t f = long_list[e];
       const int s0 = seg[f];
       long_segment_sum_wg(sorted_pos, f, s0, seg[f + 1] - s0, it.tile, LongRows{gt, B * TCH, TCH}, map, dst, tmp,
-                          src_mode, dst_mode, reinterpret_cast<f32x4 *>(spos));
+                          src_mode, dst_mode, reinterpret_cast<f32x4 *>(gsm));
     }
     return;
   }
-  const int64_t fb = (int64_t)(it.chunk - nlong) * FPB;
-  const int64_t fe = fb + FPB < N ? fb + FPB : N;
-  const int r0 = seg[fb], r1 = seg[fe];
-  const bool staged = (r1 - r0) <= kBwdPosLds;  // block-uniform
-#if SFT_BWD_BALANCE
-  if (threadIdx.x < FPB) {
-    const int64_t fi = fb + threadIdx.x;
-    const int a = fi < N ? seg[fi] : 0, e = fi < N ? seg[fi + 1] : 0;
-    s_len[threadIdx.x] = (kLongPath<TCH> && long_segment(a, e)) ? 0 : e - a;
-  }
-#endif
-  if (staged)
-    for (int i = threadIdx.x; i < r1 - r0; i += kBlock) spos[i] = sorted_pos[r0 + i];
-  __syncthreads();
-#if SFT_BWD_BALANCE
-  // A wave runs as long as its longest segment: rank the block's features by
-  // segment length (ties by index) and give each wave 8 consecutive ranks.
-  if (threadIdx.x < FPB) {
-    const int me = s_len[threadIdx.x];
-    int rank = 0;
-    for (int j = 0; j < FPB; ++j) {
-      const int o = s_len[j];
-      rank += (o > me || (o == me && j < (int)threadIdx.x)) ? 1 : 0;
-    }
-    s_perm[rank] = threadIdx.x;
-  }
-  __syncthreads();
-#endif
-  const int wave = uniform(threadIdx.x / kWave);
-  const int lane = threadIdx.x % kWave;
-  const int g = lane / TCH, t = lane % TCH;
-  const int colm = tile_col(map, it.tile, t);
-  const bool colok = colm >= 0;
-  const int64_t col4 = colm;
-  const int64_t cols4 = map.cols4;
-#if SFT_BWD_BALANCE
-  const int64_t f = fb + s_perm[wave * (kWave / TCH) + g];
-#else
-  const int64_t f = fb + wave * (kWave / TCH) + g;
-#endif
-  int s0 = 0, s1 = 0;
-  if (f < N) {
-    s0 = seg[f];
-    s1 = seg[f + 1];
-  }
-  const bool is_long = kLongPath<TCH> && f < N && long_segment(s0, s1);  // summed by the long-segment slots
-  const int n = is_long ? 0 : s1 - s0;
-  const bool wave_has_work = ballot(n > 0) != 0;  // wave-uniform
+  const GatherLds lay = gather_lds(src_mode, dst_mode);
+  int *spos = reinterpret_cast<int *>(gsm);
   const bool skip_untouched = src_mode == kSrcDst && dst_mode == kDstOut;
+  const int64_t cols4 = map.cols4;
+  const int tid = threadIdx.x;
+  const int wave = uniform(tid / kWave);
+  const int lane = tid % kWave;
+  const int64_t fb = (int64_t)(it.chunk - nlong) * kBwdFeat;
+  const int nf = (int)(N - fb < kBwdFeat ? N - fb : kBwdFeat);  // features of this block, >= 1
+
+  // round 1: segment bounds -- the range (uniform), this thread's feature for
+  // the start rows, and one feature per lane of wave 0 for the ranking
+  const int r0 = seg[fb], r1 = seg[fb + nf];
+  const int64_t fs = fb + tid / TCH;  // start-row feature of this thread
+  const int cs = tid % TCH;
+  int as = 0, es = 0;
+  if (fs < N) {
+    as = seg[fs];
+    es = seg[fs + 1];
+  }
+  int la = 0;
+  if (wave == 0) la = seg[fb + (lane < nf ? lane : nf)];
+
+  // round 2: positions, start rows, plus rows.  The range is copied in
+  // 16-byte pieces from r0 rounded down to a multiple of 4 (sorted_pos is
+  // 16-byte aligned and its buffer is padded to 256 bytes), so spos[j] holds
+  // sorted_pos[ra + j].
+  const int ra = r0 & ~3;
+  const int cnt4 = (r1 - ra + 3) >> 2;               // 16-byte pieces
+  const bool staged = cnt4 * 4 <= kBwdPosLds;         // block-uniform
+  if (staged) {
+    constexpr int U = 4;
+    const i32x4 *src = reinterpret_cast<const i32x4 *>(sorted_pos + ra);
+    i32x4 *dst4 = reinterpret_cast<i32x4 *>(spos);
+    for (int b0 = 0; b0 < cnt4; b0 += U * kBlock) {
+      i32x4 v[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int i = b0 + u * kBlock + tid;
+        v[u] = i < cnt4 ? SFT_STREAM_LOAD(src + i) : i32x4{0, 0, 0, 0};
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int i = b0 + u * kBlock + tid;
+        if (i < cnt4) dst4[i] = v[u];
+      }
+    }
+  }
+  if (lay.start >= 0 || lay.plus >= 0) {
+    const int colm = tile_col(map, it.tile, cs);
+    const bool own = fs < N && colm >= 0 && !long_segment(as, es);
+    f32x4 vs = f32x4{0.f, 0.f, 0.f, 0.f}, vp = vs;
+    if (own) {
+      const int blk = block_of(fs, dst.n, dst.start);
+      const f32x4 *d = pick(dst.p, blk) + (fs - pick(dst.start, blk)) * cols4 + colm;
+      if (src_mode == kSrcTmp) vs = tmp[fs * cols4 + colm];
+      else if (src_mode == kSrcDst && (es > as || !skip_untouched)) vs = *d;
+      if (lay.plus >= 0) vp = load_row<NT>(d);
+    }
+    if (lay.start >= 0) reinterpret_cast<f32x4 *>(gsm + lay.start)[tid] = vs;
+    if (lay.plus >= 0) reinterpret_cast<f32x4 *>(gsm + lay.plus)[tid] = vp;
+  }
+  if (wave == 0) {
+    // A wave runs as long as its longest segment: rank the features by segment
+    // length (ties by index, long segments as 0) and give each wave 8
+    // consecutive ranks.
+    const int le = __shfl_down(la, 1);
+    const bool live = lane < nf;
+    const int len = (live && !long_segment(la, le)) ? le - la : 0;
+    int rank = 0;
+    for (int j = 0; j < kBwdFeat; ++j) {
+      const int o = __builtin_amdgcn_readlane(len, j);
+      rank += (o > len || (o == len && j < lane)) ? 1 : 0;
+    }
+    if (lane < kBwdFeat) s_perm[rank] = lane;
+    if (lane <= kBwdFeat) s_seg[lane] = la;
+  }
+  __syncthreads();
+
+  const int g = lane / TCH, t = lane % TCH;
+  const int p = s_perm[wave * (kWave / TCH) + g];
+  const int64_t f = fb + p;
+  const int s0 = s_seg[p], s1 = s_seg[p + 1];
+  const bool live = p < nf;
+  const bool is_long = live && long_segment(s0, s1);  // summed by the long-segment slots
+  const int n = (live && !is_long) ? s1 - s0 : 0;
+  const bool wave_has_work = ballot(n > 0) != 0;  // wave-uniform
   if (skip_untouched && !wave_has_work) return;  // nothing to change anywhere in the wave
   int nmin, nmax;
   group_minmax<TCH>(n, nmin, nmax);
+  const int colm = tile_col(map, it.tile, t);
+  const bool colok = colm >= 0;
   const char *gtile = reinterpret_cast<const char *>(gt + (int64_t)it.tile * B * TCH);
-  const int blk = block_of(f, dst.n, dst.start);
-  f32x4 *d = pick(dst.p, blk) + (f - pick(dst.start, blk)) * cols4 + col4;
-  f32x4 *tp = tmp + f * cols4 + col4;
-  const bool mine = f < N && colok && !is_long;
   f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
-  if (mine) {
-    if (src_mode == kSrcDst && (n > 0 || !skip_untouched)) acc = *d;
-    else if (src_mode == kSrcTmp) acc = *tp;
-  }
+  if (lay.start >= 0) acc = reinterpret_cast<const f32x4 *>(gsm + lay.start)[p * TCH + t];
   if (staged)
-    bwd_tile_sum<true, TCH>(spos + (s0 - r0), n, nmin, nmax, t, colok, gtile, acc);
+    bwd_tile_sum<true, TCH>(spos + (s0 - ra), n, nmin, nmax, t, gtile, acc);
   else
-    bwd_tile_sum<false, TCH>(sorted_pos + s0, n, nmin, nmax, t, colok, gtile, acc);
-  if (!mine) return;
+    bwd_tile_sum<false, TCH>(sorted_pos + s0, n, nmin, nmax, t, gtile, acc);
+  if (!live || !colok || is_long) return;
+  const int blk = block_of(f, dst.n, dst.start);
+  f32x4 *d = pick(dst.p, blk) + (f - pick(dst.start, blk)) * cols4 + colm;
   if (dst_mode == kDstTmp) {
-    store_row<NT>(tp, acc);
+    store_row<NT>(tmp + f * cols4 + colm, acc);
   } else if (dst_mode == kDstOutPlus) {
-    const f32x4 prev = load_row<NT>(d);
-    store_row<NT>(d, prev + acc);
+    store_row<NT>(d, reinterpret_cast<const f32x4 *>(gsm + lay.plus)[p * TCH + t] + acc);
   } else if (!skip_untouched || n > 0) {
     store_row<NT>(d, acc);
   }
+}
+
+// One position chunk's tiled weight-grad gather: one workgroup per item.
+int launch_tiled_gather(bool nt, const int32_t *seg, const int32_t *pos, int64_t N, const f32x4 *gt, int64_t B,
+                        const ColMap &map, const RowDst &dst, f32x4 *tmp, int src_mode, int dst_mode, int ntiles,
+                        int ngroups, const int32_t *long_list, const int *long_count, int nlong, hipStream_t s) {
+  const int64_t items = tile_sched_items_per_xcd(ntiles, ngroups + nlong);
+  const size_t lds = (size_t)gather_lds(src_mode, dst_mode).bytes;
+  if ((uintptr_t)pos % 16 != 0)  // the sort's position buffers are 256-byte aligned workspace regions
+    return fail(SFT_EINVAL, "tiled feature gather: sorted positions not 16-byte aligned");
+  hipLaunchKernelGGL((nt ? bwd_tiled_gather_kernel<true> : bwd_tiled_gather_kernel<false>),
+                     dim3((unsigned)(items * kXcds)), dim3(kBlock), lds, s, seg, pos, N, gt, B, map, dst, tmp,
+                     src_mode, dst_mode, ntiles, ngroups, long_list, long_count, nlong);
+  return check_launch("tiled feature gather");
 }
 
 // dV[j, :] = sum over i < reps of dWb[i * period + j, :], i ascending (the
@@ -882,7 +957,7 @@ int bias_parts(int64_t B) {
 
 bool tiled_shape(int64_t B, int L, uint32_t flags) {
   return !(flags & (SFT_BWD_ATOMIC | SFT_BWD_ROWS)) && (flags & SFT_BWD_OVERWRITE) && L % 4 == 0 &&
-         ceil_div(L, 32) >= kMinTiles && B * 16 * SFT_BWD_TCH <= (int64_t)UINT32_MAX;  // 32-bit grad row offsets
+         ceil_div(L, 32) >= kMinTiles && B * 16 * kBwdTileCh <= (int64_t)UINT32_MAX;  // 32-bit grad row offsets
 }
 
 // Position chunks of the tiled gather (one launch each).
@@ -899,7 +974,7 @@ constexpr int kBwdHalves = SFT_BWD_CHUNKS;
 #endif
 int sort_chunks(int64_t B, int L, uint32_t flags) {
   if (!tiled_shape(B, L, flags) || B < kBwdHalves) return 1;
-  return B * 16 * SFT_BWD_TCH <= (int64_t)(SFT_BWD_ONE_CHUNK_BYTES) ? 1 : kBwdHalves;
+  return B * 16 * kBwdTileCh <= (int64_t)(SFT_BWD_ONE_CHUNK_BYTES) ? 1 : kBwdHalves;
 }
 int64_t half_rows(int64_t B) { return ceil_div(B, kBwdHalves); }
 
@@ -921,8 +996,8 @@ int make_layout(int64_t B, int K, int64_t N, int L, uint32_t flags, BwdLayout &l
     off = align256(off + seg_region_bytes(nc, N));
     lay.gt = off;
     if (tiled_shape(B, L, flags)) {  // the grad tiles the bias pass writes, whatever the chunk count
-      const int64_t ntiles = ceil_div(L / 4, SFT_BWD_TCH);
-      off = align256(off + (size_t)(ntiles * B * SFT_BWD_TCH) * 16);
+      const int64_t ntiles = ceil_div(L / 4, kBwdTileCh);
+      off = align256(off + (size_t)(ntiles * B * kBwdTileCh) * 16);
     }
   }
   lay.total = off;
@@ -1038,7 +1113,7 @@ int bwd_f32(const int32_t *idx, int64_t B, int K, const float *grad, int64_t N, 
   {
     const bool vec = (L % 4 == 0) && ((uintptr_t)grad % 16 == 0) && ((uintptr_t)db % 16 == 0);
     if ((rc = launch_bias_partial(grad, B, L, lay.nparts, reinterpret_cast<float *>(w + lay.partial), gt, vec, s,
-                                  SFT_BWD_TCH)) != SFT_OK)
+                                  kBwdTileCh)) != SFT_OK)
       return rc;
     if ((rc = launch_bias_final(reinterpret_cast<const float *>(w + lay.partial), lay.nparts, L, db, overwrite, vec,
                                 s)) != SFT_OK)
@@ -1089,25 +1164,20 @@ int bwd_f32(const int32_t *idx, int64_t B, int K, const float *grad, int64_t N, 
     return check_launch("weight grad zero fill");
   }
   if (tiled) {
-    constexpr int TCH = SFT_BWD_TCH;
     const int64_t cols4 = L / 4;
-    const ColMap map = plain_map((int)cols4, TCH);
+    const ColMap map = plain_map((int)cols4, kBwdTileCh);
     const int ntiles = map_tiles(map);
-    const int ngroups = (int)ceil_div(N, bwd_feat_per_block<TCH>());
-    const int nlong = kLongPath<TCH> ? kLongSlots : 0;
-    const int64_t blocks = tile_sched_items_per_xcd(ntiles, ngroups + nlong) * kXcds;
+    const int ngroups = (int)ceil_div(N, bwd_feat_per_block());
     RowDst dst{};
     dst.n = 1;
     dst.start[1] = N;
     dst.p[0] = reinterpret_cast<f32x4 *>(dW);
     for (int h = 0; h < nc; ++h) {
       ProfScope prof(kProfBwdTiled, s);
-      const bool nt = (nc > 1 ? half_rows(B) : B) * TCH * 16 >= kNtStoreTileBytes;
-      hipLaunchKernelGGL((nt ? bwd_tiled_gather_kernel<TCH, true> : bwd_tiled_gather_kernel<TCH, false>),
-                         dim3((unsigned)blocks), dim3(kBlock), 0, s, seg + (int64_t)h * N, pos, N, gt, B, map, dst,
-                         (f32x4 *)nullptr, h == 0 ? kSrcZero : kSrcDst, kDstOut, ntiles, ngroups, sb.list + h * N,
-                         sb.count + h, nlong);
-      if ((rc = check_launch("tiled feature gather")) != SFT_OK) return rc;
+      const bool nt = (nc > 1 ? half_rows(B) : B) * kBwdTileCh * 16 >= kNtStoreTileBytes;
+      rc = launch_tiled_gather(nt, seg + (int64_t)h * N, pos, N, gt, B, map, dst, nullptr, h == 0 ? kSrcZero : kSrcDst,
+                               kDstOut, ntiles, ngroups, sb.list + h * N, sb.count + h, kLongSlots, s);
+      if (rc != SFT_OK) return rc;
     }
     return SFT_OK;
   }
@@ -1191,9 +1261,7 @@ static int pair_sort_perspective(const int32_t *idx, int64_t B, int K, int64_t N
 static int pair_gather_perspective(int p, const SortedSlots &ss, int64_t B, int64_t N, const ColMap &map,
                                    const f32x4 *gt, const RowDst &dst, f32x4 *tmp, int nc, hipStream_t s) {
   const int ntiles = map_tiles(map);
-  const int ngroups = (int)ceil_div(N, bwd_feat_per_block<kBwdTileCh>());
-  static_assert(kLongPath<kBwdTileCh>, "the pair gather sums long segments in its long-segment slots");
-  const int64_t blocks = tile_sched_items_per_xcd(ntiles, ngroups + kLongSlots) * kXcds;
+  const int ngroups = (int)ceil_div(N, bwd_feat_per_block());
   for (int h = 0; h < nc; ++h) {
     int src_mode, dst_mode;
     if (p == 0) {
@@ -1205,11 +1273,8 @@ static int pair_gather_perspective(int p, const SortedSlots &ss, int64_t B, int6
     }
     ProfScope prof(kProfBwdTiled, s);
     const bool nt = (nc > 1 ? half_rows(B) : B) * kBwdTileCh * 16 >= kNtStoreTileBytes;
-    hipLaunchKernelGGL((nt ? bwd_tiled_gather_kernel<kBwdTileCh, true> : bwd_tiled_gather_kernel<kBwdTileCh, false>),
-                       dim3((unsigned)blocks), dim3(kBlock), 0, s, ss.sb.seg + (int64_t)h * N, ss.pos, N, gt, B, map,
-                       dst, tmp, src_mode, dst_mode, ntiles, ngroups, ss.sb.list + h * N, ss.sb.count + h,
-                       kLongSlots);
-    const int rc = check_launch("tiled feature gather");
+    const int rc = launch_tiled_gather(nt, ss.sb.seg + (int64_t)h * N, ss.pos, N, gt, B, map, dst, tmp, src_mode,
+                                       dst_mode, ntiles, ngroups, ss.sb.list + h * N, ss.sb.count + h, kLongSlots, s);
     if (rc != SFT_OK) return rc;
   }
   return SFT_OK;

@@ -236,11 +236,15 @@ __global__ __launch_bounds__(kBlock) void fwd_i16_kernel(const int32_t *__restri
 // The gather then runs tile by tile on each XCD (tile_sched_item), lane
 // groups of 8 lanes x 16 B covering one tile row per position, so every
 // table read after the first touch of a tile is an L2 hit.
+//
+// Each tile ends with a pad row (row N) of -0.0 in every column.  A
+// position's LDS list holds its active rows and then N up to the wave's
+// longest list, so all lanes load and add a row at every step with no
+// execution masks: x + (-0.0) == x for every x in round-to-nearest (-0.0 and
+// +0.0 included, NaN stays NaN), and the sum is the one over the active rows
+// in list order.
 constexpr int kTileF = 32;                 // floats per tile row
 constexpr int kTileCh = kTileF / 4;        // float4 chunks per tile row (= lane group size)
-#ifndef SFT_FWD_TILED_U
-#define SFT_FWD_TILED_U 4
-#endif
 #ifndef SFT_TILED_ROUNDS
 #define SFT_TILED_ROUNDS 1
 #endif
@@ -271,24 +275,27 @@ __device__ __forceinline__ f32x4 shfl_xor4(f32x4 v, int m) {
 }
 
 constexpr uint32_t kTileRowBytes = kTileCh * sizeof(f32x4);  // 128
+// Rows per fp32 table tile: the N table rows and the pad row.
+__host__ __device__ inline int64_t tile_rows(int64_t N) { return N + 1; }
 
 __device__ __forceinline__ f32x4 f32_row(const char *tbase, uint32_t lane_off, int f) {
   return *reinterpret_cast<const f32x4 *>(tbase + ((uint32_t)f * kTileRowBytes + lane_off));
 }
 
-// Rows [0, n) of one position in one tile, added onto acc in list order (the
-// order of the reference's sum).  The main loop covers the rows every lane of
-// the 8-lane group has (nmin) without masks, a masked tail the rest up to nmax.
-// PARTIAL (block-uniform: the tile has padding lanes) masks the padding lanes'
-// loads so that they fetch nothing; in a full tile every lane loads.  Row
-// addresses are 32-bit offsets from the tile's base (a tile is N x 128 B).
-template <bool PARTIAL>
-__device__ __forceinline__ f32x4 f32_tile_rows(const int *mylist, int n, int nmin, int nmax, const char *tbase,
-                                               uint32_t lane_off, bool colok, f32x4 acc) {
-  constexpr int U = SFT_FWD_TILED_U;
+// Rows [0, nmax4) of one position's list in one tile, added onto acc in list
+// order: the position's active rows, then the pad row (see above) up to the
+// wave's longest list rounded up to 4.  Padding lanes of the last tile load
+// their chunk too (it is allocated; their sums are not stored).  Row
+// addresses are 32-bit offsets from the tile's base (a tile is (N + 1) x 128 B).
+#ifndef SFT_FWD_TILED_U
+#define SFT_FWD_TILED_U 8
+#endif
+__device__ __forceinline__ f32x4 f32_tile_rows(const int *mylist, int nmax4, const char *tbase, uint32_t lane_off,
+                                               f32x4 acc) {
+  constexpr int U = SFT_FWD_TILED_U;  // rows in flight per step (a multiple of 4)
   static_assert(U % 4 == 0, "rows are read from the LDS list four at a time");
   int k = 0;
-  for (; k + U <= nmin; k += U) {
+  for (; k + U <= nmax4; k += U) {
     int fi[U];
 #pragma unroll
     for (int u = 0; u < U; u += 4) {
@@ -297,24 +304,17 @@ __device__ __forceinline__ f32x4 f32_tile_rows(const int *mylist, int n, int nmi
     }
     f32x4 w[U];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      w[u] = f32x4{0.f, 0.f, 0.f, 0.f};
-      if (!PARTIAL || colok) w[u] = f32_row(tbase, lane_off, fi[u]);
-    }
+    for (int u = 0; u < U; ++u) w[u] = f32_row(tbase, lane_off, fi[u]);
 #pragma unroll
     for (int u = 0; u < U; ++u) acc += w[u];
   }
-  for (; k < nmax; k += 4) {
+  for (; k < nmax4; k += 4) {
     const i32x4 f4 = read4(mylist, k);
     f32x4 w[4];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      w[u] = f32x4{0.f, 0.f, 0.f, 0.f};
-      if (k + u < n && (!PARTIAL || colok)) w[u] = f32_row(tbase, lane_off, f4[u]);
-    }
+    for (int u = 0; u < 4; ++u) w[u] = f32_row(tbase, lane_off, f4[u]);
 #pragma unroll
-    for (int u = 0; u < 4; ++u)
-      if (k + u < n) acc += w[u];
+    for (int u = 0; u < 4; ++u) acc += w[u];
   }
   return acc;
 }
@@ -348,22 +348,20 @@ __global__ __launch_bounds__(kBlock) void fwd_tiled_kernel(const int32_t *__rest
   const int64_t col4 = col;
   const int64_t cols4 = map.cols4;
   const f32x4 b4 = colok ? bias[col4] : f32x4{0.f, 0.f, 0.f, 0.f};
-  const char *tbase = reinterpret_cast<const char *>(Wt + (int64_t)it.tile * N * kTileCh);
+  const char *tbase = reinterpret_cast<const char *>(Wt + (int64_t)it.tile * tile_rows(N) * kTileCh);
   const uint32_t lane_off = (uint32_t)t * (uint32_t)sizeof(f32x4);
-  bool partial = false;  // block-uniform
-  for (int q = 0; q < kTileCh; ++q) partial |= tile_col(map, it.tile, q) < 0;
 
   for (int round = 0; round < kTiledRounds; ++round) {
     const int64_t pos0 = (int64_t)it.chunk * kTiledPosPerBlock + round * kTiledPosPerRound + wave * PPW;
-    compact_rows(idx, B, K, N, pos0, PPW, list, kpad, count);
+    for (int j = lane; j < PPW * kpad; j += kWave) list[j] = N;  // the pad row past each count
+    compact_rows(idx, B, K, N, pos0, PPW, list, kpad, count);      // LDS writes of one wave land in order
     wave_lds_barrier();
     const int64_t pos = pos0 + g;
     const int n = count[g];
     int nmin, nmax;
     group_minmax<kTileCh>(n, nmin, nmax);
-    const int *mylist = list + g * kpad;
-    const f32x4 acc = partial ? f32_tile_rows<true>(mylist, n, nmin, nmax, tbase, lane_off, colok, b4)
-                              : f32_tile_rows<false>(mylist, n, nmin, nmax, tbase, lane_off, colok, b4);
+    f32x4 acc = f32_tile_rows(list + g * kpad, round_up4(nmax), tbase, lane_off, b4);
+    if (!colok) acc = f32x4{0.f, 0.f, 0.f, 0.f};  // padding lanes read unwritten chunks; their raw rows stay 0
     if (!EPI) {
       f32x4 *__restrict__ out = second ? out1 : out0;
       if (pos < B && colok) __builtin_nontemporal_store(acc, out + pos * cols4 + col4);
@@ -634,19 +632,27 @@ void launch_fwd_i16(dim3 grid, size_t lds, hipStream_t s, const int32_t *idx, in
 
 }  // namespace
 
-// Wt[(t * N + r) * 8 + q] = W[r, 4 * (8 t + q) .. +3]; padding chunks of the last tile are not written.
+// Wt[(t * (N + 1) + r) * 8 + q] = W[r, 4 * (8 t + q) .. +3], and row N of
+// every tile = -0.0 (the pad row); the table's padding chunks of the last
+// tile are not written.
 static __global__ __launch_bounds__(kBlock) void tile_relayout_kernel(const f32x4 *__restrict__ W, int64_t N, int64_t cols4,
                                                                f32x4 *__restrict__ Wt) {
-  const int64_t total = N * cols4;
+  const int64_t body = N * cols4, total = body + ceil_div(cols4, (int64_t)8) * 8;
+  const int64_t rows = tile_rows(N);
   for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < total; i += (int64_t)gridDim.x * kBlock) {
-    const int64_t r = i / cols4, c = i % cols4;
-    const int64_t t = c / 8, q = c % 8;
-    Wt[(t * N + r) * 8 + q] = W[i];
+    if (i < body) {
+      const int64_t r = i / cols4, c = i % cols4;
+      const int64_t t = c / 8, q = c % 8;
+      Wt[(t * rows + r) * 8 + q] = W[i];
+    } else {
+      const int64_t t = (i - body) / 8, q = (i - body) % 8;
+      Wt[(t * rows + N) * 8 + q] = f32x4{-0.f, -0.f, -0.f, -0.f};
+    }
   }
 }
 
 void launch_tile_relayout(const f32x4 *src, int64_t rows, int64_t cols4, f32x4 *dst, hipStream_t s) {
-  const int64_t total = rows * cols4;
+  const int64_t total = rows * cols4 + ceil_div(cols4, (int64_t)8) * 8;
   hipLaunchKernelGGL(tile_relayout_kernel, dim3((unsigned)std::min<int64_t>(ceil_div(total, kBlock), 1 << 16)),
                      dim3(kBlock), 0, s, src, rows, cols4, dst);
 }
@@ -655,12 +661,19 @@ void launch_tile_relayout(const f32x4 *src, int64_t rows, int64_t cols4, f32x4 *
 // period_s] when the block has virtual rows; r' = r - start_s), added in
 // binary32 exactly as the table the reference materialises
 // (FEAT/halfka_v2_hm.py:69-70, FEAT/composed.py:49-50), and stored straight into
-// the 32-column tiles of the tiled gather.  total = N * cols4 < 2^31.
+// the 32-column tiles of the tiled gather, each closed by its pad row of
+// -0.0.  total = N * cols4 + 8 * ntiles < 2^31.
 static __global__ __launch_bounds__(kBlock) void fold_relayout_kernel(FoldSrc src, int N, ColMap map,
                                                                       f32x4 *__restrict__ Wt) {
   const int cols4 = map.cols4;
-  const int total = N * cols4;
+  const int body = N * cols4, total = body + 8 * map_tiles(map);
+  const int64_t rows = tile_rows(N);
   for (int i = blockIdx.x * kBlock + threadIdx.x; i < total; i += gridDim.x * kBlock) {
+    if (i >= body) {
+      const int t = (i - body) / 8, q = (i - body) % 8;
+      Wt[((int64_t)t * rows + N) * 8 + q] = f32x4{-0.f, -0.f, -0.f, -0.f};
+      continue;
+    }
     const int r = i / cols4, c = i - r * cols4;
     const int s = block_of(r, src.n, src.start);
     const int rl = r - (int)pick(src.start, s);
@@ -672,7 +685,7 @@ static __global__ __launch_bounds__(kBlock) void fold_relayout_kernel(FoldSrc sr
     }
     int t, q;
     tile_of_col(map, c, t, q);
-    Wt[((int64_t)t * N + r) * 8 + q] = x;
+    Wt[((int64_t)t * rows + r) * 8 + q] = x;
   }
 }
 
@@ -704,7 +717,7 @@ int fwd_f32(const int32_t *idx, int64_t B, int K, const float *W, int64_t N, int
 size_t fwd_tiled_workspace(int64_t N, int L) {
   if (L % 4 != 0) return 0;
   const int64_t ntiles = ceil_div(L, kTileF);
-  return (size_t)(ntiles * N * kTileF) * sizeof(float);
+  return (size_t)(ntiles * tile_rows(N) * kTileF) * sizeof(float);
 }
 
 #ifndef SFT_FWD_TILE_MAX_BYTES
@@ -753,6 +766,8 @@ int fwd_f32_tiled(const int32_t *idx, int64_t B, int K, const float *W, int64_t 
 }
 
 size_t map_tiles_workspace(const ColMap &m, int64_t rows) { return (size_t)map_tiles(m) * (size_t)rows * 128; }
+// The fp32 table tiles of a column map (with their pad rows).
+size_t table_tiles_workspace(const ColMap &m, int64_t N) { return map_tiles_workspace(m, tile_rows(N)); }
 
 // Fold re-layout of the composed table into `wt`, then one tiled gather of both
 // perspectives (plain outputs, or the post-FT epilogue when epi.l0 is set).
@@ -763,11 +778,11 @@ static int pair_gather(const int32_t *idx0, const int32_t *idx1, int64_t B, int 
   const int kpad = round_up4(K);
   const size_t lds = index_lds_bytes(kTileCh, K);
   if (lds > kMaxIndexLds) return fail(SFT_EUNSUPPORTED, std::string(who) + ": max_active too large for the LDS index lists");
-  if (N * (int64_t)kTileRowBytes > (int64_t)UINT32_MAX)
-    return fail(SFT_EUNSUPPORTED, std::string(who) + ": more than 2^25 table rows");
+  if (tile_rows(N) * (int64_t)kTileRowBytes > (int64_t)UINT32_MAX)
+    return fail(SFT_EUNSUPPORTED, std::string(who) + ": more than 2^25 - 1 table rows");
   {
     ProfScope prof(kProfFwdFold, s);
-    const int64_t total = N * map.cols4;
+    const int64_t total = N * map.cols4 + 8 * ntiles;
     hipLaunchKernelGGL(fold_relayout_kernel, dim3((unsigned)std::min<int64_t>(ceil_div(total, kBlock), 1 << 16)),
                        dim3(kBlock), 0, s, src, (int)N, map, wt);
   }
@@ -792,7 +807,7 @@ static int pair_gather(const int32_t *idx0, const int32_t *idx1, int64_t B, int 
 int fwd_pair_f32(const int32_t *idx0, const int32_t *idx1, int64_t B, int K, const FoldSrc &src, int64_t N, int L,
                  const float *bias, float *out0, float *out1, void *ws, size_t ws_bytes, hipStream_t s) {
   const ColMap map = plain_map(L / 4);
-  if (ws_bytes < map_tiles_workspace(map, N) || ws == nullptr || (uintptr_t)ws % 256 != 0)
+  if (ws_bytes < table_tiles_workspace(map, N) || ws == nullptr || (uintptr_t)ws % 256 != 0)
     return fail(SFT_EWORKSPACE, "sft_ft_fwd_pair_f32: workspace smaller than sft_ft_pair_workspace_size() "
                                 "or not 256-byte aligned");
   return pair_gather(idx0, idx1, B, K, src, N, map, bias, out0, out1, FwdEpilogue{}, static_cast<f32x4 *>(ws), s,
@@ -807,7 +822,7 @@ int fwd_transform_f32(const int32_t *idx0, const int32_t *idx1, int64_t B, int K
                       float *psqt, void *saved, size_t saved_bytes, void *ws, size_t ws_bytes, hipStream_t s) {
   const ColMap map = paired_map(L / 4, L1 / 8);
   const size_t raw_bytes = map_tiles_workspace(map, B);
-  if (ws_bytes < map_tiles_workspace(map, N) || ws == nullptr || (uintptr_t)ws % 256 != 0 ||
+  if (ws_bytes < table_tiles_workspace(map, N) || ws == nullptr || (uintptr_t)ws % 256 != 0 ||
       saved_bytes < 2 * raw_bytes || saved == nullptr || (uintptr_t)saved % 256 != 0)
     return fail(SFT_EWORKSPACE, "sft_ft_fwd_transform_f32: saved or workspace buffer smaller than "
                                 "sft_ft_transform_workspace_size() or not 256-byte aligned");

@@ -206,12 +206,12 @@ def test_pair_workspace_size_and_shape_checks():
     # HalfKAv2_hm: 24576 rows folded with 768 virtual rows, L = 1048
     rc = lib.sft_ft_pair_workspace_size(65536, 32, 1, _i64s(24576), _i64s(768), 1048, ctypes.byref(fb), ctypes.byref(bb))
     assert rc == 0, _native.last_error()
-    assert fb.value == 33 * 24576 * 32 * 4  # the merged table in 32-column tiles
+    assert fb.value == 33 * 24577 * 32 * 4  # the merged table in 32-column tiles, each with a pad row
     assert bb.value >= 24576 * 1048 * 4 + 33 * 65536 * 32 * 4  # tmp sums + grad tiles
     # Full_Threats + HalfKAv2_hm
     rc = lib.sft_ft_pair_workspace_size(65536, 160, 2, _i64s(60720, 24576), _i64s(0, 768), 1048, ctypes.byref(fb),
                                         ctypes.byref(bb))
-    assert rc == 0 and fb.value == 33 * 85296 * 32 * 4
+    assert rc == 0 and fb.value == 33 * 85297 * 32 * 4
     # shapes the fused path does not take
     rc = lib.sft_ft_pair_workspace_size(65536, 32, 1, _i64s(24576), _i64s(768), 136, ctypes.byref(fb), ctypes.byref(bb))
     assert rc == _native.SFT_EUNSUPPORTED and "output_size" in _native.last_error()
@@ -259,7 +259,8 @@ def test_transform_workspace_size_and_checks():
                                ctypes.byref(bb))
     assert lib.sft_ft_transform_workspace_size(*args(1040)) == 0, _native.last_error()
     # paired map: 33 tiles for the 2 x 130 chunks of L1 plus one PSQT tile, 128 B per row
-    assert sb.value == 2 * 34 * 65536 * 128 and fb.value == 34 * 24576 * 128
+    # (the table tiles with one pad row each)
+    assert sb.value == 2 * 34 * 65536 * 128 and fb.value == 34 * 24577 * 128
     assert bb.value >= 2 * 34 * 65536 * 128 + 24576 * 1048 * 4
     for l1 in (1044, 1048, 0, -8):
         assert lib.sft_ft_transform_workspace_size(*args(l1)) == _native.SFT_EUNSUPPORTED
