@@ -88,7 +88,9 @@ int sft_ft_fwd_f32_workspace_size(int64_t batch, int32_t max_active, int64_t num
  * fp32 forward with a workspace: same result, bit for bit, as sft_ft_fwd_f32.
  * With SFT_FWD_AUTO and a workspace of sft_ft_fwd_f32_workspace_size() bytes
  * (256-byte aligned), the table is first copied into 32-column tiles in the
- * workspace and gathered tile by tile, each tile from one XCD's L2.
+ * workspace (each closed by a pad row of -0.0), the index rows are compacted
+ * once into per-position lists ordered by active count, and the tiles are
+ * gathered one by one, each from one XCD's L2.
  * Replaces the same reference call as sft_ft_fwd_f32
  * (FT/kernel.py:301-312, 66-105).
  */

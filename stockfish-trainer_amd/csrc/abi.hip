@@ -15,7 +15,7 @@ int fwd_f32(const int32_t *idx, int64_t B, int K, const float *W, int64_t N, int
 int fwd_i16(const int32_t *idx, int64_t B, int K, const int16_t *W, int64_t N, int L, const int16_t *bias,
             const int32_t *psqt, int P, int16_t *out, int32_t *psqt_out, int lo, int hi, int wrap16, hipStream_t s);
 int quantize_i16(const float *x, int64_t n, float scale, int16_t *out, hipStream_t s);
-size_t fwd_tiled_workspace(int64_t N, int L);
+size_t fwd_tiled_workspace(int64_t B, int K, int64_t N, int L);
 bool fwd_tiled_supported(int64_t N, int L, const void *W, const void *bias, const void *out);
 int fwd_f32_tiled(const int32_t *idx, int64_t B, int K, const float *W, int64_t N, int L, const float *bias, float *out,
                   void *ws, size_t ws_bytes, hipStream_t s);
@@ -51,6 +51,7 @@ int encode_features(const uint8_t *boards, const uint8_t *stm, int64_t B, const 
                     int32_t *count_b, hipStream_t s);
 size_t map_tiles_workspace(const ColMap &m, int64_t rows);
 size_t table_tiles_workspace(const ColMap &m, int64_t N);
+size_t fwd_pair_workspace(const ColMap &m, int64_t B, int K, int64_t N);
 int fwd_transform_f32(const int32_t *idx0, const int32_t *idx1, int64_t B, int K, const FoldSrc &src, int64_t N,
                       int L, int L1, const float *bias, const float *us, const int64_t *psqt_idx, float *l0,
                       float *psqt, void *saved, size_t saved_bytes, void *ws, size_t ws_bytes, hipStream_t s);
@@ -219,7 +220,7 @@ const char *const kKindNames[] = {
     "bwd_bias_final",   "bwd_atomic_scatter", "bwd_zero_fill",      "fwd_i16_gather",     "quantize_i16",
     "fwd_tile_relayout", "fwd_f32_tiled_gather", "bwd_tiled_gather", "fwd_i16_tiled_gather",
     "fwd_fold_relayout", "bwd_virtual_reduce", "bwd_epilogue", "ranger22_update", "encode_features", "leb128_encode",
-    "probe_l2_gather",
+    "probe_l2_gather", "fwd_rank_lists",
 };
 static_assert(sizeof(kKindNames) / sizeof(kKindNames[0]) == kProfNumKinds, "one name per profiling kind");
 }  // namespace
@@ -306,7 +307,7 @@ int sft_ft_fwd_f32_workspace_size(int64_t batch, int32_t max_active, int64_t num
     return fail(SFT_EINVAL, "sft_ft_fwd_f32_workspace_size: " + why);
   if (flags & ~SFT_FWD_ROWS) return fail(SFT_EINVAL, "sft_ft_fwd_f32_workspace_size: unknown flags");
   const bool tiled = !(flags & SFT_FWD_ROWS) && fwd_tiled_supported(num_inputs, output_size, nullptr, nullptr, nullptr);
-  *bytes = tiled ? fwd_tiled_workspace(num_inputs, output_size) : 0;
+  *bytes = tiled ? fwd_tiled_workspace(batch, max_active, num_inputs, output_size) : 0;
   return SFT_OK;
 }
 
@@ -320,7 +321,8 @@ int sft_ft_fwd_f32_ex(const int32_t *idx, int64_t batch, int32_t max_active, con
   if (flags & ~SFT_FWD_ROWS) return fail(SFT_EINVAL, "sft_ft_fwd_f32_ex: unknown flags");
   if (batch == 0) return SFT_OK;
   const bool tiled = !(flags & SFT_FWD_ROWS) && fwd_tiled_supported(num_inputs, output_size, weight, bias, out) &&
-                     workspace != nullptr && workspace_bytes >= fwd_tiled_workspace(num_inputs, output_size);
+                     workspace != nullptr &&
+                     workspace_bytes >= fwd_tiled_workspace(batch, max_active, num_inputs, output_size);
   if (tiled)
     return fwd_f32_tiled(idx, batch, max_active, weight, num_inputs, output_size, bias, out, workspace,
                          workspace_bytes, (hipStream_t)stream);
@@ -392,7 +394,7 @@ int sft_ft_pair_workspace_size(int64_t batch, int32_t max_active, int32_t num_bl
   const int rc = check_pair_shape("sft_ft_pair_workspace_size", batch, max_active, num_blocks, block_rows,
                                   block_virtual_rows, output_size, &N);
   if (rc != SFT_OK) return rc;
-  *fwd_bytes = fwd_tiled_workspace(N, output_size);
+  *fwd_bytes = fwd_pair_workspace(plain_map(output_size / 4), batch, max_active, N);
   *bwd_bytes = bwd_pair_workspace(batch, max_active, N, output_size);
   return SFT_OK;
 }
@@ -555,7 +557,7 @@ int sft_ft_transform_workspace_size(int64_t batch, int32_t max_active, int32_t n
   if (rc != SFT_OK || (rc = check_l1(who, output_size, l1)) != SFT_OK) return rc;
   const ColMap map = paired_map(output_size / 4, l1 / 8);
   *saved_bytes = 2 * map_tiles_workspace(map, batch);
-  *fwd_bytes = table_tiles_workspace(map, N);
+  *fwd_bytes = fwd_pair_workspace(map, batch, max_active, N);
   *bwd_bytes = bwd_transform_workspace(batch, max_active, N, output_size, l1);
   return SFT_OK;
 }

@@ -80,6 +80,7 @@ enum ProfKind : int {
   kProfEncode,
   kProfLeb128,
   kProfProbeL2Gather,
+  kProfFwdRanks,
   kProfNumKinds
 };
 struct ProfScope {

@@ -282,20 +282,20 @@ __device__ __forceinline__ f32x4 f32_row(const char *tbase, uint32_t lane_off, i
   return *reinterpret_cast<const f32x4 *>(tbase + ((uint32_t)f * kTileRowBytes + lane_off));
 }
 
-// Rows [0, nmax4) of one position's list in one tile, added onto acc in list
+// Rows [0, nmax) of one position's list in one tile, added onto acc in list
 // order: the position's active rows, then the pad row (see above) up to the
-// wave's longest list rounded up to 4.  Padding lanes of the last tile load
-// their chunk too (it is allocated; their sums are not stored).  Row
-// addresses are 32-bit offsets from the tile's base (a tile is (N + 1) x 128 B).
+// wave's longest list.  Padding lanes of the last tile load their chunk too
+// (it is allocated; their sums are not stored).  Row addresses are 32-bit
+// offsets from the tile's base (a tile is (N + 1) x 128 B).
 #ifndef SFT_FWD_TILED_U
 #define SFT_FWD_TILED_U 8
 #endif
-__device__ __forceinline__ f32x4 f32_tile_rows(const int *mylist, int nmax4, const char *tbase, uint32_t lane_off,
+__device__ __forceinline__ f32x4 f32_tile_rows(const int *mylist, int nmax, const char *tbase, uint32_t lane_off,
                                                f32x4 acc) {
   constexpr int U = SFT_FWD_TILED_U;  // rows in flight per step (a multiple of 4)
   static_assert(U % 4 == 0, "rows are read from the LDS list four at a time");
   int k = 0;
-  for (; k + U <= nmax4; k += U) {
+  for (; k + U <= nmax; k += U) {
     int fi[U];
 #pragma unroll
     for (int u = 0; u < U; u += 4) {
@@ -308,7 +308,7 @@ __device__ __forceinline__ f32x4 f32_tile_rows(const int *mylist, int nmax4, con
 #pragma unroll
     for (int u = 0; u < U; ++u) acc += w[u];
   }
-  for (; k < nmax4; k += 4) {
+  for (; k + 4 <= nmax; k += 4) {
     const i32x4 f4 = read4(mylist, k);
     f32x4 w[4];
 #pragma unroll
@@ -316,32 +316,139 @@ __device__ __forceinline__ f32x4 f32_tile_rows(const int *mylist, int nmax4, con
 #pragma unroll
     for (int u = 0; u < 4; ++u) acc += w[u];
   }
+  for (; k < nmax; ++k) acc += f32_row(tbase, lane_off, mylist[k]);
   return acc;
 }
 
-// Two perspectives share one launch: chunks [0, nchunks_p) read idx0 and write
-// out0, chunks [nchunks_p, 2 nchunks_p) idx1 and out1, so an XCD gathers both
-// perspectives from a tile while it is in L2.  A single-perspective call passes
-// the same arrays twice and nchunks_p = nchunks.
+// ------------------------------------------------ rank lists of the gather ----
+// Before the tiled fp32 gather, each perspective's index rows become lists in
+// rank order: rank r holds position pos[r], its active slots (0 <= v < N) in
+// slot order and then N (the pad row) up to kpad entries.  Within each block
+// of 256 consecutive positions the ranks run through the positions by active
+// count, largest first, so the 8 consecutive ranks a wave sums have nearly
+// the same count: the wave steps as many rows as its longest list, and a step
+// costs one vector-memory instruction whatever the number of lanes with a
+// row.  The lists are built once per call instead of compacted again for
+// every column tile, and a wave loads its 8 lists with 16-byte loads (one per
+// lane at K = 32).  Ranks B .. Bpad - 1 are padding: position -1, count 0,
+// list all N.  Positions of one count are ranked in the order LDS atomics
+// hand out; a position's sum does not depend on its rank.
+constexpr int kRanksPerBlock = kWavesPerBlock * (kWave / kTileCh);  // 32: 8 per wave
+constexpr int kRankSortBlock = kBlock;                               // positions ranked together
+struct RankLists {
+  int32_t *list;   // [Bpad][kpad]
+  int32_t *pos;    // [Bpad] rank -> position, -1 for padding
+  int32_t *count;  // [Bpad] active slots of the rank's position, non-increasing within each 256 ranks
+};
+struct RankArgs {
+  const int32_t *idx[2];
+  RankLists L[2];
+};
+
+// One workgroup per 256 positions of one perspective (grid.y).  STAGE: the
+// lists are assembled in LDS (row stride kpad + 1, free of bank conflicts)
+// and stored with coalesced 16-byte stores; else each thread stores its own.
+template <bool STAGE>
+__global__ __launch_bounds__(kBlock) void rank_lists_kernel(RankArgs a, int64_t B, int64_t Bpad, int K, int N,
+                                                            int kpad, int vec) {
+  extern __shared__ int sm[];  // bins[K + 1] | offsets[K + 1] | (STAGE) 256 rows of kpad + 1
+  unsigned *bin = reinterpret_cast<unsigned *>(sm), *off = bin + (K + 1);
+  int *rows = sm + 2 * (K + 1);
+  const RankLists &L = a.L[blockIdx.y];
+  const int32_t *__restrict__ idx = a.idx[blockIdx.y];
+  const int tid = threadIdx.x;
+  const int64_t base = (int64_t)blockIdx.x * kRankSortBlock;
+  const int64_t b = base + tid;
+  const bool real = b < B;
+  const int32_t *row = idx + (real ? b : 0) * K;
+  auto slot = [&](int k) { return row[k]; };
+  for (int i = tid; i <= K; i += kBlock) bin[i] = 0u;
+  __syncthreads();
+  int c = 0;
+  if (real) {
+    if (vec) {
+      for (int k = 0; k < K; k += 4) {
+        const i32x4 v = *reinterpret_cast<const i32x4 *>(row + k);
+        c += ((unsigned)v[0] < (unsigned)N) + ((unsigned)v[1] < (unsigned)N) + ((unsigned)v[2] < (unsigned)N) +
+             ((unsigned)v[3] < (unsigned)N);
+      }
+    } else {
+      for (int k = 0; k < K; ++k) c += (unsigned)slot(k) < (unsigned)N ? 1 : 0;
+    }
+  }
+  const unsigned mine = real ? atomicAdd(&bin[c], 1u) : 0u;
+  __syncthreads();
+  if (tid == 0) {
+    unsigned acc = 0u;
+    for (int cc = K; cc >= 0; --cc) {
+      off[cc] = acc;
+      acc += bin[cc];
+    }
+  }
+  __syncthreads();
+  const int rl = real ? (int)(off[c] + mine) : tid;  // positions past B are the block's last (padding) ranks
+  const int64_t r = base + rl;
+  if (r < Bpad) {
+    L.pos[r] = real ? (int32_t)b : -1;
+    L.count[r] = real ? c : 0;
+  }
+  int *dst = STAGE ? rows + rl * (kpad + 1) : L.list + r * kpad;
+  if (STAGE || r < Bpad) {
+    int j = 0;
+    if (real)
+      for (int k = 0; k < K; ++k) {
+        const int v = slot(k);
+        if ((unsigned)v < (unsigned)N) dst[j++] = v;
+      }
+    for (; j < kpad; ++j) dst[j] = N;
+  }
+  if (STAGE) {
+    __syncthreads();
+    const int q4 = kpad / 4;
+    i32x4 *out = reinterpret_cast<i32x4 *>(L.list + base * kpad);
+    for (int i = tid; i < kRankSortBlock * q4; i += kBlock) {
+      const int rr = i / q4, q = i - rr * q4;
+      if (base + rr >= Bpad) break;  // i ascending: every later piece is past Bpad too
+      const int *src = rows + rr * (kpad + 1) + 4 * q;
+      out[i] = i32x4{src[0], src[1], src[2], src[3]};
+    }
+  }
+}
+
+// Chunk c (of 32 ranks) of a tile pass -> rank chunk: the longest lists
+// first across all sort blocks -- chunk 0 of every block, then chunk 1 of
+// every block, and so on (the last block may hold fewer chunks) -- so a tile
+// pass starts with its longest items and ends with its shortest.
+constexpr int kChunksPerSortBlock = kRankSortBlock / kRanksPerBlock;  // 8
+__device__ __forceinline__ int64_t rank_chunk(int64_t c, int64_t nchunks) {
+  const int64_t nb = (nchunks + kChunksPerSortBlock - 1) / kChunksPerSortBlock;  // sort blocks
+  const int64_t last = nchunks - (nb - 1) * kChunksPerSortBlock;                 // chunks of the last block
+  if (c < last * nb) return (c % nb) * kChunksPerSortBlock + c / nb;
+  const int64_t c2 = c - last * nb;
+  return (c2 % (nb - 1)) * kChunksPerSortBlock + last + c2 / (nb - 1);
+}
+
+// Two perspectives share one launch: chunks [0, nchunks_p) read the rank
+// lists R0 and write out0, chunks [nchunks_p, 2 nchunks_p) R1 and out1, so an
+// XCD gathers both perspectives from a tile while it is in L2.  A
+// single-perspective call passes the same lists twice and nchunks_p = nchunks.
+// A chunk is 32 ranks, 8 per wave; the waves of a workgroup do not wait for
+// each other.
 template <bool EPI>
-__global__ __launch_bounds__(kBlock) void fwd_tiled_kernel(const int32_t *__restrict__ idx0,
-                                                           const int32_t *__restrict__ idx1, int64_t B, int K, int N,
+__global__ __launch_bounds__(kBlock) void fwd_tiled_kernel(RankLists R0, RankLists R1, int N,
                                                            const f32x4 *__restrict__ Wt, ColMap map,
                                                            const f32x4 *__restrict__ bias, f32x4 *__restrict__ out0,
                                                            f32x4 *__restrict__ out1, FwdEpilogue epi, int kpad,
                                                            int ntiles, int nchunks, int nchunks_p) {
-  constexpr int PPW = kWave / kTileCh;  // 8 positions per wave per round
-  static_assert(PPW <= kCompactRows, "compact_rows takes at most kCompactRows rows");
-  extern __shared__ int smem[];
+  constexpr int PPW = kWave / kTileCh;  // 8 ranks per wave
+  extern __shared__ int smem[];         // 8 lists of kpad entries per wave
   TileItem it = tile_sched_item(blockIdx.x, ntiles, nchunks);
   if (it.tile >= ntiles) return;  // whole block: uniform
   const bool second = it.chunk >= nchunks_p;
   if (second) it.chunk -= nchunks_p;
-  const int32_t *__restrict__ idx = second ? idx1 : idx0;
+  const RankLists R = second ? R1 : R0;
   const int wave = uniform(threadIdx.x / kWave);
   const int lane = threadIdx.x % kWave;
-  int *list = smem + wave * PPW * kpad;
-  int *count = smem + kWavesPerBlock * PPW * kpad + wave * PPW;
   const int g = lane / kTileCh, t = lane % kTileCh;
   const int col = tile_col(map, it.tile, t);
   const bool colok = col >= 0;
@@ -351,35 +458,38 @@ __global__ __launch_bounds__(kBlock) void fwd_tiled_kernel(const int32_t *__rest
   const char *tbase = reinterpret_cast<const char *>(Wt + (int64_t)it.tile * tile_rows(N) * kTileCh);
   const uint32_t lane_off = (uint32_t)t * (uint32_t)sizeof(f32x4);
 
-  for (int round = 0; round < kTiledRounds; ++round) {
-    const int64_t pos0 = (int64_t)it.chunk * kTiledPosPerBlock + round * kTiledPosPerRound + wave * PPW;
-    for (int j = lane; j < PPW * kpad; j += kWave) list[j] = N;  // the pad row past each count
-    compact_rows(idx, B, K, N, pos0, PPW, list, kpad, count);      // LDS writes of one wave land in order
-    wave_lds_barrier();
-    const int64_t pos = pos0 + g;
-    const int n = count[g];
-    int nmin, nmax;
-    group_minmax<kTileCh>(n, nmin, nmax);
-    f32x4 acc = f32_tile_rows(list + g * kpad, round_up4(nmax), tbase, lane_off, b4);
-    if (!colok) acc = f32x4{0.f, 0.f, 0.f, 0.f};  // padding lanes read unwritten chunks; their raw rows stay 0
-    if (!EPI) {
-      f32x4 *__restrict__ out = second ? out1 : out0;
-      if (pos < B && colok) __builtin_nontemporal_store(acc, out + pos * cols4 + col4);
-    } else {
-      f32x4 *__restrict__ raw = second ? epi.raw1 : epi.raw0;
-      if (pos < B) __builtin_nontemporal_store(acc, raw + (pos * ntiles + it.tile) * kTileCh + t);
-      if (it.tile < map.t1) {  // block-uniform
-        const f32x4 partner = shfl_xor4(acc, 4);
-        if (t < 4 && colok && pos < B) {
-          const bool white_to_move = epi.us[pos] != 0.f;
-          const int64_t half = (second ? white_to_move : !white_to_move) ? map.half4 : 0;
-          const f32x4 pw = clamp01(acc) * clamp01(partner);
-          const f32x4 v = pw * (127.0f / 128.0f);
-          __builtin_nontemporal_store(v, epi.l0 + pos * (2 * (int64_t)map.half4) + half + col4);
-        }
+  const int64_t r0 = rank_chunk(it.chunk, nchunks_p) * kRanksPerBlock + wave * PPW;  // the wave's first rank
+  int *list = smem + wave * PPW * kpad;
+  {
+    const i32x4 *__restrict__ src = reinterpret_cast<const i32x4 *>(R.list + r0 * kpad);
+    i32x4 *dst = reinterpret_cast<i32x4 *>(list);
+    for (int j = lane; j < PPW * kpad / 4; j += kWave) dst[j] = src[j];
+  }
+  const int nmax = R.count[r0];  // counts fall with rank within each 256 ranks: the wave's longest list
+  const int32_t *__restrict__ rp = R.pos + r0;
+  int pos = rp[0];
+#pragma unroll
+  for (int u = 1; u < PPW; ++u) pos = g == u ? rp[u] : pos;
+  wave_lds_barrier();
+  f32x4 acc = f32_tile_rows(list + g * kpad, nmax, tbase, lane_off, b4);
+  if (!colok) acc = f32x4{0.f, 0.f, 0.f, 0.f};  // padding lanes read unwritten chunks; their raw rows stay 0
+  if (pos < 0) return;                          // a padding rank
+  if (!EPI) {
+    f32x4 *__restrict__ out = second ? out1 : out0;
+    if (colok) __builtin_nontemporal_store(acc, out + pos * cols4 + col4);
+  } else {
+    f32x4 *__restrict__ raw = second ? epi.raw1 : epi.raw0;
+    __builtin_nontemporal_store(acc, raw + ((int64_t)pos * ntiles + it.tile) * kTileCh + t);
+    if (it.tile < map.t1) {  // block-uniform
+      const f32x4 partner = shfl_xor4(acc, 4);
+      if (t < 4 && colok) {
+        const bool white_to_move = epi.us[pos] != 0.f;
+        const int64_t half = (second ? white_to_move : !white_to_move) ? map.half4 : 0;
+        const f32x4 pw = clamp01(acc) * clamp01(partner);
+        const f32x4 v = pw * (127.0f / 128.0f);
+        __builtin_nontemporal_store(v, epi.l0 + (int64_t)pos * (2 * (int64_t)map.half4) + half + col4);
       }
     }
-    wave_lds_barrier();
   }
 }
 
@@ -714,10 +824,57 @@ int fwd_f32(const int32_t *idx, int64_t B, int K, const float *W, int64_t N, int
   return check_launch("sft_ft_fwd_f32");
 }
 
-size_t fwd_tiled_workspace(int64_t N, int L) {
+static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+// ---- rank lists (host side) ----
+static int64_t rank_pad(int64_t B) { return ceil_div(B, (int64_t)kRanksPerBlock) * kRanksPerBlock; }
+// One perspective's rank lists, each array 256-byte aligned.
+size_t rank_lists_bytes(int64_t B, int K) {
+  const int64_t Bp = rank_pad(B);
+  return align256((size_t)(Bp * round_up4(K)) * 4) + 2 * align256((size_t)Bp * 4);
+}
+static RankLists rank_lists_at(char *p, int64_t B, int K) {
+  const int64_t Bp = rank_pad(B);
+  RankLists r;
+  r.list = reinterpret_cast<int32_t *>(p);
+  p += align256((size_t)(Bp * round_up4(K)) * 4);
+  r.pos = reinterpret_cast<int32_t *>(p);
+  p += align256((size_t)Bp * 4);
+  r.count = reinterpret_cast<int32_t *>(p);
+  return r;
+}
+// LDS of the tiled gather: the 32 lists of a workgroup.
+static size_t rank_lds_bytes(int K) { return (size_t)kRanksPerBlock * round_up4(K) * sizeof(int); }
+// Lists staged in LDS up to kpad = 32 (33 KB); longer ones are stored by their threads.
+constexpr int kRankStageMaxPad = 32;
+
+// Rank lists of np perspectives (idx[p] -> R[p]) in one launch.
+static int build_rank_lists(const int32_t *idx0, const int32_t *idx1, int np, int64_t B, int K, int N,
+                            const RankLists &R0, const RankLists &R1, hipStream_t s, const char *who) {
+  RankArgs a;
+  a.idx[0] = idx0;
+  a.idx[1] = idx1;
+  a.L[0] = R0;
+  a.L[1] = R1;
+  const int64_t Bp = rank_pad(B);
+  const int kpad = round_up4(K);
+  const int vec = K % 4 == 0 && (uintptr_t)idx0 % 16 == 0 && (uintptr_t)idx1 % 16 == 0;
+  const bool stage = kpad <= kRankStageMaxPad;
+  const size_t lds = (size_t)(2 * (K + 1)) * 4 + (stage ? (size_t)kRankSortBlock * (kpad + 1) * 4 : 0);
+  const dim3 grid((unsigned)ceil_div(Bp, (int64_t)kRankSortBlock), (unsigned)np);
+  ProfScope prof(kProfFwdRanks, s);
+  if (stage)
+    hipLaunchKernelGGL(rank_lists_kernel<true>, grid, dim3(kBlock), lds, s, a, B, Bp, K, N, kpad, vec);
+  else
+    hipLaunchKernelGGL(rank_lists_kernel<false>, grid, dim3(kBlock), lds, s, a, B, Bp, K, N, kpad, vec);
+  return check_launch((std::string(who) + " (rank lists)").c_str());
+}
+
+// Table tiles (with their pad rows), then the rank lists of one perspective.
+size_t fwd_tiled_workspace(int64_t B, int K, int64_t N, int L) {
   if (L % 4 != 0) return 0;
   const int64_t ntiles = ceil_div(L, kTileF);
-  return (size_t)(ntiles * tile_rows(N) * kTileF) * sizeof(float);
+  return align256((size_t)(ntiles * tile_rows(N) * kTileF) * sizeof(float)) + rank_lists_bytes(B, K);
 }
 
 #ifndef SFT_FWD_TILE_MAX_BYTES
@@ -738,29 +895,32 @@ bool fwd_tiled_supported(int64_t N, int L, const void *W, const void *bias, cons
 
 int fwd_f32_tiled(const int32_t *idx, int64_t B, int K, const float *W, int64_t N, int L, const float *bias, float *out,
                   void *ws, size_t ws_bytes, hipStream_t s) {
-  if (ws_bytes < fwd_tiled_workspace(N, L) || ws == nullptr || (uintptr_t)ws % 256 != 0)
+  const char *who = "sft_ft_fwd_f32_ex";
+  if (ws_bytes < fwd_tiled_workspace(B, K, N, L) || ws == nullptr || (uintptr_t)ws % 256 != 0)
     return fail(SFT_EWORKSPACE, "sft_ft_fwd_f32_ex: workspace smaller than sft_ft_fwd_f32_workspace_size() "
                                 "or not 256-byte aligned");
   const int64_t cols4 = L / 4;
   const int ntiles = (int)ceil_div(L, kTileF);
   const int kpad = round_up4(K);
-  const size_t lds = index_lds_bytes(kTileCh, K);
+  const size_t lds = rank_lds_bytes(K);
   if (lds > kMaxIndexLds) return fail(SFT_EUNSUPPORTED, "sft_ft_fwd_f32_ex: max_active too large for the LDS index lists");
   f32x4 *wt = static_cast<f32x4 *>(ws);
+  const RankLists R = rank_lists_at(static_cast<char *>(ws) + align256((size_t)(ntiles * tile_rows(N) * kTileF) * 4),
+                                    B, K);
   {
     ProfScope prof(kProfFwdRelayout, s);
     launch_tile_relayout(reinterpret_cast<const f32x4 *>(W), N, cols4, wt, s);
   }
   int rc = check_launch("sft_ft_fwd_f32_ex (relayout)");
   if (rc != SFT_OK) return rc;
-  const int nchunks = (int)ceil_div(B, kTiledPosPerBlock);
+  if ((rc = build_rank_lists(idx, idx, 1, B, K, (int)N, R, R, s, who)) != SFT_OK) return rc;
+  const int nchunks = (int)(rank_pad(B) / kRanksPerBlock);
   const int64_t blocks = tile_sched_items_per_xcd(ntiles, nchunks) * kXcds;
   {
     ProfScope prof(kProfFwdTiled, s);
-    hipLaunchKernelGGL(fwd_tiled_kernel<false>, dim3((unsigned)blocks), dim3(kBlock), lds, s, idx, idx, B, K,
-                       (int)N, wt, plain_map((int)cols4), reinterpret_cast<const f32x4 *>(bias),
-                       reinterpret_cast<f32x4 *>(out), reinterpret_cast<f32x4 *>(out), FwdEpilogue{}, kpad, ntiles,
-                       nchunks, nchunks);
+    hipLaunchKernelGGL(fwd_tiled_kernel<false>, dim3((unsigned)blocks), dim3(kBlock), lds, s, R, R, (int)N, wt,
+                       plain_map((int)cols4), reinterpret_cast<const f32x4 *>(bias), reinterpret_cast<f32x4 *>(out),
+                       reinterpret_cast<f32x4 *>(out), FwdEpilogue{}, kpad, ntiles, nchunks, nchunks);
   }
   return check_launch("sft_ft_fwd_f32_ex (tiled gather)");
 }
@@ -768,15 +928,24 @@ int fwd_f32_tiled(const int32_t *idx, int64_t B, int K, const float *W, int64_t 
 size_t map_tiles_workspace(const ColMap &m, int64_t rows) { return (size_t)map_tiles(m) * (size_t)rows * 128; }
 // The fp32 table tiles of a column map (with their pad rows).
 size_t table_tiles_workspace(const ColMap &m, int64_t N) { return map_tiles_workspace(m, tile_rows(N)); }
+// Forward workspace of a two-perspective call: the table tiles, then both
+// perspectives' rank lists.
+size_t fwd_pair_workspace(const ColMap &m, int64_t B, int K, int64_t N) {
+  return align256(table_tiles_workspace(m, N)) + 2 * rank_lists_bytes(B, K);
+}
 
-// Fold re-layout of the composed table into `wt`, then one tiled gather of both
-// perspectives (plain outputs, or the post-FT epilogue when epi.l0 is set).
+// Fold re-layout of the composed table into the workspace's tiles, rank lists
+// of both perspectives after them, then one tiled gather of both perspectives
+// (plain outputs, or the post-FT epilogue when epi.l0 is set).
 static int pair_gather(const int32_t *idx0, const int32_t *idx1, int64_t B, int K, const FoldSrc &src, int64_t N,
                        const ColMap &map, const float *bias, float *out0, float *out1, const FwdEpilogue &epi,
-                       f32x4 *wt, hipStream_t s, const char *who) {
+                       void *ws, hipStream_t s, const char *who) {
   const int ntiles = map_tiles(map);
   const int kpad = round_up4(K);
-  const size_t lds = index_lds_bytes(kTileCh, K);
+  const size_t lds = rank_lds_bytes(K);
+  f32x4 *wt = static_cast<f32x4 *>(ws);
+  char *lists = static_cast<char *>(ws) + align256(table_tiles_workspace(map, N));
+  const RankLists R0 = rank_lists_at(lists, B, K), R1 = rank_lists_at(lists + rank_lists_bytes(B, K), B, K);
   if (lds > kMaxIndexLds) return fail(SFT_EUNSUPPORTED, std::string(who) + ": max_active too large for the LDS index lists");
   if (tile_rows(N) * (int64_t)kTileRowBytes > (int64_t)UINT32_MAX)
     return fail(SFT_EUNSUPPORTED, std::string(who) + ": more than 2^25 - 1 table rows");
@@ -788,17 +957,18 @@ static int pair_gather(const int32_t *idx0, const int32_t *idx1, int64_t B, int 
   }
   int rc = check_launch(who);
   if (rc != SFT_OK || B == 0) return rc;
-  const int nchunks_p = (int)ceil_div(B, kTiledPosPerBlock);
+  if ((rc = build_rank_lists(idx0, idx1, 2, B, K, (int)N, R0, R1, s, who)) != SFT_OK) return rc;
+  const int nchunks_p = (int)(rank_pad(B) / kRanksPerBlock);
   const int64_t blocks = tile_sched_items_per_xcd(ntiles, 2 * nchunks_p) * kXcds;
   {
     ProfScope prof(kProfFwdTiled, s);
     if (epi.l0 != nullptr)
-      hipLaunchKernelGGL(fwd_tiled_kernel<true>, dim3((unsigned)blocks), dim3(kBlock), lds, s, idx0, idx1, B, K,
-                         (int)N, wt, map, reinterpret_cast<const f32x4 *>(bias), (f32x4 *)nullptr, (f32x4 *)nullptr,
-                         epi, kpad, ntiles, 2 * nchunks_p, nchunks_p);
+      hipLaunchKernelGGL(fwd_tiled_kernel<true>, dim3((unsigned)blocks), dim3(kBlock), lds, s, R0, R1, (int)N, wt,
+                         map, reinterpret_cast<const f32x4 *>(bias), (f32x4 *)nullptr, (f32x4 *)nullptr, epi, kpad,
+                         ntiles, 2 * nchunks_p, nchunks_p);
     else
-      hipLaunchKernelGGL(fwd_tiled_kernel<false>, dim3((unsigned)blocks), dim3(kBlock), lds, s, idx0, idx1, B, K,
-                         (int)N, wt, map, reinterpret_cast<const f32x4 *>(bias), reinterpret_cast<f32x4 *>(out0),
+      hipLaunchKernelGGL(fwd_tiled_kernel<false>, dim3((unsigned)blocks), dim3(kBlock), lds, s, R0, R1, (int)N, wt,
+                         map, reinterpret_cast<const f32x4 *>(bias), reinterpret_cast<f32x4 *>(out0),
                          reinterpret_cast<f32x4 *>(out1), epi, kpad, ntiles, 2 * nchunks_p, nchunks_p);
   }
   return check_launch(who);
@@ -807,22 +977,21 @@ static int pair_gather(const int32_t *idx0, const int32_t *idx1, int64_t B, int 
 int fwd_pair_f32(const int32_t *idx0, const int32_t *idx1, int64_t B, int K, const FoldSrc &src, int64_t N, int L,
                  const float *bias, float *out0, float *out1, void *ws, size_t ws_bytes, hipStream_t s) {
   const ColMap map = plain_map(L / 4);
-  if (ws_bytes < table_tiles_workspace(map, N) || ws == nullptr || (uintptr_t)ws % 256 != 0)
+  if (ws_bytes < fwd_pair_workspace(map, B, K, N) || ws == nullptr || (uintptr_t)ws % 256 != 0)
     return fail(SFT_EWORKSPACE, "sft_ft_fwd_pair_f32: workspace smaller than sft_ft_pair_workspace_size() "
                                 "or not 256-byte aligned");
-  return pair_gather(idx0, idx1, B, K, src, N, map, bias, out0, out1, FwdEpilogue{}, static_cast<f32x4 *>(ws), s,
-                     "sft_ft_fwd_pair_f32");
+  return pair_gather(idx0, idx1, B, K, src, N, map, bias, out0, out1, FwdEpilogue{}, ws, s, "sft_ft_fwd_pair_f32");
 }
 
 // Forward of the composed table with the post-FT epilogue.  `saved` holds the
 // raw pre-activations of both perspectives in paired tiles (map_tiles x B x
-// 128 B each) for the backward; `ws` the table tiles.
+// 128 B each) for the backward; `ws` the table tiles and rank lists.
 int fwd_transform_f32(const int32_t *idx0, const int32_t *idx1, int64_t B, int K, const FoldSrc &src, int64_t N,
                       int L, int L1, const float *bias, const float *us, const int64_t *psqt_idx, float *l0,
                       float *psqt, void *saved, size_t saved_bytes, void *ws, size_t ws_bytes, hipStream_t s) {
   const ColMap map = paired_map(L / 4, L1 / 8);
   const size_t raw_bytes = map_tiles_workspace(map, B);
-  if (ws_bytes < table_tiles_workspace(map, N) || ws == nullptr || (uintptr_t)ws % 256 != 0 ||
+  if (ws_bytes < fwd_pair_workspace(map, B, K, N) || ws == nullptr || (uintptr_t)ws % 256 != 0 ||
       saved_bytes < 2 * raw_bytes || saved == nullptr || (uintptr_t)saved % 256 != 0)
     return fail(SFT_EWORKSPACE, "sft_ft_fwd_transform_f32: saved or workspace buffer smaller than "
                                 "sft_ft_transform_workspace_size() or not 256-byte aligned");
@@ -831,7 +1000,7 @@ int fwd_transform_f32(const int32_t *idx0, const int32_t *idx1, int64_t B, int K
   epi.l0 = reinterpret_cast<f32x4 *>(l0);
   epi.raw0 = static_cast<f32x4 *>(saved);
   epi.raw1 = reinterpret_cast<f32x4 *>(static_cast<char *>(saved) + raw_bytes);
-  int rc = pair_gather(idx0, idx1, B, K, src, N, map, bias, nullptr, nullptr, epi, static_cast<f32x4 *>(ws), s,
+  int rc = pair_gather(idx0, idx1, B, K, src, N, map, bias, nullptr, nullptr, epi, ws, s,
                        "sft_ft_fwd_transform_f32");
   if (rc != SFT_OK || B == 0) return rc;
   hipLaunchKernelGGL(psqt_out_kernel, dim3((unsigned)ceil_div(B, kBlock)), dim3(kBlock), 0, s, epi.raw0, epi.raw1,

@@ -200,18 +200,31 @@ def _i64s(*v):
     return (ctypes.c_int64 * len(v))(*v)
 
 
+def _a256(v):
+    return (v + 255) // 256 * 256
+
+
+def rank_lists_bytes(B, K):
+    """The forward's rank lists of one perspective: [Bpad][kpad] lists and two
+    [Bpad] int32 arrays (position, count), each 256-byte aligned; Bpad = B
+    rounded up to 32, kpad = K rounded up to 4."""
+    bp, kpad = -(-B // 32) * 32, -(-K // 4) * 4
+    return _a256(bp * kpad * 4) + 2 * _a256(bp * 4)
+
+
 def test_pair_workspace_size_and_shape_checks():
     lib = _native.lib()
     fb, bb = ctypes.c_size_t(0), ctypes.c_size_t(0)
     # HalfKAv2_hm: 24576 rows folded with 768 virtual rows, L = 1048
     rc = lib.sft_ft_pair_workspace_size(65536, 32, 1, _i64s(24576), _i64s(768), 1048, ctypes.byref(fb), ctypes.byref(bb))
     assert rc == 0, _native.last_error()
-    assert fb.value == 33 * 24577 * 32 * 4  # the merged table in 32-column tiles, each with a pad row
+    # the merged table in 32-column tiles, each with a pad row, then both perspectives' rank lists
+    assert fb.value == _a256(33 * 24577 * 32 * 4) + 2 * rank_lists_bytes(65536, 32)
     assert bb.value >= 24576 * 1048 * 4 + 33 * 65536 * 32 * 4  # tmp sums + grad tiles
     # Full_Threats + HalfKAv2_hm
     rc = lib.sft_ft_pair_workspace_size(65536, 160, 2, _i64s(60720, 24576), _i64s(0, 768), 1048, ctypes.byref(fb),
                                         ctypes.byref(bb))
-    assert rc == 0 and fb.value == 33 * 85297 * 32 * 4
+    assert rc == 0 and fb.value == _a256(33 * 85297 * 32 * 4) + 2 * rank_lists_bytes(65536, 160)
     # shapes the fused path does not take
     rc = lib.sft_ft_pair_workspace_size(65536, 32, 1, _i64s(24576), _i64s(768), 136, ctypes.byref(fb), ctypes.byref(bb))
     assert rc == _native.SFT_EUNSUPPORTED and "output_size" in _native.last_error()
@@ -260,7 +273,7 @@ def test_transform_workspace_size_and_checks():
     assert lib.sft_ft_transform_workspace_size(*args(1040)) == 0, _native.last_error()
     # paired map: 33 tiles for the 2 x 130 chunks of L1 plus one PSQT tile, 128 B per row
     # (the table tiles with one pad row each)
-    assert sb.value == 2 * 34 * 65536 * 128 and fb.value == 34 * 24577 * 128
+    assert sb.value == 2 * 34 * 65536 * 128 and fb.value == _a256(34 * 24577 * 128) + 2 * rank_lists_bytes(65536, 32)
     assert bb.value >= 2 * 34 * 65536 * 128 + 24576 * 1048 * 4
     for l1 in (1044, 1048, 0, -8):
         assert lib.sft_ft_transform_workspace_size(*args(l1)) == _native.SFT_EUNSUPPORTED

@@ -84,12 +84,16 @@ def test_fwd_unaligned_views_use_the_scalar_path():
 
 
 def test_tiled_workspace_query():
-    # 32-column tiles of N table rows and one pad row, 128 bytes per row
+    from test_abi_cpu import _a256, rank_lists_bytes
+
+    # 32-column tiles of N table rows and one pad row, 128 bytes per row, then the rank lists
     n = _native._workspace_bytes("fwd", 65536, 32, 23232, 1048, _native.SFT_FWD_AUTO, DEV)
-    assert n == 33 * 23233 * 32 * 4
-    assert _native._workspace_bytes("fwd", 65536, 32, 23232, 136, _native.SFT_FWD_AUTO, DEV) == 5 * 23233 * 32 * 4
+    assert n == _a256(33 * 23233 * 32 * 4) + rank_lists_bytes(65536, 32)
+    assert _native._workspace_bytes("fwd", 65536, 32, 23232, 136, _native.SFT_FWD_AUTO, DEV) == \
+        _a256(5 * 23233 * 32 * 4) + rank_lists_bytes(65536, 32)
     assert _native._workspace_bytes("fwd", 65536, 32, 23232, 96, _native.SFT_FWD_AUTO, DEV) == 0  # 3 tiles
-    assert _native._workspace_bytes("fwd", 65536, 32, 85296, 1048, _native.SFT_FWD_AUTO, DEV) == 33 * 85297 * 32 * 4
+    assert _native._workspace_bytes("fwd", 65536, 32, 85296, 1048, _native.SFT_FWD_AUTO, DEV) == \
+        _a256(33 * 85297 * 32 * 4) + rank_lists_bytes(65536, 32)
     assert _native._workspace_bytes("fwd", 65536, 32, 600000, 1048, _native.SFT_FWD_AUTO, DEV) == 0  # tile > 64 MiB
     assert _native._workspace_bytes("fwd", 65536, 32, 23232, 1048, _native.SFT_FWD_ROWS, DEV) == 0
 
