@@ -339,11 +339,25 @@ struct RankLists {
   int32_t *list;   // [Bpad][kpad]
   int32_t *pos;    // [Bpad] rank -> position, -1 for padding
   int32_t *count;  // [Bpad] active slots of the rank's position, non-increasing within each 256 ranks
+  i32x4 *cut;      // [Bpad] table parts (nparts > 1): see "Table parts" below
 };
 struct RankArgs {
   const int32_t *idx[2];
   RankLists L[2];
+  int nparts, part_rows;
 };
+
+// ---- table parts ----
+// A table whose 32-column tile (N + 1 rows of 128 B) is larger than an XCD's
+// L2 is gathered in nparts passes, pass p reading table rows [p part_rows,
+// (p + 1) part_rows) only.  For each position its list is cut into the runs
+// of each part, in list (= slot) order: pass p adds list[lo_p, hi_p) onto the
+// sum the previous passes left in the output, so the position's adds keep the
+// reference order -- which needs the list's parts to be non-decreasing.  A
+// position whose list goes back to an earlier part does all its adds in pass
+// 0.  cut[r] = {start of part 1, of part 2, of part 3, final pass}; lo_p =
+// (p == 0 ? 0 : cut[p - 1]), hi_p = (p == final ? count : cut[p]).
+constexpr int kMaxParts = 4;
 
 // One workgroup per 256 positions of one perspective (grid.y).  STAGE: the
 // lists are assembled in LDS (row stride kpad + 1, free of bank conflicts)
@@ -395,12 +409,25 @@ __global__ __launch_bounds__(kBlock) void rank_lists_kernel(RankArgs a, int64_t 
   int *dst = STAGE ? rows + rl * (kpad + 1) : L.list + r * kpad;
   if (STAGE || r < Bpad) {
     int j = 0;
+    int cut[kMaxParts - 1] = {c, c, c};
+    int part = 0;
+    bool mono = true;
     if (real)
       for (int k = 0; k < K; ++k) {
         const int v = slot(k);
-        if ((unsigned)v < (unsigned)N) dst[j++] = v;
+        if ((unsigned)v < (unsigned)N) {
+          if (a.nparts > 1) {
+            const int pv = v / a.part_rows;
+            mono = mono && pv >= part;
+            for (; part < pv; ++part)
+              if (part < kMaxParts - 1) cut[part] = j;
+          }
+          dst[j++] = v;
+        }
       }
     for (; j < kpad; ++j) dst[j] = N;
+    if (a.nparts > 1 && r < Bpad)
+      L.cut[r] = mono ? i32x4{cut[0], cut[1], cut[2], a.nparts - 1} : i32x4{c, c, c, 0};
   }
   if (STAGE) {
     __syncthreads();
@@ -439,7 +466,8 @@ __global__ __launch_bounds__(kBlock) void fwd_tiled_kernel(RankLists R0, RankLis
                                                            const f32x4 *__restrict__ Wt, ColMap map,
                                                            const f32x4 *__restrict__ bias, f32x4 *__restrict__ out0,
                                                            f32x4 *__restrict__ out1, FwdEpilogue epi, int kpad,
-                                                           int ntiles, int nchunks, int nchunks_p) {
+                                                           int ntiles, int nchunks, int nchunks_p, int part,
+                                                           int nparts) {
   constexpr int PPW = kWave / kTileCh;  // 8 ranks per wave
   extern __shared__ int smem[];         // 8 lists of kpad entries per wave
   TileItem it = tile_sched_item(blockIdx.x, ntiles, nchunks);
@@ -460,26 +488,58 @@ __global__ __launch_bounds__(kBlock) void fwd_tiled_kernel(RankLists R0, RankLis
 
   const int64_t r0 = rank_chunk(it.chunk, nchunks_p) * kRanksPerBlock + wave * PPW;  // the wave's first rank
   int *list = smem + wave * PPW * kpad;
-  {
-    const i32x4 *__restrict__ src = reinterpret_cast<const i32x4 *>(R.list + r0 * kpad);
-    i32x4 *dst = reinterpret_cast<i32x4 *>(list);
-    for (int j = lane; j < PPW * kpad / 4; j += kWave) dst[j] = src[j];
-  }
-  const int nmax = R.count[r0];  // counts fall with rank within each 256 ranks: the wave's longest list
   const int32_t *__restrict__ rp = R.pos + r0;
   int pos = rp[0];
 #pragma unroll
   for (int u = 1; u < PPW; ++u) pos = g == u ? rp[u] : pos;
+  int nmax, lo = 0;
+  bool work = true, final_pass = true;
+  if (nparts == 1) {  // launch-uniform: whole lists
+    const i32x4 *__restrict__ src = reinterpret_cast<const i32x4 *>(R.list + r0 * kpad);
+    i32x4 *dst = reinterpret_cast<i32x4 *>(list);
+    for (int j = lane; j < PPW * kpad / 4; j += kWave) dst[j] = src[j];
+    nmax = R.count[r0];  // counts fall with rank within each 256 ranks: the wave's longest list
+  } else {
+    // this pass's run [lo, hi) of each list (table parts, above), padded with
+    // the pad row to the wave's longest run
+    const int64_t r = r0 + g;
+    const i32x4 cv = R.cut[r];
+    const int cnt = R.count[r];
+    const int fin = cv[3];
+    final_pass = part == fin;
+    lo = part == 0 ? 0 : (part == 1 ? cv[0] : (part == 2 ? cv[1] : cv[2]));
+    const int hi = final_pass ? cnt : (part == 0 ? cv[0] : (part == 1 ? cv[1] : cv[2]));
+    work = part <= fin && (hi > lo || final_pass);
+    const int len = work ? hi - lo : 0;
+    int mx = len;
+#pragma unroll
+    for (int off = kTileCh; off < kWave; off <<= 1) mx = max(mx, __shfl_xor(mx, off));
+    nmax = uniform(mx);
+    const int32_t *__restrict__ src = R.list + r * kpad + lo;
+    int *dst = list + g * kpad;
+    for (int j = t; j < round_up4(nmax); j += kTileCh) dst[j] = j < len ? src[j] : N;
+  }
   wave_lds_barrier();
-  f32x4 acc = f32_tile_rows(list + g * kpad, nmax, tbase, lane_off, b4);
+  f32x4 start = b4;
+  f32x4 *__restrict__ raw = nullptr;
+  if (EPI) raw = (second ? epi.raw1 : epi.raw0) + ((int64_t)(pos < 0 ? 0 : pos) * ntiles + it.tile) * kTileCh + t;
+  if (lo > 0 && pos >= 0 && work) {  // the sum earlier passes left
+    if (EPI) start = *raw;
+    else if (colok) start = (second ? out1 : out0)[pos * cols4 + col4];
+  }
+  f32x4 acc = f32_tile_rows(list + g * kpad, nmax, tbase, lane_off, start);
   if (!colok) acc = f32x4{0.f, 0.f, 0.f, 0.f};  // padding lanes read unwritten chunks; their raw rows stay 0
-  if (pos < 0) return;                          // a padding rank
+  if (pos < 0 || !work) return;                 // a padding rank, or nothing to do in this pass
+  if (!final_pass) {
+    if (EPI) __builtin_nontemporal_store(acc, raw);
+    else if (colok) __builtin_nontemporal_store(acc, (second ? out1 : out0) + pos * cols4 + col4);
+    return;
+  }
   if (!EPI) {
     f32x4 *__restrict__ out = second ? out1 : out0;
     if (colok) __builtin_nontemporal_store(acc, out + pos * cols4 + col4);
   } else {
-    f32x4 *__restrict__ raw = second ? epi.raw1 : epi.raw0;
-    __builtin_nontemporal_store(acc, raw + ((int64_t)pos * ntiles + it.tile) * kTileCh + t);
+    __builtin_nontemporal_store(acc, raw);
     if (it.tile < map.t1) {  // block-uniform
       const f32x4 partner = shfl_xor4(acc, 4);
       if (t < 4 && colok) {
@@ -831,7 +891,7 @@ static int64_t rank_pad(int64_t B) { return ceil_div(B, (int64_t)kRanksPerBlock)
 // One perspective's rank lists, each array 256-byte aligned.
 size_t rank_lists_bytes(int64_t B, int K) {
   const int64_t Bp = rank_pad(B);
-  return align256((size_t)(Bp * round_up4(K)) * 4) + 2 * align256((size_t)Bp * 4);
+  return align256((size_t)(Bp * round_up4(K)) * 4) + 2 * align256((size_t)Bp * 4) + align256((size_t)Bp * 16);
 }
 static RankLists rank_lists_at(char *p, int64_t B, int K) {
   const int64_t Bp = rank_pad(B);
@@ -841,8 +901,21 @@ static RankLists rank_lists_at(char *p, int64_t B, int K) {
   r.pos = reinterpret_cast<int32_t *>(p);
   p += align256((size_t)Bp * 4);
   r.count = reinterpret_cast<int32_t *>(p);
+  p += align256((size_t)Bp * 4);
+  r.cut = reinterpret_cast<i32x4 *>(p);
   return r;
 }
+
+// Table parts of a gather over N rows (see "Table parts"): as many as keep a
+// part's tile rows within SFT_FWD_PART_BYTES, at most kMaxParts.
+#ifndef SFT_FWD_PART_BYTES
+#define SFT_FWD_PART_BYTES (7 << 19)
+#endif
+static int table_parts(int64_t N) {
+  const int64_t p = ceil_div(tile_rows(N) * (int64_t)kTileRowBytes, (int64_t)(SFT_FWD_PART_BYTES));
+  return (int)std::min<int64_t>(std::max<int64_t>(p, 1), kMaxParts);
+}
+static int part_rows_of(int64_t N, int nparts) { return (int)ceil_div(std::max<int64_t>(N, 1), nparts); }
 // LDS of the tiled gather: the 32 lists of a workgroup.
 static size_t rank_lds_bytes(int K) { return (size_t)kRanksPerBlock * round_up4(K) * sizeof(int); }
 // Lists staged in LDS up to kpad = 32 (33 KB); longer ones are stored by their threads.
@@ -850,12 +923,14 @@ constexpr int kRankStageMaxPad = 32;
 
 // Rank lists of np perspectives (idx[p] -> R[p]) in one launch.
 static int build_rank_lists(const int32_t *idx0, const int32_t *idx1, int np, int64_t B, int K, int N,
-                            const RankLists &R0, const RankLists &R1, hipStream_t s, const char *who) {
+                            const RankLists &R0, const RankLists &R1, int nparts, hipStream_t s, const char *who) {
   RankArgs a;
   a.idx[0] = idx0;
   a.idx[1] = idx1;
   a.L[0] = R0;
   a.L[1] = R1;
+  a.nparts = nparts;
+  a.part_rows = part_rows_of(N, nparts);
   const int64_t Bp = rank_pad(B);
   const int kpad = round_up4(K);
   const int vec = K % 4 == 0 && (uintptr_t)idx0 % 16 == 0 && (uintptr_t)idx1 % 16 == 0;
@@ -913,16 +988,18 @@ int fwd_f32_tiled(const int32_t *idx, int64_t B, int K, const float *W, int64_t 
   }
   int rc = check_launch("sft_ft_fwd_f32_ex (relayout)");
   if (rc != SFT_OK) return rc;
-  if ((rc = build_rank_lists(idx, idx, 1, B, K, (int)N, R, R, s, who)) != SFT_OK) return rc;
+  const int nparts = table_parts(N);
+  if ((rc = build_rank_lists(idx, idx, 1, B, K, (int)N, R, R, nparts, s, who)) != SFT_OK) return rc;
   const int nchunks = (int)(rank_pad(B) / kRanksPerBlock);
   const int64_t blocks = tile_sched_items_per_xcd(ntiles, nchunks) * kXcds;
-  {
+  for (int part = 0; part < nparts; ++part) {
     ProfScope prof(kProfFwdTiled, s);
     hipLaunchKernelGGL(fwd_tiled_kernel<false>, dim3((unsigned)blocks), dim3(kBlock), lds, s, R, R, (int)N, wt,
                        plain_map((int)cols4), reinterpret_cast<const f32x4 *>(bias), reinterpret_cast<f32x4 *>(out),
-                       reinterpret_cast<f32x4 *>(out), FwdEpilogue{}, kpad, ntiles, nchunks, nchunks);
+                       reinterpret_cast<f32x4 *>(out), FwdEpilogue{}, kpad, ntiles, nchunks, nchunks, part, nparts);
+    if ((rc = check_launch("sft_ft_fwd_f32_ex (tiled gather)")) != SFT_OK) return rc;
   }
-  return check_launch("sft_ft_fwd_f32_ex (tiled gather)");
+  return SFT_OK;
 }
 
 size_t map_tiles_workspace(const ColMap &m, int64_t rows) { return (size_t)map_tiles(m) * (size_t)rows * 128; }
@@ -957,21 +1034,23 @@ static int pair_gather(const int32_t *idx0, const int32_t *idx1, int64_t B, int 
   }
   int rc = check_launch(who);
   if (rc != SFT_OK || B == 0) return rc;
-  if ((rc = build_rank_lists(idx0, idx1, 2, B, K, (int)N, R0, R1, s, who)) != SFT_OK) return rc;
+  const int nparts = table_parts(N);
+  if ((rc = build_rank_lists(idx0, idx1, 2, B, K, (int)N, R0, R1, nparts, s, who)) != SFT_OK) return rc;
   const int nchunks_p = (int)(rank_pad(B) / kRanksPerBlock);
   const int64_t blocks = tile_sched_items_per_xcd(ntiles, 2 * nchunks_p) * kXcds;
-  {
+  for (int part = 0; part < nparts; ++part) {
     ProfScope prof(kProfFwdTiled, s);
     if (epi.l0 != nullptr)
       hipLaunchKernelGGL(fwd_tiled_kernel<true>, dim3((unsigned)blocks), dim3(kBlock), lds, s, R0, R1, (int)N, wt,
                          map, reinterpret_cast<const f32x4 *>(bias), (f32x4 *)nullptr, (f32x4 *)nullptr, epi, kpad,
-                         ntiles, 2 * nchunks_p, nchunks_p);
+                         ntiles, 2 * nchunks_p, nchunks_p, part, nparts);
     else
       hipLaunchKernelGGL(fwd_tiled_kernel<false>, dim3((unsigned)blocks), dim3(kBlock), lds, s, R0, R1, (int)N, wt,
                          map, reinterpret_cast<const f32x4 *>(bias), reinterpret_cast<f32x4 *>(out0),
-                         reinterpret_cast<f32x4 *>(out1), epi, kpad, ntiles, 2 * nchunks_p, nchunks_p);
+                         reinterpret_cast<f32x4 *>(out1), epi, kpad, ntiles, 2 * nchunks_p, nchunks_p, part, nparts);
+    if ((rc = check_launch(who)) != SFT_OK) return rc;
   }
-  return check_launch(who);
+  return SFT_OK;
 }
 
 int fwd_pair_f32(const int32_t *idx0, const int32_t *idx1, int64_t B, int K, const FoldSrc &src, int64_t N, int L,

@@ -25,8 +25,8 @@ SHAPES = [
     (10, 5, 3, 70, 12, 0, 3, False),          # K > 64: two compaction rounds
     (11, 1000, 24576, 32, 256, 0, 32, False),  # largest table the tiled gather takes; 8 tiles
     (12, 77, 900, 13, 1040, 0, 13, False),    # K = 13: four rows per ballot
-    (13, 700, 40000, 32, 1048, 16, 32, True),  # 32-column tile > 4 MB: 16-column tiles
-    (14, 300, 85296, 160, 1048, 32, 160, False),  # threat-sized table, 16-column tiles
+    (13, 700, 40000, 32, 1048, 16, 32, True),  # 32-column tile of 5.1 MB: two table parts
+    (14, 300, 85296, 160, 1048, 32, 160, False),  # threat-sized table (4 parts), unsorted rows: all in pass 0
     (15, 500, 3000, 32, 100, 0, 32, False),   # 4 tiles, the last holding one 16-byte chunk
     (16, 400, 2500, 24, 228, 8, 24, True),    # 8 tiles, the last holding one chunk
     (17, 300, 1200, 32, 96, 0, 32, False),    # 3 tiles: row gather
@@ -110,3 +110,42 @@ def test_fwd_full_workload(wid):
             out = torch.empty(w.B, w.L, device=DEV)
             _native.ft_fwd_f32(dev(d[key]), Wt, bt, out, rows=rows)
             assert np.array_equal(host(out), ref), (key, rows)
+
+
+@pytest.mark.parametrize("pair", [False, True])
+def test_fwd_table_parts_mixed_rows(pair):
+    """A table of four parts (N = 85296 rows: 10.9 MB per 32-column tile) with
+    rows whose parts rise (spread over the passes), rows that go back to an
+    earlier part (all adds in the first pass), rows inside one part, rows that
+    repeat a feature across a part boundary, empty rows and rows at the table's
+    ends -- bit-exact with the ordered oracle in every case."""
+    announce(f"fwd table parts, mixed rows, pair={pair}")
+    g = np.random.default_rng(21)
+    B, N, K, L = 3000, 85296, 160, 1048
+    part = -(-N // 4)
+    idx = workloads.make_indices(g, B, N, K, 32, 160, sort=True)
+    idx[1::7] = workloads.make_indices(g, len(idx[1::7]), N, K, 32, 160, sort=False)  # unsorted rows
+    idx[2::7, :] = -1
+    for r in range(3, B, 7):  # one part only
+        p = (r // 7) % 4
+        n = 1 + r % K
+        idx[r, :n] = np.sort(g.choice(np.arange(p * part, min(N, (p + 1) * part)), n, replace=False))
+    idx[4::7, 10:] = -1
+    idx[4::7, 9] = idx[4::7, 0]  # a repeat of the first (part 0) feature after later parts: non-monotone
+    idx[5::7, :3] = [0, part - 1, part]  # part boundary, rising
+    idx[5::7, 3:] = -1
+    idx[6::7, :4] = [N - 1, -1, N - 1, -1]  # last row twice
+    idx[6::7, 4:] = -1
+    W = (g.standard_normal((N, L)) * 0.01).astype(np.float32)
+    b = g.uniform(-0.1, 0.1, L).astype(np.float32)
+    ref = ft_oracle.fwd_f32(idx, W, b)
+    if not pair:
+        out = torch.empty(B, L, device=DEV)
+        _native.ft_fwd_f32(dev(idx), dev(W), dev(b), out)
+        assert np.array_equal(host(out), ref)
+    else:
+        o0, o1 = torch.empty(B, L, device=DEV), torch.empty(B, L, device=DEV)
+        idx1 = idx[::-1].copy()
+        _native.ft_fwd_pair_f32(dev(idx), dev(idx1), [dev(W)], [None], dev(b), o0, o1)
+        assert np.array_equal(host(o0), ref)
+        assert np.array_equal(host(o1), ft_oracle.fwd_f32(idx1, W, b))
