@@ -64,3 +64,26 @@ def test_ft_section_matches_oracle(name, l1):
     want = leb.ft_section(ft.HASH, l1, host(ft.bias), host(ft.get_export_weights()), blocks, q.ft_quantized_one,
                           q.psqt_scale)
     assert got == want
+
+
+@pytest.mark.parametrize("name,l1,mode", [("HalfKAv2_hm^", 64, "layer"), ("Full_Threats+HalfKAv2_hm^", 32, "moe"),
+                                          ("HalfKAv2_hm^", 32, "none")])
+def test_whole_nnue_file(name, l1, mode):
+    """The whole file with the FT section written on the GPU: its FT bytes are
+    the oracle's, and the header, router and FC buckets parse back to the
+    quantized layers (tests/test_nnue_writer_cpu.py checks the same layout with
+    the CPU FT section)."""
+    from nnue_model import Model
+    from test_nnue_writer_cpu import _check_file
+    from src.scripts.serialize import NNUEWriter
+
+    announce(f"whole .nnue {name} L1={l1} {mode}")
+    m = Model(name, L1=l1, count=8, stacks="none" if mode == "none" else "layer", moe=mode == "moe", device=DEV)
+    buf = bytes(NNUEWriter(m, description="gpu").buf)
+    _check_file(m, buf, mode)
+    blocks = [(int(f.NUM_REAL_FEATURES), "int8" if f.EXPORT_WEIGHT_DTYPE == torch.int8 else "int16")
+              for f in m.input.features]
+    q = m.quantization
+    want_ft = leb.ft_section(m.input.HASH, l1, host(m.input.bias), host(m.input.get_export_weights()), blocks,
+                             q.ft_quantized_one, q.psqt_scale)
+    assert buf[12 + 3:12 + 3 + len(want_ft)] == want_ft
