@@ -1076,7 +1076,9 @@ def run_fp32(args, w, dev, zipf=None, traffic=None, l2_attainable=None, graph=Tr
         log(f"[bench]   {kind:22s} {avg:8.4f} ms x {lps:.0f}/step"
             + (f"  {kern[kind]['gbs']:8.1f} GB/s algorithmic" if per_launch else "")
             + (f"  {kern[kind]['traffic_per_launch'] / 1e6:7.1f} MB traffic" if kind in kt else ""))
-    dom = max(prof, key=lambda k: prof[k][0])
+    # the roofline's kernel: the one with the most time per step among those
+    # with an algorithmic byte count (the sort and segment passes have none)
+    dom = max((k for k in prof if kern[k]["bytes_per_launch"]), key=lambda k: prof[k][0])
     dk = kern[dom]
     compulsory = workloads.step_compulsory_bytes(w.B, w.K, w.N, w.L)
     out = {

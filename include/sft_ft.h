@@ -53,6 +53,8 @@ extern "C" {
                                    order of the adds is not deterministic       */
 #define SFT_BWD_ROWS 0x2u       /* sorted algorithm with whole-row gathers only
                                    (no column tiling); same results            */
+#define SFT_BWD_PREPARED 0x20u  /* sizes: the workspace of sft_ft_bwd_f32_prepared,
+                                   without the sort the prepared buffer holds  */
 
 /* sft_ft_fwd_i16 flags */
 #define SFT_Q16_ACC32 0x0u  /* exact int32 accumulation, then clamp            */
@@ -122,6 +124,41 @@ int sft_ft_bwd_f32_workspace_size(int64_t batch, int32_t max_active, int64_t num
 int sft_ft_bwd_f32(const int32_t *idx, int64_t batch, int32_t max_active, const float *grad_out,
                    int64_t num_inputs, int32_t output_size, float *weight_grad, float *bias_grad,
                    void *workspace, size_t workspace_bytes, uint32_t flags, void *stream);
+
+/*
+ * The backward's sort, run ahead under the forward.  The sort of the slots by
+ * feature and its segment starts depend on the indices only, so
+ * sft_ft_fwd_f32_prep sorts them into a prepared buffer on a side stream while
+ * its forward kernels run (joined before it returns), and
+ * sft_ft_bwd_f32_prepared takes that buffer instead of sorting: its critical
+ * path is the bias pass and the gathers alone.  Results are those of
+ * sft_ft_fwd_f32_ex and sft_ft_bwd_f32, bit for bit.  The buffer must be
+ * filled with the same indices, sizes and backward flags that the prepared
+ * backward is called with, and is read once.
+ * No reference counterpart: the reference sorts inside the backward
+ * (FT/kernel.py:108-138), which this splits off its call
+ * (FT/functions.py:12-48 forward, :50-72 backward).
+ */
+/* Bytes of the prepared buffer: 0 when the backward sorts nothing, or when
+ * sorting under the forward would cost more than it saves (the sort grows with
+ * max_active, the backward's bias pass it would otherwise run beside with
+ * output_size: prepared from max_active >= output_size / 20).  With 0 bytes the
+ * prepared calls behave as sft_ft_fwd_f32_ex and sft_ft_bwd_f32. */
+int sft_ft_bwd_f32_prep_size(int64_t batch, int32_t max_active, int64_t num_inputs,
+                             int32_t output_size, uint32_t bwd_flags, size_t *bytes);
+/* sft_ft_fwd_f32_ex, and the backward's sort into prep (256-byte aligned). */
+int sft_ft_fwd_f32_prep(const int32_t *idx, int64_t batch, int32_t max_active, const float *weight,
+                        int64_t num_inputs, int32_t output_size, const float *bias, float *out,
+                        void *workspace, size_t workspace_bytes, uint32_t flags, void *prep,
+                        size_t prep_bytes, uint32_t bwd_flags, void *stream);
+/* sft_ft_bwd_f32 from a prepared buffer; workspace of
+ * sft_ft_bwd_f32_workspace_size(..., flags | SFT_BWD_PREPARED) bytes.  The
+ * buffer may be overwritten (a grad whose alignment rules out the tiled
+ * gather is sorted again into it, on the call's stream). */
+int sft_ft_bwd_f32_prepared(const int32_t *idx, int64_t batch, int32_t max_active,
+                            const float *grad_out, int64_t num_inputs, int32_t output_size,
+                            float *weight_grad, float *bias_grad, void *prep, size_t prep_bytes,
+                            void *workspace, size_t workspace_bytes, uint32_t flags, void *stream);
 
 /*
  * int16 quantized inference forward (no reference counterpart: the reference's

@@ -31,7 +31,10 @@ int fwd_i16_packed(const int32_t *idx0, const int32_t *idx1, int64_t B, int K, c
                    const int16_t *bias, int P, int16_t *out0, int16_t *out1, int32_t *psqt_out0, int32_t *psqt_out1,
                    int lo, int hi, int wrap16, hipStream_t s, const char *who);
 int bwd_f32(const int32_t *idx, int64_t B, int K, const float *grad, int64_t N, int L, float *dW, float *db,
-            void *ws, size_t ws_bytes, uint32_t flags, hipStream_t s);
+            void *ws, size_t ws_bytes, uint32_t flags, hipStream_t s, void *prep = nullptr, size_t prep_bytes = 0);
+int bwd_prep_bytes(int64_t B, int K, int64_t N, int L, uint32_t flags, size_t *bytes);
+int bwd_prepare(const int32_t *idx, int64_t B, int K, int64_t N, int L, uint32_t flags, void *prep,
+                size_t prep_bytes, hipStream_t s);
 size_t index_lds_bytes(int G, int K);
 int fwd_pair_f32(const int32_t *idx0, const int32_t *idx1, int64_t B, int K, const FoldSrc &src, int64_t N, int L,
                  const float *bias, float *out0, float *out1, void *ws, size_t ws_bytes, hipStream_t s);
@@ -336,9 +339,77 @@ int sft_ft_bwd_f32_workspace_size(int64_t batch, int32_t max_active, int64_t num
   if (!bytes) return fail(SFT_EINVAL, "sft_ft_bwd_f32_workspace_size: null pointer");
   if (bad_sizes(batch, max_active, num_inputs, output_size, why))
     return fail(SFT_EINVAL, "sft_ft_bwd_f32_workspace_size: " + why);
-  if (flags & ~(SFT_BWD_OVERWRITE | SFT_BWD_ATOMIC | SFT_BWD_ROWS))
+  if (flags & ~(SFT_BWD_OVERWRITE | SFT_BWD_ATOMIC | SFT_BWD_ROWS | SFT_BWD_PREPARED))
     return fail(SFT_EINVAL, "sft_ft_bwd_f32_workspace_size: unknown flags");
   return bwd_workspace(batch, max_active, num_inputs, output_size, flags, bytes);
+}
+
+int sft_ft_bwd_f32_prep_size(int64_t batch, int32_t max_active, int64_t num_inputs, int32_t output_size,
+                             uint32_t flags, size_t *bytes) {
+  clear_error();
+  std::string why;
+  if (!bytes) return fail(SFT_EINVAL, "sft_ft_bwd_f32_prep_size: null pointer");
+  if (bad_sizes(batch, max_active, num_inputs, output_size, why))
+    return fail(SFT_EINVAL, "sft_ft_bwd_f32_prep_size: " + why);
+  if (flags & ~(SFT_BWD_OVERWRITE | SFT_BWD_ATOMIC | SFT_BWD_ROWS | SFT_BWD_PREPARED))
+    return fail(SFT_EINVAL, "sft_ft_bwd_f32_prep_size: unknown flags");
+  return bwd_prep_bytes(batch, max_active, num_inputs, output_size, flags, bytes);
+}
+
+int sft_ft_fwd_f32_prep(const int32_t *idx, int64_t batch, int32_t max_active, const float *weight,
+                        int64_t num_inputs, int32_t output_size, const float *bias, float *out, void *workspace,
+                        size_t workspace_bytes, uint32_t flags, void *prep, size_t prep_bytes, uint32_t bwd_flags,
+                        void *stream) {
+  clear_error();
+  std::string why;
+  if (bad_sizes(batch, max_active, num_inputs, output_size, why)) return fail(SFT_EINVAL, "sft_ft_fwd_f32_prep: " + why);
+  if (!weight || !bias || (batch > 0 && (!idx || !out))) return fail(SFT_EINVAL, "sft_ft_fwd_f32_prep: null pointer");
+  if (flags & ~SFT_FWD_ROWS) return fail(SFT_EINVAL, "sft_ft_fwd_f32_prep: unknown flags");
+  if (bwd_flags & ~(SFT_BWD_OVERWRITE | SFT_BWD_ATOMIC | SFT_BWD_ROWS | SFT_BWD_PREPARED))
+    return fail(SFT_EINVAL, "sft_ft_fwd_f32_prep: unknown backward flags");
+  if (batch == 0) return SFT_OK;
+  size_t need = 0;
+  bwd_prep_bytes(batch, max_active, num_inputs, output_size, bwd_flags, &need);
+  if (need > 0 && (prep == nullptr || prep_bytes < need || (uintptr_t)prep % 256 != 0))
+    return fail(SFT_EWORKSPACE, "sft_ft_fwd_f32_prep: prepared buffer smaller than sft_ft_bwd_f32_prep_size() "
+                                "or not 256-byte aligned");
+  // The backward's sort needs the indices only: it runs on the side stream
+  // beside the forward's kernels and is joined before the call returns.
+  const hipStream_t s = (hipStream_t)stream;
+  if (need == 0)
+    return sft_ft_fwd_f32_ex(idx, batch, max_active, weight, num_inputs, output_size, bias, out, workspace,
+                             workspace_bytes, flags, stream);
+  hipStream_t side;
+  int rc = fork_side(s, &side);
+  if (rc != SFT_OK) return rc;
+  SideJoinGuard side_join(s);
+  if ((rc = bwd_prepare(idx, batch, max_active, num_inputs, output_size, bwd_flags, prep, prep_bytes, side)) != SFT_OK)
+    return rc;
+  const bool tiled = !(flags & SFT_FWD_ROWS) && fwd_tiled_supported(num_inputs, output_size, weight, bias, out) &&
+                     workspace != nullptr &&
+                     workspace_bytes >= fwd_tiled_workspace(batch, max_active, num_inputs, output_size);
+  rc = tiled ? fwd_f32_tiled(idx, batch, max_active, weight, num_inputs, output_size, bias, out, workspace,
+                             workspace_bytes, s)
+             : fwd_f32(idx, batch, max_active, weight, num_inputs, output_size, bias, out, s);
+  if (rc != SFT_OK) return rc;
+  side_join.release();
+  return join_side(s);
+}
+
+int sft_ft_bwd_f32_prepared(const int32_t *idx, int64_t batch, int32_t max_active, const float *grad_out,
+                            int64_t num_inputs, int32_t output_size, float *weight_grad, float *bias_grad,
+                            void *prep, size_t prep_bytes, void *workspace, size_t workspace_bytes, uint32_t flags,
+                            void *stream) {
+  clear_error();
+  std::string why;
+  if (bad_sizes(batch, max_active, num_inputs, output_size, why))
+    return fail(SFT_EINVAL, "sft_ft_bwd_f32_prepared: " + why);
+  if (!weight_grad || !bias_grad || (batch > 0 && (!idx || !grad_out)))
+    return fail(SFT_EINVAL, "sft_ft_bwd_f32_prepared: null pointer");
+  if (flags & ~(SFT_BWD_OVERWRITE | SFT_BWD_ATOMIC | SFT_BWD_ROWS | SFT_BWD_PREPARED))
+    return fail(SFT_EINVAL, "sft_ft_bwd_f32_prepared: unknown flags");
+  return bwd_f32(idx, batch, max_active, grad_out, num_inputs, output_size, weight_grad, bias_grad, workspace,
+                 workspace_bytes, flags | SFT_BWD_PREPARED, (hipStream_t)stream, prep, prep_bytes);
 }
 
 int sft_ft_bwd_f32(const int32_t *idx, int64_t batch, int32_t max_active, const float *grad_out, int64_t num_inputs,

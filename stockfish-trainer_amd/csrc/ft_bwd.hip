@@ -35,6 +35,7 @@ size_t slot_sort_workspace(int64_t M);
 int slot_sort(const int32_t *idx, int64_t M, int K, int64_t N, int chunk_rows, int nchunks, void *ws,
               unsigned **keys_sorted, int **pos_sorted, unsigned **digit_totals, int *digit_count, int *clear,
               int nclear, hipStream_t s);
+int *slot_sort_positions(int64_t M, int64_t N, int nchunks, void *ws);
 
 namespace {
 
@@ -980,7 +981,10 @@ int64_t half_rows(int64_t B) { return ceil_div(B, kBwdHalves); }
 
 // The sort and offsets buffers are sized for the tiled (chunked) key space,
 // which also covers the one-chunk key space of the row gather, so the choice
-// between the two can wait for the pointers' alignment at call time.
+// between the two can wait for the pointers' alignment at call time.  With
+// SFT_BWD_PREPARED they live in the caller's prepared buffer instead
+// (make_prep_layout) and the workspace holds the rest.
+bool prep_pays(int64_t B, int K, int L, uint32_t flags);
 int make_layout(int64_t B, int K, int64_t N, int L, uint32_t flags, BwdLayout &lay) {
   const int64_t M = B * K;
   lay.nparts = bias_parts(B);
@@ -990,10 +994,12 @@ int make_layout(int64_t B, int K, int64_t N, int L, uint32_t flags, BwdLayout &l
   lay.sort = lay.seg = lay.gt = off;
   if (!(flags & SFT_BWD_ATOMIC) && M > 0) {
     const int nc = sort_chunks(B, L, flags);
-    lay.sort = off;
-    off = align256(off + slot_sort_workspace(M));
-    lay.seg = off;
-    off = align256(off + seg_region_bytes(nc, N));
+    if (!((flags & SFT_BWD_PREPARED) && prep_pays(B, K, L, flags))) {
+      lay.sort = off;
+      off = align256(off + slot_sort_workspace(M));
+      lay.seg = off;
+      off = align256(off + seg_region_bytes(nc, N));
+    }
     lay.gt = off;
     if (tiled_shape(B, L, flags)) {  // the grad tiles the bias pass writes, whatever the chunk count
       const int64_t ntiles = ceil_div(L / 4, kBwdTileCh);
@@ -1058,7 +1064,72 @@ int launch_segments(const unsigned *keys, int64_t M, int nc, int64_t nfeat, cons
   return check_launch("segment offsets");
 }
 
+// The prepared buffer: the sort's workspace, then the segment region of the
+// tiled key space (nc chunks); empty when the backward sorts nothing or when
+// sorting under the forward does not pay.  Beside the backward's bias pass the
+// sort costs only what it outlasts that pass; beside the forward's gather it
+// slows the gather (workload 1, K = 32, L = 1048: the forward +17 us, the
+// backward -12 us per perspective).  The sort grows with the slots, the bias
+// pass with the columns: the sort is prepared from K >= L / 20 (L = 136:
+// step 0.530 -> 0.504 ms; L = 1048, K = 160: the K = 160 sort outlasts the
+// bias pass by ~180 us).
+#ifndef SFT_BWD_PREP_K_PER_L
+#define SFT_BWD_PREP_K_PER_L 20
+#endif
+bool prep_pays(int64_t B, int K, int L, uint32_t flags) {
+  return !(flags & SFT_BWD_ATOMIC) && B * K > 0 && (int64_t)K * SFT_BWD_PREP_K_PER_L >= L;
+}
+struct PrepLayout {
+  size_t sort, seg, total;
+  int nc;
+};
+void make_prep_layout(int64_t B, int K, int64_t N, int L, uint32_t flags, PrepLayout &p) {
+  const int64_t M = B * K;
+  p.nc = sort_chunks(B, L, flags);
+  p.sort = p.seg = p.total = 0;
+  if (!prep_pays(B, K, L, flags)) return;
+  p.seg = align256(slot_sort_workspace(M));
+  p.total = p.seg + align256(seg_region_bytes(p.nc, N));
+}
+
+// Sort of the slots into nc position chunks and their segment starts, on s.
+int sort_and_segments(const int32_t *idx, int64_t B, int K, int64_t N, int nc, void *sort_ws, int32_t *seg,
+                      int32_t **pos, hipStream_t s) {
+  const int64_t M = B * K;
+  const SegBufs sb = seg_bufs(seg, nc, N);
+  unsigned *keys = nullptr, *totals = nullptr;
+  int ntot = 0, rc;
+  {
+    ProfScope prof(kProfBwdSort, s);
+    if ((rc = slot_sort(idx, M, K, N, (int)(nc > 1 ? half_rows(B) : B), nc, sort_ws, &keys, pos, &totals, &ntot,
+                        sb.count, nc, s)) != SFT_OK)
+      return rc;
+  }
+  return launch_segments(keys, M, nc, N, totals, ntot, sb, s);
+}
+
 }  // namespace
+
+int bwd_prep_bytes(int64_t B, int K, int64_t N, int L, uint32_t flags, size_t *bytes) {
+  PrepLayout p;
+  make_prep_layout(B, K, N, L, flags, p);
+  *bytes = p.total;
+  return SFT_OK;
+}
+
+// Fills a prepared buffer for a later bwd_f32 with SFT_BWD_PREPARED and the
+// same indices, sizes and flags.
+int bwd_prepare(const int32_t *idx, int64_t B, int K, int64_t N, int L, uint32_t flags, void *prep,
+                size_t prep_bytes, hipStream_t s) {
+  PrepLayout p;
+  make_prep_layout(B, K, N, L, flags, p);
+  if (p.total == 0) return SFT_OK;
+  if (prep == nullptr || prep_bytes < p.total || (uintptr_t)prep % 256 != 0)
+    return fail(SFT_EWORKSPACE, "prepared buffer smaller than sft_ft_bwd_f32_prep_size() or not 256-byte aligned");
+  char *w = static_cast<char *>(prep);
+  int32_t *pos = nullptr;
+  return sort_and_segments(idx, B, K, N, p.nc, w + p.sort, reinterpret_cast<int32_t *>(w + p.seg), &pos, s);
+}
 
 int bwd_workspace(int64_t B, int K, int64_t N, int L, uint32_t flags, size_t *bytes) {
   BwdLayout lay;
@@ -1069,7 +1140,7 @@ int bwd_workspace(int64_t B, int K, int64_t N, int L, uint32_t flags, size_t *by
 }
 
 int bwd_f32(const int32_t *idx, int64_t B, int K, const float *grad, int64_t N, int L, float *dW, float *db,
-            void *ws, size_t ws_bytes, uint32_t flags, hipStream_t s) {
+            void *ws, size_t ws_bytes, uint32_t flags, hipStream_t s, void *prep, size_t prep_bytes) {
   BwdLayout lay;
   int rc = make_layout(B, K, N, L, flags, lay);
   if (rc != SFT_OK) return rc;
@@ -1089,25 +1160,30 @@ int bwd_f32(const int32_t *idx, int64_t B, int K, const float *grad, int64_t N, 
   // ---- sort of the slots and their segments: they need only the indices, so
   // they run on the side stream while the bias pass streams the grad ----
   const bool sorted = !(flags & SFT_BWD_ATOMIC) && M > 0;
+  const bool prepared = (flags & SFT_BWD_PREPARED) && prep_pays(B, K, L, flags);
   const int nc = tiled ? sort_chunks(B, L, flags) : 1;
   int32_t *seg = reinterpret_cast<int32_t *>(w + lay.seg);
-  const SegBufs sb = seg_bufs(seg, nc, N);
-  unsigned *keys = nullptr, *totals = nullptr;
   int32_t *pos = nullptr;
-  int ntot = 0;
   std::optional<SideJoinGuard> side_join;  // joins the side stream on every early return
-  if (sorted) {
+  if (sorted && prepared) {
+    PrepLayout pl;
+    make_prep_layout(B, K, N, L, flags, pl);
+    if (prep == nullptr || prep_bytes < pl.total || (uintptr_t)prep % 256 != 0)
+      return fail(SFT_EWORKSPACE, "prepared buffer smaller than sft_ft_bwd_f32_prep_size() or not 256-byte aligned");
+    char *pw = static_cast<char *>(prep);
+    seg = reinterpret_cast<int32_t *>(pw + pl.seg);
+    if (nc == pl.nc) {
+      pos = slot_sort_positions(M, N, nc, pw + pl.sort);
+    } else if ((rc = sort_and_segments(idx, B, K, N, nc, pw + pl.sort, seg, &pos, s)) != SFT_OK) {
+      return rc;  // the grad's alignment rules out the tiled gather: sorted again for one chunk
+    }
+  } else if (sorted) {
     hipStream_t side;
     if ((rc = fork_side(s, &side)) != SFT_OK) return rc;
     side_join.emplace(s);
-    {
-      ProfScope prof(kProfBwdSort, side);
-      if ((rc = slot_sort(idx, M, K, N, (int)(nc > 1 ? half_rows(B) : B), nc, w + lay.sort, &keys, &pos, &totals,
-                          &ntot, sb.count, nc, side)) != SFT_OK)
-        return rc;
-    }
-    if ((rc = launch_segments(keys, M, nc, N, totals, ntot, sb, side)) != SFT_OK) return rc;
+    if ((rc = sort_and_segments(idx, B, K, N, nc, w + lay.sort, seg, &pos, side)) != SFT_OK) return rc;
   }
+  const SegBufs sb = seg_bufs(seg, nc, N);
 
   // ---- bias grad ----
   {
@@ -1119,7 +1195,7 @@ int bwd_f32(const int32_t *idx, int64_t B, int K, const float *grad, int64_t N, 
                                 s)) != SFT_OK)
       return rc;
   }
-  if (sorted) {
+  if (side_join) {
     if ((rc = join_side(s)) != SFT_OK) return rc;
     side_join->release();
   }

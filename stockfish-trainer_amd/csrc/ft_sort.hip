@@ -306,6 +306,26 @@ size_t slot_sort_workspace(int64_t M) {
   return 4 * align256((size_t)M * 4) + align256((size_t)(kMaxRadix * ntiles) * 4) + align256(kMaxRadix * 4);
 }
 
+// Digit width and pass count for keys below nkeys: 9-bit digits when they
+// save a pass.
+static void sort_passes(int64_t nkeys, int &rb, int &passes) {
+  const unsigned bits = key_bits(nkeys - 1 > 0 ? nkeys - 1 : 1);  // real keys < nkeys
+  rb = 8;
+  passes = (int)ceil_div(bits, 8);
+  if (passes > 1 && ceil_div(bits, 9) < passes) {
+    rb = 9;
+    passes = (int)ceil_div(bits, 9);
+  }
+}
+
+// Where slot_sort leaves the sorted positions in its workspace.
+int *slot_sort_positions(int64_t M, int64_t N, int nchunks, void *ws) {
+  int rb, passes;
+  sort_passes((int64_t)nchunks * N, rb, passes);
+  const size_t a = align256((size_t)M * 4);
+  return reinterpret_cast<int *>(static_cast<char *>(ws) + (((passes - 1) & 1) ? 3 * a : a));
+}
+
 int slot_sort(const int32_t *idx, int64_t M, int K, int64_t N, int chunk_rows, int nchunks, void *ws,
               unsigned **keys_sorted, int **pos_sorted, unsigned **digit_totals, int *digit_count, int *clear,
               int nclear, hipStream_t s) {
@@ -320,12 +340,8 @@ int slot_sort(const int32_t *idx, int64_t M, int K, int64_t N, int chunk_rows, i
   unsigned *totals = reinterpret_cast<unsigned *>(w + 4 * a + align256((size_t)(kMaxRadix * max_tiles) * 4));
   const unsigned nkeys = (unsigned)((int64_t)nchunks * N);
   const SlotKey sk{idx, (unsigned)N, FastDiv((uint32_t)K), FastDiv((uint32_t)chunk_rows), nkeys};
-  const unsigned bits = key_bits((int64_t)nkeys - 1 > 0 ? (int64_t)nkeys - 1 : 1);  // real keys < nkeys
-  int rb = 8, passes = (int)ceil_div(bits, 8);
-  if (passes > 1 && ceil_div(bits, 9) < passes) {
-    rb = 9;
-    passes = (int)ceil_div(bits, 9);
-  }
+  int rb, passes;
+  sort_passes(nkeys, rb, passes);
   int rc;
   if (big)
     rc = rb == 9 ? run_passes<9, kSortItemsBig>(sk, M, passes, kbuf, vbuf, hist, totals, ntiles, clear, nclear, s)

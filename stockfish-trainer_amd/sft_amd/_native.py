@@ -28,6 +28,7 @@ SFT_BWD_OVERWRITE = 0x1
 SFT_BWD_SORTED = 0x00
 SFT_BWD_ATOMIC = 0x10
 SFT_BWD_ROWS = 0x2
+SFT_BWD_PREPARED = 0x20
 SFT_Q16_ACC32 = 0x0
 SFT_Q16_WRAP16 = 0x1
 SFT_Q16_ROWS = 0x2
@@ -52,6 +53,14 @@ SIGNATURES = {
         ctypes.c_int, [_i64, _i32, _i64, _i32, _u32, ctypes.POINTER(ctypes.c_size_t)]),
     "sft_ft_bwd_f32": (
         ctypes.c_int, [_vp, _i64, _i32, _vp, _i64, _i32, _vp, _vp, _vp, ctypes.c_size_t, _u32, _vp]),
+    "sft_ft_bwd_f32_prep_size": (
+        ctypes.c_int, [_i64, _i32, _i64, _i32, _u32, ctypes.POINTER(ctypes.c_size_t)]),
+    "sft_ft_fwd_f32_prep": (
+        ctypes.c_int,
+        [_vp, _i64, _i32, _vp, _i64, _i32, _vp, _vp, _vp, ctypes.c_size_t, _u32, _vp, ctypes.c_size_t, _u32, _vp]),
+    "sft_ft_bwd_f32_prepared": (
+        ctypes.c_int,
+        [_vp, _i64, _i32, _vp, _i64, _i32, _vp, _vp, _vp, ctypes.c_size_t, _vp, ctypes.c_size_t, _u32, _vp]),
     "sft_ft_fwd_i16": (
         ctypes.c_int,
         [_vp, _i64, _i32, _vp, _i64, _i32, _vp, _vp, _i32, _vp, _vp, _i32, _i32, _u32, _vp]),
@@ -191,16 +200,35 @@ def ft_fwd_f32(idx: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor, out:
 _ws_cache: dict = {}
 
 
+_SIZE_FNS = {"fwd": "sft_ft_fwd_f32_workspace_size", "bwd": "sft_ft_bwd_f32_workspace_size",
+             "prep": "sft_ft_bwd_f32_prep_size"}
+
+
 def _workspace_bytes(which: str, B: int, K: int, N: int, L: int, flags: int, device: torch.device) -> int:
+    """Bytes of the forward or backward workspace, or of the backward's prepared
+    sort ("prep"); a host-only computation, cached per shape."""
     key = (which, device.index, B, K, N, L, flags)
     got = _ws_cache.get(key)
     if got is None:
         n = ctypes.c_size_t(0)
-        fn = lib().sft_ft_fwd_f32_workspace_size if which == "fwd" else lib().sft_ft_bwd_f32_workspace_size
-        with torch.cuda.device(device):
-            _check(fn(B, K, N, L, flags, ctypes.byref(n)), f"sft_ft_{which}_f32_workspace_size")
+        name = _SIZE_FNS[which]
+        _check(getattr(lib(), name)(B, K, N, L, flags, ctypes.byref(n)), name)
         got = _ws_cache[key] = int(n.value)
     return got
+
+
+def prep_buffer_bytes(B: int, K: int, N: int, L: int, flags: int, device: torch.device) -> int:
+    """Size of the uint8 tensor ft_fwd_f32_prep returns: the prepared sort plus
+    room to align it to 256 bytes (0 when the backward sorts nothing)."""
+    n = _workspace_bytes("prep", B, K, N, L, flags, device)
+    return n + 256 if n else 0
+
+
+def _aligned(buf: torch.Tensor):
+    if buf.numel() == 0:
+        return None, 0
+    off = (-buf.data_ptr()) % 256
+    return ctypes.c_void_p(buf.data_ptr() + off), buf.numel() - off
 
 
 def bwd_workspace_bytes(B: int, K: int, N: int, L: int, flags: int, device: torch.device) -> int:
@@ -231,6 +259,51 @@ def ft_bwd_f32(idx: torch.Tensor, weight_grad: torch.Tensor, bias_grad: torch.Te
     with torch.cuda.device(idx.device):
         _check(lib().sft_ft_bwd_f32(_ptr(idx), B, K, _ptr(grad_out), N, L, _ptr(weight_grad), _ptr(bias_grad),
                                     ptr, nbytes, flags, _stream(idx.device)), "sft_ft_bwd_f32")
+    del ws
+
+
+def ft_fwd_f32_prep(idx: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor, out: torch.Tensor,
+                    bwd_flags: int = SFT_BWD_OVERWRITE) -> torch.Tensor:
+    """ft_fwd_f32, and the backward's sort of idx run beside it: returns the
+    prepared buffer for ft_bwd_f32_prepared with the same idx, sizes and flags."""
+    _require(idx.dim() == 2 and idx.dtype == torch.int32, "idx must be int32 [B, K]")
+    _require(weight.dim() == 2 and weight.dtype == torch.float32, "weight must be float32 [N, L]")
+    B, K = idx.shape
+    N, L = weight.shape
+    _require(bias.shape == (L,) and bias.dtype == torch.float32, "bias must be float32 [L]")
+    _require(out.shape == (B, L) and out.dtype == torch.float32, "out must be float32 [B, L]")
+    _on_gpu(idx.device, idx, weight, bias, out)
+    prep = torch.empty(prep_buffer_bytes(B, K, N, L, bwd_flags, idx.device), dtype=torch.uint8, device=idx.device)
+    pptr, pbytes = _aligned(prep)
+    nbytes = _workspace_bytes("fwd", B, K, N, L, SFT_FWD_AUTO, idx.device)
+    ws, ptr = _workspace(nbytes, idx.device)
+    with torch.cuda.device(idx.device):
+        _check(lib().sft_ft_fwd_f32_prep(_ptr(idx), B, K, _ptr(weight), N, L, _ptr(bias), _ptr(out), ptr, nbytes,
+                                         SFT_FWD_AUTO, pptr, pbytes, bwd_flags, _stream(idx.device)),
+               "sft_ft_fwd_f32_prep")
+    del ws
+    return prep
+
+
+def ft_bwd_f32_prepared(idx: torch.Tensor, weight_grad: torch.Tensor, bias_grad: torch.Tensor,
+                        grad_out: torch.Tensor, prep: torch.Tensor, flags: int = SFT_BWD_OVERWRITE) -> None:
+    """ft_bwd_f32 from the buffer ft_fwd_f32_prep returned for the same idx and flags."""
+    _require(idx.dim() == 2 and idx.dtype == torch.int32, "idx must be int32 [B, K]")
+    _require(weight_grad.dim() == 2 and weight_grad.dtype == torch.float32, "weight_grad must be float32 [N, L]")
+    B, K = idx.shape
+    N, L = weight_grad.shape
+    _require(bias_grad.shape == (L,) and bias_grad.dtype == torch.float32, "bias_grad must be float32 [L]")
+    _require(grad_out.shape == (B, L) and grad_out.dtype == torch.float32, "grad_out must be float32 [B, L]")
+    _require(prep.dtype == torch.uint8 and prep.numel() == prep_buffer_bytes(B, K, N, L, flags, idx.device),
+             "prep must be the buffer ft_fwd_f32_prep returned for these sizes and flags")
+    _on_gpu(idx.device, idx, weight_grad, bias_grad, grad_out, prep)
+    pptr, pbytes = _aligned(prep)
+    nbytes = bwd_workspace_bytes(B, K, N, L, flags | SFT_BWD_PREPARED, idx.device)
+    ws, ptr = _workspace(nbytes, idx.device)
+    with torch.cuda.device(idx.device):
+        _check(lib().sft_ft_bwd_f32_prepared(_ptr(idx), B, K, _ptr(grad_out), N, L, _ptr(weight_grad),
+                                             _ptr(bias_grad), pptr, pbytes, ptr, nbytes, flags, _stream(idx.device)),
+               "sft_ft_bwd_f32_prepared")
     del ws
 
 

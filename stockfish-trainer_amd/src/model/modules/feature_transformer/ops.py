@@ -21,36 +21,43 @@ from torch import Tensor
 
 from sft_amd import _native
 
-from .kernel import make_sparse_input_linear_backward_kernel, make_sparse_input_linear_forward_kernel
 
 
 # ---- SparseLinearFunction (FT/functions.py:12-72) ----
+# The forward also sorts the indices for the backward (the sort needs nothing
+# else), on a side stream beside its gather, into a buffer the autograd
+# Function keeps until its backward: the backward then runs the bias pass and
+# the gathers only.  The reference sorts inside the backward (FT/kernel.py:108-138).
 @torch.library.custom_op("sft::sparse_linear_fwd", mutates_args=(), device_types="cuda")
-def sparse_linear_fwd(feature_indices: Tensor, weight: Tensor, bias: Tensor) -> Tensor:
+def sparse_linear_fwd(feature_indices: Tensor, weight: Tensor, bias: Tensor) -> tuple[Tensor, Tensor]:
     out = torch.empty(feature_indices.shape[0], weight.shape[1], dtype=torch.float32, device=feature_indices.device)
-    make_sparse_input_linear_forward_kernel(feature_indices.shape[1], weight.shape[1])(feature_indices, weight, bias,
-                                                                                        out)
-    return out
+    prep = _native.ft_fwd_f32_prep(feature_indices, weight, bias, out, _native.SFT_BWD_OVERWRITE)
+    return out, prep
 
 
 @sparse_linear_fwd.register_fake
 def _(feature_indices, weight, bias):
-    return feature_indices.new_empty((feature_indices.shape[0], weight.shape[1]), dtype=torch.float32)
+    B, K = feature_indices.shape
+    N, L = weight.shape
+    nbytes = _native.prep_buffer_bytes(B, K, N, L, _native.SFT_BWD_OVERWRITE, feature_indices.device)
+    return (feature_indices.new_empty((B, L), dtype=torch.float32),
+            feature_indices.new_empty((nbytes,), dtype=torch.uint8))
 
 
 @torch.library.custom_op("sft::sparse_linear_bwd", mutates_args=(), device_types="cuda")
-def sparse_linear_bwd(feature_indices: Tensor, grad_output: Tensor, num_inputs: int) -> tuple[Tensor, Tensor]:
+def sparse_linear_bwd(feature_indices: Tensor, grad_output: Tensor, num_inputs: int,
+                      prep: Tensor) -> tuple[Tensor, Tensor]:
     L = grad_output.shape[1]
     dev = feature_indices.device
     weight_grad = torch.empty(num_inputs, L, dtype=torch.float32, device=dev)
     bias_grad = torch.empty(L, dtype=torch.float32, device=dev)
-    make_sparse_input_linear_backward_kernel(feature_indices.shape[1], L)(
-        feature_indices, weight_grad, bias_grad, grad_output, accumulate=False)
+    _native.ft_bwd_f32_prepared(feature_indices, weight_grad, bias_grad, grad_output, prep,
+                                _native.SFT_BWD_OVERWRITE)
     return weight_grad, bias_grad
 
 
 @sparse_linear_bwd.register_fake
-def _(feature_indices, grad_output, num_inputs):
+def _(feature_indices, grad_output, num_inputs, prep):
     L = grad_output.shape[1]
     return grad_output.new_empty((num_inputs, L)), grad_output.new_empty((L,))
 

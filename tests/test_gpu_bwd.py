@@ -202,3 +202,61 @@ def test_atomic_bwd_full_workload(wid):
     _native.ft_bwd_f32(dev(idx), dW, db, dev(G), _native.SFT_BWD_OVERWRITE | _native.SFT_BWD_ATOMIC)
     r64, _ = ft_oracle.bwd_f64(idx, G, w.N)
     assert dw_rel_err(host(dW), r64) <= 1e-4
+
+
+def _prepared(idx, G, N, W=None, grad_offset=0):
+    """The forward with the backward's sort beside it, then the prepared
+    backward; grad_offset > 0 passes the grad as an unaligned view."""
+    B, L = G.shape
+    W = np.zeros((N, L), np.float32) if W is None else W
+    out = torch.empty(B, L, device=DEV)
+    i = dev(idx)
+    prep = _native.ft_fwd_f32_prep(i, dev(W), torch.zeros(L, device=DEV), out, _native.SFT_BWD_OVERWRITE)
+    if grad_offset:
+        big = torch.zeros(B * L + grad_offset, device=DEV)
+        big[grad_offset:] = dev(G).view(-1)
+        g = big[grad_offset:].view(B, L)
+    else:
+        g = dev(G)
+    dW = torch.full((N, L), float("nan"), device=DEV)
+    db = torch.full((L,), float("nan"), device=DEV)
+    _native.ft_bwd_f32_prepared(i, dW, db, g, prep, _native.SFT_BWD_OVERWRITE)
+    return host(out), host(dW), host(db)
+
+
+@pytest.mark.parametrize("seed,B,N,K,L,lo,hi,sort", SHAPES)
+def test_prepared_bwd_matches_the_backward(seed, B, N, K, L, lo, hi, sort):
+    """Sorting under the forward changes nothing: the forward and the prepared
+    backward are bit-identical to the ordinary calls (tiled and row gathers, one
+    and two position chunks, long segments)."""
+    announce(f"prepared bwd seed={seed} B={B} N={N} K={K} L={L}")
+    idx, W, b, G = case(seed, B, N, K, L, lo, hi, sort)
+    out, dW, db = _prepared(idx, G, N, W)
+    assert np.array_equal(out, ft_oracle.fwd_f32(idx, W, np.zeros(L, np.float32)))
+    dW0, db0 = run_bwd(idx, G, N, _native.SFT_BWD_OVERWRITE)
+    assert np.array_equal(dW, dW0)
+    assert np.array_equal(db, db0)
+
+
+@pytest.mark.parametrize("B,L", [(40000, 256), (3000, 256)])
+def test_prepared_bwd_unaligned_grad_sorts_again(B, L):
+    """A grad view that is not 16-byte aligned rules out the tiled gather, whose
+    sort (two position chunks at B = 40000) the forward prepared (K = 32 >= L /
+    20): the backward sorts again for one chunk into the same buffer and still
+    matches the reference order."""
+    announce(f"prepared bwd, unaligned grad B={B} L={L}")
+    idx, W, b, G = case(31, B, 900, 32, L, 0, 32, True)
+    assert _native.prep_buffer_bytes(B, 32, 900, L, _native.SFT_BWD_OVERWRITE, DEV) > 0
+    _, dW, db = _prepared(idx, G, 900, grad_offset=1)
+    ref, _ = ft_oracle.bwd_f32(idx, G, 900)
+    assert np.array_equal(dW, ref)
+    assert rel_err(db, G.astype(np.float64).sum(0)) <= 1e-5
+
+
+def test_prepared_bwd_no_active_slots():
+    announce("prepared bwd, every slot inactive")
+    idx = np.full((50, 8), -1, np.int32)
+    G = np.random.default_rng(4).standard_normal((50, 64)).astype(np.float32)
+    _, dW, db = _prepared(idx, G, 30)
+    assert not dW.any()
+    assert rel_err(db, G.astype(np.float64).sum(0)) <= 1e-5
