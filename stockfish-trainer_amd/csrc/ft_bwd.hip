@@ -72,20 +72,26 @@ __host__ __device__ inline bool long_segment(int64_t s0, int64_t s1) { return sf
 // Segment starts and the lists of long segments of one sort: seg[0 .. nc N]
 // (nc position chunks of nfeat features), then per chunk c a list of its long
 // features (list + c nfeat, count[c] entries; listed in no particular order).
+// After them, 16-byte aligned: pos16[i] = the i-th sorted slot's position as an
+// offset from its position chunk's first position (M entries), the stream the
+// tiled gather stages (half the bytes of the positions themselves).
 struct SegBufs {
   int32_t *seg, *list;
   int *count;
+  uint16_t *pos16;
 };
-inline size_t seg_region_bytes(int nc, int64_t nfeat) {
-  return (size_t)(2 * nc * nfeat + 1 + nc) * sizeof(int32_t);
+inline size_t seg_ints(int nc, int64_t nfeat) { return (size_t)(2 * nc * nfeat + 1 + nc); }
+inline size_t seg_region_bytes(int nc, int64_t nfeat, int64_t M) {
+  return (seg_ints(nc, nfeat) * sizeof(int32_t) + 15) / 16 * 16 + (size_t)M * sizeof(uint16_t) + 16;
 }
 inline SegBufs seg_bufs(void *base, int nc, int64_t nfeat) {
   int32_t *seg = static_cast<int32_t *>(base);
-  return SegBufs{seg, seg + nc * nfeat + 1, seg + 2 * nc * nfeat + 1};
+  char *p16 = static_cast<char *>(base) + (seg_ints(nc, nfeat) * sizeof(int32_t) + 15) / 16 * 16;
+  return SegBufs{seg, seg + nc * nfeat + 1, seg + 2 * nc * nfeat + 1, reinterpret_cast<uint16_t *>(p16)};
 }
 
 // seg_start[k] for k in [0, N]: index of the first sorted key >= k, N = key
-// count.  The sorted array holds the active slots only; their number is the
+// count; with pos16, also each slot's 16-bit chunk offset (SegBufs).  The sorted array holds the active slots only; their number is the
 // sum of the sort's last digit totals (read here, on the device, once per
 // workgroup by one wave).  Grid-stride over the sorted slots.  Long segments
 // are appended to their chunk's list (key = chunk * nfeat + feature; the
@@ -94,7 +100,9 @@ __global__ __launch_bounds__(kBlock) void seg_offsets_kernel(const unsigned *__r
                                                              const unsigned *__restrict__ totals, int ntot,
                                                              int32_t *__restrict__ seg_start, int64_t nfeat,
                                                              int32_t *__restrict__ long_list,
-                                                             int *__restrict__ long_count) {
+                                                             int *__restrict__ long_count,
+                                                             const int32_t *__restrict__ pos,
+                                                             uint16_t *__restrict__ pos16, int chunk_rows) {
   __shared__ unsigned s_active;
   if (threadIdx.x < kWave) {
     unsigned v = 0;
@@ -108,6 +116,7 @@ __global__ __launch_bounds__(kBlock) void seg_offsets_kernel(const unsigned *__r
   for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i <= M; i += (int64_t)gridDim.x * kBlock) {
     const int64_t cur = i < M ? (int64_t)keys[i] : N + 1;
     const int64_t prev = i > 0 ? (int64_t)keys[i - 1] : -1;
+    if (pos16 != nullptr && i < M) pos16[i] = (uint16_t)(pos[i] - (int)(cur / nfeat) * chunk_rows);
     const int64_t hi = cur < N ? cur : N;
     for (int64_t f = prev + 1; f <= hi; ++f) seg_start[f] = (int32_t)i;
     if (long_listed_at(keys, M, i, kLongSeg)) {
@@ -416,8 +425,8 @@ constexpr int kBwdPosLds = SFT_BWD_POS_LDS;  // staged positions per workgroup
 // loads, padding lanes of the last tile included (a tile holds all TCH chunks
 // of each row; the caller does not store a padding lane's sum), so the loads
 // carry no execution masks.
-template <bool FROM_LDS, int TCH>
-__device__ __forceinline__ void bwd_tile_sum(const int32_t *list, int n, int nmin, int nmax, int t,
+template <bool FROM_LDS, int TCH, typename P>
+__device__ __forceinline__ void bwd_tile_sum(const P *list, int n, int nmin, int nmax, int t,
                                              const char *__restrict__ gtile, f32x4 &acc) {
   const uint32_t lane_off = (uint32_t)t * (uint32_t)sizeof(f32x4);
   auto row = [&](int b) {
@@ -429,9 +438,9 @@ __device__ __forceinline__ void bwd_tile_sum(const int32_t *list, int n, int nmi
     int b[U];
     if (FROM_LDS) {
 #pragma unroll
-      for (int u = 0; u < U; ++u) b[u] = list[k + u];
+      for (int u = 0; u < U; ++u) b[u] = (int)list[k + u];
     } else {
-      const int mine = list[k + t];
+      const int mine = (int)list[k + t];
 #pragma unroll
       for (int u = 0; u < U; ++u) b[u] = __shfl(mine, u, TCH);
     }
@@ -445,9 +454,9 @@ __device__ __forceinline__ void bwd_tile_sum(const int32_t *list, int n, int nmi
     int b[U];
     if (FROM_LDS) {
 #pragma unroll
-      for (int u = 0; u < U; ++u) b[u] = (k + u < n) ? list[k + u] : 0;
+      for (int u = 0; u < U; ++u) b[u] = (k + u < n) ? (int)list[k + u] : 0;
     } else {
-      const int mine = (k + t < n) ? list[k + t] : 0;
+      const int mine = (k + t < n) ? (int)list[k + t] : 0;
 #pragma unroll
       for (int u = 0; u < U; ++u) b[u] = __shfl(mine, u, TCH);
     }
@@ -503,9 +512,11 @@ __host__ __device__ inline GatherLds gather_lds(int src_mode, int dst_mode) {
   return l;
 }
 
-template <bool NT>
+template <bool NT, bool P16>
 __global__ __launch_bounds__(kBlock) void bwd_tiled_gather_kernel(const int32_t *__restrict__ seg,
-                                                                  const int32_t *__restrict__ sorted_pos, int64_t N,
+                                                                  const int32_t *__restrict__ sorted_pos,
+                                                                  const uint16_t *__restrict__ pos16, int chunk_base,
+                                                                  int64_t N,
                                                                   const f32x4 *__restrict__ gt, int64_t B,
                                                                   ColMap map, RowDst dst, f32x4 *__restrict__ tmp,
                                                                   int src_mode, int dst_mode, int ntiles, int ngroups,
@@ -550,15 +561,18 @@ __global__ __launch_bounds__(kBlock) void bwd_tiled_gather_kernel(const int32_t 
   if (wave == 0) la = seg[fb + (lane < nf ? lane : nf)];
 
   // round 2: positions, start rows, plus rows.  The range is copied in
-  // 16-byte pieces from r0 rounded down to a multiple of 4 (sorted_pos is
-  // 16-byte aligned and its buffer is padded to 256 bytes), so spos[j] holds
-  // sorted_pos[ra + j].
-  const int ra = r0 & ~3;
-  const int cnt4 = (r1 - ra + 3) >> 2;               // 16-byte pieces
-  const bool staged = cnt4 * 4 <= kBwdPosLds;         // block-uniform
+  // 16-byte pieces from r0 rounded down to a piece boundary (the position
+  // streams are 16-byte aligned and padded by 16 bytes), so spos[j] holds
+  // entry ra + j: from the 16-bit chunk offsets (P16: eight per piece, widened
+  // to ints in LDS), else from the positions (four per piece).
+  constexpr int PER = P16 ? 8 : 4;  // entries per 16-byte piece
+  const int ra = r0 & ~(PER - 1);
+  const int cnt4 = (r1 - ra + PER - 1) / PER;           // 16-byte pieces
+  const bool staged = cnt4 * PER <= kBwdPosLds;         // block-uniform
   if (staged) {
     constexpr int U = 4;
-    const i32x4 *src = reinterpret_cast<const i32x4 *>(sorted_pos + ra);
+    const i32x4 *src = P16 ? reinterpret_cast<const i32x4 *>(pos16 + ra)
+                           : reinterpret_cast<const i32x4 *>(sorted_pos + ra);
     i32x4 *dst4 = reinterpret_cast<i32x4 *>(spos);
     for (int b0 = 0; b0 < cnt4; b0 += U * kBlock) {
       i32x4 v[U];
@@ -570,7 +584,14 @@ __global__ __launch_bounds__(kBlock) void bwd_tiled_gather_kernel(const int32_t 
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int i = b0 + u * kBlock + tid;
-        if (i < cnt4) dst4[i] = v[u];
+        if (i >= cnt4) continue;
+        if (P16) {
+          const uint32_t w0 = (uint32_t)v[u][0], w1 = (uint32_t)v[u][1], w2 = (uint32_t)v[u][2], w3 = (uint32_t)v[u][3];
+          dst4[2 * i] = i32x4{(int)(w0 & 0xffffu), (int)(w0 >> 16), (int)(w1 & 0xffffu), (int)(w1 >> 16)};
+          dst4[2 * i + 1] = i32x4{(int)(w2 & 0xffffu), (int)(w2 >> 16), (int)(w3 & 0xffffu), (int)(w3 >> 16)};
+        } else {
+          dst4[i] = v[u];
+        }
       }
     }
   }
@@ -621,8 +642,9 @@ __global__ __launch_bounds__(kBlock) void bwd_tiled_gather_kernel(const int32_t 
   const char *gtile = reinterpret_cast<const char *>(gt + (int64_t)it.tile * B * TCH);
   f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
   if (lay.start >= 0) acc = reinterpret_cast<const f32x4 *>(gsm + lay.start)[p * TCH + t];
-  if (staged)
-    bwd_tile_sum<true, TCH>(spos + (s0 - ra), n, nmin, nmax, t, gtile, acc);
+  if (staged)  // P16: offsets from the chunk's first grad row
+    bwd_tile_sum<true, TCH>(spos + (s0 - ra), n, nmin, nmax, t,
+                            P16 ? gtile + (size_t)chunk_base * (TCH * sizeof(f32x4)) : gtile, acc);
   else
     bwd_tile_sum<false, TCH>(sorted_pos + s0, n, nmin, nmax, t, gtile, acc);
   if (!live || !colok || is_long) return;
@@ -638,16 +660,26 @@ __global__ __launch_bounds__(kBlock) void bwd_tiled_gather_kernel(const int32_t 
 }
 
 // One position chunk's tiled weight-grad gather: one workgroup per item.
-int launch_tiled_gather(bool nt, const int32_t *seg, const int32_t *pos, int64_t N, const f32x4 *gt, int64_t B,
-                        const ColMap &map, const RowDst &dst, f32x4 *tmp, int src_mode, int dst_mode, int ntiles,
-                        int ngroups, const int32_t *long_list, const int *long_count, int nlong, hipStream_t s) {
+// pos16: the slots' 16-bit chunk offsets (null when a chunk has more than
+// 65536 positions), chunk_base the first position of this launch's chunk.
+int launch_tiled_gather(bool nt, const int32_t *seg, const int32_t *pos, const uint16_t *pos16, int64_t chunk_base,
+                        int64_t N, const f32x4 *gt, int64_t B, const ColMap &map, const RowDst &dst, f32x4 *tmp,
+                        int src_mode, int dst_mode, int ntiles, int ngroups, const int32_t *long_list,
+                        const int *long_count, int nlong, hipStream_t s) {
   const int64_t items = tile_sched_items_per_xcd(ntiles, ngroups + nlong);
   const size_t lds = (size_t)gather_lds(src_mode, dst_mode).bytes;
-  if ((uintptr_t)pos % 16 != 0)  // the sort's position buffers are 256-byte aligned workspace regions
+  if ((uintptr_t)pos % 16 != 0 || (uintptr_t)pos16 % 16 != 0)  // 256-byte / 16-byte aligned workspace regions
     return fail(SFT_EINVAL, "tiled feature gather: sorted positions not 16-byte aligned");
-  hipLaunchKernelGGL((nt ? bwd_tiled_gather_kernel<true> : bwd_tiled_gather_kernel<false>),
-                     dim3((unsigned)(items * kXcds)), dim3(kBlock), lds, s, seg, pos, N, gt, B, map, dst, tmp,
-                     src_mode, dst_mode, ntiles, ngroups, long_list, long_count, nlong);
+  const dim3 grid((unsigned)(items * kXcds));
+  const int cb = (int)chunk_base;
+  if (pos16 != nullptr)
+    hipLaunchKernelGGL((nt ? bwd_tiled_gather_kernel<true, true> : bwd_tiled_gather_kernel<false, true>), grid,
+                       dim3(kBlock), lds, s, seg, pos, pos16, cb, N, gt, B, map, dst, tmp, src_mode, dst_mode, ntiles,
+                       ngroups, long_list, long_count, nlong);
+  else
+    hipLaunchKernelGGL((nt ? bwd_tiled_gather_kernel<true, false> : bwd_tiled_gather_kernel<false, false>), grid,
+                       dim3(kBlock), lds, s, seg, pos, pos16, cb, N, gt, B, map, dst, tmp, src_mode, dst_mode, ntiles,
+                       ngroups, long_list, long_count, nlong);
   return check_launch("tiled feature gather");
 }
 
@@ -998,7 +1030,7 @@ int make_layout(int64_t B, int K, int64_t N, int L, uint32_t flags, BwdLayout &l
       lay.sort = off;
       off = align256(off + slot_sort_workspace(M));
       lay.seg = off;
-      off = align256(off + seg_region_bytes(nc, N));
+      off = align256(off + seg_region_bytes(nc, N, M));
     }
     lay.gt = off;
     if (tiled_shape(B, L, flags)) {  // the grad tiles the bias pass writes, whatever the chunk count
@@ -1057,10 +1089,12 @@ int launch_bias_final(const float *partial, int nparts, int L, float *db, int ov
 // Segment starts of one sort and its lists of long segments (the counts
 // were zeroed by the sort).
 int launch_segments(const unsigned *keys, int64_t M, int nc, int64_t nfeat, const unsigned *totals, int ntot,
-                    const SegBufs &sb, hipStream_t s) {
+                    const SegBufs &sb, const int32_t *pos, int64_t chunk_rows, hipStream_t s) {
   ProfScope prof(kProfBwdOffsets, s);
+  uint16_t *p16 = chunk_rows <= 65536 ? sb.pos16 : nullptr;
   hipLaunchKernelGGL(seg_offsets_kernel, dim3((unsigned)std::min<int64_t>(ceil_div(M + 1, kBlock), kSegBlocks)),
-                     dim3(kBlock), 0, s, keys, (int64_t)nc * nfeat, totals, ntot, sb.seg, nfeat, sb.list, sb.count);
+                     dim3(kBlock), 0, s, keys, (int64_t)nc * nfeat, totals, ntot, sb.seg, nfeat, sb.list, sb.count,
+                     pos, p16, (int)std::min<int64_t>(chunk_rows, 65536));
   return check_launch("segment offsets");
 }
 
@@ -1089,7 +1123,7 @@ void make_prep_layout(int64_t B, int K, int64_t N, int L, uint32_t flags, PrepLa
   p.sort = p.seg = p.total = 0;
   if (!prep_pays(B, K, L, flags)) return;
   p.seg = align256(slot_sort_workspace(M));
-  p.total = p.seg + align256(seg_region_bytes(p.nc, N));
+  p.total = p.seg + align256(seg_region_bytes(p.nc, N, M));
 }
 
 // Sort of the slots into nc position chunks and their segment starts, on s.
@@ -1105,7 +1139,7 @@ int sort_and_segments(const int32_t *idx, int64_t B, int K, int64_t N, int nc, v
                         sb.count, nc, s)) != SFT_OK)
       return rc;
   }
-  return launch_segments(keys, M, nc, N, totals, ntot, sb, s);
+  return launch_segments(keys, M, nc, N, totals, ntot, sb, *pos, nc > 1 ? half_rows(B) : B, s);
 }
 
 }  // namespace
@@ -1251,7 +1285,9 @@ int bwd_f32(const int32_t *idx, int64_t B, int K, const float *grad, int64_t N, 
     for (int h = 0; h < nc; ++h) {
       ProfScope prof(kProfBwdTiled, s);
       const bool nt = (nc > 1 ? half_rows(B) : B) * kBwdTileCh * 16 >= kNtStoreTileBytes;
-      rc = launch_tiled_gather(nt, seg + (int64_t)h * N, pos, N, gt, B, map, dst, nullptr, h == 0 ? kSrcZero : kSrcDst,
+      const int64_t crow = nc > 1 ? half_rows(B) : B;
+      rc = launch_tiled_gather(nt, seg + (int64_t)h * N, pos, crow <= 65536 ? sb.pos16 : nullptr, h * crow, N, gt, B,
+                               map, dst, nullptr, h == 0 ? kSrcZero : kSrcDst,
                                kDstOut, ntiles, ngroups, sb.list + h * N, sb.count + h, kLongSlots, s);
       if (rc != SFT_OK) return rc;
     }
@@ -1294,7 +1330,7 @@ void make_pair_layout(int64_t B, int K, int64_t N, int L, PairLayout &lay) {
     lay.sort[p] = off;
     off = align256(off + slot_sort_workspace(std::max<int64_t>(M, 1)));
     lay.seg[p] = off;
-    off = align256(off + seg_region_bytes(lay.nc, N));
+    off = align256(off + seg_region_bytes(lay.nc, N, M));
   }
   for (int p = 0; p < 2; ++p) {  // grad tiles of each perspective
     lay.gt[p] = off;
@@ -1328,7 +1364,7 @@ static int pair_sort_perspective(const int32_t *idx, int64_t B, int K, int64_t N
                         &ntot, out.sb.count, nc, s)) != SFT_OK)
       return rc;
   }
-  return launch_segments(keys, M, nc, N, totals, ntot, out.sb, s);
+  return launch_segments(keys, M, nc, N, totals, ntot, out.sb, out.pos, nc > 1 ? half_rows(B) : B, s);
 }
 
 // One perspective's position-chunk launches of the tiled gather: perspective 0
@@ -1349,7 +1385,9 @@ static int pair_gather_perspective(int p, const SortedSlots &ss, int64_t B, int6
     }
     ProfScope prof(kProfBwdTiled, s);
     const bool nt = (nc > 1 ? half_rows(B) : B) * kBwdTileCh * 16 >= kNtStoreTileBytes;
-    const int rc = launch_tiled_gather(nt, ss.sb.seg + (int64_t)h * N, ss.pos, N, gt, B, map, dst, tmp, src_mode,
+    const int64_t crow = nc > 1 ? half_rows(B) : B;
+    const int rc = launch_tiled_gather(nt, ss.sb.seg + (int64_t)h * N, ss.pos, crow <= 65536 ? ss.sb.pos16 : nullptr,
+                                       h * crow, N, gt, B, map, dst, tmp, src_mode,
                                        dst_mode, ntiles, ngroups, ss.sb.list + h * N, ss.sb.count + h, kLongSlots, s);
     if (rc != SFT_OK) return rc;
   }
@@ -1446,7 +1484,7 @@ void make_transform_layout(int64_t B, int K, int64_t N, int L, int L1, Transform
     lay.sort[p] = off;
     off = align256(off + slot_sort_workspace(std::max<int64_t>(M, 1)));
     lay.seg[p] = off;
-    off = align256(off + seg_region_bytes(lay.nc, N));
+    off = align256(off + seg_region_bytes(lay.nc, N, M));
   }
   lay.gt0 = off;
   off = align256(off + gtb);
