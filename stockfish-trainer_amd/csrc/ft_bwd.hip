@@ -143,16 +143,26 @@ __device__ __forceinline__ void group_minmax(int v, int &vmin, int &vmax) {
 }
 
 // Where a launch starts and leaves each feature's sum:
-//   src_mode kSrcZero: acc = 0;  kSrcDst: acc = dst row;  kSrcTmp: acc = tmp row
-//   dst_mode kDstOut: dst row = acc (skipped for untouched features when the
-//            sum continues from dst);  kDstTmp: tmp row = acc;
-//            kDstOutPlus: dst row = dst row + acc (every feature).
-// One perspective: (zero, out), then (dst, out) per further position chunk.
-// A second perspective sums onto 0 in tmp and its last launch adds its total
-// to the first's: dW = dW_0 + dW_1, the sum autograd forms for the composed
-// table (FEAT/composed.py:52-53).  dst rows are split into blocks (RowDst).
-enum { kSrcZero = 0, kSrcDst = 1, kSrcTmp = 2 };
+//   src_mode kSrcZero: acc = 0;  kSrcTmp: acc = tmp row
+//   dst_mode kDstOut: dst row = acc;  kDstTmp: tmp row = acc;
+//            kDstOutPlus: dst row = dst row + acc.
+// One perspective: (zero, tmp), (tmp, tmp) ..., (tmp, out) over its position
+// chunks; (zero, out) with one chunk.  A second perspective ends with
+// kDstOutPlus instead: dW = dW_0 + dW_1, the sum autograd forms for the
+// composed table (FEAT/composed.py:52-53).  dst rows are split into blocks
+// (RowDst).
+enum { kSrcZero = 0, kSrcTmp = 2 };
 enum { kDstOut = 0, kDstTmp = 1, kDstOutPlus = 2 };
+
+// The sums carried from one position chunk to the next are kept tile-major:
+// the 8 chunks (32 columns) of tile t for feature f at tmp + tmp_row(t, f, N),
+// so a row is one aligned 128-byte line and a workgroup's 32 features are 4 KB
+// of consecutive lines.  (A row-major [N, L] row puts tile t at byte 4L f + 128 t,
+// which for L % 32 != 0 straddles two lines three times in four -- lines that
+// the neighbouring tiles, gathered on other XCDs, also touch.)
+__host__ __device__ inline int64_t tmp_row(int tile, int64_t f, int64_t nfeat) {
+  return ((int64_t)tile * nfeat + f) * 8;
+}
 
 // Rows of column block cb for position p: 8 chunks at base + cb * blk_stride
 // + p * pos_stride (grad tiles: blk_stride = B * 8, pos_stride = 8; row-major
@@ -170,18 +180,17 @@ struct LongEnds {
   int ccol;
 };
 __device__ __forceinline__ LongEnds long_ends(int64_t f, int cb, int lane, const ColMap &map, const RowDst &dst,
-                                              f32x4 *tmp) {
+                                              f32x4 *tmp, int64_t nfeat) {
   LongEnds e{nullptr, nullptr, lane < 32 ? tile_col(map, cb, lane >> 2) : -1};
   if (e.ccol >= 0) {
     const int blk = block_of(f, dst.n, dst.start);
     e.dp = reinterpret_cast<float *>(pick(dst.p, blk) + (f - pick(dst.start, blk)) * map.cols4 + e.ccol) + (lane & 3);
-    if (tmp != nullptr) e.tp = reinterpret_cast<float *>(tmp + f * map.cols4 + e.ccol) + (lane & 3);
+    if (tmp != nullptr) e.tp = reinterpret_cast<float *>(tmp + tmp_row(cb, f, nfeat) + (lane >> 2)) + (lane & 3);
   }
   return e;
 }
 __device__ __forceinline__ float long_start(const LongEnds &e, int src_mode) {
   if (e.ccol < 0) return 0.f;
-  if (src_mode == kSrcDst) return *e.dp;
   if (src_mode == kSrcTmp) return *e.tp;
   return 0.f;
 }
@@ -201,12 +210,12 @@ __device__ __forceinline__ void long_store(const LongEnds &e, int dst_mode, floa
 constexpr int kWgLongRows = 128;  // 128 x 128 B = 16 KB of LDS
 __device__ __forceinline__ void long_segment_sum_wg(const int32_t *__restrict__ sorted_pos, int64_t f, int s0, int n,
                                                     int cb, const LongRows &rows, const ColMap &map,
-                                                    const RowDst &dst, f32x4 *__restrict__ tmp, int src_mode,
-                                                    int dst_mode, f32x4 *buf) {
+                                                    const RowDst &dst, f32x4 *__restrict__ tmp, int64_t nfeat,
+                                                    int src_mode, int dst_mode, f32x4 *buf) {
   constexpr int kRowsPerPass = kBlock / 8;
   constexpr int kPass = kWgLongRows / kRowsPerPass;
   const bool stager = threadIdx.x < kBlock;
-  const LongEnds ends = long_ends(f, cb, (int)threadIdx.x, map, dst, tmp);
+  const LongEnds ends = long_ends(f, cb, (int)threadIdx.x, map, dst, tmp, nfeat);
   float acc = long_start(ends, src_mode);
   const int q = threadIdx.x & 7, r0 = threadIdx.x >> 3;  // staging: chunk q of rows r0 + 32 u
   const bool qok = tile_col(map, cb, q) >= 0;
@@ -280,7 +289,7 @@ __global__ __launch_bounds__(kBlock) void gather_rows_kernel(const int32_t *__re
         const int64_t f = long_list[k / nblk];
         const int s0 = seg_start[f];
         long_segment_sum_wg(sorted_pos, f, s0, seg_start[f + 1] - s0, (int)(k % nblk), LongRows{grad, 8, cols}, map,
-                            dst, nullptr, kSrcZero, overwrite ? kDstOut : kDstOutPlus, lbuf);
+                            dst, nullptr, N, kSrcZero, overwrite ? kDstOut : kDstOutPlus, lbuf);
       }
     }
     return;
@@ -400,6 +409,7 @@ __device__ __forceinline__ f32x4 load_row(const f32x4 *p) {
   else return *p;
 }
 constexpr int kBwdTileCh = 8;  // float4 chunks per 32-column tile row (grad tiles and weight-grad blocks)
+static_assert(kBwdTileCh == 8, "tmp_row and the long-segment lanes hold 8 chunks per tile");
 // Features per workgroup of the tiled gather: one per 8-lane group.
 constexpr int bwd_feat_per_block() { return kWavesPerBlock * (kWave / kBwdTileCh); }
 // Long segments are summed in 32-column blocks by the tiled gather's
@@ -533,13 +543,12 @@ __global__ __launch_bounds__(kBlock) void bwd_tiled_gather_kernel(const int32_t 
       const int64_t f = long_list[e];
       const int s0 = seg[f];
       long_segment_sum_wg(sorted_pos, f, s0, seg[f + 1] - s0, it.tile, LongRows{gt, B * TCH, TCH}, map, dst, tmp,
-                          src_mode, dst_mode, reinterpret_cast<f32x4 *>(gsm));
+                          N, src_mode, dst_mode, reinterpret_cast<f32x4 *>(gsm));
     }
     return;
   }
   const GatherLds lay = gather_lds(src_mode, dst_mode);
   int *spos = reinterpret_cast<int *>(gsm);
-  const bool skip_untouched = src_mode == kSrcDst && dst_mode == kDstOut;
   const int64_t cols4 = map.cols4;
   const int tid = threadIdx.x;
   const int wave = uniform(tid / kWave);
@@ -600,11 +609,11 @@ __global__ __launch_bounds__(kBlock) void bwd_tiled_gather_kernel(const int32_t 
     const bool own = fs < N && colm >= 0 && !long_segment(as, es);
     f32x4 vs = f32x4{0.f, 0.f, 0.f, 0.f}, vp = vs;
     if (own) {
-      const int blk = block_of(fs, dst.n, dst.start);
-      const f32x4 *d = pick(dst.p, blk) + (fs - pick(dst.start, blk)) * cols4 + colm;
-      if (src_mode == kSrcTmp) vs = tmp[fs * cols4 + colm];
-      else if (src_mode == kSrcDst && (es > as || !skip_untouched)) vs = *d;
-      if (lay.plus >= 0) vp = load_row<NT>(d);
+      if (src_mode == kSrcTmp) vs = tmp[tmp_row(it.tile, fs, N) + cs];
+      if (lay.plus >= 0) {
+        const int blk = block_of(fs, dst.n, dst.start);
+        vp = load_row<NT>(pick(dst.p, blk) + (fs - pick(dst.start, blk)) * cols4 + colm);
+      }
     }
     if (lay.start >= 0) reinterpret_cast<f32x4 *>(gsm + lay.start)[tid] = vs;
     if (lay.plus >= 0) reinterpret_cast<f32x4 *>(gsm + lay.plus)[tid] = vp;
@@ -633,8 +642,6 @@ __global__ __launch_bounds__(kBlock) void bwd_tiled_gather_kernel(const int32_t 
   const bool live = p < nf;
   const bool is_long = live && long_segment(s0, s1);  // summed by the long-segment slots
   const int n = (live && !is_long) ? s1 - s0 : 0;
-  const bool wave_has_work = ballot(n > 0) != 0;  // wave-uniform
-  if (skip_untouched && !wave_has_work) return;  // nothing to change anywhere in the wave
   int nmin, nmax;
   group_minmax<TCH>(n, nmin, nmax);
   const int colm = tile_col(map, it.tile, t);
@@ -651,10 +658,10 @@ __global__ __launch_bounds__(kBlock) void bwd_tiled_gather_kernel(const int32_t 
   const int blk = block_of(f, dst.n, dst.start);
   f32x4 *d = pick(dst.p, blk) + (f - pick(dst.start, blk)) * cols4 + colm;
   if (dst_mode == kDstTmp) {
-    store_row<NT>(tmp + f * cols4 + colm, acc);
+    store_row<NT>(tmp + tmp_row(it.tile, f, N) + t, acc);
   } else if (dst_mode == kDstOutPlus) {
     store_row<NT>(d, reinterpret_cast<const f32x4 *>(gsm + lay.plus)[p * TCH + t] + acc);
-  } else if (!skip_untouched || n > 0) {
+  } else {
     store_row<NT>(d, acc);
   }
 }
@@ -980,7 +987,7 @@ void launch_gather(dim3 grid, hipStream_t s, const int32_t *seg_start, const int
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 struct BwdLayout {
-  size_t sort, seg, partial, gt, total;
+  size_t sort, seg, partial, gt, tmp, total;
   int nparts;
 };
 
@@ -1023,7 +1030,7 @@ int make_layout(int64_t B, int K, int64_t N, int L, uint32_t flags, BwdLayout &l
   size_t off = 0;
   lay.partial = off;
   off = align256(off + (size_t)lay.nparts * (size_t)L * sizeof(float));
-  lay.sort = lay.seg = lay.gt = off;
+  lay.sort = lay.seg = lay.gt = lay.tmp = off;
   if (!(flags & SFT_BWD_ATOMIC) && M > 0) {
     const int nc = sort_chunks(B, L, flags);
     if (!((flags & SFT_BWD_PREPARED) && prep_pays(B, K, L, flags))) {
@@ -1036,6 +1043,8 @@ int make_layout(int64_t B, int K, int64_t N, int L, uint32_t flags, BwdLayout &l
     if (tiled_shape(B, L, flags)) {  // the grad tiles the bias pass writes, whatever the chunk count
       const int64_t ntiles = ceil_div(L / 4, kBwdTileCh);
       off = align256(off + (size_t)(ntiles * B * kBwdTileCh) * 16);
+      lay.tmp = off;
+      if (nc > 1) off = align256(off + (size_t)(ntiles * N * kBwdTileCh) * 16);  // sums between chunks
     }
   }
   lay.total = off;
@@ -1282,13 +1291,14 @@ int bwd_f32(const int32_t *idx, int64_t B, int K, const float *grad, int64_t N, 
     dst.n = 1;
     dst.start[1] = N;
     dst.p[0] = reinterpret_cast<f32x4 *>(dW);
+    f32x4 *tmp = reinterpret_cast<f32x4 *>(w + lay.tmp);
     for (int h = 0; h < nc; ++h) {
       ProfScope prof(kProfBwdTiled, s);
       const bool nt = (nc > 1 ? half_rows(B) : B) * kBwdTileCh * 16 >= kNtStoreTileBytes;
       const int64_t crow = nc > 1 ? half_rows(B) : B;
       rc = launch_tiled_gather(nt, seg + (int64_t)h * N, pos, crow <= 65536 ? sb.pos16 : nullptr, h * crow, N, gt, B,
-                               map, dst, nullptr, h == 0 ? kSrcZero : kSrcDst,
-                               kDstOut, ntiles, ngroups, sb.list + h * N, sb.count + h, kLongSlots, s);
+                               map, dst, tmp, h == 0 ? kSrcZero : kSrcTmp, h == nc - 1 ? kDstOut : kDstTmp, ntiles,
+                               ngroups, sb.list + h * N, sb.count + h, kLongSlots, s);
       if (rc != SFT_OK) return rc;
     }
     return SFT_OK;
@@ -1313,7 +1323,7 @@ int bwd_f32(const int32_t *idx, int64_t B, int K, const float *grad, int64_t N, 
 
 // ------------------------------------------- composed table, two perspectives ----
 // Workspace: bias partials of both grads | sort buffers | segment starts |
-// grad tiles of each perspective | tmp (the second perspective's sums, [N, L]).
+// grad tiles of each perspective | tmp (sums between position chunks, tile-major).
 struct PairLayout {
   size_t partial, sort[2], seg[2], gt[2], tmp, total;
   int nparts, nc;
@@ -1337,7 +1347,7 @@ void make_pair_layout(int64_t B, int K, int64_t N, int L, PairLayout &lay) {
     off = align256(off + (size_t)(ceil_div(L, 32) * B * 32) * sizeof(float));
   }
   lay.tmp = off;
-  off = align256(off + (size_t)N * (size_t)L * sizeof(float));
+  off = align256(off + (size_t)(ceil_div(L, 32) * N * 32) * sizeof(float));
   lay.total = off;
 }
 
@@ -1367,22 +1377,17 @@ static int pair_sort_perspective(const int32_t *idx, int64_t B, int K, int64_t N
   return launch_segments(keys, M, nc, N, totals, ntot, out.sb, out.pos, nc > 1 ? half_rows(B) : B, s);
 }
 
-// One perspective's position-chunk launches of the tiled gather: perspective 0
-// stores to dst, perspective 1 sums onto 0 in tmp and its last launch stores
-// dst + tmp.
+// One perspective's position-chunk launches of the tiled gather, the sums
+// carried between chunks in tmp: perspective 0's last launch stores its sums to
+// dst, perspective 1's adds them to dst.
 static int pair_gather_perspective(int p, const SortedSlots &ss, int64_t B, int64_t N, const ColMap &map,
                                    const f32x4 *gt, const RowDst &dst, f32x4 *tmp, int nc, hipStream_t s) {
   const int ntiles = map_tiles(map);
   const int ngroups = (int)ceil_div(N, bwd_feat_per_block());
   for (int h = 0; h < nc; ++h) {
     int src_mode, dst_mode;
-    if (p == 0) {
-      src_mode = h == 0 ? kSrcZero : kSrcDst;
-      dst_mode = kDstOut;
-    } else {
-      src_mode = h == 0 ? kSrcZero : kSrcTmp;
-      dst_mode = h == nc - 1 ? kDstOutPlus : kDstTmp;
-    }
+    src_mode = h == 0 ? kSrcZero : kSrcTmp;
+    dst_mode = h < nc - 1 ? kDstTmp : p == 0 ? kDstOut : kDstOutPlus;
     ProfScope prof(kProfBwdTiled, s);
     const bool nt = (nc > 1 ? half_rows(B) : B) * kBwdTileCh * 16 >= kNtStoreTileBytes;
     const int64_t crow = nc > 1 ? half_rows(B) : B;
@@ -1465,7 +1470,7 @@ int bwd_pair_f32(const int32_t *idx0, const int32_t *idx1, int64_t B, int K, con
 
 // ------------------------------------------- composed table + post-FT epilogue ----
 // Workspace: bias partials | sort buffers | segment starts | grad tiles of both
-// perspectives (paired map) | tmp [N, L].
+// perspectives (paired map) | tmp (tile-major, paired map).
 struct TransformLayout {
   size_t partial, sort[2], seg[2], gt0, gt1, tmp, total;
   int nparts, nc;
@@ -1491,7 +1496,7 @@ void make_transform_layout(int64_t B, int K, int64_t N, int L, int L1, Transform
   lay.gt1 = off;
   off = align256(off + gtb);
   lay.tmp = off;
-  off = align256(off + (size_t)N * (size_t)L * sizeof(float));
+  off = align256(off + (size_t)map_tiles(map) * (size_t)N * 128);
   lay.total = off;
 }
 
