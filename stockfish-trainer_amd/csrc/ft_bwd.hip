@@ -383,20 +383,20 @@ __global__ __launch_bounds__(kBlock) void gather_rows_kernel(const int32_t *__re
 // dW[f, tile] for one 32-column tile, from the grad re-laid out as column
 // tiles (Gt: tile t holds columns [32t, 32t + 32) of every position, 128 B per
 // position).  The slots are sorted by (position half, feature), and the batch
-// is done in two launches: half 0 stores dW[f, tile] = its sum, half 1 loads
-// that value and keeps adding.  Either way a feature's sum is acc = 0,
+// is done in two launches: half 0 stores its sum for (f, tile) to a tile-major
+// buffer (tmp_row), half 1 loads that value and keeps adding.  Either way a feature's sum is acc = 0,
 // acc += grad[b] over its positions ascending: the reference order
 // (FT/kernel.py:122, 178-181), bit for bit.  A lane group of 8 lanes x 16 B
 // owns one feature's tile row; tiles go to XCDs whole (tile_sched_item), so an
 // XCD reads one tile-half of Gt at a time: 32768 x 128 B = 4 MB, its L2.
-// The weight-grad tile rows are written once per launch and read back, if at
-// all, by the next launch.  When a tile-half of the grad tiles takes half of an
+// The summed tile rows are written once per launch and read back, if at all,
+// by the next launch.  When a tile-half of the grad tiles takes half of an
 // XCD's L2 or more, non-temporal stores keep them from evicting it (220 -> 215
 // us per launch at B = 65536); with smaller batches the grad tile fits anyway
 // and the read-back is cheaper from the cache (B = 16384: 90 vs 99 us), so the
 // host picks per launch (kNtStoreTileBytes; a template parameter, as the
 // compiler merges a runtime choice between the two stores into a plain one).
-// Non-temporal loads of the values read back made the gather slower.
+// The carried sums are read back with the same policy (207.3 -> 204.8 us).
 constexpr int64_t kNtStoreTileBytes = 2 << 20;
 template <bool NT>
 __device__ __forceinline__ void store_row(f32x4 *p, f32x4 v) {
@@ -609,7 +609,7 @@ __global__ __launch_bounds__(kBlock) void bwd_tiled_gather_kernel(const int32_t 
     const bool own = fs < N && colm >= 0 && !long_segment(as, es);
     f32x4 vs = f32x4{0.f, 0.f, 0.f, 0.f}, vp = vs;
     if (own) {
-      if (src_mode == kSrcTmp) vs = tmp[tmp_row(it.tile, fs, N) + cs];
+      if (src_mode == kSrcTmp) vs = load_row<NT>(tmp + tmp_row(it.tile, fs, N) + cs);  // stored with NT too
       if (lay.plus >= 0) {
         const int blk = block_of(fs, dst.n, dst.start);
         vp = load_row<NT>(pick(dst.p, blk) + (fs - pick(dst.start, blk)) * cols4 + colm);

@@ -333,13 +333,19 @@ __device__ __forceinline__ f32x4 f32_tile_rows(const int *mylist, int nmax, cons
 // lane at K = 32).  Ranks B .. Bpad - 1 are padding: position -1, count 0,
 // list all N.  Positions of one count are ranked in the order LDS atomics
 // hand out; a position's sum does not depend on its rank.
+// Narrow lists (`narrow`: tables of at most 65 535 rows gathered in one pass,
+// kpad a multiple of 8 and the lists staged in LDS) hold 16-bit entries, eight
+// per 16-byte piece, widened to ints in the gather's LDS: every column tile
+// pass streams the lists through the L2 that holds the table tile, and this
+// halves them.
 constexpr int kRanksPerBlock = kWavesPerBlock * (kWave / kTileCh);  // 32: 8 per wave
 constexpr int kRankSortBlock = kBlock;                               // positions ranked together
 struct RankLists {
-  int32_t *list;   // [Bpad][kpad]
+  int32_t *list;   // [Bpad][kpad] (narrow: uint16_t entries)
   int32_t *pos;    // [Bpad] rank -> position, -1 for padding
   int32_t *count;  // [Bpad] active slots of the rank's position, non-increasing within each 256 ranks
   i32x4 *cut;      // [Bpad] table parts (nparts > 1): see "Table parts" below
+  int narrow;      // 16-bit list entries (STAGE builds only, nparts == 1)
 };
 struct RankArgs {
   const int32_t *idx[2];
@@ -429,7 +435,18 @@ __global__ __launch_bounds__(kBlock) void rank_lists_kernel(RankArgs a, int64_t 
     if (a.nparts > 1 && r < Bpad)
       L.cut[r] = mono ? i32x4{cut[0], cut[1], cut[2], a.nparts - 1} : i32x4{c, c, c, 0};
   }
-  if (STAGE) {
+  if (STAGE && L.narrow) {  // entries <= N <= 65535
+    __syncthreads();
+    const int q8 = kpad / 8;
+    i32x4 *out = reinterpret_cast<i32x4 *>(reinterpret_cast<uint16_t *>(L.list) + base * kpad);
+    auto pack = [](int lo, int hi) { return (int)(((uint32_t)lo & 0xffffu) | ((uint32_t)hi << 16)); };
+    for (int i = tid; i < kRankSortBlock * q8; i += kBlock) {
+      const int rr = i / q8, q = i - rr * q8;
+      if (base + rr >= Bpad) break;  // i ascending: every later piece is past Bpad too
+      const int *src = rows + rr * (kpad + 1) + 8 * q;
+      out[i] = i32x4{pack(src[0], src[1]), pack(src[2], src[3]), pack(src[4], src[5]), pack(src[6], src[7])};
+    }
+  } else if (STAGE) {
     __syncthreads();
     const int q4 = kpad / 4;
     i32x4 *out = reinterpret_cast<i32x4 *>(L.list + base * kpad);
@@ -495,9 +512,20 @@ __global__ __launch_bounds__(kBlock) void fwd_tiled_kernel(RankLists R0, RankLis
   int nmax, lo = 0;
   bool work = true, final_pass = true;
   if (nparts == 1) {  // launch-uniform: whole lists
-    const i32x4 *__restrict__ src = reinterpret_cast<const i32x4 *>(R.list + r0 * kpad);
     i32x4 *dst = reinterpret_cast<i32x4 *>(list);
-    for (int j = lane; j < PPW * kpad / 4; j += kWave) dst[j] = src[j];
+    if (R.narrow) {  // launch-uniform: 16-bit entries, widened
+      const i32x4 *__restrict__ src =
+          reinterpret_cast<const i32x4 *>(reinterpret_cast<const uint16_t *>(R.list) + r0 * kpad);
+      for (int j = lane; j < PPW * kpad / 8; j += kWave) {
+        const i32x4 v = src[j];
+        const uint32_t w0 = (uint32_t)v[0], w1 = (uint32_t)v[1], w2 = (uint32_t)v[2], w3 = (uint32_t)v[3];
+        dst[2 * j] = i32x4{(int)(w0 & 0xffffu), (int)(w0 >> 16), (int)(w1 & 0xffffu), (int)(w1 >> 16)};
+        dst[2 * j + 1] = i32x4{(int)(w2 & 0xffffu), (int)(w2 >> 16), (int)(w3 & 0xffffu), (int)(w3 >> 16)};
+      }
+    } else {
+      const i32x4 *__restrict__ src = reinterpret_cast<const i32x4 *>(R.list + r0 * kpad);
+      for (int j = lane; j < PPW * kpad / 4; j += kWave) dst[j] = src[j];
+    }
     nmax = R.count[r0];  // counts fall with rank within each 256 ranks: the wave's longest list
   } else {
     // this pass's run [lo, hi) of each list (table parts, above), padded with
@@ -893,9 +921,10 @@ size_t rank_lists_bytes(int64_t B, int K) {
   const int64_t Bp = rank_pad(B);
   return align256((size_t)(Bp * round_up4(K)) * 4) + 2 * align256((size_t)Bp * 4) + align256((size_t)Bp * 16);
 }
-static RankLists rank_lists_at(char *p, int64_t B, int K) {
+static RankLists rank_lists_at(char *p, int64_t B, int K, int narrow) {
   const int64_t Bp = rank_pad(B);
   RankLists r;
+  r.narrow = narrow;
   r.list = reinterpret_cast<int32_t *>(p);
   p += align256((size_t)(Bp * round_up4(K)) * 4);
   r.pos = reinterpret_cast<int32_t *>(p);
@@ -920,6 +949,11 @@ static int part_rows_of(int64_t N, int nparts) { return (int)ceil_div(std::max<i
 static size_t rank_lds_bytes(int K) { return (size_t)kRanksPerBlock * round_up4(K) * sizeof(int); }
 // Lists staged in LDS up to kpad = 32 (33 KB); longer ones are stored by their threads.
 constexpr int kRankStageMaxPad = 32;
+// 16-bit lists: one table pass, entries up to N <= 65535, staged rows of 8-entry pieces.
+static int lists_narrow(int K, int64_t N, int nparts) {
+  const int kpad = round_up4(K);
+  return nparts == 1 && N <= 65535 && kpad % 8 == 0 && kpad <= kRankStageMaxPad;
+}
 
 // Rank lists of np perspectives (idx[p] -> R[p]) in one launch.
 static int build_rank_lists(const int32_t *idx0, const int32_t *idx1, int np, int64_t B, int K, int N,
@@ -935,6 +969,8 @@ static int build_rank_lists(const int32_t *idx0, const int32_t *idx1, int np, in
   const int kpad = round_up4(K);
   const int vec = K % 4 == 0 && (uintptr_t)idx0 % 16 == 0 && (uintptr_t)idx1 % 16 == 0;
   const bool stage = kpad <= kRankStageMaxPad;
+  if ((R0.narrow || R1.narrow) && (!stage || kpad % 8 != 0 || N > 65535))
+    return fail(SFT_EINVAL, std::string(who) + ": 16-bit rank lists need staged lists of 8-entry pieces");
   const size_t lds = (size_t)(2 * (K + 1)) * 4 + (stage ? (size_t)kRankSortBlock * (kpad + 1) * 4 : 0);
   const dim3 grid((unsigned)ceil_div(Bp, (int64_t)kRankSortBlock), (unsigned)np);
   ProfScope prof(kProfFwdRanks, s);
@@ -980,15 +1016,15 @@ int fwd_f32_tiled(const int32_t *idx, int64_t B, int K, const float *W, int64_t 
   const size_t lds = rank_lds_bytes(K);
   if (lds > kMaxIndexLds) return fail(SFT_EUNSUPPORTED, "sft_ft_fwd_f32_ex: max_active too large for the LDS index lists");
   f32x4 *wt = static_cast<f32x4 *>(ws);
+  const int nparts = table_parts(N);
   const RankLists R = rank_lists_at(static_cast<char *>(ws) + align256((size_t)(ntiles * tile_rows(N) * kTileF) * 4),
-                                    B, K);
+                                    B, K, lists_narrow(K, N, nparts));
   {
     ProfScope prof(kProfFwdRelayout, s);
     launch_tile_relayout(reinterpret_cast<const f32x4 *>(W), N, cols4, wt, s);
   }
   int rc = check_launch("sft_ft_fwd_f32_ex (relayout)");
   if (rc != SFT_OK) return rc;
-  const int nparts = table_parts(N);
   if ((rc = build_rank_lists(idx, idx, 1, B, K, (int)N, R, R, nparts, s, who)) != SFT_OK) return rc;
   const int nchunks = (int)(rank_pad(B) / kRanksPerBlock);
   const int64_t blocks = tile_sched_items_per_xcd(ntiles, nchunks) * kXcds;
@@ -1022,7 +1058,10 @@ static int pair_gather(const int32_t *idx0, const int32_t *idx1, int64_t B, int 
   const size_t lds = rank_lds_bytes(K);
   f32x4 *wt = static_cast<f32x4 *>(ws);
   char *lists = static_cast<char *>(ws) + align256(table_tiles_workspace(map, N));
-  const RankLists R0 = rank_lists_at(lists, B, K), R1 = rank_lists_at(lists + rank_lists_bytes(B, K), B, K);
+  const int nparts = table_parts(N);
+  const int narrow = lists_narrow(K, N, nparts);
+  const RankLists R0 = rank_lists_at(lists, B, K, narrow),
+                  R1 = rank_lists_at(lists + rank_lists_bytes(B, K), B, K, narrow);
   if (lds > kMaxIndexLds) return fail(SFT_EUNSUPPORTED, std::string(who) + ": max_active too large for the LDS index lists");
   if (tile_rows(N) * (int64_t)kTileRowBytes > (int64_t)UINT32_MAX)
     return fail(SFT_EUNSUPPORTED, std::string(who) + ": more than 2^25 - 1 table rows");
@@ -1034,7 +1073,6 @@ static int pair_gather(const int32_t *idx0, const int32_t *idx1, int64_t B, int 
   }
   int rc = check_launch(who);
   if (rc != SFT_OK || B == 0) return rc;
-  const int nparts = table_parts(N);
   if ((rc = build_rank_lists(idx0, idx1, 2, B, K, (int)N, R0, R1, nparts, s, who)) != SFT_OK) return rc;
   const int nchunks_p = (int)(rank_pad(B) / kRanksPerBlock);
   const int64_t blocks = tile_sched_items_per_xcd(ntiles, 2 * nchunks_p) * kXcds;
