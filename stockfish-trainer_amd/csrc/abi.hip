@@ -54,7 +54,7 @@ int encode_features(const uint8_t *boards, const uint8_t *stm, int64_t B, const 
                     int32_t *count_b, hipStream_t s);
 size_t map_tiles_workspace(const ColMap &m, int64_t rows);
 size_t table_tiles_workspace(const ColMap &m, int64_t N);
-size_t fwd_pair_workspace(const ColMap &m, int64_t B, int K, int64_t N);
+size_t fwd_pair_workspace(const ColMap &m, int64_t B, int K, int64_t N, bool carry);
 int fwd_transform_f32(const int32_t *idx0, const int32_t *idx1, int64_t B, int K, const FoldSrc &src, int64_t N,
                       int L, int L1, const float *bias, const float *us, const int64_t *psqt_idx, float *l0,
                       float *psqt, void *saved, size_t saved_bytes, void *ws, size_t ws_bytes, hipStream_t s);
@@ -465,7 +465,7 @@ int sft_ft_pair_workspace_size(int64_t batch, int32_t max_active, int32_t num_bl
   const int rc = check_pair_shape("sft_ft_pair_workspace_size", batch, max_active, num_blocks, block_rows,
                                   block_virtual_rows, output_size, &N);
   if (rc != SFT_OK) return rc;
-  *fwd_bytes = fwd_pair_workspace(plain_map(output_size / 4), batch, max_active, N);
+  *fwd_bytes = fwd_pair_workspace(plain_map(output_size / 4), batch, max_active, N, true);
   *bwd_bytes = bwd_pair_workspace(batch, max_active, N, output_size);
   return SFT_OK;
 }
@@ -628,7 +628,7 @@ int sft_ft_transform_workspace_size(int64_t batch, int32_t max_active, int32_t n
   if (rc != SFT_OK || (rc = check_l1(who, output_size, l1)) != SFT_OK) return rc;
   const ColMap map = paired_map(output_size / 4, l1 / 8);
   *saved_bytes = 2 * map_tiles_workspace(map, batch);
-  *fwd_bytes = fwd_pair_workspace(map, batch, max_active, N);
+  *fwd_bytes = fwd_pair_workspace(map, batch, max_active, N, false);
   *bwd_bytes = bwd_transform_workspace(batch, max_active, N, output_size, l1);
   return SFT_OK;
 }

@@ -477,14 +477,19 @@ __device__ __forceinline__ int64_t rank_chunk(int64_t c, int64_t nchunks) {
 // XCD gathers both perspectives from a tile while it is in L2.  A
 // single-perspective call passes the same lists twice and nchunks_p = nchunks.
 // A chunk is 32 ranks, 8 per wave; the waves of a workgroup do not wait for
-// each other.
-template <bool EPI>
+// each other.  With table parts the sums carried from pass to pass go to
+// carry0 / carry1 (tile-major: tile t, position b at (t B + b) 8 chunks, one
+// aligned 128-byte line each; the epilogue's raw tiles serve instead under
+// EPI), not to the row-major outputs, whose 32-column slices straddle two
+// lines three times in four at L = 1048.
+template <bool EPI, bool PARTS>  // PARTS: nparts > 1
 __global__ __launch_bounds__(kBlock) void fwd_tiled_kernel(RankLists R0, RankLists R1, int N,
                                                            const f32x4 *__restrict__ Wt, ColMap map,
                                                            const f32x4 *__restrict__ bias, f32x4 *__restrict__ out0,
                                                            f32x4 *__restrict__ out1, FwdEpilogue epi, int kpad,
                                                            int ntiles, int nchunks, int nchunks_p, int part,
-                                                           int nparts) {
+                                                           int nparts, f32x4 *__restrict__ carry0,
+                                                           f32x4 *__restrict__ carry1, int64_t B) {
   constexpr int PPW = kWave / kTileCh;  // 8 ranks per wave
   extern __shared__ int smem[];         // 8 lists of kpad entries per wave
   TileItem it = tile_sched_item(blockIdx.x, ntiles, nchunks);
@@ -511,7 +516,7 @@ __global__ __launch_bounds__(kBlock) void fwd_tiled_kernel(RankLists R0, RankLis
   for (int u = 1; u < PPW; ++u) pos = g == u ? rp[u] : pos;
   int nmax, lo = 0;
   bool work = true, final_pass = true;
-  if (nparts == 1) {  // launch-uniform: whole lists
+  if (!PARTS) {  // whole lists
     i32x4 *dst = reinterpret_cast<i32x4 *>(list);
     if (R.narrow) {  // launch-uniform: 16-bit entries, widened
       const i32x4 *__restrict__ src =
@@ -550,17 +555,16 @@ __global__ __launch_bounds__(kBlock) void fwd_tiled_kernel(RankLists R0, RankLis
   wave_lds_barrier();
   f32x4 start = b4;
   f32x4 *__restrict__ raw = nullptr;
-  if (EPI) raw = (second ? epi.raw1 : epi.raw0) + ((int64_t)(pos < 0 ? 0 : pos) * ntiles + it.tile) * kTileCh + t;
-  if (lo > 0 && pos >= 0 && work) {  // the sum earlier passes left
-    if (EPI) start = *raw;
-    else if (colok) start = (second ? out1 : out0)[pos * cols4 + col4];
-  }
+  const int64_t pz = pos < 0 ? 0 : pos;
+  if (EPI) raw = (second ? epi.raw1 : epi.raw0) + (pz * ntiles + it.tile) * kTileCh + t;
+  else if (PARTS) raw = (second ? carry1 : carry0) + ((int64_t)it.tile * B + pz) * kTileCh + t;
+  if (PARTS && lo > 0 && pos >= 0 && work)  // the sum earlier passes left
+    start = EPI ? *raw : __builtin_nontemporal_load(raw);
   f32x4 acc = f32_tile_rows(list + g * kpad, nmax, tbase, lane_off, start);
   if (!colok) acc = f32x4{0.f, 0.f, 0.f, 0.f};  // padding lanes read unwritten chunks; their raw rows stay 0
   if (pos < 0 || !work) return;                 // a padding rank, or nothing to do in this pass
-  if (!final_pass) {
-    if (EPI) __builtin_nontemporal_store(acc, raw);
-    else if (colok) __builtin_nontemporal_store(acc, (second ? out1 : out0) + pos * cols4 + col4);
+  if (PARTS && !final_pass) {
+    __builtin_nontemporal_store(acc, raw);
     return;
   }
   if (!EPI) {
@@ -982,10 +986,13 @@ static int build_rank_lists(const int32_t *idx0, const int32_t *idx1, int np, in
 }
 
 // Table tiles (with their pad rows), then the rank lists of one perspective.
+// Table tiles, rank lists, then (table parts) the carried sums.
+static size_t carry_bytes(int64_t ntiles, int64_t B) { return align256((size_t)(ntiles * B) * kTileRowBytes); }
 size_t fwd_tiled_workspace(int64_t B, int K, int64_t N, int L) {
   if (L % 4 != 0) return 0;
   const int64_t ntiles = ceil_div(L, kTileF);
-  return align256((size_t)(ntiles * tile_rows(N) * kTileF) * sizeof(float)) + rank_lists_bytes(B, K);
+  return align256((size_t)(ntiles * tile_rows(N) * kTileF) * sizeof(float)) + rank_lists_bytes(B, K) +
+         (table_parts(N) > 1 ? carry_bytes(ntiles, B) : 0);
 }
 
 #ifndef SFT_FWD_TILE_MAX_BYTES
@@ -1017,8 +1024,9 @@ int fwd_f32_tiled(const int32_t *idx, int64_t B, int K, const float *W, int64_t 
   if (lds > kMaxIndexLds) return fail(SFT_EUNSUPPORTED, "sft_ft_fwd_f32_ex: max_active too large for the LDS index lists");
   f32x4 *wt = static_cast<f32x4 *>(ws);
   const int nparts = table_parts(N);
-  const RankLists R = rank_lists_at(static_cast<char *>(ws) + align256((size_t)(ntiles * tile_rows(N) * kTileF) * 4),
-                                    B, K, lists_narrow(K, N, nparts));
+  char *lists = static_cast<char *>(ws) + align256((size_t)(ntiles * tile_rows(N) * kTileF) * 4);
+  const RankLists R = rank_lists_at(lists, B, K, lists_narrow(K, N, nparts));
+  f32x4 *carry = nparts > 1 ? reinterpret_cast<f32x4 *>(lists + rank_lists_bytes(B, K)) : nullptr;
   {
     ProfScope prof(kProfFwdRelayout, s);
     launch_tile_relayout(reinterpret_cast<const f32x4 *>(W), N, cols4, wt, s);
@@ -1030,9 +1038,11 @@ int fwd_f32_tiled(const int32_t *idx, int64_t B, int K, const float *W, int64_t 
   const int64_t blocks = tile_sched_items_per_xcd(ntiles, nchunks) * kXcds;
   for (int part = 0; part < nparts; ++part) {
     ProfScope prof(kProfFwdTiled, s);
-    hipLaunchKernelGGL(fwd_tiled_kernel<false>, dim3((unsigned)blocks), dim3(kBlock), lds, s, R, R, (int)N, wt,
+    hipLaunchKernelGGL((nparts > 1 ? fwd_tiled_kernel<false, true> : fwd_tiled_kernel<false, false>),
+                       dim3((unsigned)blocks), dim3(kBlock), lds, s, R, R, (int)N, wt,
                        plain_map((int)cols4), reinterpret_cast<const f32x4 *>(bias), reinterpret_cast<f32x4 *>(out),
-                       reinterpret_cast<f32x4 *>(out), FwdEpilogue{}, kpad, ntiles, nchunks, nchunks, part, nparts);
+                       reinterpret_cast<f32x4 *>(out), FwdEpilogue{}, kpad, ntiles, nchunks, nchunks, part, nparts,
+                       carry, carry, B);
     if ((rc = check_launch("sft_ft_fwd_f32_ex (tiled gather)")) != SFT_OK) return rc;
   }
   return SFT_OK;
@@ -1042,9 +1052,11 @@ size_t map_tiles_workspace(const ColMap &m, int64_t rows) { return (size_t)map_t
 // The fp32 table tiles of a column map (with their pad rows).
 size_t table_tiles_workspace(const ColMap &m, int64_t N) { return map_tiles_workspace(m, tile_rows(N)); }
 // Forward workspace of a two-perspective call: the table tiles, then both
-// perspectives' rank lists.
-size_t fwd_pair_workspace(const ColMap &m, int64_t B, int K, int64_t N) {
-  return align256(table_tiles_workspace(m, N)) + 2 * rank_lists_bytes(B, K);
+// perspectives' rank lists, then (carry: plain outputs and table parts) both
+// perspectives' carried sums.
+size_t fwd_pair_workspace(const ColMap &m, int64_t B, int K, int64_t N, bool carry) {
+  return align256(table_tiles_workspace(m, N)) + 2 * rank_lists_bytes(B, K) +
+         (carry && table_parts(N) > 1 ? 2 * carry_bytes(map_tiles(m), B) : 0);
 }
 
 // Fold re-layout of the composed table into the workspace's tiles, rank lists
@@ -1062,6 +1074,11 @@ static int pair_gather(const int32_t *idx0, const int32_t *idx1, int64_t B, int 
   const int narrow = lists_narrow(K, N, nparts);
   const RankLists R0 = rank_lists_at(lists, B, K, narrow),
                   R1 = rank_lists_at(lists + rank_lists_bytes(B, K), B, K, narrow);
+  f32x4 *carry0 = nullptr, *carry1 = nullptr;
+  if (epi.l0 == nullptr && nparts > 1) {
+    carry0 = reinterpret_cast<f32x4 *>(lists + 2 * rank_lists_bytes(B, K));
+    carry1 = reinterpret_cast<f32x4 *>(lists + 2 * rank_lists_bytes(B, K) + carry_bytes(ntiles, B));
+  }
   if (lds > kMaxIndexLds) return fail(SFT_EUNSUPPORTED, std::string(who) + ": max_active too large for the LDS index lists");
   if (tile_rows(N) * (int64_t)kTileRowBytes > (int64_t)UINT32_MAX)
     return fail(SFT_EUNSUPPORTED, std::string(who) + ": more than 2^25 - 1 table rows");
@@ -1079,13 +1096,16 @@ static int pair_gather(const int32_t *idx0, const int32_t *idx1, int64_t B, int 
   for (int part = 0; part < nparts; ++part) {
     ProfScope prof(kProfFwdTiled, s);
     if (epi.l0 != nullptr)
-      hipLaunchKernelGGL(fwd_tiled_kernel<true>, dim3((unsigned)blocks), dim3(kBlock), lds, s, R0, R1, (int)N, wt,
+      hipLaunchKernelGGL((nparts > 1 ? fwd_tiled_kernel<true, true> : fwd_tiled_kernel<true, false>),
+                         dim3((unsigned)blocks), dim3(kBlock), lds, s, R0, R1, (int)N, wt,
                          map, reinterpret_cast<const f32x4 *>(bias), (f32x4 *)nullptr, (f32x4 *)nullptr, epi, kpad,
-                         ntiles, 2 * nchunks_p, nchunks_p, part, nparts);
+                         ntiles, 2 * nchunks_p, nchunks_p, part, nparts, carry0, carry1, B);
     else
-      hipLaunchKernelGGL(fwd_tiled_kernel<false>, dim3((unsigned)blocks), dim3(kBlock), lds, s, R0, R1, (int)N, wt,
+      hipLaunchKernelGGL((nparts > 1 ? fwd_tiled_kernel<false, true> : fwd_tiled_kernel<false, false>),
+                         dim3((unsigned)blocks), dim3(kBlock), lds, s, R0, R1, (int)N, wt,
                          map, reinterpret_cast<const f32x4 *>(bias), reinterpret_cast<f32x4 *>(out0),
-                         reinterpret_cast<f32x4 *>(out1), epi, kpad, ntiles, 2 * nchunks_p, nchunks_p, part, nparts);
+                         reinterpret_cast<f32x4 *>(out1), epi, kpad, ntiles, 2 * nchunks_p, nchunks_p, part, nparts,
+                         carry0, carry1, B);
     if ((rc = check_launch(who)) != SFT_OK) return rc;
   }
   return SFT_OK;
@@ -1094,7 +1114,7 @@ static int pair_gather(const int32_t *idx0, const int32_t *idx1, int64_t B, int 
 int fwd_pair_f32(const int32_t *idx0, const int32_t *idx1, int64_t B, int K, const FoldSrc &src, int64_t N, int L,
                  const float *bias, float *out0, float *out1, void *ws, size_t ws_bytes, hipStream_t s) {
   const ColMap map = plain_map(L / 4);
-  if (ws_bytes < fwd_pair_workspace(map, B, K, N) || ws == nullptr || (uintptr_t)ws % 256 != 0)
+  if (ws_bytes < fwd_pair_workspace(map, B, K, N, true) || ws == nullptr || (uintptr_t)ws % 256 != 0)
     return fail(SFT_EWORKSPACE, "sft_ft_fwd_pair_f32: workspace smaller than sft_ft_pair_workspace_size() "
                                 "or not 256-byte aligned");
   return pair_gather(idx0, idx1, B, K, src, N, map, bias, out0, out1, FwdEpilogue{}, ws, s, "sft_ft_fwd_pair_f32");
@@ -1108,7 +1128,7 @@ int fwd_transform_f32(const int32_t *idx0, const int32_t *idx1, int64_t B, int K
                       float *psqt, void *saved, size_t saved_bytes, void *ws, size_t ws_bytes, hipStream_t s) {
   const ColMap map = paired_map(L / 4, L1 / 8);
   const size_t raw_bytes = map_tiles_workspace(map, B);
-  if (ws_bytes < fwd_pair_workspace(map, B, K, N) || ws == nullptr || (uintptr_t)ws % 256 != 0 ||
+  if (ws_bytes < fwd_pair_workspace(map, B, K, N, false) || ws == nullptr || (uintptr_t)ws % 256 != 0 ||
       saved_bytes < 2 * raw_bytes || saved == nullptr || (uintptr_t)saved % 256 != 0)
     return fail(SFT_EWORKSPACE, "sft_ft_fwd_transform_f32: saved or workspace buffer smaller than "
                                 "sft_ft_transform_workspace_size() or not 256-byte aligned");

@@ -225,7 +225,9 @@ def test_pair_workspace_size_and_shape_checks():
     # Full_Threats + HalfKAv2_hm
     rc = lib.sft_ft_pair_workspace_size(65536, 160, 2, _i64s(60720, 24576), _i64s(0, 768), 1048, ctypes.byref(fb),
                                         ctypes.byref(bb))
-    assert rc == 0 and fb.value == _a256(33 * 85297 * 32 * 4) + 2 * rank_lists_bytes(65536, 160)
+    # three table parts: both perspectives' sums carried between the passes, one 128 B line per position and tile
+    assert rc == 0 and fb.value == (_a256(33 * 85297 * 32 * 4) + 2 * rank_lists_bytes(65536, 160) +
+                                    2 * _a256(33 * 65536 * 128))
     # shapes the fused path does not take
     rc = lib.sft_ft_pair_workspace_size(65536, 32, 1, _i64s(24576), _i64s(768), 136, ctypes.byref(fb), ctypes.byref(bb))
     assert rc == _native.SFT_EUNSUPPORTED and "output_size" in _native.last_error()

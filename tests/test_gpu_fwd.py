@@ -92,8 +92,9 @@ def test_tiled_workspace_query():
     assert _native._workspace_bytes("fwd", 65536, 32, 23232, 136, _native.SFT_FWD_AUTO, DEV) == \
         _a256(5 * 23233 * 32 * 4) + rank_lists_bytes(65536, 32)
     assert _native._workspace_bytes("fwd", 65536, 32, 23232, 96, _native.SFT_FWD_AUTO, DEV) == 0  # 3 tiles
+    # a table gathered in parts: then the sums carried between the passes, one 128-byte line per position and tile
     assert _native._workspace_bytes("fwd", 65536, 32, 85296, 1048, _native.SFT_FWD_AUTO, DEV) == \
-        _a256(33 * 85297 * 32 * 4) + rank_lists_bytes(65536, 32)
+        _a256(33 * 85297 * 32 * 4) + rank_lists_bytes(65536, 32) + _a256(33 * 65536 * 128)
     assert _native._workspace_bytes("fwd", 65536, 32, 600000, 1048, _native.SFT_FWD_AUTO, DEV) == 0  # tile > 64 MiB
     assert _native._workspace_bytes("fwd", 65536, 32, 23232, 1048, _native.SFT_FWD_ROWS, DEV) == 0
 
