@@ -341,10 +341,11 @@ __device__ __forceinline__ f32x4 f32_tile_rows(const int *mylist, int nmax, cons
 constexpr int kRanksPerBlock = kWavesPerBlock * (kWave / kTileCh);  // 32: 8 per wave
 constexpr int kRankSortBlock = kBlock;                               // positions ranked together
 struct RankLists {
-  int32_t *list;   // [Bpad][kpad] (narrow: uint16_t entries)
+  int32_t *list;   // [Bpad][kpad] (narrow: uint16_t entries); table parts: the packed runs
   int32_t *pos;    // [Bpad] rank -> position, -1 for padding
   int32_t *count;  // [Bpad] active slots of the rank's position, non-increasing within each 256 ranks
   i32x4 *cut;      // [Bpad] table parts (nparts > 1): see "Table parts" below
+  i32x4 *roff;     // [Bpad] table parts: where each pass's run of the rank starts in `list`
   int narrow;      // 16-bit list entries (STAGE builds only, nparts == 1)
 };
 struct RankArgs {
@@ -363,6 +364,12 @@ struct RankArgs {
 // position whose list goes back to an earlier part does all its adds in pass
 // 0.  cut[r] = {start of part 1, of part 2, of part 3, final pass}; lo_p =
 // (p == 0 ? 0 : cut[p - 1]), hi_p = (p == final ? count : cut[p]).
+// The runs are stored packed instead of the lists: within each block of 256
+// ranks, the runs of pass 0 for the ranks in rank order, then those of pass 1,
+// and so on (at most 256 kpad entries in all), and roff[r][p] gives where the
+// run of rank r for pass p starts -- so a pass reads only its runs, and a
+// wave's 8 runs lie together, instead of a stretch from the middle of each of
+// 8 padded list rows (Full_Threats: most of a pass's list bytes).
 constexpr int kMaxParts = 4;
 
 // One workgroup per 256 positions of one perspective (grid.y).  STAGE: the
@@ -371,7 +378,7 @@ constexpr int kMaxParts = 4;
 template <bool STAGE>
 __global__ __launch_bounds__(kBlock) void rank_lists_kernel(RankArgs a, int64_t B, int64_t Bpad, int K, int N,
                                                             int kpad, int vec) {
-  extern __shared__ int sm[];  // bins[K + 1] | offsets[K + 1] | (STAGE) 256 rows of kpad + 1
+  extern __shared__ int sm[];  // bins[K + 1] | offsets[K + 1] | (STAGE) 256 rows of kpad + 1 | (parts) run scans
   unsigned *bin = reinterpret_cast<unsigned *>(sm), *off = bin + (K + 1);
   int *rows = sm + 2 * (K + 1);
   const RankLists &L = a.L[blockIdx.y];
@@ -412,28 +419,76 @@ __global__ __launch_bounds__(kBlock) void rank_lists_kernel(RankArgs a, int64_t 
     L.pos[r] = real ? (int32_t)b : -1;
     L.count[r] = real ? c : 0;
   }
-  int *dst = STAGE ? rows + rl * (kpad + 1) : L.list + r * kpad;
-  if (STAGE || r < Bpad) {
-    int j = 0;
+  if (a.nparts > 1) {  // launch-uniform: packed runs (see "Table parts")
     int cut[kMaxParts - 1] = {c, c, c};
-    int part = 0;
+    int part = 0, j = 0;
     bool mono = true;
     if (real)
       for (int k = 0; k < K; ++k) {
         const int v = slot(k);
         if ((unsigned)v < (unsigned)N) {
-          if (a.nparts > 1) {
-            const int pv = v / a.part_rows;
-            mono = mono && pv >= part;
-            for (; part < pv; ++part)
-              if (part < kMaxParts - 1) cut[part] = j;
-          }
-          dst[j++] = v;
+          const int pv = v / a.part_rows;
+          mono = mono && pv >= part;
+          for (; part < pv; ++part)
+            if (part < kMaxParts - 1) cut[part] = j;
+          ++j;
         }
       }
+    const i32x4 cv = mono ? i32x4{cut[0], cut[1], cut[2], a.nparts - 1} : i32x4{c, c, c, 0};
+    int len[kMaxParts];
+#pragma unroll
+    for (int p = 0; p < kMaxParts; ++p) {
+      const int lo = p == 0 ? 0 : cv[p - 1];
+      const int hi = p == cv[3] ? c : (p < kMaxParts - 1 ? cv[p] : c);
+      len[p] = (p < a.nparts && p <= cv[3]) ? hi - lo : 0;
+    }
+    // exclusive scans of the run lengths in rank order, one per pass
+    int *scan = rows;  // [kMaxParts][kRankSortBlock]
+#pragma unroll
+    for (int p = 0; p < kMaxParts; ++p) scan[p * kRankSortBlock + rl] = len[p];
+    __syncthreads();
+    for (int d = 1; d < kRankSortBlock; d <<= 1) {
+      int v[kMaxParts];
+#pragma unroll
+      for (int p = 0; p < kMaxParts; ++p)
+        v[p] = scan[p * kRankSortBlock + tid] + (tid >= d ? scan[p * kRankSortBlock + tid - d] : 0);
+      __syncthreads();
+#pragma unroll
+      for (int p = 0; p < kMaxParts; ++p) scan[p * kRankSortBlock + tid] = v[p];
+      __syncthreads();
+    }
+    int start[kMaxParts];
+    int64_t pbase = base * kpad;  // this block's region of the runs
+#pragma unroll
+    for (int p = 0; p < kMaxParts; ++p) {
+      start[p] = (int)(pbase + scan[p * kRankSortBlock + rl] - len[p]);
+      pbase += scan[p * kRankSortBlock + kRankSortBlock - 1];
+    }
+    if (r < Bpad) {
+      L.cut[r] = cv;
+      L.roff[r] = i32x4{start[0], start[1], start[2], start[3]};
+    }
+    if (real) {
+      int w[kMaxParts] = {0, 0, 0, 0};
+      for (int k = 0; k < K; ++k) {
+        const int v = slot(k);
+        if ((unsigned)v < (unsigned)N) {
+          const int p = mono ? v / a.part_rows : 0;
+          L.list[start[p] + w[p]++] = v;
+        }
+      }
+    }
+    return;
+  }
+  int *dst = STAGE ? rows + rl * (kpad + 1) : L.list + r * kpad;
+  if (STAGE || r < Bpad) {
+    int j = 0;
+    if (real)
+      for (int k = 0; k < K; ++k) {
+        const int v = slot(k);
+        if ((unsigned)v < (unsigned)N) dst[j++] = v;
+      }
     for (; j < kpad; ++j) dst[j] = N;
-    if (a.nparts > 1 && r < Bpad)
-      L.cut[r] = mono ? i32x4{cut[0], cut[1], cut[2], a.nparts - 1} : i32x4{c, c, c, 0};
   }
   if (STAGE && L.narrow) {  // entries <= N <= 65535
     __syncthreads();
@@ -548,7 +603,8 @@ __global__ __launch_bounds__(kBlock) void fwd_tiled_kernel(RankLists R0, RankLis
 #pragma unroll
     for (int off = kTileCh; off < kWave; off <<= 1) mx = max(mx, __shfl_xor(mx, off));
     nmax = uniform(mx);
-    const int32_t *__restrict__ src = R.list + r * kpad + lo;
+    const i32x4 ro = R.roff[r];
+    const int32_t *__restrict__ src = R.list + (part == 0 ? ro[0] : (part == 1 ? ro[1] : (part == 2 ? ro[2] : ro[3])));
     int *dst = list + g * kpad;
     for (int j = t; j < round_up4(nmax); j += kTileCh) dst[j] = j < len ? src[j] : N;
   }
@@ -923,7 +979,7 @@ static int64_t rank_pad(int64_t B) { return ceil_div(B, (int64_t)kRanksPerBlock)
 // One perspective's rank lists, each array 256-byte aligned.
 size_t rank_lists_bytes(int64_t B, int K) {
   const int64_t Bp = rank_pad(B);
-  return align256((size_t)(Bp * round_up4(K)) * 4) + 2 * align256((size_t)Bp * 4) + align256((size_t)Bp * 16);
+  return align256((size_t)(Bp * round_up4(K)) * 4) + 2 * align256((size_t)Bp * 4) + 2 * align256((size_t)Bp * 16);
 }
 static RankLists rank_lists_at(char *p, int64_t B, int K, int narrow) {
   const int64_t Bp = rank_pad(B);
@@ -936,6 +992,8 @@ static RankLists rank_lists_at(char *p, int64_t B, int K, int narrow) {
   r.count = reinterpret_cast<int32_t *>(p);
   p += align256((size_t)Bp * 4);
   r.cut = reinterpret_cast<i32x4 *>(p);
+  p += align256((size_t)Bp * 16);
+  r.roff = reinterpret_cast<i32x4 *>(p);
   return r;
 }
 
@@ -973,9 +1031,13 @@ static int build_rank_lists(const int32_t *idx0, const int32_t *idx1, int np, in
   const int kpad = round_up4(K);
   const int vec = K % 4 == 0 && (uintptr_t)idx0 % 16 == 0 && (uintptr_t)idx1 % 16 == 0;
   const bool stage = kpad <= kRankStageMaxPad;
+  if (nparts > 1 && Bp * kpad > (int64_t)INT32_MAX)
+    return fail(SFT_EUNSUPPORTED, std::string(who) + ": batch x max_active too large for the packed table-part runs");
   if ((R0.narrow || R1.narrow) && (!stage || kpad % 8 != 0 || N > 65535))
     return fail(SFT_EINVAL, std::string(who) + ": 16-bit rank lists need staged lists of 8-entry pieces");
-  const size_t lds = (size_t)(2 * (K + 1)) * 4 + (stage ? (size_t)kRankSortBlock * (kpad + 1) * 4 : 0);
+  const size_t rows_lds = stage ? (size_t)kRankSortBlock * (kpad + 1) * 4 : 0;
+  const size_t scan_lds = nparts > 1 ? (size_t)kMaxParts * kRankSortBlock * 4 : 0;  // run scans, over the rows
+  const size_t lds = (size_t)(2 * (K + 1)) * 4 + std::max(rows_lds, scan_lds);
   const dim3 grid((unsigned)ceil_div(Bp, (int64_t)kRankSortBlock), (unsigned)np);
   ProfScope prof(kProfFwdRanks, s);
   if (stage)

@@ -207,10 +207,10 @@ def _a256(v):
 def rank_lists_bytes(B, K):
     """The forward's rank lists of one perspective: [Bpad][kpad] lists, two
     [Bpad] int32 arrays (position, count) and the [Bpad] 16-byte table-part
-    cuts, each 256-byte aligned; Bpad = B rounded up to 32, kpad = K rounded up
-    to 4."""
+    cuts and run offsets, each 256-byte aligned; Bpad = B rounded up to 32,
+    kpad = K rounded up to 4."""
     bp, kpad = -(-B // 32) * 32, -(-K // 4) * 4
-    return _a256(bp * kpad * 4) + 2 * _a256(bp * 4) + _a256(bp * 16)
+    return _a256(bp * kpad * 4) + 2 * _a256(bp * 4) + 2 * _a256(bp * 16)
 
 
 def test_pair_workspace_size_and_shape_checks():
