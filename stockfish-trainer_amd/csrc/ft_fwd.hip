@@ -391,8 +391,21 @@ __global__ __launch_bounds__(kBlock) void rank_lists_kernel(RankArgs a, int64_t 
   auto slot = [&](int k) { return row[k]; };
   for (int i = tid; i <= K; i += kBlock) bin[i] = 0u;
   __syncthreads();
+  // Rows of up to 32 slots (staged, 16-byte aligned) are loaded once, into
+  // registers, for both the count and the list.
+  constexpr int kRegRow = 8;  // 16-byte pieces: the staged kpad <= 32
+  const bool regrow = STAGE && vec && K <= 4 * kRegRow;
+  i32x4 rv[kRegRow];
   int c = 0;
-  if (real) {
+  if (regrow) {
+#pragma unroll
+    for (int u = 0; u < kRegRow; ++u)
+      rv[u] = (real && 4 * u < K) ? *reinterpret_cast<const i32x4 *>(row + 4 * u) : i32x4{-1, -1, -1, -1};
+#pragma unroll
+    for (int u = 0; u < kRegRow; ++u)
+      c += ((unsigned)rv[u][0] < (unsigned)N) + ((unsigned)rv[u][1] < (unsigned)N) +
+           ((unsigned)rv[u][2] < (unsigned)N) + ((unsigned)rv[u][3] < (unsigned)N);
+  } else if (real) {
     if (vec) {
       for (int k = 0; k < K; k += 4) {
         const i32x4 v = *reinterpret_cast<const i32x4 *>(row + k);
@@ -483,11 +496,18 @@ __global__ __launch_bounds__(kBlock) void rank_lists_kernel(RankArgs a, int64_t 
   int *dst = STAGE ? rows + rl * (kpad + 1) : L.list + r * kpad;
   if (STAGE || r < Bpad) {
     int j = 0;
-    if (real)
+    if (regrow) {
+#pragma unroll
+      for (int u = 0; u < kRegRow; ++u)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if ((unsigned)rv[u][e] < (unsigned)N) dst[j++] = rv[u][e];
+    } else if (real) {
       for (int k = 0; k < K; ++k) {
         const int v = slot(k);
         if ((unsigned)v < (unsigned)N) dst[j++] = v;
       }
+    }
     for (; j < kpad; ++j) dst[j] = N;
   }
   if (STAGE && L.narrow) {  // entries <= N <= 65535
@@ -1011,6 +1031,7 @@ static int part_rows_of(int64_t N, int nparts) { return (int)ceil_div(std::max<i
 static size_t rank_lds_bytes(int K) { return (size_t)kRanksPerBlock * round_up4(K) * sizeof(int); }
 // Lists staged in LDS up to kpad = 32 (33 KB); longer ones are stored by their threads.
 constexpr int kRankStageMaxPad = 32;
+static_assert(kRankStageMaxPad == 32, "rank_lists_kernel holds a staged row in 8 16-byte registers");
 // 16-bit lists: one table pass, entries up to N <= 65535, staged rows of 8-entry pieces.
 static int lists_narrow(int K, int64_t N, int nparts) {
   const int kpad = round_up4(K);
