@@ -352,6 +352,7 @@ struct RankArgs {
   const int32_t *idx[2];
   RankLists L[2];
   int nparts, part_rows;
+  FastDiv part_of;  // v / part_rows
 };
 
 // ---- table parts ----
@@ -418,11 +419,19 @@ __global__ __launch_bounds__(kBlock) void rank_lists_kernel(RankArgs a, int64_t 
   }
   const unsigned mine = real ? atomicAdd(&bin[c], 1u) : 0u;
   __syncthreads();
-  if (tid == 0) {
-    unsigned acc = 0u;
-    for (int cc = K; cc >= 0; --cc) {
-      off[cc] = acc;
-      acc += bin[cc];
+  if (tid < kWave) {  // off[cc] = sum of bin[cc + 1 .. K]: wave 0, 64 bins per step, largest count first
+    unsigned carry = 0u;
+    for (int top = K; top >= 0; top -= kWave) {
+      const int cc = top - tid;
+      const unsigned v = cc >= 0 ? bin[cc] : 0u;
+      unsigned incl = v;  // inclusive scan over lanes 0 .. tid (bins top .. cc)
+#pragma unroll
+      for (int d = 1; d < kWave; d <<= 1) {
+        const unsigned o = __shfl_up(incl, d);
+        if (tid >= d) incl += o;
+      }
+      if (cc >= 0) off[cc] = carry + incl - v;
+      carry += __shfl(incl, kWave - 1);
     }
   }
   __syncthreads();
@@ -433,20 +442,34 @@ __global__ __launch_bounds__(kBlock) void rank_lists_kernel(RankArgs a, int64_t 
     L.count[r] = real ? c : 0;
   }
   if (a.nparts > 1) {  // launch-uniform: packed runs (see "Table parts")
+    // fn(v) for the row's active slots in slot order (16-byte loads, several in flight)
+    auto each_active = [&](auto &&fn) {
+      if (!real) return;
+      if (vec) {
+#pragma unroll 4
+        for (int k = 0; k < K; k += 4) {
+          const i32x4 v4 = *reinterpret_cast<const i32x4 *>(row + k);
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if ((unsigned)v4[e] < (unsigned)N) fn(v4[e]);
+        }
+      } else {
+        for (int k = 0; k < K; ++k) {
+          const int v = slot(k);
+          if ((unsigned)v < (unsigned)N) fn(v);
+        }
+      }
+    };
     int cut[kMaxParts - 1] = {c, c, c};
     int part = 0, j = 0;
     bool mono = true;
-    if (real)
-      for (int k = 0; k < K; ++k) {
-        const int v = slot(k);
-        if ((unsigned)v < (unsigned)N) {
-          const int pv = v / a.part_rows;
-          mono = mono && pv >= part;
-          for (; part < pv; ++part)
-            if (part < kMaxParts - 1) cut[part] = j;
-          ++j;
-        }
-      }
+    each_active([&](int v) {
+      const int pv = (int)a.part_of((uint32_t)v);
+      mono = mono && pv >= part;
+      for (; part < pv; ++part)
+        if (part < kMaxParts - 1) cut[part] = j;
+      ++j;
+    });
     const i32x4 cv = mono ? i32x4{cut[0], cut[1], cut[2], a.nparts - 1} : i32x4{c, c, c, 0};
     int len[kMaxParts];
 #pragma unroll
@@ -481,16 +504,12 @@ __global__ __launch_bounds__(kBlock) void rank_lists_kernel(RankArgs a, int64_t 
       L.cut[r] = cv;
       L.roff[r] = i32x4{start[0], start[1], start[2], start[3]};
     }
-    if (real) {
-      int w[kMaxParts] = {0, 0, 0, 0};
-      for (int k = 0; k < K; ++k) {
-        const int v = slot(k);
-        if ((unsigned)v < (unsigned)N) {
-          const int p = mono ? v / a.part_rows : 0;
-          L.list[start[p] + w[p]++] = v;
-        }
-      }
-    }
+    int w[kMaxParts] = {0, 0, 0, 0};
+    each_active([&](int v) {
+      const int p = mono ? (int)a.part_of((uint32_t)v) : 0;
+      const int at = p == 0 ? start[0] + w[0]++ : p == 1 ? start[1] + w[1]++ : p == 2 ? start[2] + w[2]++ : start[3] + w[3]++;
+      L.list[at] = v;
+    });
     return;
   }
   int *dst = STAGE ? rows + rl * (kpad + 1) : L.list + r * kpad;
@@ -502,6 +521,14 @@ __global__ __launch_bounds__(kBlock) void rank_lists_kernel(RankArgs a, int64_t 
 #pragma unroll
         for (int e = 0; e < 4; ++e)
           if ((unsigned)rv[u][e] < (unsigned)N) dst[j++] = rv[u][e];
+    } else if (real && vec) {
+#pragma unroll 4
+      for (int k = 0; k < K; k += 4) {
+        const i32x4 v4 = *reinterpret_cast<const i32x4 *>(row + k);
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if ((unsigned)v4[e] < (unsigned)N) dst[j++] = v4[e];
+      }
     } else if (real) {
       for (int k = 0; k < K; ++k) {
         const int v = slot(k);
@@ -1048,6 +1075,7 @@ static int build_rank_lists(const int32_t *idx0, const int32_t *idx1, int np, in
   a.L[1] = R1;
   a.nparts = nparts;
   a.part_rows = part_rows_of(N, nparts);
+  a.part_of = FastDiv((uint32_t)a.part_rows);
   const int64_t Bp = rank_pad(B);
   const int kpad = round_up4(K);
   const int vec = K % 4 == 0 && (uintptr_t)idx0 % 16 == 0 && (uintptr_t)idx1 % 16 == 0;
