@@ -259,6 +259,29 @@ int sft_ft_fwd_i16_packed(const int32_t *idx0, const int32_t *idx1, int64_t batc
                           void *stream);
 
 /*
+ * Bytes of device workspace sft_ft_fwd_i16_packed_ex uses for a batch of
+ * `perspectives` (1 or 2) index matrices [batch, max_active]: the per-call
+ * rank lists of the gather.  Host-only computation.
+ */
+int sft_ft_fwd_i16_packed_workspace_size(int64_t batch, int32_t max_active, int32_t perspectives,
+                                         size_t *bytes);
+
+/*
+ * sft_ft_fwd_i16_packed with a workspace (256-byte aligned, at least
+ * sft_ft_fwd_i16_packed_workspace_size() bytes): the same arguments, checks and
+ * results, bit for bit.  Each perspective's index rows are turned once into
+ * lists ranked by active count (16-bit entries for tables of up to 65 535
+ * rows), which every column tile pass then reads, instead of compacting the
+ * index rows again for each tile.  No reference counterpart.
+ */
+int sft_ft_fwd_i16_packed_ex(const int32_t *idx0, const int32_t *idx1, int64_t batch,
+                             int32_t max_active, const void *packed, size_t packed_bytes,
+                             int64_t num_inputs, int32_t output_size, const int16_t *bias,
+                             int32_t psqt_size, int16_t *out0, int16_t *out1, int32_t *psqt_out0,
+                             int32_t *psqt_out1, int32_t clip_lo, int32_t clip_hi, void *workspace,
+                             size_t workspace_bytes, uint32_t flags, void *stream);
+
+/*
  * ---- Composed table, both perspectives in one call ----
  * The table is num_blocks (1..4) row blocks concatenated in order (the feature
  * sets of a composed transformer, FEAT/composed.py:49-50).  Block s has

@@ -30,6 +30,11 @@ int i16_pack(const int16_t *W, int64_t N, int L, const int32_t *psqt, int P, voi
 int fwd_i16_packed(const int32_t *idx0, const int32_t *idx1, int64_t B, int K, const void *packed, int64_t N, int L,
                    const int16_t *bias, int P, int16_t *out0, int16_t *out1, int32_t *psqt_out0, int32_t *psqt_out1,
                    int lo, int hi, int wrap16, hipStream_t s, const char *who);
+size_t fwd_i16_ranked_workspace(int64_t B, int K, int persp);
+int fwd_i16_packed_ranked(const int32_t *idx0, const int32_t *idx1, int64_t B, int K, const void *packed, int64_t N,
+                          int L, const int16_t *bias, int P, int16_t *out0, int16_t *out1, int32_t *psqt_out0,
+                          int32_t *psqt_out1, int lo, int hi, int wrap16, void *ws, size_t ws_bytes, hipStream_t s,
+                          const char *who);
 int bwd_f32(const int32_t *idx, int64_t B, int K, const float *grad, int64_t N, int L, float *dW, float *db,
             void *ws, size_t ws_bytes, uint32_t flags, hipStream_t s, void *prep = nullptr, size_t prep_bytes = 0);
 int bwd_prep_bytes(int64_t B, int K, int64_t N, int L, uint32_t flags, size_t *bytes);
@@ -824,14 +829,13 @@ int sft_ft_i16_pack(const int16_t *weight, int64_t num_inputs, int32_t output_si
                   "sft_ft_i16_pack");
 }
 
-int sft_ft_fwd_i16_packed(const int32_t *idx0, const int32_t *idx1, int64_t batch, int32_t max_active,
-                          const void *packed, size_t packed_bytes, int64_t num_inputs, int32_t output_size,
-                          const int16_t *bias,
-                          int32_t psqt_size, int16_t *out0, int16_t *out1, int32_t *psqt_out0, int32_t *psqt_out1,
-                          int32_t clip_lo, int32_t clip_hi, uint32_t flags, void *stream) {
-  clear_error();
+// The checks both packed-table forwards make before anything runs.
+static int check_i16_packed_call(const char *w, const int32_t *idx0, const int32_t *idx1, int64_t batch,
+                                 int32_t max_active, const void *packed, size_t packed_bytes, int64_t num_inputs,
+                                 int32_t output_size, const int16_t *bias, int32_t psqt_size, int16_t *out0,
+                                 int16_t *out1, int32_t *psqt_out0, int32_t *psqt_out1, int32_t clip_lo,
+                                 int32_t clip_hi, uint32_t flags) {
   std::string why;
-  const char *w = "sft_ft_fwd_i16_packed";
   if (bad_sizes(batch, max_active, num_inputs, output_size, why)) return fail(SFT_EINVAL, std::string(w) + ": " + why);
   if (max_active >= 65536) return fail(SFT_EINVAL, std::string(w) + ": max_active must be < 65536");
   if (!packed || !bias) return fail(SFT_EINVAL, std::string(w) + ": null pointer");
@@ -848,9 +852,48 @@ int sft_ft_fwd_i16_packed(const int32_t *idx0, const int32_t *idx1, int64_t batc
                                                    "or bias / outputs not 16-byte aligned");
   if (packed_bytes < fwd_i16_tiled_workspace(num_inputs, output_size, psqt_size))
     return fail(SFT_EINVAL, std::string(w) + ": packed_bytes smaller than sft_ft_i16_packed_size() for these sizes");
+  return SFT_OK;
+}
+
+int sft_ft_fwd_i16_packed(const int32_t *idx0, const int32_t *idx1, int64_t batch, int32_t max_active,
+                          const void *packed, size_t packed_bytes, int64_t num_inputs, int32_t output_size,
+                          const int16_t *bias,
+                          int32_t psqt_size, int16_t *out0, int16_t *out1, int32_t *psqt_out0, int32_t *psqt_out1,
+                          int32_t clip_lo, int32_t clip_hi, uint32_t flags, void *stream) {
+  clear_error();
+  const char *w = "sft_ft_fwd_i16_packed";
+  const int rc = check_i16_packed_call(w, idx0, idx1, batch, max_active, packed, packed_bytes, num_inputs, output_size,
+                                       bias, psqt_size, out0, out1, psqt_out0, psqt_out1, clip_lo, clip_hi, flags);
+  if (rc != SFT_OK) return rc;
   return fwd_i16_packed(idx0, idx1, batch, max_active, packed, num_inputs, output_size, bias, psqt_size, out0, out1,
                         psqt_size > 0 ? psqt_out0 : nullptr, psqt_size > 0 ? psqt_out1 : nullptr, clip_lo, clip_hi,
                         (flags & SFT_Q16_WRAP16) ? 1 : 0, (hipStream_t)stream, w);
+}
+
+int sft_ft_fwd_i16_packed_workspace_size(int64_t batch, int32_t max_active, int32_t perspectives, size_t *bytes) {
+  clear_error();
+  if (!bytes) return fail(SFT_EINVAL, "sft_ft_fwd_i16_packed_workspace_size: null pointer");
+  if (batch < 0 || max_active < 0 || max_active >= 65536 || (perspectives != 1 && perspectives != 2))
+    return fail(SFT_EINVAL, "sft_ft_fwd_i16_packed_workspace_size: need batch >= 0, 0 <= max_active < 65536 and "
+                            "perspectives 1 or 2");
+  *bytes = fwd_i16_ranked_workspace(batch, max_active, perspectives);
+  return SFT_OK;
+}
+
+int sft_ft_fwd_i16_packed_ex(const int32_t *idx0, const int32_t *idx1, int64_t batch, int32_t max_active,
+                             const void *packed, size_t packed_bytes, int64_t num_inputs, int32_t output_size,
+                             const int16_t *bias, int32_t psqt_size, int16_t *out0, int16_t *out1, int32_t *psqt_out0,
+                             int32_t *psqt_out1, int32_t clip_lo, int32_t clip_hi, void *workspace,
+                             size_t workspace_bytes, uint32_t flags, void *stream) {
+  clear_error();
+  const char *w = "sft_ft_fwd_i16_packed_ex";
+  const int rc = check_i16_packed_call(w, idx0, idx1, batch, max_active, packed, packed_bytes, num_inputs, output_size,
+                                       bias, psqt_size, out0, out1, psqt_out0, psqt_out1, clip_lo, clip_hi, flags);
+  if (rc != SFT_OK) return rc;
+  return fwd_i16_packed_ranked(idx0, idx1, batch, max_active, packed, num_inputs, output_size, bias, psqt_size, out0,
+                               out1, psqt_size > 0 ? psqt_out0 : nullptr, psqt_size > 0 ? psqt_out1 : nullptr,
+                               clip_lo, clip_hi, (flags & SFT_Q16_WRAP16) ? 1 : 0, workspace, workspace_bytes,
+                               (hipStream_t)stream, w);
 }
 
 int sft_quantize_i16(const float *x, int64_t n, float scale, int16_t *out, void *stream) {

@@ -574,6 +574,26 @@ __device__ __forceinline__ int64_t rank_chunk(int64_t c, int64_t nchunks) {
   return (c2 % (nb - 1)) * kChunksPerSortBlock + last + c2 / (nb - 1);
 }
 
+// The whole lists of ranks r0 .. r0 + 7 (a wave's 8, padded to kpad) into the
+// wave's LDS lists, 16-bit entries widened to ints.
+__device__ __forceinline__ void stage_rank_lists(const RankLists &R, int64_t r0, int kpad, int *list, int lane) {
+  constexpr int PPW = kWave / kTileCh;
+  i32x4 *dst = reinterpret_cast<i32x4 *>(list);
+  if (R.narrow) {  // launch-uniform
+    const i32x4 *__restrict__ src =
+        reinterpret_cast<const i32x4 *>(reinterpret_cast<const uint16_t *>(R.list) + r0 * kpad);
+    for (int j = lane; j < PPW * kpad / 8; j += kWave) {
+      const i32x4 v = src[j];
+      const uint32_t w0 = (uint32_t)v[0], w1 = (uint32_t)v[1], w2 = (uint32_t)v[2], w3 = (uint32_t)v[3];
+      dst[2 * j] = i32x4{(int)(w0 & 0xffffu), (int)(w0 >> 16), (int)(w1 & 0xffffu), (int)(w1 >> 16)};
+      dst[2 * j + 1] = i32x4{(int)(w2 & 0xffffu), (int)(w2 >> 16), (int)(w3 & 0xffffu), (int)(w3 >> 16)};
+    }
+  } else {
+    const i32x4 *__restrict__ src = reinterpret_cast<const i32x4 *>(R.list + r0 * kpad);
+    for (int j = lane; j < PPW * kpad / 4; j += kWave) dst[j] = src[j];
+  }
+}
+
 // Two perspectives share one launch: chunks [0, nchunks_p) read the rank
 // lists R0 and write out0, chunks [nchunks_p, 2 nchunks_p) R1 and out1, so an
 // XCD gathers both perspectives from a tile while it is in L2.  A
@@ -619,20 +639,7 @@ __global__ __launch_bounds__(kBlock) void fwd_tiled_kernel(RankLists R0, RankLis
   int nmax, lo = 0;
   bool work = true, final_pass = true;
   if (!PARTS) {  // whole lists
-    i32x4 *dst = reinterpret_cast<i32x4 *>(list);
-    if (R.narrow) {  // launch-uniform: 16-bit entries, widened
-      const i32x4 *__restrict__ src =
-          reinterpret_cast<const i32x4 *>(reinterpret_cast<const uint16_t *>(R.list) + r0 * kpad);
-      for (int j = lane; j < PPW * kpad / 8; j += kWave) {
-        const i32x4 v = src[j];
-        const uint32_t w0 = (uint32_t)v[0], w1 = (uint32_t)v[1], w2 = (uint32_t)v[2], w3 = (uint32_t)v[3];
-        dst[2 * j] = i32x4{(int)(w0 & 0xffffu), (int)(w0 >> 16), (int)(w1 & 0xffffu), (int)(w1 >> 16)};
-        dst[2 * j + 1] = i32x4{(int)(w2 & 0xffffu), (int)(w2 >> 16), (int)(w3 & 0xffffu), (int)(w3 >> 16)};
-      }
-    } else {
-      const i32x4 *__restrict__ src = reinterpret_cast<const i32x4 *>(R.list + r0 * kpad);
-      for (int j = lane; j < PPW * kpad / 4; j += kWave) dst[j] = src[j];
-    }
+    stage_rank_lists(R, r0, kpad, list, lane);
     nmax = R.count[r0];  // counts fall with rank within each 256 ranks: the wave's longest list
   } else {
     // this pass's run [lo, hi) of each list (table parts, above), padded with
@@ -859,6 +866,71 @@ __global__ __launch_bounds__(kBlock) void fwd_i16_tiled_kernel(const int32_t *__
       }
     }
     wave_lds_barrier();
+  }
+}
+
+// The int16 gather over rank lists (sft_ft_fwd_i16_packed_ex): the packed
+// 64-column tiles of fwd_i16_tiled_kernel, gathered from the lists the fp32
+// tiled gather uses (rank_lists_kernel, built once per call for both
+// perspectives, 16-bit entries for tables of up to 65 535 rows) instead of
+// compacting every position's index row again for each of the 17 column tiles.
+// A wave's 8 ranks hold nearly the same number of rows: it steps its longest
+// list with an unmasked loop up to its shortest.  The packed table has no pad
+// row, so the entries past a rank's count are masked.
+__global__ __launch_bounds__(kBlock) void fwd_i16_ranked_kernel(RankLists R0, RankLists R1, int N,
+                                                                const i16x8 *__restrict__ Wt, int64_t cols8, int pch,
+                                                                const i16x8 *__restrict__ bias, int P,
+                                                                i16x8 *__restrict__ out0, i16x8 *__restrict__ out1,
+                                                                int32_t *__restrict__ psqt_out0,
+                                                                int32_t *__restrict__ psqt_out1, int clip_lo,
+                                                                int clip_hi, int wrap16, int kpad, int ntiles,
+                                                                int nchunks, int nchunks_p) {
+  constexpr int PPW = kWave / kTileCh;  // 8 ranks per wave
+  extern __shared__ int smem[];         // 8 lists of kpad entries per wave
+  TileItem it = tile_sched_item(blockIdx.x, ntiles, nchunks);
+  if (it.tile >= ntiles) return;  // whole block: uniform
+  const bool second = it.chunk >= nchunks_p;  // block-uniform
+  if (second) it.chunk -= nchunks_p;
+  const RankLists R = second ? R1 : R0;
+  i16x8 *__restrict__ out = second ? out1 : out0;
+  int32_t *__restrict__ psqt_out = second ? psqt_out1 : psqt_out0;
+  const int wave = uniform(threadIdx.x / kWave);
+  const int lane = threadIdx.x % kWave;
+  const int g = lane / kTileCh, t = lane % kTileCh;
+  const int64_t col = (int64_t)it.tile * kTileCh + t;
+  const bool colok = col < cols8;
+  const bool is_psqt = !colok && col < cols8 + pch;
+  const int pj = (int)(col - cols8) * 4;                        // first PSQT column of a PSQT lane
+  const bool mixed = (int64_t)(it.tile + 1) * kTileCh > cols8;  // block-uniform
+  const char *tbase = reinterpret_cast<const char *>(Wt + (int64_t)it.tile * N * kTileCh);
+  const uint32_t lane_off = (uint32_t)t * (uint32_t)sizeof(i16x8);
+  const i32x8 b8 = colok ? Q16<i16x8>::widen(bias[col]) : (i32x8)0;
+
+  const int64_t r0 = rank_chunk(it.chunk, nchunks_p) * kRanksPerBlock + wave * PPW;  // the wave's first rank
+  int *list = smem + wave * PPW * kpad;
+  const int32_t *__restrict__ rp = R.pos + r0;
+  const int32_t *__restrict__ rc = R.count + r0;
+  int pos = rp[0], n = rc[0];
+#pragma unroll
+  for (int u = 1; u < PPW; ++u) {
+    pos = g == u ? rp[u] : pos;
+    n = g == u ? rc[u] : n;
+  }
+  const int nmax = uniform(rc[0]), nmin = uniform(rc[PPW - 1]);  // counts fall with rank within each 256 ranks
+  stage_rank_lists(R, r0, kpad, list, lane);
+  wave_lds_barrier();
+  const int *mylist = list + g * kpad;
+  i32x8 acc = b8;
+  if (mixed)
+    i16_tile_rows<true>(mylist, n, nmin, nmax, tbase, lane_off, colok || is_psqt, is_psqt, acc);
+  else
+    i16_tile_rows<false>(mylist, n, nmin, nmax, tbase, lane_off, true, false, acc);
+  if (pos < 0) return;  // a padding rank
+  if (colok) __builtin_nontemporal_store(Q16<i16x8>::finish(acc, clip_lo, clip_hi, wrap16), out + pos * cols8 + col);
+  if (is_psqt) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (pj + e < P) psqt_out[(int64_t)pos * P + pj + e] = acc[e];
   }
 }
 
@@ -1309,6 +1381,44 @@ int fwd_i16_packed(const int32_t *idx0, const int32_t *idx1, int64_t B, int K, c
                        nchunks_p);
   }
   return check_launch((std::string(who) + " (tiled gather)").c_str());
+}
+
+// Workspace of the ranked int16 gather: the rank lists of each perspective.
+size_t fwd_i16_ranked_workspace(int64_t B, int K, int persp) { return (size_t)persp * rank_lists_bytes(B, K); }
+
+// fwd_i16_packed over rank lists built in the workspace (fwd_i16_ranked_kernel).
+int fwd_i16_packed_ranked(const int32_t *idx0, const int32_t *idx1, int64_t B, int K, const void *packed, int64_t N,
+                          int L, const int16_t *bias, int P, int16_t *out0, int16_t *out1, int32_t *psqt_out0,
+                          int32_t *psqt_out1, int lo, int hi, int wrap16, void *ws, size_t ws_bytes, hipStream_t s,
+                          const char *who) {
+  const int persp = idx1 != nullptr ? 2 : 1;
+  if (ws_bytes < fwd_i16_ranked_workspace(B, K, persp) || ws == nullptr || (uintptr_t)ws % 256 != 0)
+    return fail(SFT_EWORKSPACE, std::string(who) + ": workspace smaller than sft_ft_fwd_i16_packed_workspace_size() "
+                                                   "or not 256-byte aligned");
+  const int cols8 = L / 8;
+  const int pch = i16_psqt_chunks(P);
+  const int ntiles = (int)ceil_div(cols8 + pch, kTileCh);
+  const int kpad = round_up4(K);
+  const size_t lds = rank_lds_bytes(K);
+  if (lds > kMaxIndexLds) return fail(SFT_EUNSUPPORTED, std::string(who) + ": max_active too large for the LDS index lists");
+  if (B == 0) return SFT_OK;
+  const int narrow = lists_narrow(K, N, 1);
+  char *w = static_cast<char *>(ws);
+  const RankLists R0 = rank_lists_at(w, B, K, narrow);
+  const RankLists R1 = persp == 2 ? rank_lists_at(w + rank_lists_bytes(B, K), B, K, narrow) : R0;
+  int rc = build_rank_lists(idx0, persp == 2 ? idx1 : idx0, persp, B, K, (int)N, R0, R1, 1, s, who);
+  if (rc != SFT_OK) return rc;
+  const int nchunks_p = (int)(rank_pad(B) / kRanksPerBlock);
+  const int64_t blocks = tile_sched_items_per_xcd(ntiles, persp * nchunks_p) * kXcds;
+  {
+    ProfScope prof(kProfFwdI16Tiled, s);
+    hipLaunchKernelGGL(fwd_i16_ranked_kernel, dim3((unsigned)blocks), dim3(kBlock), lds, s, R0, R1, (int)N,
+                       static_cast<const i16x8 *>(packed), (int64_t)cols8, pch, reinterpret_cast<const i16x8 *>(bias),
+                       P, reinterpret_cast<i16x8 *>(out0), reinterpret_cast<i16x8 *>(persp == 2 ? out1 : out0),
+                       psqt_out0, persp == 2 ? psqt_out1 : psqt_out0, lo, hi, wrap16, kpad, ntiles,
+                       persp * nchunks_p, nchunks_p);
+  }
+  return check_launch((std::string(who) + " (ranked gather)").c_str());
 }
 
 int fwd_i16_tiled(const int32_t *idx, int64_t B, int K, const int16_t *W, int64_t N, int L, const int16_t *bias,

@@ -78,6 +78,11 @@ SIGNATURES = {
         ctypes.c_int,
         [_vp, _vp, _i64, _i32, _vp, ctypes.c_size_t, _i64, _i32, _vp, _i32, _vp, _vp, _vp, _vp, _i32, _i32, _u32,
          _vp]),
+    "sft_ft_fwd_i16_packed_workspace_size": (ctypes.c_int, [_i64, _i32, _i32, ctypes.POINTER(ctypes.c_size_t)]),
+    "sft_ft_fwd_i16_packed_ex": (
+        ctypes.c_int,
+        [_vp, _vp, _i64, _i32, _vp, ctypes.c_size_t, _i64, _i32, _vp, _i32, _vp, _vp, _vp, _vp, _i32, _i32, _vp,
+         ctypes.c_size_t, _u32, _vp]),
     "sft_ft_pair_workspace_size": (
         ctypes.c_int,
         [_i64, _i32, _i32, ctypes.POINTER(_i64), ctypes.POINTER(_i64), _i32, ctypes.POINTER(ctypes.c_size_t),
@@ -411,8 +416,10 @@ def i16_pack(weight: torch.Tensor, psqt_weight: torch.Tensor | None = None) -> t
 def ft_fwd_i16_packed(packed: torch.Tensor, N: int, L: int, P: int, bias: torch.Tensor, idx0: torch.Tensor,
                       out0: torch.Tensor, psqt_out0: torch.Tensor | None, idx1: torch.Tensor | None = None,
                       out1: torch.Tensor | None = None, psqt_out1: torch.Tensor | None = None,
-                      clip_lo: int = 0, clip_hi: int = 127, wrap16: bool = False) -> None:
-    """int16 forward of one (idx1 None) or both perspectives from a table packed by i16_pack."""
+                      clip_lo: int = 0, clip_hi: int = 127, wrap16: bool = False, ranked: bool = True) -> None:
+    """int16 forward of one (idx1 None) or both perspectives from a table packed by i16_pack.
+    ranked: through sft_ft_fwd_i16_packed_ex (rank lists in a workspace), else
+    sft_ft_fwd_i16_packed (index rows compacted per tile, no workspace)."""
     _require(packed.dtype == torch.uint8 and packed.dim() == 1, "packed must come from i16_pack")
     _require(idx0.dim() == 2 and idx0.dtype == torch.int32, "idx0 must be int32 [B, K]")
     B, K = idx0.shape
@@ -429,11 +436,23 @@ def ft_fwd_i16_packed(packed: torch.Tensor, N: int, L: int, P: int, bias: torch.
                      "psqt_out must be int32 [B, P]")
             tensors.append(po)
     _on_gpu(idx0.device, *tensors)
+    flags = SFT_Q16_WRAP16 if wrap16 else SFT_Q16_ACC32
     with torch.cuda.device(idx0.device):
-        _check(lib().sft_ft_fwd_i16_packed(_ptr(idx0), _ptr(idx1), B, K, _ptr(packed), packed.numel(), N, L,
-                                           _ptr(bias), P, _ptr(out0), _ptr(out1), _ptr(psqt_out0), _ptr(psqt_out1),
-                                           clip_lo, clip_hi, SFT_Q16_WRAP16 if wrap16 else SFT_Q16_ACC32,
-                                           _stream(idx0.device)), "sft_ft_fwd_i16_packed")
+        if not ranked:
+            _check(lib().sft_ft_fwd_i16_packed(_ptr(idx0), _ptr(idx1), B, K, _ptr(packed), packed.numel(), N, L,
+                                               _ptr(bias), P, _ptr(out0), _ptr(out1), _ptr(psqt_out0),
+                                               _ptr(psqt_out1), clip_lo, clip_hi, flags, _stream(idx0.device)),
+                   "sft_ft_fwd_i16_packed")
+            return
+        n = ctypes.c_size_t(0)
+        _check(lib().sft_ft_fwd_i16_packed_workspace_size(B, K, 1 if idx1 is None else 2, ctypes.byref(n)),
+               "sft_ft_fwd_i16_packed_workspace_size")
+        ws = torch.empty(n.value + 256, dtype=torch.uint8, device=idx0.device)
+        wp, wn = _aligned(ws)
+        _check(lib().sft_ft_fwd_i16_packed_ex(_ptr(idx0), _ptr(idx1), B, K, _ptr(packed), packed.numel(), N, L,
+                                              _ptr(bias), P, _ptr(out0), _ptr(out1), _ptr(psqt_out0), _ptr(psqt_out1),
+                                              clip_lo, clip_hi, wp, wn, flags, _stream(idx0.device)),
+               "sft_ft_fwd_i16_packed_ex")
 
 
 # ---- composed table, both perspectives ----

@@ -154,6 +154,41 @@ def test_i16_packed_forward_rejects_before_launch():
     assert call(batch=0, packed_bytes=need - 1) == -1  # sizes are checked even for an empty batch
 
 
+def test_i16_packed_ex_workspace_and_rejects_before_launch():
+    """The ranked packed forward: its workspace is both perspectives' rank lists;
+    it makes the packed forward's checks, then rejects a short or misaligned
+    workspace, all before anything runs."""
+    lib = _native.lib()
+    n = ctypes.c_size_t(0)
+    assert lib.sft_ft_fwd_i16_packed_workspace_size(65536, 32, 2, ctypes.byref(n)) == 0
+    assert n.value == 2 * rank_lists_bytes(65536, 32)
+    assert lib.sft_ft_fwd_i16_packed_workspace_size(65536, 32, 1, ctypes.byref(n)) == 0
+    assert n.value == rank_lists_bytes(65536, 32)
+    assert lib.sft_ft_fwd_i16_packed_workspace_size(65536, 32, 3, ctypes.byref(n)) == -1
+    assert lib.sft_ft_fwd_i16_packed_workspace_size(65536, 65536, 1, ctypes.byref(n)) == -1
+    assert lib.sft_ft_fwd_i16_packed_workspace_size(65536, 32, 1, None) == -1
+    need = 17 * 22528 * 128
+    wsn = 2 * rank_lists_bytes(4, 32)
+    ok = (P, P, 4, 32, P, need, 22528, 1040, P, 8, P, P, P, P, 0, 127, P, wsn, 0, None)
+
+    def call(**kw):
+        names = ["idx0", "idx1", "batch", "max_active", "packed", "packed_bytes", "num_inputs", "output_size",
+                 "bias", "psqt_size", "out0", "out1", "psqt_out0", "psqt_out1", "clip_lo", "clip_hi", "workspace",
+                 "workspace_bytes", "flags", "stream"]
+        a = dict(zip(names, ok))
+        a.update(kw)
+        return lib.sft_ft_fwd_i16_packed_ex(*[a[k] for k in names])
+
+    assert call(packed_bytes=need - 1) == -1 and "packed_bytes" in _native.last_error()
+    assert call(flags=0x2) == -1 and "flags" in _native.last_error()
+    assert call(out1=None) == -1 and "null" in _native.last_error()
+    assert call(psqt_size=9) == _native.SFT_EUNSUPPORTED
+    assert call(workspace_bytes=wsn - 1) == _native.SFT_EWORKSPACE and "workspace" in _native.last_error()
+    assert call(workspace=None) == _native.SFT_EWORKSPACE
+    assert call(workspace=ctypes.c_void_p(0x1010)) == _native.SFT_EWORKSPACE  # not 256-byte aligned
+    assert call(idx1=None, workspace_bytes=rank_lists_bytes(4, 32) - 1) == _native.SFT_EWORKSPACE
+
+
 @pytest.mark.parametrize("B", [1, 2, 9000, 16384, 32768, 32769, 65536])
 def test_bwd_workspace_holds_the_grad_tiles(B):
     """The tiled backward's bias pass writes ceil(L/32) x B x 128 bytes of grad

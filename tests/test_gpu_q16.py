@@ -73,10 +73,12 @@ def test_q16_extreme_values(wrap16, rows):
     (21, 300, 1000, 32, 1040, 8), (22, 77, 500, 13, 1024, 0), (23, 129, 800, 20, 2104, 5), (24, 1, 64, 4, 512, 3),
     (25, 1000, 22528, 32, 1040, 8)])
 @pytest.mark.parametrize("wrap16", [False, True])
-def test_packed_table_matches_oracle(seed, B, N, K, L, P, wrap16):
-    """sft_ft_i16_pack + sft_ft_fwd_i16_packed, both perspectives in one launch and
-    one perspective alone, against the oracle."""
-    announce(f"q16 packed seed={seed} B={B} N={N} K={K} L={L} P={P} wrap16={wrap16}")
+@pytest.mark.parametrize("ranked", [True, False])
+def test_packed_table_matches_oracle(seed, B, N, K, L, P, wrap16, ranked):
+    """sft_ft_i16_pack + sft_ft_fwd_i16_packed_ex (ranked: rank lists in a
+    workspace) or sft_ft_fwd_i16_packed, both perspectives in one launch and one
+    perspective alone, against the oracle."""
+    announce(f"q16 packed seed={seed} B={B} N={N} K={K} L={L} P={P} wrap16={wrap16} ranked={ranked}")
     g = np.random.default_rng(seed)
     i0 = workloads.make_indices(g, B, N, K, 0, K, sort=False)
     i1 = workloads.make_indices(g, B, N, K, 0, K, sort=False)
@@ -88,9 +90,10 @@ def test_packed_table_matches_oracle(seed, B, N, K, L, P, wrap16):
     for lo, hi in ((0, 127), (-32768, 32767)):
         o = [torch.empty(B, L, dtype=torch.int16, device=DEV) for _ in range(3)]
         po = [torch.empty(B, P, dtype=torch.int32, device=DEV) if P else None for _ in range(3)]
-        _native.ft_fwd_i16_packed(packed, N, L, P, dev(bq), dev(i0), o[0], po[0], dev(i1), o[1], po[1], lo, hi, wrap16)
+        _native.ft_fwd_i16_packed(packed, N, L, P, dev(bq), dev(i0), o[0], po[0], dev(i1), o[1], po[1], lo, hi, wrap16,
+                                  ranked=ranked)
         _native.ft_fwd_i16_packed(packed, N, L, P, dev(bq), dev(i1), o[2], po[2], clip_lo=lo, clip_hi=hi,
-                                  wrap16=wrap16)
+                                  wrap16=wrap16, ranked=ranked)
         for j, idx in ((0, i0), (1, i1), (2, i1)):
             ro, rp = ft_oracle.fwd_i16(idx, Wq, bq, ps, lo, hi, wrap16)
             assert np.array_equal(host(o[j]), ro), j
