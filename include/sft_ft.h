@@ -178,9 +178,10 @@ int sft_ft_fwd_i16(const int32_t *idx, int64_t batch, int32_t max_active, const 
 
 /*
  * Bytes of device workspace sft_ft_fwd_i16_ex uses (0 when the shape runs the
- * row gather); it grows with psqt_size, whose PSQT columns are stored in the
- * tiles beside the int16 columns, so query with the psqt_size of the call.
- * Host-only computation.  No reference counterpart.
+ * row gather): the packed tiles, which grow with psqt_size (the PSQT columns
+ * are stored beside the int16 columns, so query with the psqt_size of the
+ * call), then the rank lists of the batch.  Host-only computation.  No
+ * reference counterpart.
  */
 int sft_ft_fwd_i16_workspace_size(int64_t batch, int32_t max_active, int64_t num_inputs,
                                   int32_t output_size, int32_t psqt_size, uint32_t flags,
@@ -191,7 +192,8 @@ int sft_ft_fwd_i16_workspace_size(int64_t batch, int32_t max_active, int64_t num
  * Unless SFT_Q16_ROWS is set, shapes with output_size % 8 == 0, at least 8
  * column tiles of 64 and psqt_size <= 8 copy the table, with the PSQT columns
  * appended to each row, into 64-column tiles in the workspace and gather them
- * XCD by XCD from L2.
+ * XCD by XCD from L2, reading the index rows as rank lists built once in the
+ * workspace (as sft_ft_fwd_i16_packed_ex).
  */
 int sft_ft_fwd_i16_ex(const int32_t *idx, int64_t batch, int32_t max_active,
                       const int16_t *weight, int64_t num_inputs, int32_t output_size,
@@ -204,7 +206,9 @@ int sft_ft_fwd_i16_ex(const int32_t *idx, int64_t batch, int32_t max_active,
  * counterpart: it is for callers that cannot allocate device memory (code
  * under HIP graph capture, serving loops, harnesses that forbid hipMalloc).
  * Same arguments, flags and results, bit for bit, as sft_ft_fwd_i16_ex with a
- * workspace of sft_ft_fwd_i16_workspace_size() bytes.  The packed tiles go to
+ * workspace of sft_ft_fwd_i16_workspace_size() bytes (it compacts the index
+ * rows once per column tile, as sft_ft_fwd_i16_packed, instead of building rank
+ * lists, so its scratch need does not grow with the batch).  The packed tiles go to
  * a static device array of SFT_NOALLOC_SCRATCH_BYTES that each GPU holds until
  * the process ends; a tiled shape whose packed table is larger returns
  * SFT_EWORKSPACE and launches nothing (shapes outside the tiled path run the

@@ -21,6 +21,7 @@ int fwd_f32_tiled(const int32_t *idx, int64_t B, int K, const float *W, int64_t 
                   void *ws, size_t ws_bytes, hipStream_t s);
 int bwd_workspace(int64_t B, int K, int64_t N, int L, uint32_t flags, size_t *bytes);
 size_t fwd_i16_tiled_workspace(int64_t N, int L, int P);
+size_t fwd_i16_ex_workspace(int64_t B, int K, int64_t N, int L, int P);
 bool fwd_i16_tiled_supported(int64_t N, int L, int P, const void *W, const void *bias, const void *out);
 int fwd_i16_tiled(const int32_t *idx, int64_t B, int K, const int16_t *W, int64_t N, int L, const int16_t *bias,
                   const int32_t *psqt, int P, int16_t *out, int32_t *psqt_out, int lo, int hi, int wrap16, void *ws,
@@ -777,7 +778,7 @@ int sft_ft_fwd_i16_workspace_size(int64_t batch, int32_t max_active, int64_t num
   if (flags & ~(SFT_Q16_WRAP16 | SFT_Q16_ROWS)) return fail(SFT_EINVAL, "sft_ft_fwd_i16_workspace_size: unknown flags");
   const bool tiled = !(flags & SFT_Q16_ROWS) &&
                      fwd_i16_tiled_supported(num_inputs, output_size, psqt_size, nullptr, nullptr, nullptr);
-  *bytes = tiled ? fwd_i16_tiled_workspace(num_inputs, output_size, psqt_size) : 0;
+  *bytes = tiled ? fwd_i16_ex_workspace(batch, max_active, num_inputs, output_size, psqt_size) : 0;
   return SFT_OK;
 }
 
@@ -793,7 +794,8 @@ int sft_ft_fwd_i16_ex(const int32_t *idx, int64_t batch, int32_t max_active, con
   const int P = psqt_weight ? psqt_size : 0;
   const int wrap = (flags & SFT_Q16_WRAP16) ? 1 : 0;
   const bool tiled = !(flags & SFT_Q16_ROWS) && fwd_i16_tiled_supported(num_inputs, output_size, P, weight, bias, out) &&
-                     workspace != nullptr && workspace_bytes >= fwd_i16_tiled_workspace(num_inputs, output_size, P);
+                     workspace != nullptr &&
+                     workspace_bytes >= fwd_i16_ex_workspace(batch, max_active, num_inputs, output_size, P);
   if (tiled)
     return fwd_i16_tiled(idx, batch, max_active, weight, num_inputs, output_size, bias, psqt_weight, P, out, psqt_out,
                          clip_lo, clip_hi, wrap, workspace, workspace_bytes, (hipStream_t)stream);

@@ -1421,18 +1421,25 @@ int fwd_i16_packed_ranked(const int32_t *idx0, const int32_t *idx1, int64_t B, i
   return check_launch((std::string(who) + " (ranked gather)").c_str());
 }
 
+// Workspace of the per-call tiled int16 forward: the packed table, then the rank lists.
+size_t fwd_i16_ex_workspace(int64_t B, int K, int64_t N, int L, int P) {
+  return align256(fwd_i16_tiled_workspace(N, L, P)) + fwd_i16_ranked_workspace(B, K, 1);
+}
+
 int fwd_i16_tiled(const int32_t *idx, int64_t B, int K, const int16_t *W, int64_t N, int L, const int16_t *bias,
                   const int32_t *psqt, int P, int16_t *out, int32_t *psqt_out, int lo, int hi, int wrap16, void *ws,
                   size_t ws_bytes, hipStream_t s) {
-  if (ws_bytes < fwd_i16_tiled_workspace(N, L, P) || ws == nullptr || (uintptr_t)ws % 256 != 0)
+  const char *who = "sft_ft_fwd_i16_ex";
+  if (ws_bytes < fwd_i16_ex_workspace(B, K, N, L, P) || ws == nullptr || (uintptr_t)ws % 256 != 0)
     return fail(SFT_EWORKSPACE, "sft_ft_fwd_i16_ex: workspace smaller than sft_ft_fwd_i16_workspace_size() "
                                 "or not 256-byte aligned");
-  if (index_lds_bytes(kTileCh, K) > kMaxIndexLds)
+  if (rank_lds_bytes(K) > kMaxIndexLds)
     return fail(SFT_EUNSUPPORTED, "sft_ft_fwd_i16_ex: max_active too large for the LDS index lists");
-  int rc = i16_pack(W, N, L, psqt, P, ws, ws_bytes, s, "sft_ft_fwd_i16_ex");
+  const size_t packed = align256(fwd_i16_tiled_workspace(N, L, P));
+  int rc = i16_pack(W, N, L, psqt, P, ws, packed, s, who);
   if (rc != SFT_OK) return rc;
-  return fwd_i16_packed(idx, nullptr, B, K, ws, N, L, bias, P, out, nullptr, psqt_out, nullptr, lo, hi, wrap16, s,
-                        "sft_ft_fwd_i16_ex");
+  return fwd_i16_packed_ranked(idx, nullptr, B, K, ws, N, L, bias, P, out, nullptr, psqt_out, nullptr, lo, hi, wrap16,
+                               static_cast<char *>(ws) + packed, ws_bytes - packed, s, who);
 }
 
 int fwd_i16(const int32_t *idx, int64_t B, int K, const int16_t *W, int64_t N, int L, const int16_t *bias,
