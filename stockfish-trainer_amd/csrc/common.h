@@ -196,7 +196,16 @@ __device__ __forceinline__ void compact_rows(const int32_t *__restrict__ idx, in
 #ifndef SFT_MIN_TILES
 #define SFT_MIN_TILES 8
 #endif
-constexpr int kMinTiles = SFT_MIN_TILES;  // fewest column tiles for which the tiled kernels are used
+constexpr int kMinTiles = SFT_MIN_TILES;  // fewest column tiles for which the int16 tiled forward is used
+// The fp32 backward tiles from 4 column tiles (L > 96): with the leftover
+// tiles shared evenly over the XCDs (tile_sched_item), L = 136 (5 tiles) runs
+// its gathers in 2 x 37.8 us per perspective against 107.7 us for the row
+// gather, and the bias pass, which then also writes the grad tiles, 20.7
+// against 10.5 us (step 0.495 -> 0.406 ms).
+#ifndef SFT_BWD_MIN_TILES
+#define SFT_BWD_MIN_TILES 4
+#endif
+constexpr int kBwdMinTiles = SFT_BWD_MIN_TILES;
 
 // ---- composed tables ----
 // A composed feature transformer's table is the concatenation of up to

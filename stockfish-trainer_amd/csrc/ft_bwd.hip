@@ -997,7 +997,7 @@ int bias_parts(int64_t B) {
 
 bool tiled_shape(int64_t B, int L, uint32_t flags) {
   return !(flags & (SFT_BWD_ATOMIC | SFT_BWD_ROWS)) && (flags & SFT_BWD_OVERWRITE) && L % 4 == 0 &&
-         ceil_div(L, 32) >= kMinTiles && B * 16 * kBwdTileCh <= (int64_t)UINT32_MAX;  // 32-bit grad row offsets
+         ceil_div(L, 32) >= kBwdMinTiles && B * 16 * kBwdTileCh <= (int64_t)UINT32_MAX;  // 32-bit grad row offsets
 }
 
 // Position chunks of the tiled gather (one launch each).

@@ -1181,11 +1181,9 @@ size_t fwd_tiled_workspace(int64_t B, int K, int64_t N, int L) {
 #ifndef SFT_FWD_TILE_MAX_BYTES
 #define SFT_FWD_TILE_MAX_BYTES (64ll << 20)
 #endif
-// The fp32 forward tiles from 4 column tiles up (L > 96): at L = 136 (5 tiles,
-// the leftover groups of XCDs sharing each) the tiled gather and its re-layout
-// take 86 us against 95 us for the row gather.  The backward keeps kMinTiles:
-// its tiled path needs the grad tiles of the bias pass, which cost more than
-// they save at that width.
+// The fp32 forward tiles from 4 column tiles up (L > 96): at L = 136 (5 tiles)
+// the tiled gather and its re-layout take 86 us against 95 us for the row
+// gather.
 #ifndef SFT_FWD_MIN_TILES
 #define SFT_FWD_MIN_TILES 4
 #endif

@@ -46,20 +46,23 @@ struct FastDiv {
 // on XCD i % 8), and each XCD has its own 4 MB L2.  Tiled kernels give every
 // XCD whole column tiles: workgroup i serves the (i / 8)-th item of XCD i % 8,
 // where XCD x owns tiles x, x + 8, ... (all chunks of one tile, then the next).
-// The rem = ntiles % 8 tiles left after the last full round each go to a
-// group of 8 / rem (rounded down or up) XCDs -- XCD x to leftover tile
-// x * rem / 8 -- whose members take its chunks in turn, so an XCD still reads
-// one tile.  A workgroup with no item gets tile = ntiles.  Any other placement
-// only costs locality, never results.
+// The rem = ntiles % 8 tiles left after the last full round are cut into 8
+// strands each -- strand s of leftover tile t holds its chunks s, s + 8, ...,
+// so every strand has the same mix of early (long) and late chunks -- and XCD
+// x takes the rem consecutive strands [x rem, (x + 1) rem) of the sequence
+// (t, s): every XCD gets the same work (rem strands, +-1 chunk each) from at
+// most two leftover tiles, the first one's strands before the second's, in
+// chunk order.  (With rem = 5 tiles, whole tiles per XCD group would leave two
+// XCDs alone on a tile each while the others share one.)  A workgroup with no
+// item gets tile = ntiles.  Any other placement only costs locality, never
+// results.
 constexpr int kXcds = 8;
 struct TileItem {
   int tile, chunk;
 };
 SFT_HD inline int64_t tile_sched_items_per_xcd(int ntiles, int nchunks) {
   const int full = ntiles / kXcds, rem = ntiles % kXcds;
-  if (rem == 0) return (int64_t)full * nchunks;
-  const int gmin = kXcds / rem;  // smallest group
-  return (int64_t)full * nchunks + ((int64_t)nchunks + gmin - 1) / gmin;
+  return (int64_t)full * nchunks + (int64_t)rem * ((nchunks + kXcds - 1) / kXcds);
 }
 SFT_HD inline TileItem tile_sched_item(int64_t bid, int ntiles, int nchunks) {
   const int xcd = (int)(bid % kXcds);
@@ -68,11 +71,21 @@ SFT_HD inline TileItem tile_sched_item(int64_t bid, int ntiles, int nchunks) {
   const int64_t fj = (int64_t)full * nchunks;
   if (j < fj) return TileItem{xcd + kXcds * (int)(j / nchunks), (int)(j % nchunks)};
   if (rem == 0) return TileItem{ntiles, 0};  // no work
-  const int t = xcd * rem / kXcds;                              // leftover tile of this XCD's group
-  const int x0 = (t * kXcds + rem - 1) / rem;                   // first XCD of the group
-  const int gs = ((t + 1) * kXcds + rem - 1) / rem - x0;        // group size
-  const int64_t c = (xcd - x0) + (j - fj) * gs;
-  if (c >= nchunks) return TileItem{ntiles, 0};  // no work
+  const int64_t rounds = (nchunks + kXcds - 1) / kXcds;  // chunks per strand, the last round partial
+  const int s0 = xcd * rem;                              // first strand of this XCD
+  const int ta = s0 / kXcds;                             // its first leftover tile
+  const int na = ((ta + 1) * kXcds < s0 + rem ? (ta + 1) * kXcds : s0 + rem) - s0;  // strands of tile ta
+  int64_t i = j - fj;
+  int t = ta, s = s0 % kXcds, n = na;
+  if (i >= rounds * na) {  // strands 0 .. rem - na - 1 of the next leftover tile
+    i -= rounds * na;
+    t = ta + 1;
+    s = 0;
+    n = rem - na;
+    if (n <= 0) return TileItem{ntiles, 0};  // no work
+  }
+  const int64_t c = (i / n) * kXcds + s + i % n;
+  if (c >= nchunks) return TileItem{ntiles, 0};  // no work: past a strand's end
   return TileItem{kXcds * full + t, (int)c};
 }
 

@@ -6,6 +6,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <random>
+#include <utility>
 #include <vector>
 
 #include "index_math.h"
@@ -44,8 +45,11 @@ static void check_fastdiv(uint32_t d) {
 
 // Every (tile, chunk) of ntiles x nchunks is served by exactly one workgroup of
 // the launch (tile_sched_items_per_xcd * 8 of them), the others get no work,
-// each XCD serves its own tiles only, and the leftover tiles are split among
-// XCD groups that together hold every XCD.
+// each XCD serves its own tiles only, and the leftover tiles are shared out
+// evenly: every XCD gets between rem * floor(nchunks / 8) and
+// rem * ceil(nchunks / 8) of their chunks, from at most two consecutive
+// leftover tiles (the first one's chunks first), each tile's part a union of
+// whole residue classes of the chunk index mod 8.
 static void check_schedule(int ntiles, int nchunks) {
   const int64_t blocks = tile_sched_items_per_xcd(ntiles, nchunks) * kXcds;
   std::vector<int> seen((size_t)ntiles * nchunks, 0);
@@ -71,12 +75,43 @@ static void check_schedule(int ntiles, int nchunks) {
   for (int x = 0; x < kXcds; ++x)
     for (int t : xcd_tiles[x])
       if (t < full * kXcds) CHECK(t % kXcds == x, "ntiles=%d xcd %d got tile %d", ntiles, x, t);
-  // a leftover tile is read by the XCDs of one group only
+  // the leftover tiles: even shares, at most two tiles per XCD in order,
+  // whole residue classes mod 8
   const int rem = ntiles % kXcds;
-  for (int x = 0; x < kXcds && rem; ++x)
-    for (int t : xcd_tiles[x])
-      if (t >= full * kXcds) CHECK(t - full * kXcds == x * rem / kXcds, "ntiles=%d xcd %d leftover tile %d", ntiles,
-                                   x, t);
+  if (rem) {
+    std::vector<std::vector<std::pair<int, int>>> left(kXcds);  // (tile, chunk) in launch order
+    for (int64_t b = 0; b < blocks; ++b) {
+      const TileItem it = tile_sched_item(b, ntiles, nchunks);
+      if (it.tile >= full * kXcds && it.tile < ntiles) left[b % kXcds].push_back({it.tile, it.chunk});
+    }
+    const int64_t lo = (int64_t)rem * (nchunks / kXcds), hi = (int64_t)rem * ((nchunks + kXcds - 1) / kXcds);
+    for (int x = 0; x < kXcds; ++x) {
+      const auto &v = left[x];
+      CHECK((int64_t)v.size() >= lo && (int64_t)v.size() <= hi, "ntiles=%d nchunks=%d xcd %d has %zu leftover items",
+            ntiles, nchunks, x, v.size());
+      for (size_t k = 1; k < v.size(); ++k) {
+        CHECK(v[k].first == v[k - 1].first || v[k].first == v[k - 1].first + 1,
+              "ntiles=%d nchunks=%d xcd %d: leftover tiles out of order", ntiles, nchunks, x);
+        if (v[k].first == v[k - 1].first)
+          CHECK(v[k].second > v[k - 1].second, "ntiles=%d nchunks=%d xcd %d: chunks out of order", ntiles, nchunks, x);
+      }
+      if (!v.empty())
+        CHECK(v.back().first - v.front().first <= 1, "ntiles=%d nchunks=%d xcd %d reads more than two leftover tiles",
+              ntiles, nchunks, x);
+      for (int t = full * kXcds; t < ntiles; ++t) {
+        bool cls[kXcds] = {};
+        int n = 0;
+        for (const auto &e : v)
+          if (e.first == t) {
+            cls[e.second % kXcds] = true;
+            ++n;
+          }
+        int want = 0;
+        for (int c = 0; c < nchunks; ++c) want += cls[c % kXcds] ? 1 : 0;
+        CHECK(n == want, "ntiles=%d nchunks=%d xcd %d tile %d: partial residue class", ntiles, nchunks, x, t);
+      }
+    }
+  }
 }
 
 // tile_col and tile_of_col are inverse: every chunk of a row lands on exactly

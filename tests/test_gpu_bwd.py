@@ -23,6 +23,8 @@ SHAPES = [
     (9, 333, 4000, 48, 520, 0, 48, False),
     (10, 40000, 700, 32, 256, 0, 32, True),  # two position chunks (B x 128 B > 4 MB), long segments
     (11, 34000, 5, 3, 1040, 0, 3, False),    # five features: every segment crosses the chunk boundary
+    (12, 40000, 3000, 16, 200, 0, 16, True),  # 7 tiles (leftover strands of two tiles per XCD), two chunks
+    (13, 5000, 1000, 8, 100, 0, 8, False),    # 4 tiles, the last holding one 16-byte chunk
 ]
 
 
@@ -74,7 +76,8 @@ def skewed_indices(g, B, N, K, hot, p_hot):
 @pytest.mark.parametrize("seed,B,N,K,L,hot,p_hot", [
     (21, 40000, 3000, 32, 1048, 12, 0.35),  # tiled: long segments in both position chunks
     (24, 9000, 3000, 32, 1048, 12, 0.35),   # tiled, one position chunk (B x 128 B <= 4 MB)
-    (22, 5000, 400, 24, 136, 40, 0.2),      # narrow rows (row gather)
+    (22, 5000, 400, 24, 136, 40, 0.2),      # narrow rows: 5 tiles, or the row gather (rows)
+    (25, 40000, 3000, 16, 136, 12, 0.35),   # 5 tiles over 8 XCDs, long segments in both position chunks
     (23, 1200, 50, 16, 520, 6, 0.9),        # segments just above and below the long threshold
 ])
 @pytest.mark.parametrize("overwrite", [False, True])

@@ -30,6 +30,7 @@ SHAPES = [
     (15, 500, 3000, 32, 100, 0, 32, False),   # 4 tiles, the last holding one 16-byte chunk
     (16, 400, 2500, 24, 228, 8, 24, True),    # 8 tiles, the last holding one chunk
     (17, 300, 1200, 32, 96, 0, 32, False),    # 3 tiles: row gather
+    (18, 900, 3000, 32, 200, 8, 32, True),    # 7 tiles: leftover strands of two tiles per XCD
 ]
 
 
