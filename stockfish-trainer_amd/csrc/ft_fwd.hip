@@ -398,25 +398,57 @@ __global__ __launch_bounds__(kBlock) void rank_lists_kernel(RankArgs a, int64_t 
   const bool regrow = STAGE && vec && K <= 4 * kRegRow;
   i32x4 rv[kRegRow];
   int c = 0;
+  // With table parts the same pass also finds the runs: cut[p] = the number of
+  // active slots before the first slot of a part above p, and whether the
+  // parts never go back along the row (mono).  (A second pass over the row for
+  // them took 49 of 156 us per call at K = 160; with it folded in here and 8
+  // row loads in flight per thread in both passes, the call takes 128 us.)
+  int cut[kMaxParts - 1], part = 0;
+  bool mono = true;
+  auto count_slot = [&](int v) {
+    if ((unsigned)v >= (unsigned)N) return;
+    if (a.nparts > 1) {  // launch-uniform
+      const int pv = (int)a.part_of((uint32_t)v);
+      mono = mono && pv >= part;
+      for (; part < pv; ++part)
+        if (part < kMaxParts - 1) cut[part] = c;
+    }
+    ++c;
+  };
   if (regrow) {
 #pragma unroll
     for (int u = 0; u < kRegRow; ++u)
       rv[u] = (real && 4 * u < K) ? *reinterpret_cast<const i32x4 *>(row + 4 * u) : i32x4{-1, -1, -1, -1};
+    if (a.nparts > 1) {
 #pragma unroll
-    for (int u = 0; u < kRegRow; ++u)
-      c += ((unsigned)rv[u][0] < (unsigned)N) + ((unsigned)rv[u][1] < (unsigned)N) +
-           ((unsigned)rv[u][2] < (unsigned)N) + ((unsigned)rv[u][3] < (unsigned)N);
+      for (int u = 0; u < kRegRow; ++u)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) count_slot(rv[u][e]);
+    } else {
+#pragma unroll
+      for (int u = 0; u < kRegRow; ++u)
+        c += ((unsigned)rv[u][0] < (unsigned)N) + ((unsigned)rv[u][1] < (unsigned)N) +
+             ((unsigned)rv[u][2] < (unsigned)N) + ((unsigned)rv[u][3] < (unsigned)N);
+    }
   } else if (real) {
-    if (vec) {
+    if (vec && a.nparts > 1) {
+#pragma unroll 8
+      for (int k = 0; k < K; k += 4) {
+        const i32x4 v = *reinterpret_cast<const i32x4 *>(row + k);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) count_slot(v[e]);
+      }
+    } else if (vec) {
       for (int k = 0; k < K; k += 4) {
         const i32x4 v = *reinterpret_cast<const i32x4 *>(row + k);
         c += ((unsigned)v[0] < (unsigned)N) + ((unsigned)v[1] < (unsigned)N) + ((unsigned)v[2] < (unsigned)N) +
              ((unsigned)v[3] < (unsigned)N);
       }
     } else {
-      for (int k = 0; k < K; ++k) c += (unsigned)slot(k) < (unsigned)N ? 1 : 0;
+      for (int k = 0; k < K; ++k) count_slot(slot(k));
     }
   }
+  for (; part < kMaxParts - 1; ++part) cut[part] = c;  // parts after the row's last
   const unsigned mine = real ? atomicAdd(&bin[c], 1u) : 0u;
   __syncthreads();
   if (tid < kWave) {  // off[cc] = sum of bin[cc + 1 .. K]: wave 0, 64 bins per step, largest count first
@@ -446,12 +478,17 @@ __global__ __launch_bounds__(kBlock) void rank_lists_kernel(RankArgs a, int64_t 
     auto each_active = [&](auto &&fn) {
       if (!real) return;
       if (vec) {
-#pragma unroll 4
-        for (int k = 0; k < K; k += 4) {
-          const i32x4 v4 = *reinterpret_cast<const i32x4 *>(row + k);
+        constexpr int U = 8;  // row loads issued before the batch's stores
+        for (int k0 = 0; k0 < K; k0 += 4 * U) {
+          i32x4 v4[U];
 #pragma unroll
-          for (int e = 0; e < 4; ++e)
-            if ((unsigned)v4[e] < (unsigned)N) fn(v4[e]);
+          for (int u = 0; u < U; ++u)
+            v4[u] = k0 + 4 * u < K ? *reinterpret_cast<const i32x4 *>(row + k0 + 4 * u) : i32x4{-1, -1, -1, -1};
+#pragma unroll
+          for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if ((unsigned)v4[u][e] < (unsigned)N) fn(v4[u][e]);
         }
       } else {
         for (int k = 0; k < K; ++k) {
@@ -460,16 +497,6 @@ __global__ __launch_bounds__(kBlock) void rank_lists_kernel(RankArgs a, int64_t 
         }
       }
     };
-    int cut[kMaxParts - 1] = {c, c, c};
-    int part = 0, j = 0;
-    bool mono = true;
-    each_active([&](int v) {
-      const int pv = (int)a.part_of((uint32_t)v);
-      mono = mono && pv >= part;
-      for (; part < pv; ++part)
-        if (part < kMaxParts - 1) cut[part] = j;
-      ++j;
-    });
     const i32x4 cv = mono ? i32x4{cut[0], cut[1], cut[2], a.nparts - 1} : i32x4{c, c, c, 0};
     int len[kMaxParts];
 #pragma unroll
