@@ -421,7 +421,8 @@ def bench_composed(args, dev) -> int:
         kern[kind] = {"avg_ms": avg, "launches_per_step": cnt / args.steps, "bytes_per_launch": per_launch,
                       "gbs": (per_launch / (avg * 1e-3) / 1e9) if per_launch else None}
         log(f"[bench]   {kind:22s} {avg:8.4f} ms x {cnt / args.steps:.0f}/step")
-    dom = max(prof, key=lambda k: prof[k][0])
+    # dominant kernel: the largest time per step among those with an algorithmic byte count
+    dom = max((k for k in prof if kern[k]["bytes_per_launch"]), key=lambda k: prof[k][0])
     dom_avg = prof[dom][0] / prof[dom][1]
     dom_bytes = kern[dom]["bytes_per_launch"]
     step_bytes = workloads.step_bytes(idx[0], idx[1], N, L)
@@ -526,7 +527,8 @@ def bench_transform(args, dev) -> int:
         kern[kind] = {"avg_ms": avg, "launches_per_step": cnt / args.steps, "bytes_per_launch": per_launch,
                       "gbs": (per_launch / (avg * 1e-3) / 1e9) if per_launch else None}
         log(f"[bench]   {kind:22s} {avg:8.4f} ms x {cnt / args.steps:.0f}/step")
-    dom = max(prof, key=lambda kk: prof[kk][0])
+    # dominant kernel: the largest time per step among those with an algorithmic byte count
+    dom = max((kk for kk in prof if kern[kk]["bytes_per_launch"]), key=lambda kk: prof[kk][0])
     dom_avg = prof[dom][0] / prof[dom][1]
     dom_bytes = kern[dom]["bytes_per_launch"]
     result = {
