@@ -221,7 +221,7 @@ def cpu_baseline(w, d, seconds: float) -> dict:
     if env_threads and env_threads.isdigit():
         threads = min(threads, int(env_threads))
     torch.set_num_threads(threads)
-    Bs = min(w.B, 4096)
+    Bs = w.B  # the whole batch of the workload, as the GPU step
     step = CpuFtStep(d["idx_w"][:Bs], d["idx_b"][:Bs], d["W"], d["bias"], d["g_w"][:Bs], d["g_b"][:Bs])
     step()  # warm-up
     n, t0 = 0, time.perf_counter()
@@ -229,7 +229,7 @@ def cpu_baseline(w, d, seconds: float) -> dict:
         step()
         n += 1
         el = time.perf_counter() - t0
-        if el >= seconds or n >= 200:
+        if (el >= seconds and n >= 2) or n >= 200:
             break
     model = ""
     try:
@@ -246,7 +246,7 @@ def cpu_baseline(w, d, seconds: float) -> dict:
         "unit": "positions/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"{n} fwd+bwd steps of both perspectives on the first {Bs} positions of {w.name} "
+        "sample": f"{n} fwd+bwd steps of both perspectives on all {Bs} positions of {w.name} "
                   f"(N={w.N}, L={w.L}), torch {torch.__version__} embedding_bag on {threads} threads, "
                   f"{el:.1f} s; cpu: {model}",
     }
@@ -956,9 +956,14 @@ def main() -> int:
             elif cw.quantized:
                 entry = run_q16(args, cw, dev, l2_attainable=l2["gbs"], traffic=committed_traffic(cw.name))
             else:
-                entry, _ = run_fp32(args, cw, dev, traffic=committed_traffic(cw.name), l2_attainable=l2["gbs"],
-                                    graph=args.graph)
+                entry, cd = run_fp32(args, cw, dev, traffic=committed_traffic(cw.name), l2_attainable=l2["gbs"],
+                                     graph=args.graph)
                 entry = dict(entry, workload=cw.name, dtype="fp32")
+                if wid == 0 and not args.no_cpu:  # the CPU-runnable configuration: its own CPU baseline
+                    log(f"[bench] cpu baseline of {cw.name} ({min(args.cpu_seconds, 8.0):.0f} s budget)")
+                    entry["cpu_baseline"] = cpu_baseline(cw, cd, min(args.cpu_seconds, 8.0))
+                    entry["gpu_over_cpu"] = entry["positions_per_s"] / entry["cpu_baseline"]["value"]
+                del cd
             entry.pop("kernels", None)
             configs.append(entry)
             r = entry["roofline"]

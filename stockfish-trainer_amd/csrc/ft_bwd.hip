@@ -508,13 +508,12 @@ __device__ __forceinline__ void bwd_tile_sum(const P *list, int n, int nmin, int
 // chunks each, present when used); at least the long-segment row buffer.
 constexpr int kBwdFeat = bwd_feat_per_block();  // 32
 struct GatherLds {
-  int start, plus, bytes;  // byte offsets (-1: absent) and size
+  int plus, bytes;  // byte offset (-1: absent) and size
 };
 __host__ __device__ inline GatherLds gather_lds(int src_mode, int dst_mode) {
+  (void)src_mode;
   GatherLds l;
   int off = kBwdPosLds * 4;
-  l.start = src_mode != kSrcZero ? off : -1;
-  off += src_mode != kSrcZero ? kBlock * 16 : 0;
   l.plus = dst_mode == kDstOutPlus ? off : -1;
   off += dst_mode == kDstOutPlus ? kBlock * 16 : 0;
   const int long_buf = kWgLongRows * 8 * (int)sizeof(f32x4);
@@ -604,19 +603,14 @@ __global__ __launch_bounds__(kBlock) void bwd_tiled_gather_kernel(const int32_t 
       }
     }
   }
-  if (lay.start >= 0 || lay.plus >= 0) {
+  if (lay.plus >= 0) {
     const int colm = tile_col(map, it.tile, cs);
-    const bool own = fs < N && colm >= 0 && !long_segment(as, es);
-    f32x4 vs = f32x4{0.f, 0.f, 0.f, 0.f}, vp = vs;
-    if (own) {
-      if (src_mode == kSrcTmp) vs = load_row<NT>(tmp + tmp_row(it.tile, fs, N) + cs);  // stored with NT too
-      if (lay.plus >= 0) {
-        const int blk = block_of(fs, dst.n, dst.start);
-        vp = load_row<NT>(pick(dst.p, blk) + (fs - pick(dst.start, blk)) * cols4 + colm);
-      }
+    f32x4 vp = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (fs < N && colm >= 0 && !long_segment(as, es)) {
+      const int blk = block_of(fs, dst.n, dst.start);
+      vp = load_row<NT>(pick(dst.p, blk) + (fs - pick(dst.start, blk)) * cols4 + colm);
     }
-    if (lay.start >= 0) reinterpret_cast<f32x4 *>(gsm + lay.start)[tid] = vs;
-    if (lay.plus >= 0) reinterpret_cast<f32x4 *>(gsm + lay.plus)[tid] = vp;
+    reinterpret_cast<f32x4 *>(gsm + lay.plus)[tid] = vp;
   }
   if (wave == 0) {
     // A wave runs as long as its longest segment: rank the features by segment
@@ -647,8 +641,13 @@ __global__ __launch_bounds__(kBlock) void bwd_tiled_gather_kernel(const int32_t 
   const int colm = tile_col(map, it.tile, t);
   const bool colok = colm >= 0;
   const char *gtile = reinterpret_cast<const char *>(gt + (int64_t)it.tile * B * TCH);
+  // The sum the previous position chunk left: loaded by the lane itself here,
+  // just before its first row loads, so its latency overlaps theirs (staging
+  // it through LDS put it in front of the workgroup's barrier).  It is still
+  // the first operand of the adds.
   f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
-  if (lay.start >= 0) acc = reinterpret_cast<const f32x4 *>(gsm + lay.start)[p * TCH + t];
+  if (src_mode == kSrcTmp && live && !is_long && colok)
+    acc = load_row<NT>(tmp + tmp_row(it.tile, f, N) + t);  // stored with NT too
   if (staged)  // P16: offsets from the chunk's first grad row
     bwd_tile_sum<true, TCH>(spos + (s0 - ra), n, nmin, nmax, t,
                             P16 ? gtile + (size_t)chunk_base * (TCH * sizeof(f32x4)) : gtile, acc);
