@@ -358,13 +358,17 @@ struct RankArgs {
 // ---- table parts ----
 // A table whose 32-column tile (N + 1 rows of 128 B) is larger than an XCD's
 // L2 is gathered in nparts passes, pass p reading table rows [p part_rows,
-// (p + 1) part_rows) only.  For each position its list is cut into the runs
-// of each part, in list (= slot) order: pass p adds list[lo_p, hi_p) onto the
-// sum the previous passes left in the output, so the position's adds keep the
-// reference order -- which needs the list's parts to be non-decreasing.  A
-// position whose list goes back to an earlier part does all its adds in pass
-// 0.  cut[r] = {start of part 1, of part 2, of part 3, final pass}; lo_p =
-// (p == 0 ? 0 : cut[p - 1]), hi_p = (p == final ? count : cut[p]).
+// (p + 1) part_rows).  For each position its list is cut into nparts runs,
+// in list (= slot) order: slot k goes to pass max(part of slots 0 .. k) (the
+// running maximum), so pass p adds list[lo_p, hi_p) onto the sum the previous
+// passes left and the position's adds keep the reference order.  For a list
+// whose parts never decrease (sorted rows) that is each slot's own part; a
+// list that goes back to an earlier part (the encoders emit threats by colour
+// and piece: about a fifth of the rows of random positions, most going back
+// once near a part boundary) reads those few rows in a later pass, from beyond
+// that pass's L2 working set, and keeps every other slot in its own part's
+// pass.  cut[r] = {start of pass 1's run, of pass 2's, of pass 3's, final
+// pass}; lo_p = (p == 0 ? 0 : cut[p - 1]), hi_p = (p == final ? count : cut[p]).
 // The runs are stored packed instead of the lists: within each block of 256
 // ranks, the runs of pass 0 for the ranks in rank order, then those of pass 1,
 // and so on (at most 256 kpad entries in all), and roff[r][p] gives where the
@@ -399,17 +403,15 @@ __global__ __launch_bounds__(kBlock) void rank_lists_kernel(RankArgs a, int64_t 
   i32x4 rv[kRegRow];
   int c = 0;
   // With table parts the same pass also finds the runs: cut[p] = the number of
-  // active slots before the first slot of a part above p, and whether the
-  // parts never go back along the row (mono).  (A second pass over the row for
-  // them took 49 of 156 us per call at K = 160; with it folded in here and 8
-  // row loads in flight per thread in both passes, the call takes 128 us.)
-  int cut[kMaxParts - 1], part = 0;
-  bool mono = true;
+  // active slots before the first slot whose running maximum of parts exceeds
+  // p.  (A second pass over the row for them took 49 of 156 us per call at
+  // K = 160; with it folded in here and 8 row loads in flight per thread in
+  // both passes, the call takes 128 us.)
+  int cut[kMaxParts - 1], part = 0;  // part: the running maximum
   auto count_slot = [&](int v) {
     if ((unsigned)v >= (unsigned)N) return;
     if (a.nparts > 1) {  // launch-uniform
       const int pv = (int)a.part_of((uint32_t)v);
-      mono = mono && pv >= part;
       for (; part < pv; ++part)
         if (part < kMaxParts - 1) cut[part] = c;
     }
@@ -497,7 +499,7 @@ __global__ __launch_bounds__(kBlock) void rank_lists_kernel(RankArgs a, int64_t 
         }
       }
     };
-    const i32x4 cv = mono ? i32x4{cut[0], cut[1], cut[2], a.nparts - 1} : i32x4{c, c, c, 0};
+    const i32x4 cv = i32x4{cut[0], cut[1], cut[2], a.nparts - 1};
     int len[kMaxParts];
 #pragma unroll
     for (int p = 0; p < kMaxParts; ++p) {
@@ -532,8 +534,11 @@ __global__ __launch_bounds__(kBlock) void rank_lists_kernel(RankArgs a, int64_t 
       L.roff[r] = i32x4{start[0], start[1], start[2], start[3]};
     }
     int w[kMaxParts] = {0, 0, 0, 0};
+    int rmax = 0;  // the running maximum of parts: the pass of this slot
     each_active([&](int v) {
-      const int p = mono ? (int)a.part_of((uint32_t)v) : 0;
+      const int pv = (int)a.part_of((uint32_t)v);
+      rmax = pv > rmax ? pv : rmax;
+      const int p = rmax;
       const int at = p == 0 ? start[0] + w[0]++ : p == 1 ? start[1] + w[1]++ : p == 2 ? start[2] + w[2]++ : start[3] + w[3]++;
       L.list[at] = v;
     });

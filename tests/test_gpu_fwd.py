@@ -116,9 +116,9 @@ def test_fwd_full_workload(wid):
 
 @pytest.mark.parametrize("pair", [False, True])
 def test_fwd_table_parts_mixed_rows(pair):
-    """A table of four parts (N = 85296 rows: 10.9 MB per 32-column tile) with
+    """A table of several parts (N = 85296 rows: 10.9 MB per 32-column tile) with
     rows whose parts rise (spread over the passes), rows that go back to an
-    earlier part (all adds in the first pass), rows inside one part, rows that
+    earlier part (each slot in the pass of the largest part up to it), rows inside one part, rows that
     repeat a feature across a part boundary, empty rows and rows at the table's
     ends -- bit-exact with the ordered oracle in every case."""
     announce(f"fwd table parts, mixed rows, pair={pair}")
@@ -151,3 +151,36 @@ def test_fwd_table_parts_mixed_rows(pair):
         _native.ft_fwd_pair_f32(dev(idx), dev(idx1), [dev(W)], [None], dev(b), o0, o1)
         assert np.array_equal(host(o0), ref)
         assert np.array_equal(host(o1), ft_oracle.fwd_f32(idx1, W, b))
+
+
+@pytest.mark.parametrize("pair", [False, True])
+def test_fwd_table_parts_encoder_rows(pair):
+    """Index rows as the feature encoder emits them for Full_Threats+HalfKAv2_hm
+    (threats by colour and piece, then HalfKAv2_hm, offset by 60720): about a
+    fifth of the rows go back to an earlier table part, most once near a part
+    boundary.  Bit-exact with the ordered oracle."""
+    from oracle import feature_oracle
+    from sft_amd.positions import random_positions
+
+    announce(f"fwd table parts, encoder rows, pair={pair}")
+    boards, stm = random_positions(4000, seed=17)
+    enc = feature_oracle.encode(boards, stm, ["Full_Threats", "HalfKAv2_hm"])
+    idx0, idx1 = enc["white"], enc["black"]
+    B, K = idx0.shape
+    N, L = 85296, 1048
+    part = -(-N // 3)
+    back = sum(not np.all(np.diff(r[r >= 0] // part) >= 0) for r in idx0)
+    assert back > B // 20  # the case this test is for
+    g = np.random.default_rng(23)
+    W = (g.standard_normal((N, L)) * 0.01).astype(np.float32)
+    b = g.uniform(-0.1, 0.1, L).astype(np.float32)
+    ref0, ref1 = ft_oracle.fwd_f32(idx0, W, b), ft_oracle.fwd_f32(idx1, W, b)
+    if not pair:
+        out = torch.empty(B, L, device=DEV)
+        _native.ft_fwd_f32(dev(idx0), dev(W), dev(b), out)
+        assert np.array_equal(host(out), ref0)
+    else:
+        o0, o1 = torch.empty(B, L, device=DEV), torch.empty(B, L, device=DEV)
+        _native.ft_fwd_pair_f32(dev(idx0), dev(idx1), [dev(W)], [None], dev(b), o0, o1)
+        assert np.array_equal(host(o0), ref0)
+        assert np.array_equal(host(o1), ref1)
