@@ -415,7 +415,7 @@ constexpr int bwd_feat_per_block() { return kWavesPerBlock * (kWave / kBwdTileCh
 // Long segments are summed in 32-column blocks by the tiled gather's
 // long-segment slots.
 #ifndef SFT_BWD_LONG_SLOTS
-#define SFT_BWD_LONG_SLOTS 256
+#define SFT_BWD_LONG_SLOTS 128
 #endif
 constexpr int kLongSlots = SFT_BWD_LONG_SLOTS;  // long-segment workgroups per tile
 #ifndef SFT_BWD_ROW_LONG_BLOCKS
@@ -499,10 +499,13 @@ __device__ __forceinline__ void bwd_tile_sum(const P *list, int n, int nmin, int
 // the start row after it made a chain of about ten dependent round trips that
 // took half of a launch at B = 65536.)
 //
-// Each tile's items start with nlong long-segment slots: slot j sums the
-// chunk's listed long segments j, j + nlong, ... for this tile with the
-// whole workgroup (long_segment_sum_wg), while the tile is in the XCD's L2;
-// the feature blocks follow.
+// The launch starts with nlong long-segment slots per tile (every tile of an
+// XCD, in its tile order): slot j sums the chunk's listed long segments j,
+// j + nlong, ... for its tile with the whole workgroup (long_segment_sum_wg);
+// the feature blocks follow, tile by tile.  A long segment is a chain of
+// dependent adds, so the chains of an XCD's tiles run side by side instead of
+// one tile after another (Zipf alpha = 1.0, B = 65536: 415.6 -> 365.3 us per
+// launch at 128 slots, uniform features 204.1 -> 205.7 us).
 //
 // Dynamic LDS: positions (kBwdPosLds ints) | start rows | plus rows (256
 // chunks each, present when used); at least the long-segment row buffer.
@@ -534,9 +537,16 @@ __global__ __launch_bounds__(kBlock) void bwd_tiled_gather_kernel(const int32_t 
   constexpr int TCH = kBwdTileCh;
   extern __shared__ __align__(16) char gsm[];
   __shared__ int s_seg[kBwdFeat + 1], s_perm[kBwdFeat];
-  const TileItem it = tile_sched_item(blockIdx.x, ntiles, ngroups + nlong);
+  // The long-segment slots of every tile come first in the launch (each XCD's
+  // in its tile order), then the feature blocks: the long chains of an XCD's
+  // tiles, each a sequence of dependent adds, run side by side instead of one
+  // tile after another.
+  const int64_t nl_items = tile_sched_items_per_xcd(ntiles, nlong) * kXcds;
+  const bool long_item = (int64_t)blockIdx.x < nl_items;  // whole block: uniform
+  const TileItem it = long_item ? tile_sched_item(blockIdx.x, ntiles, nlong)
+                                : tile_sched_item(blockIdx.x - nl_items, ntiles, ngroups);
   if (it.tile >= ntiles) return;  // whole block: uniform
-  if (it.chunk < nlong) {         // whole block: uniform
+  if (long_item) {
     const int cnt = *long_count;
     for (int e = it.chunk; e < cnt; e += nlong) {
       const int64_t f = long_list[e];
@@ -552,7 +562,7 @@ __global__ __launch_bounds__(kBlock) void bwd_tiled_gather_kernel(const int32_t 
   const int tid = threadIdx.x;
   const int wave = uniform(tid / kWave);
   const int lane = tid % kWave;
-  const int64_t fb = (int64_t)(it.chunk - nlong) * kBwdFeat;
+  const int64_t fb = (int64_t)it.chunk * kBwdFeat;
   const int nf = (int)(N - fb < kBwdFeat ? N - fb : kBwdFeat);  // features of this block, >= 1
 
   // round 1: segment bounds -- the range (uniform), this thread's feature for
@@ -672,7 +682,7 @@ int launch_tiled_gather(bool nt, const int32_t *seg, const int32_t *pos, const u
                         int64_t N, const f32x4 *gt, int64_t B, const ColMap &map, const RowDst &dst, f32x4 *tmp,
                         int src_mode, int dst_mode, int ntiles, int ngroups, const int32_t *long_list,
                         const int *long_count, int nlong, hipStream_t s) {
-  const int64_t items = tile_sched_items_per_xcd(ntiles, ngroups + nlong);
+  const int64_t items = tile_sched_items_per_xcd(ntiles, nlong) + tile_sched_items_per_xcd(ntiles, ngroups);
   const size_t lds = (size_t)gather_lds(src_mode, dst_mode).bytes;
   if ((uintptr_t)pos % 16 != 0 || (uintptr_t)pos16 % 16 != 0)  // 256-byte / 16-byte aligned workspace regions
     return fail(SFT_EINVAL, "tiled feature gather: sorted positions not 16-byte aligned");
