@@ -490,14 +490,16 @@ __device__ __forceinline__ void bwd_tile_sum(const P *list, int n, int nmin, int
 //
 // In front of the gather a workgroup makes two rounds of global loads, each
 // issued whole before anything waits on it: (1) the segment bounds; (2) the
-// positions (8 loads per thread in flight) together with the rows the sums
-// start from and, for kDstOutPlus, the rows they add onto -- thread i loads
-// chunk i % 8 of feature i / 8 into LDS.  Meanwhile wave 0 ranks the 32
-// features by segment length with cross-lane reads.  One barrier, then each
-// lane group sums one feature.  (Staging one position per thread per round
-// trip, reading the segment bounds again after the ranking barrier and loading
-// the start row after it made a chain of about ten dependent round trips that
-// took half of a launch at B = 65536.)
+// positions (8 loads per thread in flight) together with, for kDstOutPlus, the
+// rows the sums add onto -- thread i loads chunk i % 8 of feature i / 8 into
+// LDS.  Meanwhile wave 0 ranks the 32 features by segment length with
+// cross-lane reads.  One barrier, then each lane group sums one feature,
+// starting from the sum the previous position chunk left, which the lane
+// loads itself beside its first row loads.  (Staging one position per thread
+// per round trip, reading the segment bounds again after the ranking barrier
+// and loading the start row after it, each waited for on its own, made a chain
+// of about ten dependent round trips that took half of a launch at
+// B = 65536.)
 //
 // The launch starts with nlong long-segment slots per tile (every tile of an
 // XCD, in its tile order): slot j sums the chunk's listed long segments j,
@@ -507,14 +509,13 @@ __device__ __forceinline__ void bwd_tile_sum(const P *list, int n, int nmin, int
 // one tile after another (Zipf alpha = 1.0, B = 65536: 415.6 -> 365.3 us per
 // launch at 128 slots, uniform features 204.1 -> 205.7 us).
 //
-// Dynamic LDS: positions (kBwdPosLds ints) | start rows | plus rows (256
-// chunks each, present when used); at least the long-segment row buffer.
+// Dynamic LDS: positions (kBwdPosLds ints) | plus rows (256 chunks, present
+// for kDstOutPlus); at least the long-segment row buffer.
 constexpr int kBwdFeat = bwd_feat_per_block();  // 32
 struct GatherLds {
   int plus, bytes;  // byte offset (-1: absent) and size
 };
-__host__ __device__ inline GatherLds gather_lds(int src_mode, int dst_mode) {
-  (void)src_mode;
+__host__ __device__ inline GatherLds gather_lds(int dst_mode) {
   GatherLds l;
   int off = kBwdPosLds * 4;
   l.plus = dst_mode == kDstOutPlus ? off : -1;
@@ -537,10 +538,6 @@ __global__ __launch_bounds__(kBlock) void bwd_tiled_gather_kernel(const int32_t 
   constexpr int TCH = kBwdTileCh;
   extern __shared__ __align__(16) char gsm[];
   __shared__ int s_seg[kBwdFeat + 1], s_perm[kBwdFeat];
-  // The long-segment slots of every tile come first in the launch (each XCD's
-  // in its tile order), then the feature blocks: the long chains of an XCD's
-  // tiles, each a sequence of dependent adds, run side by side instead of one
-  // tile after another.
   const int64_t nl_items = tile_sched_items_per_xcd(ntiles, nlong) * kXcds;
   const bool long_item = (int64_t)blockIdx.x < nl_items;  // whole block: uniform
   const TileItem it = long_item ? tile_sched_item(blockIdx.x, ntiles, nlong)
@@ -556,7 +553,7 @@ __global__ __launch_bounds__(kBlock) void bwd_tiled_gather_kernel(const int32_t 
     }
     return;
   }
-  const GatherLds lay = gather_lds(src_mode, dst_mode);
+  const GatherLds lay = gather_lds(dst_mode);
   int *spos = reinterpret_cast<int *>(gsm);
   const int64_t cols4 = map.cols4;
   const int tid = threadIdx.x;
@@ -683,7 +680,7 @@ int launch_tiled_gather(bool nt, const int32_t *seg, const int32_t *pos, const u
                         int src_mode, int dst_mode, int ntiles, int ngroups, const int32_t *long_list,
                         const int *long_count, int nlong, hipStream_t s) {
   const int64_t items = tile_sched_items_per_xcd(ntiles, nlong) + tile_sched_items_per_xcd(ntiles, ngroups);
-  const size_t lds = (size_t)gather_lds(src_mode, dst_mode).bytes;
+  const size_t lds = (size_t)gather_lds(dst_mode).bytes;
   if ((uintptr_t)pos % 16 != 0 || (uintptr_t)pos16 % 16 != 0)  // 256-byte / 16-byte aligned workspace regions
     return fail(SFT_EINVAL, "tiled feature gather: sorted positions not 16-byte aligned");
   const dim3 grid((unsigned)(items * kXcds));
