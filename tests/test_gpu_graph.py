@@ -112,3 +112,32 @@ def test_graph_fused_transform():
         return [l0, psqt] + [p.grad for p in ft.parameters()]
 
     _capture_and_compare(step, 0)
+
+
+def test_graph_fused_composed():
+    """The fused two-perspective op (ComposedSparseLinearFunction) at a batch
+    whose backward runs two position chunks: the side-stream sorts, each
+    perspective's bias pass before its gathers and the second perspective's
+    sum onto the first all capture and replay bit for bit."""
+    announce("graph: fused composed fwd+bwd, two position chunks")
+    B = 34000
+    torch.manual_seed(6)
+    ft = get_feature_cls("HalfKAv2_hm^")(1048).to(DEV)
+    with torch.no_grad():
+        ft.features[0].weight.normal_(0, 0.05)
+        ft.features[0].virtual_weight.normal_(0, 0.02)
+    assert ft.fused
+    g = np.random.default_rng(10)
+    iw = dev(workloads.make_indices(g, B, 24576, 32, 16, 32))
+    ib = dev(workloads.make_indices(g, B, 24576, 32, 16, 32, sort=False))
+    gw = torch.randn(B, 1048, device=DEV)
+    gb = torch.randn(B, 1048, device=DEV)
+
+    def step():
+        for p in ft.parameters():
+            p.grad = None
+        ow, ob = ft(iw, ib)
+        torch.autograd.backward([ow, ob], [gw, gb])
+        return [ow, ob] + [p.grad for p in ft.parameters()]
+
+    _capture_and_compare(step, 0)
