@@ -562,7 +562,7 @@ __global__ __launch_bounds__(kBlock) void bwd_tiled_gather_kernel(const int32_t 
   const int64_t fb = (int64_t)it.chunk * kBwdFeat;
   const int nf = (int)(N - fb < kBwdFeat ? N - fb : kBwdFeat);  // features of this block, >= 1
 
-  // round 1: segment bounds -- the range (uniform), this thread's feature for
+  // load round 1: segment bounds -- the range (uniform), this thread's feature for
   // the start rows, and one feature per lane of wave 0 for the ranking
   const int r0 = seg[fb], r1 = seg[fb + nf];
   const int64_t fs = fb + tid / TCH;  // start-row feature of this thread
@@ -575,7 +575,7 @@ __global__ __launch_bounds__(kBlock) void bwd_tiled_gather_kernel(const int32_t 
   int la = 0;
   if (wave == 0) la = seg[fb + (lane < nf ? lane : nf)];
 
-  // round 2: positions, start rows, plus rows.  The range is copied in
+  // load round 2: positions, start rows, plus rows.  The range is copied in
   // 16-byte pieces from r0 rounded down to a piece boundary (the position
   // streams are 16-byte aligned and padded by 16 bytes), so spos[j] holds
   // entry ra + j: from the 16-bit chunk offsets (P16: eight per piece, widened

@@ -14,7 +14,7 @@ counter reads for it.  The caller must not have initialised the GPU in its own
 process when it starts the passes (a profiled child of a process holding the
 GPU is not allowed on the target machines).
 
-  python stockfish-trainer_amd/sft_amd/traffic.py --workload 1 --dir gpurun_out/pmc \
+  python stockfish-trainer_amd/sft_amd/traffic.py --workload 1 --dir /tmp/sft_pmc \
       --md profiles/pmc_traffic_halfka_b65536.md
 """
 
@@ -29,6 +29,7 @@ import re
 import shutil
 import subprocess
 import sys
+import tempfile
 
 PKG = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 ROOT = os.path.dirname(PKG)
@@ -156,7 +157,7 @@ def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--workload", type=int, default=1)
     ap.add_argument("--steps", type=int, default=3)
-    ap.add_argument("--dir", default=os.path.join(ROOT, "gpurun_out", "pmc"))
+    ap.add_argument("--dir", default=None, help="where rocprofv3 writes its passes (default: a new temporary directory)")
     ap.add_argument("--md", default=None, help="write the summary table to this file")
     ap.add_argument("--json", default=None, help="write the per-kind bytes per step (bench.py reads it) here")
     ap.add_argument("--title", default=None)
@@ -164,7 +165,8 @@ def main() -> int:
     sys.path.insert(0, PKG)
     from sft_amd import workloads
 
-    t = measure(args.workload, args.dir, args.steps)
+    out_dir = args.dir or tempfile.mkdtemp(prefix="sft_pmc_")
+    t = measure(args.workload, out_dir, args.steps)
     text = summary_md(t, args.title or workloads.WORKLOADS[args.workload].name)
     if args.md:
         with open(args.md, "w") as f:
