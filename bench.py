@@ -11,16 +11,18 @@ dominant kernel, a CPU baseline (the PyTorch-CPU restatement timed on a bounded
 sample of the same workload) and, under "configs", the same measurements for
 every workload 0-4.
 
-Rooflines: a gather kernel's algorithmic bytes per launch (the rows it
-requests) over its average HIP-event duration, against the L2's peak (every
-requested byte passes the L2) and the measured ceiling of L2-served row
-gathers (sft_probe_l2_gather); a streaming kernel's against HBM's 8 TB/s.  The
-memory-side bytes the counters report (two rocprofv3 passes run in child
-processes before this process touches the GPU, or the committed summary) give
-each kernel's HBM view, and the step's compulsory bytes (what it cannot avoid
-moving) its HBM fraction.
+Roofline of the dominant kernel (the most time per step among kernels with an
+algorithmic byte count): the memory-side bytes the counters report per launch
+(rocprofv3 FETCH_SIZE x 2 + WRITE_SIZE, from two passes run in child processes
+before this process touches the GPU, or the committed summary) over its average
+HIP-event duration, against HBM's published 8 TB/s.  Beside it, as "logical",
+the algorithmic bytes of the byte model (every requested row counted, including
+the re-reads the L2 serves, so that fraction can exceed 1), and for gathers the
+L2-side figures: a derived L2 peak and the measured ceiling of L2-served row
+gathers (sft_probe_l2_gather).  Every timed leg is the median of --reps
+repetitions of --steps steps, with their minimum and maximum.
 
-  python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--warmup-s 0.25] [--workload 1]
+  python bench.py [--gpus 1] [--steps 20] [--reps 5] [--warmup 5] [--warmup-s 0.25] [--workload 1]
                   [--bwd sorted|atomic] [--cpu-seconds 12] [--no-cpu] [--no-graph]
                   [--no-configs] [--traffic live|profile|off]
   python bench.py --composed halfka|threats   (module surface, fused vs reference composition)
@@ -82,7 +84,8 @@ def kernel_step_bytes(kind: str, w, idx_pair) -> float | None:
 
 # What the L2 can deliver to the CUs: 8 XCDs x 16 L2 channels x 128 B per clock at
 # the 2.4 GHz peak engine clock (the CDNA L2 width; MI355X has 4 MB of L2 per XCD).
-L2_PEAK_GBS = 8 * 16 * 128 * 2.4
+# A derived figure, not a published one: reported beside the HBM roofline only.
+L2_DERIVED_PEAK_GBS = 8 * 16 * 128 * 2.4
 
 # Kernels that fetch rows at random from a table or grad tile: every byte they
 # request passes the L2, whether it hits there or comes from MALL or HBM.
@@ -92,29 +95,64 @@ GATHER_KINDS = {"fwd_f32_gather", "fwd_f32_tiled_gather", "bwd_feature_gather", 
 
 def roofline(kind: str, bytes_per_launch: float, avg_ms: float, traffic: float | None = None,
              traffic_source: str | None = None, l2_attainable: float | None = None) -> dict:
-    """A kernel against the bound that limits it.
+    """A kernel against HBM's published peak.
 
-    Gathers are priced against the L2's peak (their algorithmic bytes are the rows
-    they request, nearly all of which the tiled design serves from L2), with the
-    measured ceiling of L2-served row gathers beside it; kernels that stream each
-    byte through HBM once (re-layouts, bias sums) against HBM's peak.  `traffic`
-    is the memory-side bytes per launch the counters report (MALL hits included):
-    the `hbm` entry prices that against 8 TB/s, so every fraction is at most 1.
-    """
-    achieved = bytes_per_launch / (avg_ms * 1e-3) / 1e9
-    gather = kind in GATHER_KINDS
-    peak = L2_PEAK_GBS if gather else HBM_PEAK_GBS
-    r = {"kernel": kind, "bound": "l2" if gather else "hbm", "achieved": achieved, "peak": peak, "unit": "GB/s",
-         "frac": achieved / peak, "traffic": traffic}
-    if gather and l2_attainable:
-        r["attainable"] = l2_attainable
-        r["frac_of_attainable"] = achieved / l2_attainable
+    achieved = the memory-side bytes the counters count per launch (`traffic`:
+    FETCH_SIZE x 2 + WRITE_SIZE, MALL hits included, so an upper bound of the HBM
+    bytes) / the average launch time; frac = achieved / 8 TB/s.  Without counter
+    traffic (--traffic off) the algorithmic bytes stand in and the basis says so.
+    "logical" prices the algorithmic bytes per launch (the byte model's rows,
+    re-reads served by the L2 included) against the same peak; for gathers that
+    can exceed 1.  Gathers also get the L2 view: the derived L2 peak and the
+    measured ceiling of L2-served 128-byte row gathers."""
+    logical = bytes_per_launch / (avg_ms * 1e-3) / 1e9
+    r = {"kernel": kind, "bound": "hbm", "peak": HBM_PEAK_GBS, "unit": "GB/s", "avg_launch_ms": avg_ms}
     if traffic:
         hbm = traffic / (avg_ms * 1e-3) / 1e9
-        r["hbm"] = {"achieved": hbm, "peak": HBM_PEAK_GBS, "frac": hbm / HBM_PEAK_GBS, "source": traffic_source}
-    r["algorithmic_bytes_per_launch"] = bytes_per_launch
-    r["avg_launch_ms"] = avg_ms
+        r.update(achieved=hbm, frac=hbm / HBM_PEAK_GBS, traffic=traffic, traffic_source=traffic_source,
+                 basis="memory-side bytes per launch (rocprofv3 FETCH_SIZE x 2 + WRITE_SIZE) / average launch time")
+    else:
+        r.update(achieved=logical, frac=logical / HBM_PEAK_GBS, traffic=None,
+                 basis="algorithmic bytes per launch / average launch time (no counter traffic in this run)")
+    r["logical"] = {"bytes_per_launch": bytes_per_launch, "achieved": logical,
+                    "frac_of_hbm_peak": logical / HBM_PEAK_GBS,
+                    "note": "algorithmic bytes of the byte model (4K + 4L(n+1) per position and direction, "
+                            "4NL per weight-grad write): every requested row, L2-served re-reads included"}
+    if kind in GATHER_KINDS:
+        r["l2"] = {"derived_peak": L2_DERIVED_PEAK_GBS, "frac_of_derived_peak": logical / L2_DERIVED_PEAK_GBS,
+                   "note": "derived (8 XCDs x 16 channels x 128 B x 2.4 GHz), not a published figure"}
+        if l2_attainable:
+            r["l2"]["measured_ceiling"] = l2_attainable
+            r["l2"]["frac_of_measured_ceiling"] = logical / l2_attainable
     return r
+
+
+def timed_reps(fn, steps: int, reps: int) -> list:
+    """ms per call of fn in each of `reps` repetitions of `steps` back-to-back
+    calls, each bracketed by HIP events on the current stream and a
+    synchronisation on both sides."""
+    import torch
+
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    out = []
+    for _ in range(reps):
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(steps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        out.append(e0.elapsed_time(e1) / steps)
+    return out
+
+
+def rep_stats(ms: list) -> dict:
+    """Median (the reported figure), minimum and maximum of the repetitions."""
+    import statistics
+
+    return {"ms_per_step": statistics.median(ms), "ms_per_step_min": min(ms), "ms_per_step_max": max(ms),
+            "reps": len(ms), "ms_per_step_reps": ms}
 
 
 def committed_traffic(name: str) -> dict | None:
@@ -269,14 +307,8 @@ def run_q16(args, w, dev, l2_attainable=None, traffic=None) -> dict:
     iw = torch.from_numpy(d["idx_w"]).to(dev)
     ib = torch.from_numpy(d["idx_b"]).to(dev)
     warm_up(lambda: qft(iw, ib), args.warmup, args.warmup_s)
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(args.steps):
-        qft(iw, ib)
-    e1.record()
-    torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / args.steps
+    timing = rep_stats(timed_reps(lambda: qft(iw, ib), args.steps, args.reps))
+    ms = timing["ms_per_step"]
     _native.prof_enable(True)  # per-kernel durations from a separate pass with the launch events
     for _ in range(args.steps):
         qft(iw, ib)
@@ -310,18 +342,13 @@ def run_q16(args, w, dev, l2_attainable=None, traffic=None) -> dict:
             quantized_ft_forward(i, qft.weight_q, qft.bias_q, qft.psqt_q, 0, 127)
 
     warm_up(per_call, args.warmup, args.warmup_s)
-    p0.record()
-    for _ in range(args.steps):
-        per_call()
-    p1.record()
-    torch.cuda.synchronize()
-    per_call_ms = p0.elapsed_time(p1) / args.steps
+    per_call_ms = rep_stats(timed_reps(per_call, args.steps, args.reps))["ms_per_step"]
     compulsory = workloads.q16_compulsory_bytes(w.B, w.K, w.N, w.L, w.psqt)
     return {
         "workload": w.name, "dtype": "int16", "feature_set": w.feature_set, "batch": w.B, "num_inputs": w.N,
         "max_active": w.K, "active": [w.lo, w.hi], "output_size": w.L, "psqt": w.psqt, "quant_scale": 127,
         "clip": [0, 127], "step": "int16 forward of both perspectives from the packed table",
-        "ms_per_step": ms, "positions_per_s": w.B / (ms * 1e-3), "step_bytes": step_bytes,
+        **timing, "positions_per_s": w.B / (ms * 1e-3), "step_bytes": step_bytes,
         "step_gbs": step_bytes / (ms * 1e-3) / 1e9,
         "step_compulsory_bytes": compulsory,
         "step_compulsory_frac_of_hbm_peak": compulsory / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
@@ -336,7 +363,9 @@ def bench_q16(args, w, dev) -> int:
     result = {
         "metric": "int16 FT forward positions/sec (both perspectives) @B=65536,L1=1040",
         "value": c["positions_per_s"], "unit": "positions/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "warmup_s": args.warmup_s, "ms_per_step": c["ms_per_step"], "higher_is_better": True,
+        "warmup": args.warmup, "warmup_s": args.warmup_s, "ms_per_step": c["ms_per_step"],
+        **{k: c[k] for k in ("reps", "ms_per_step_min", "ms_per_step_max", "ms_per_step_reps")},
+        "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "int16", "data": "synthetic",
         "config": {"workload": w.name, "feature_set": w.feature_set, "batch": w.B, "num_inputs": w.N,
                    "max_active": w.K, "active": [w.lo, w.hi], "output_size": w.L, "psqt": w.psqt,
@@ -837,6 +866,8 @@ def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--reps", type=int, default=5,
+                    help="timed repetitions of --steps steps per leg; the median is reported, with min and max")
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--warmup-s", type=float, default=0.25,
                     help="warm-up also runs until this many seconds have passed (GPU clock ramp)")
@@ -902,7 +933,8 @@ def main() -> int:
         return bench_q16(args, w, dev)
 
     l2 = l2_gather_ceiling(dev, args.warmup_s)
-    log(f"[bench] L2-served 128-byte row gathers (probe): {l2['gbs']:.0f} GB/s; L2 peak {L2_PEAK_GBS:.0f} GB/s")
+    log(f"[bench] L2-served 128-byte row gathers (probe): {l2['gbs']:.0f} GB/s; derived L2 peak "
+        f"{L2_DERIVED_PEAK_GBS:.0f} GB/s")
     head, d = run_fp32(args, w, dev, zipf=args.zipf, traffic=traffic, l2_attainable=l2["gbs"], graph=args.graph,
                        hashes=True)
     ms = head["ms_per_step"]
@@ -914,6 +946,8 @@ def main() -> int:
         "steps": args.steps,
         "warmup": args.warmup, "warmup_s": args.warmup_s,
         "ms_per_step": ms,
+        "reps": head["reps"], "ms_per_step_min": head["ms_per_step_min"], "ms_per_step_max": head["ms_per_step_max"],
+        "ms_per_step_reps": head["ms_per_step_reps"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -967,9 +1001,9 @@ def main() -> int:
             entry.pop("kernels", None)
             configs.append(entry)
             r = entry["roofline"]
-            log(f"[bench] config {wid} {cw.name}: {entry['ms_per_step']:.3f} ms/step, "
-                f"{entry['positions_per_s'] / 1e6:.1f} M positions/s; {r['kernel']} {r['bound']} frac {r['frac']:.2f}"
-                + (f", hbm frac {r['hbm']['frac']:.2f}" if r.get("hbm") else ""))
+            log(f"[bench] config {wid} {cw.name}: {entry['ms_per_step']:.3f} ms/step (median of {entry['reps']}), "
+                f"{entry['positions_per_s'] / 1e6:.1f} M positions/s; {r['kernel']} hbm frac {r['frac']:.2f}, "
+                f"logical {r['logical']['frac_of_hbm_peak']:.2f}")
             torch.cuda.empty_cache()
         result["configs"] = configs
         # Robustness, not the headline: the headline workload with Zipf-like
@@ -1035,25 +1069,17 @@ def run_fp32(args, w, dev, zipf=None, traffic=None, l2_attainable=None, graph=Tr
 
     # The eager step, then per-kernel durations from a second eager pass with the
     # library's launch events (which add ~0.1 ms per step of their own).
-    torch.cuda.synchronize()
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
-    t0 = time.perf_counter()
-    e0.record()
-    for _ in range(args.steps):
-        step()
-    e1.record()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    eager_ms = e0.elapsed_time(e1) / args.steps
-    log(f"[bench] eager {args.steps} steps: {eager_ms:.3f} ms/step (wall {wall * 1e3 / args.steps:.3f} ms/step)")
+    eager = rep_stats(timed_reps(step, args.steps, args.reps))
+    eager_ms = eager["ms_per_step"]
+    log(f"[bench] eager {args.reps} x {args.steps} steps: {eager_ms:.3f} ms/step (median; "
+        f"{eager['ms_per_step_min']:.3f}-{eager['ms_per_step_max']:.3f})")
     _native.prof_enable(True)
     for _ in range(args.steps):
         step()
     torch.cuda.synchronize()
     prof = _native.prof_collect()
     _native.prof_enable(False)
-    ms = eager_ms
+    timing = eager
     if graph:
         # The whole step (both forwards, autograd backward, the grad sum) as one
         # HIP graph: the library makes no host synchronisation inside its calls.
@@ -1068,16 +1094,11 @@ def run_fp32(args, w, dev, zipf=None, traffic=None, l2_attainable=None, graph=Tr
         with torch.cuda.graph(g):
             step()
         warm_up(g.replay, args.warmup, args.warmup_s)
-        t0 = time.perf_counter()
-        e0.record()
-        for _ in range(args.steps):
-            g.replay()
-        e1.record()
-        torch.cuda.synchronize()
-        wall = time.perf_counter() - t0
-        ms = e0.elapsed_time(e1) / args.steps
-        log(f"[bench] graph {args.steps} replays: {ms:.3f} ms/step (wall {wall * 1e3 / args.steps:.3f} ms/step)")
+        timing = rep_stats(timed_reps(g.replay, args.steps, args.reps))
+        log(f"[bench] graph {args.reps} x {args.steps} replays: {timing['ms_per_step']:.3f} ms/step (median; "
+            f"{timing['ms_per_step_min']:.3f}-{timing['ms_per_step_max']:.3f})")
         del g
+    ms = timing["ms_per_step"]
     if restore is not None:
         ftk._BackwardKernel.__call__ = restore
 
@@ -1103,7 +1124,7 @@ def run_fp32(args, w, dev, zipf=None, traffic=None, l2_attainable=None, graph=Tr
     out = {
         "feature_set": w.feature_set, "batch": w.B, "num_inputs": w.N, "max_active": w.K, "active": [w.lo, w.hi],
         "output_size": w.L, "step": "fwd + bwd of both perspectives through SparseLinearFunction",
-        "ms_per_step": ms, "eager_ms_per_step": eager_ms, "positions_per_s": w.B / (ms * 1e-3),
+        **timing, "eager_ms_per_step": eager_ms, "positions_per_s": w.B / (ms * 1e-3),
         "step_bytes": step_bytes, "step_gbs": step_bytes / (ms * 1e-3) / 1e9,
         "step_compulsory_bytes": compulsory,
         "step_compulsory_frac_of_hbm_peak": compulsory / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,

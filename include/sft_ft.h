@@ -134,7 +134,8 @@ int sft_ft_bwd_f32(const int32_t *idx, int64_t batch, int32_t max_active, const 
  * path is the bias pass and the gathers alone.  Results are those of
  * sft_ft_fwd_f32_ex and sft_ft_bwd_f32, bit for bit.  The buffer must be
  * filled with the same indices, sizes and backward flags that the prepared
- * backward is called with, and is read once.
+ * backward is called with; the backward only reads it, so it may be read by
+ * more than one backward (a graph's backward run again with retain_graph).
  * No reference counterpart: the reference sorts inside the backward
  * (FT/kernel.py:108-138), which this splits off its call
  * (FT/functions.py:12-48 forward, :50-72 backward).
@@ -153,8 +154,10 @@ int sft_ft_fwd_f32_prep(const int32_t *idx, int64_t batch, int32_t max_active, c
                         size_t prep_bytes, uint32_t bwd_flags, void *stream);
 /* sft_ft_bwd_f32 from a prepared buffer; workspace of
  * sft_ft_bwd_f32_workspace_size(..., flags | SFT_BWD_PREPARED) bytes.  The
- * buffer may be overwritten (a grad whose alignment rules out the tiled
- * gather is sorted again into it, on the call's stream). */
+ * buffer is not written.  When the prepared sort is in position chunks (the
+ * tiled gather at batch > 32768), weight_grad must be 16-byte aligned
+ * (SFT_EINVAL otherwise: the row gather the unaligned grad would need sorts in
+ * one chunk); grad_out and bias_grad may have any 4-byte alignment. */
 int sft_ft_bwd_f32_prepared(const int32_t *idx, int64_t batch, int32_t max_active,
                             const float *grad_out, int64_t num_inputs, int32_t output_size,
                             float *weight_grad, float *bias_grad, void *prep, size_t prep_bytes,
@@ -202,25 +205,10 @@ int sft_ft_fwd_i16_ex(const int32_t *idx, int64_t batch, int32_t max_active,
                       void *workspace, size_t workspace_bytes, uint32_t flags, void *stream);
 
 /*
- * int16 forward that allocates nothing and takes no workspace.  No reference
- * counterpart: it is for callers that cannot allocate device memory (code
- * under HIP graph capture, serving loops, harnesses that forbid hipMalloc).
- * Same arguments, flags and results, bit for bit, as sft_ft_fwd_i16_ex with a
- * workspace of sft_ft_fwd_i16_workspace_size() bytes (it compacts the index
- * rows once per column tile, as sft_ft_fwd_i16_packed, instead of building rank
- * lists, so its scratch need does not grow with the batch).  The packed tiles go to
- * a static device array of SFT_NOALLOC_SCRATCH_BYTES that each GPU holds until
- * the process ends; a tiled shape whose packed table is larger returns
- * SFT_EWORKSPACE and launches nothing (shapes outside the tiled path run the
- * row gather, which needs no scratch).  All calls on one GPU share its array:
- * calls that overlap on one GPU (other threads or streams) race; serialise them.
+ * The int16 forward that allocates nothing, sft_ft_fwd_i16_noalloc, is in its
+ * own library, libsft_ft_noalloc.so (sft_ft_noalloc.h): its static device
+ * scratch is reserved only in processes that load that library.
  */
-#define SFT_NOALLOC_SCRATCH_BYTES (64u << 20)
-int sft_ft_fwd_i16_noalloc(const int32_t *idx, int64_t batch, int32_t max_active,
-                           const int16_t *weight, int64_t num_inputs, int32_t output_size,
-                           const int16_t *bias, const int32_t *psqt_weight, int32_t psqt_size,
-                           int16_t *out, int32_t *psqt_out, int32_t clip_lo, int32_t clip_hi,
-                           uint32_t flags, void *stream);
 
 /*
  * ---- int16 table packed once, forward of one or both perspectives ----

@@ -878,10 +878,12 @@ __global__ __launch_bounds__(kBlock) void zero_kernel(float *__restrict__ p, int
 // lane l owns chunks c0 + l + 64 j like the row gathers; the four wave sums
 // are combined in a fixed order.  Deterministic.
 //
-// When gt is not null (T = f32x4 only), each grad chunk read is also stored to
-// the column-tile layout of the tiled gather, tiles of 2^gt_shift chunks:
-// gt[(c >> gt_shift) * B + r][c mod 2^gt_shift], so the grad crosses HBM once
-// for both the bias sum and the re-layout.
+// When gt is not null, each grad element read (a 16-byte chunk for T = f32x4,
+// a float for T = float) is also stored to the column-tile layout of the tiled
+// gather, tiles of 2^gt_shift elements: gt[(c >> gt_shift) * B + r][c mod
+// 2^gt_shift] -- the same bytes for a float4 c with shift s as for its floats
+// with shift s + 2 -- so the grad crosses HBM once for both the bias sum and
+// the re-layout.
 template <typename T, int CPL>
 __global__ __launch_bounds__(kBlock) void bias_partial_kernel(const T *__restrict__ grad, int64_t B, int64_t cols,
                                                               int64_t rows_per_block, T *__restrict__ partial,
@@ -1059,7 +1061,8 @@ int make_layout(int64_t B, int K, int64_t N, int L, uint32_t flags, BwdLayout &l
 
 int launch_bias_partial(const float *grad, int64_t B, int L, int nparts, float *partial, f32x4 *gt, bool vec,
                         hipStream_t s, int gt_tch = 8) {
-  const int gt_shift = gt_tch == 4 ? 2 : gt_tch == 16 ? 4 : 3;
+  // tile width in the kernel's element type: gt_tch 16-byte chunks, or 4 x as many floats
+  const int gt_shift = (gt_tch == 4 ? 2 : gt_tch == 16 ? 4 : 3) + (vec ? 0 : 2);
   const int64_t cols = vec ? L / 4 : L;
   const int64_t rows = ceil_div(std::max<int64_t>(B, 1), nparts);
   const int cpl = (int)std::min<int64_t>(ceil_div(cols, kWave), kMaxCpl);
@@ -1201,9 +1204,9 @@ int bwd_f32(const int32_t *idx, int64_t B, int K, const float *grad, int64_t N, 
   const int64_t M = B * K;
 
   // The tiled weight-grad gather reads the grad in column tiles; the bias pass
-  // writes that layout while it streams the grad.
-  const bool tiled = !(flags & SFT_BWD_ATOMIC) && M > 0 && tiled_shape(B, L, flags) && (uintptr_t)grad % 16 == 0 &&
-                     (uintptr_t)dW % 16 == 0 && (uintptr_t)db % 16 == 0;
+  // writes that layout while it streams the grad (16-byte loads when the grad
+  // allows them, 4-byte loads otherwise), and stores 16-byte weight-grad chunks.
+  const bool tiled = !(flags & SFT_BWD_ATOMIC) && M > 0 && tiled_shape(B, L, flags) && (uintptr_t)dW % 16 == 0;
   f32x4 *gt = tiled ? reinterpret_cast<f32x4 *>(w + lay.gt) : nullptr;
 
   // ---- sort of the slots and their segments: they need only the indices, so
@@ -1219,13 +1222,16 @@ int bwd_f32(const int32_t *idx, int64_t B, int K, const float *grad, int64_t N, 
     make_prep_layout(B, K, N, L, flags, pl);
     if (prep == nullptr || prep_bytes < pl.total || (uintptr_t)prep % 256 != 0)
       return fail(SFT_EWORKSPACE, "prepared buffer smaller than sft_ft_bwd_f32_prep_size() or not 256-byte aligned");
+    // The prepared buffer is only read: a later backward over the same buffer
+    // (a graph backward run twice) finds it as the forward left it.  Its sort
+    // was made for the chunks of the tiled gather, which only a weight grad
+    // that is not 16-byte aligned rules out.
+    if (nc != pl.nc)
+      return fail(SFT_EINVAL, "sft_ft_bwd_f32_prepared: weight_grad must be 16-byte aligned when the prepared sort "
+                              "is in position chunks (batch above 32768 with the tiled gather)");
     char *pw = static_cast<char *>(prep);
     seg = reinterpret_cast<int32_t *>(pw + pl.seg);
-    if (nc == pl.nc) {
-      pos = slot_sort_positions(M, N, nc, pw + pl.sort);
-    } else if ((rc = sort_and_segments(idx, B, K, N, nc, pw + pl.sort, seg, &pos, s)) != SFT_OK) {
-      return rc;  // the grad's alignment rules out the tiled gather: sorted again for one chunk
-    }
+    pos = slot_sort_positions(M, N, nc, pw + pl.sort);
   } else if (sorted) {
     hipStream_t side;
     if ((rc = fork_side(s, &side)) != SFT_OK) return rc;

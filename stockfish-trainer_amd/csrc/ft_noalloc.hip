@@ -1,6 +1,8 @@
 // Allocation-free int16 forward (sft_ft_fwd_i16_noalloc) for callers that
 // cannot allocate device memory: code under HIP graph capture, tight serving
-// loops, harnesses that forbid hipMalloc.
+// loops, harnesses that forbid hipMalloc.  Built alone into
+// libsft_ft_noalloc.so, which links libsft_ft.so for the kernels, so that only
+// the processes that load it reserve the scratch array below.
 //
 // It computes exactly what sft_ft_fwd_i16_ex computes with a workspace of
 // sft_ft_fwd_i16_workspace_size() bytes: the table and its PSQT columns are
@@ -19,6 +21,7 @@
 #include <mutex>
 
 #include "common.h"
+#include "sft_ft_noalloc.h"
 
 namespace sft {
 

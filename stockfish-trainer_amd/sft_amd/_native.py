@@ -17,6 +17,8 @@ import torch
 PKG_ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 # SFT_LIB selects another build of the library (e.g. one compiled with other tuning constants).
 LIB_PATH = os.environ.get("SFT_LIB") or os.path.join(PKG_ROOT, "lib", "libsft_ft.so")
+# The allocation-free int16 forward (include/sft_ft_noalloc.h), a library of its own.
+NOALLOC_LIB_PATH = os.path.join(PKG_ROOT, "lib", "libsft_ft_noalloc.so")
 
 SFT_OK = 0
 SFT_EWORKSPACE = -2
@@ -69,9 +71,6 @@ SIGNATURES = {
     "sft_ft_fwd_i16_ex": (
         ctypes.c_int,
         [_vp, _i64, _i32, _vp, _i64, _i32, _vp, _vp, _i32, _vp, _vp, _i32, _i32, _vp, ctypes.c_size_t, _u32, _vp]),
-    "sft_ft_fwd_i16_noalloc": (
-        ctypes.c_int,
-        [_vp, _i64, _i32, _vp, _i64, _i32, _vp, _vp, _i32, _vp, _vp, _i32, _i32, _u32, _vp]),
     "sft_ft_i16_packed_size": (ctypes.c_int, [_i64, _i32, _i32, ctypes.POINTER(ctypes.c_size_t)]),
     "sft_ft_i16_pack": (ctypes.c_int, [_vp, _i64, _i32, _vp, _i32, _vp, ctypes.c_size_t, _vp]),
     "sft_ft_fwd_i16_packed": (
@@ -121,7 +120,15 @@ SIGNATURES = {
         ctypes.c_int, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int64), ctypes.c_int]),
 }
 
+# name -> (restype, argtypes); mirrors include/sft_ft_noalloc.h
+NOALLOC_SIGNATURES = {
+    "sft_ft_fwd_i16_noalloc": (
+        ctypes.c_int,
+        [_vp, _i64, _i32, _vp, _i64, _i32, _vp, _vp, _i32, _vp, _vp, _i32, _i32, _u32, _vp]),
+}
+
 _lib = None
+_noalloc_lib = None
 _lock = threading.Lock()
 
 
@@ -147,6 +154,27 @@ def lib() -> ctypes.CDLL:
                 fn.argtypes = args
             _lib = handle
     return _lib
+
+
+def noalloc_lib() -> ctypes.CDLL:
+    """Load libsft_ft_noalloc.so once (after libsft_ft.so, which it links); raise
+    if it has not been built."""
+    global _noalloc_lib
+    lib()
+    if _noalloc_lib is not None:
+        return _noalloc_lib
+    with _lock:
+        if _noalloc_lib is None:
+            if not os.path.exists(NOALLOC_LIB_PATH):
+                raise NativeLibraryMissing(f"{NOALLOC_LIB_PATH} not found: build it with "
+                                           "`make -C stockfish-trainer_amd/csrc`")
+            handle = ctypes.CDLL(NOALLOC_LIB_PATH)
+            for name, (res, args) in NOALLOC_SIGNATURES.items():
+                fn = getattr(handle, name)
+                fn.restype = res
+                fn.argtypes = args
+            _noalloc_lib = handle
+    return _noalloc_lib
 
 
 def last_error() -> str:
@@ -227,6 +255,38 @@ def prep_buffer_bytes(B: int, K: int, N: int, L: int, flags: int, device: torch.
     room to align it to 256 bytes (0 when the backward sorts nothing)."""
     n = _workspace_bytes("prep", B, K, N, L, flags, device)
     return n + 256 if n else 0
+
+
+# The library's prepared-buffer layout (make_prep_layout in csrc/ft_bwd.hip:
+# the radix sort's workspace, then the segment region of nc position chunks)
+# restated in integer arithmetic.  Torch's fake tensors call it with symbolic
+# sizes (SymInt), which the C size query cannot take; CPU tests check that it
+# equals sft_ft_bwd_f32_prep_size over a sweep of shapes.
+_SORT_TILE = 2048              # kBlock * kSortItems (csrc/ft_sort.hip)
+_SORT_MAX_RADIX = 512          # kMaxRadix
+_BWD_MIN_TILES = 4             # SFT_BWD_MIN_TILES (csrc/common.h)
+_BWD_TILE_BYTES = 128          # one 32-column grad tile row
+_BWD_ONE_CHUNK_BYTES = 4 << 20  # SFT_BWD_ONE_CHUNK_BYTES
+_BWD_CHUNKS = 2                # SFT_BWD_CHUNKS
+_BWD_PREP_K_PER_L = 20         # SFT_BWD_PREP_K_PER_L
+
+
+def _a256(x):
+    return (x + 255) // 256 * 256
+
+
+def prep_buffer_bytes_formula(B, K, N, L, flags: int):
+    """prep_buffer_bytes for sizes that may be symbolic (SymInt)."""
+    if (flags & SFT_BWD_ATOMIC) or not (B * K > 0) or not (K * _BWD_PREP_K_PER_L >= L):
+        return 0
+    M = B * K
+    tiled = (not (flags & (SFT_BWD_ATOMIC | SFT_BWD_ROWS)) and bool(flags & SFT_BWD_OVERWRITE) and L % 4 == 0
+             and (L + 31) // 32 >= _BWD_MIN_TILES and B * _BWD_TILE_BYTES <= 0xFFFFFFFF)
+    nc = _BWD_CHUNKS if (tiled and B >= _BWD_CHUNKS and B * _BWD_TILE_BYTES > _BWD_ONE_CHUNK_BYTES) else 1
+    sort_ws = 4 * _a256(M * 4) + _a256(_SORT_MAX_RADIX * ((M + _SORT_TILE - 1) // _SORT_TILE) * 4) \
+        + _a256(_SORT_MAX_RADIX * 4)
+    seg_region = ((2 * nc * N + 1 + nc) * 4 + 15) // 16 * 16 + M * 2 + 16
+    return _a256(sort_ws) + _a256(seg_region) + 256
 
 
 def _aligned(buf: torch.Tensor):
@@ -355,8 +415,9 @@ def ft_fwd_i16(idx: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor, out:
 def ft_fwd_i16_noalloc(idx: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor, out: torch.Tensor,
                        psqt_weight: torch.Tensor | None = None, psqt_out: torch.Tensor | None = None,
                        clip_lo: int = 0, clip_hi: int = 127, wrap16: bool = False, rows: bool = False) -> None:
-    """ft_fwd_i16 through sft_ft_fwd_i16_noalloc: no workspace, nothing allocated by
-    the library; the packed tiles go to its static per-GPU scratch array."""
+    """ft_fwd_i16 through sft_ft_fwd_i16_noalloc (libsft_ft_noalloc.so): no
+    workspace, nothing allocated by the library; the packed tiles go to its
+    static per-GPU scratch array."""
     _require(idx.dim() == 2 and idx.dtype == torch.int32, "idx must be int32 [B, K]")
     _require(weight.dim() == 2 and weight.dtype == torch.int16, "weight must be int16 [N, L]")
     B, K = idx.shape
@@ -375,7 +436,7 @@ def ft_fwd_i16_noalloc(idx: torch.Tensor, weight: torch.Tensor, bias: torch.Tens
     _on_gpu(idx.device, *tensors)
     flags = (SFT_Q16_WRAP16 if wrap16 else SFT_Q16_ACC32) | (SFT_Q16_ROWS if rows else 0)
     with torch.cuda.device(idx.device):
-        _check(lib().sft_ft_fwd_i16_noalloc(_ptr(idx), B, K, _ptr(weight), N, L, _ptr(bias), _ptr(psqt_weight), P,
+        _check(noalloc_lib().sft_ft_fwd_i16_noalloc(_ptr(idx), B, K, _ptr(weight), N, L, _ptr(bias), _ptr(psqt_weight), P,
                                             _ptr(out), _ptr(psqt_out), clip_lo, clip_hi, flags,
                                             _stream(idx.device)), "sft_ft_fwd_i16_noalloc")
 

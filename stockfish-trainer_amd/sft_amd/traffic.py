@@ -45,6 +45,8 @@ KINDS = [
     (r"\btile_relayout_kernel\b", "fwd_tile_relayout"),
     (r"\bfold_relayout_kernel\b", "fwd_fold_relayout"),
     (r"\bfwd_i16_tiled_kernel\b", "fwd_i16_tiled_gather"),
+    (r"\bfwd_i16_ranked_kernel\b", "fwd_i16_tiled_gather"),
+    (r"\brank_lists_kernel\b", "fwd_rank_lists"),
     (r"\bi16_relayout_kernel\b", "fwd_tile_relayout"),
     (r"\bfwd_i16_kernel<", "fwd_i16_gather"),
     (r"\bbwd_tiled_gather_kernel<", "bwd_tiled_gather"),

@@ -39,7 +39,10 @@ def sparse_linear_fwd(feature_indices: Tensor, weight: Tensor, bias: Tensor) -> 
 def _(feature_indices, weight, bias):
     B, K = feature_indices.shape
     N, L = weight.shape
-    nbytes = _native.prep_buffer_bytes(B, K, N, L, _native.SFT_BWD_OVERWRITE, feature_indices.device)
+    if all(type(v) is int for v in (B, K, N, L)):
+        nbytes = _native.prep_buffer_bytes(B, K, N, L, _native.SFT_BWD_OVERWRITE, feature_indices.device)
+    else:  # symbolic sizes (dynamic shapes): the same layout in SymInt arithmetic
+        nbytes = _native.prep_buffer_bytes_formula(B, K, N, L, _native.SFT_BWD_OVERWRITE)
     return (feature_indices.new_empty((B, L), dtype=torch.float32),
             feature_indices.new_empty((nbytes,), dtype=torch.uint8))
 

@@ -11,22 +11,28 @@ from conftest import ROOT
 from sft_amd import _native
 
 HEADER = os.path.join(ROOT, "include", "sft_ft.h")
+NOALLOC_HEADER = os.path.join(ROOT, "include", "sft_ft_noalloc.h")
 
 
-def header_functions():
-    text = open(HEADER).read()
+def header_functions(path=HEADER):
+    text = open(path).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     return sorted(set(re.findall(r"\b(sft_\w+)\s*\(", text)))
 
 
 def test_header_declares_the_binding_table():
     assert header_functions() == sorted(_native.SIGNATURES)
+    assert header_functions(NOALLOC_HEADER) == sorted(_native.NOALLOC_SIGNATURES)
 
 
 def test_library_exports_every_declared_symbol():
     lib = _native.lib()
     for name in header_functions():
         assert hasattr(lib, name), name
+    noalloc = _native.noalloc_lib()
+    for name in header_functions(NOALLOC_HEADER):
+        assert hasattr(noalloc, name), name
+        assert not hasattr(lib, name), name  # the static scratch lives in the separate library only
 
 
 def test_abi_version_matches_header():
@@ -94,8 +100,8 @@ def test_i16_rejects():
 def test_i16_noalloc_rejects_before_launch():
     """sft_ft_fwd_i16_noalloc validates like sft_ft_fwd_i16 and refuses a tiled
     shape whose packed table exceeds its static scratch, before any HIP call."""
-    lib = _native.lib()
-    m = re.search(r"#define SFT_NOALLOC_SCRATCH_BYTES \((\d+)u << (\d+)\)", open(HEADER).read())
+    lib = _native.noalloc_lib()
+    m = re.search(r"#define SFT_NOALLOC_SCRATCH_BYTES \((\d+)u << (\d+)\)", open(NOALLOC_HEADER).read())
     limit = int(m.group(1)) << int(m.group(2))
     base = [P, 4, 32, P, 22528, 1040, P, P, 8, P, P, 0, 127, 0, None]
     a = list(base); a[10] = None  # psqt weight without output

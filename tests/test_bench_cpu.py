@@ -1,7 +1,8 @@
 """bench.py's contract on the CPU: the one-GPU rule, the roofline pricing
-(every fraction a true fraction of the bound it names) and the algorithmic
-byte counts the rooflines divide, against a brute-force count over a tiny
-index matrix."""
+(frac = counter memory-side bytes per launch over HBM's published peak, the
+byte model's logical bytes and the L2 view beside it), the repetition
+statistics, and the algorithmic byte counts against a brute-force count over a
+tiny index matrix."""
 
 import importlib.util
 import os
@@ -29,24 +30,33 @@ def test_more_than_one_gpu_is_refused():
     assert "one GPU" in r.stderr and r.stdout == ""
 
 
-def test_roofline_gather_priced_against_l2(bench):
+def test_roofline_gather_priced_against_hbm_from_counter_bytes(bench):
     # 3.35 GB of requested rows in 0.205 ms, 612 MB of memory-side traffic
     r = bench.roofline("bwd_tiled_gather", 3.35e9, 0.205, traffic=612e6, traffic_source="test", l2_attainable=33281.0)
-    assert r["bound"] == "l2" and r["unit"] == "GB/s"
-    assert r["achieved"] == pytest.approx(3.35e9 / 0.205e-3 / 1e9)
-    assert r["peak"] == pytest.approx(8 * 16 * 128 * 2.4)  # 39 321.6 GB/s
-    assert 0 < r["frac"] <= 1 and r["frac"] == pytest.approx(r["achieved"] / r["peak"])
-    assert r["frac_of_attainable"] == pytest.approx(r["achieved"] / 33281.0)
-    assert r["hbm"]["peak"] == 8000.0
-    assert r["hbm"]["frac"] == pytest.approx(612e6 / 0.205e-3 / 1e9 / 8000.0)
-    assert 0 < r["hbm"]["frac"] <= 1
+    assert r["bound"] == "hbm" and r["unit"] == "GB/s" and r["peak"] == 8000.0
+    assert r["traffic"] == 612e6
+    assert r["achieved"] == pytest.approx(612e6 / 0.205e-3 / 1e9)
+    assert r["frac"] == pytest.approx(r["achieved"] / 8000.0) and 0 < r["frac"] <= 1
+    lg = r["logical"]  # the byte model's rows, L2-served re-reads included: above HBM's peak here
+    assert lg["achieved"] == pytest.approx(3.35e9 / 0.205e-3 / 1e9)
+    assert lg["frac_of_hbm_peak"] == pytest.approx(lg["achieved"] / 8000.0) and lg["frac_of_hbm_peak"] > 1
+    assert r["l2"]["derived_peak"] == pytest.approx(8 * 16 * 128 * 2.4)  # 39 321.6 GB/s
+    assert 0 < r["l2"]["frac_of_derived_peak"] <= 1
+    assert r["l2"]["frac_of_measured_ceiling"] == pytest.approx(lg["achieved"] / 33281.0)
 
 
-def test_roofline_streaming_kernel_priced_against_hbm(bench):
+def test_roofline_without_counter_traffic_says_so(bench):
     r = bench.roofline("fwd_tile_relayout", 194.8e6, 0.0346)
-    assert r["bound"] == "hbm" and r["peak"] == 8000.0
+    assert r["bound"] == "hbm" and r["peak"] == 8000.0 and r["traffic"] is None
     assert r["frac"] == pytest.approx(194.8e6 / 0.0346e-3 / 1e9 / 8000.0)
-    assert "hbm" not in r and "attainable" not in r
+    assert "algorithmic" in r["basis"]
+    assert "l2" not in r  # a streaming kernel: no L2 view
+
+
+def test_repetition_statistics(bench):
+    st = bench.rep_stats([1.9, 1.7, 1.72, 1.71, 2.5])
+    assert st["ms_per_step"] == 1.72 and st["ms_per_step_min"] == 1.7 and st["ms_per_step_max"] == 2.5
+    assert st["reps"] == 5
 
 
 class _W:

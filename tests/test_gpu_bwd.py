@@ -207,24 +207,40 @@ def test_atomic_bwd_full_workload(wid):
     assert dw_rel_err(host(dW), r64) <= 1e-4
 
 
-def _prepared(idx, G, N, W=None, grad_offset=0):
-    """The forward with the backward's sort beside it, then the prepared
-    backward; grad_offset > 0 passes the grad as an unaligned view."""
-    B, L = G.shape
+def _unaligned(t: torch.Tensor, offset: int) -> torch.Tensor:
+    """A copy of t as a view offset by `offset` floats (offset 1: 4-byte aligned only)."""
+    if not offset:
+        return t
+    big = torch.zeros(t.numel() + offset, device=DEV)
+    big[offset:] = t.reshape(-1)
+    return big[offset:].view(t.shape)
+
+
+def _prepare(idx, N, L, W=None):
+    """The forward with the backward's sort beside it -> (out, idx on the device, prep)."""
+    B = idx.shape[0]
     W = np.zeros((N, L), np.float32) if W is None else W
     out = torch.empty(B, L, device=DEV)
     i = dev(idx)
     prep = _native.ft_fwd_f32_prep(i, dev(W), torch.zeros(L, device=DEV), out, _native.SFT_BWD_OVERWRITE)
-    if grad_offset:
-        big = torch.zeros(B * L + grad_offset, device=DEV)
-        big[grad_offset:] = dev(G).view(-1)
-        g = big[grad_offset:].view(B, L)
-    else:
-        g = dev(G)
-    dW = torch.full((N, L), float("nan"), device=DEV)
+    return host(out), i, prep
+
+
+def _prepared_bwd(i, G, N, prep, grad_offset=0, dw_offset=0):
+    """The prepared backward; the offsets pass the grad or the weight grad as
+    views that are only 4-byte aligned."""
+    B, L = G.shape
+    g = _unaligned(dev(G), grad_offset)
+    dW = _unaligned(torch.full((N, L), float("nan"), device=DEV), dw_offset)
     db = torch.full((L,), float("nan"), device=DEV)
     _native.ft_bwd_f32_prepared(i, dW, db, g, prep, _native.SFT_BWD_OVERWRITE)
-    return host(out), host(dW), host(db)
+    return host(dW), host(db)
+
+
+def _prepared(idx, G, N, W=None, grad_offset=0):
+    out, i, prep = _prepare(idx, N, G.shape[1], W)
+    dW, db = _prepared_bwd(i, G, N, prep, grad_offset)
+    return out, dW, db
 
 
 @pytest.mark.parametrize("seed,B,N,K,L,lo,hi,sort", SHAPES)
@@ -242,18 +258,53 @@ def test_prepared_bwd_matches_the_backward(seed, B, N, K, L, lo, hi, sort):
 
 
 @pytest.mark.parametrize("B,L", [(40000, 256), (3000, 256)])
-def test_prepared_bwd_unaligned_grad_sorts_again(B, L):
-    """A grad view that is not 16-byte aligned rules out the tiled gather, whose
-    sort (two position chunks at B = 40000) the forward prepared (K = 32 >= L /
-    20): the backward sorts again for one chunk into the same buffer and still
-    matches the reference order."""
-    announce(f"prepared bwd, unaligned grad B={B} L={L}")
+def test_prepared_bwd_reads_the_buffer_only(B, L):
+    """Two backwards over one prepared buffer (autograd's retain_graph), the
+    first with a grad that is only 4-byte aligned (the bias pass reads floats and
+    still writes the grad tiles), the second aligned: both match the reference
+    order, so the first left the buffer as the forward made it (K = 32 >= L / 20;
+    two position chunks at B = 40000, one at 3000)."""
+    announce(f"prepared bwd twice, unaligned then aligned grad B={B} L={L}")
     idx, W, b, G = case(31, B, 900, 32, L, 0, 32, True)
     assert _native.prep_buffer_bytes(B, 32, 900, L, _native.SFT_BWD_OVERWRITE, DEV) > 0
-    _, dW, db = _prepared(idx, G, 900, grad_offset=1)
+    _, i, prep = _prepare(idx, 900, L)
     ref, _ = ft_oracle.bwd_f32(idx, G, 900)
-    assert np.array_equal(dW, ref)
-    assert rel_err(db, G.astype(np.float64).sum(0)) <= 1e-5
+    db64 = G.astype(np.float64).sum(0)
+    for offset in (1, 0):
+        dW, db = _prepared_bwd(i, G, 900, prep, grad_offset=offset)
+        assert np.array_equal(dW, ref), offset
+        assert rel_err(db, db64) <= 1e-5
+
+
+def test_prepared_bwd_unaligned_weight_grad():
+    """A weight grad that is only 4-byte aligned needs the row gather, which
+    sorts in one position chunk: refused (before any launch) when the prepared
+    sort is in two chunks, and bit-exact when it is in one."""
+    announce("prepared bwd, unaligned weight grad")
+    for B, chunks in ((40000, 2), (3000, 1)):
+        idx, W, b, G = case(32, B, 900, 32, 256, 0, 32, True)
+        _, i, prep = _prepare(idx, 900, 256)
+        if chunks == 2:
+            with pytest.raises(RuntimeError, match="16-byte aligned"):
+                _prepared_bwd(i, G, 900, prep, dw_offset=1)
+        else:
+            dW, _ = _prepared_bwd(i, G, 900, prep, dw_offset=1)
+            assert np.array_equal(dW, ft_oracle.bwd_f32(idx, G, 900)[0])
+        dW, _ = _prepared_bwd(i, G, 900, prep)  # the buffer is still good
+        assert np.array_equal(dW, ft_oracle.bwd_f32(idx, G, 900)[0])
+
+
+@pytest.mark.parametrize("offset", [1, 2])
+def test_bwd_unaligned_grad_keeps_the_tiled_gather(offset):
+    """The plain backward with a grad view that is 4- or 8-byte aligned: the bias
+    pass reads floats and writes the same grad tiles (two position chunks)."""
+    announce(f"bwd unaligned grad offset={offset}")
+    idx, W, b, G = case(33, 40000, 700, 32, 1048, 16, 32, True)
+    dW = torch.full((700, 1048), float("nan"), device=DEV)
+    db = torch.full((1048,), float("nan"), device=DEV)
+    _native.ft_bwd_f32(dev(idx), dW, db, _unaligned(dev(G), offset), _native.SFT_BWD_OVERWRITE)
+    assert np.array_equal(host(dW), ft_oracle.bwd_f32(idx, G, 700)[0])
+    assert rel_err(host(db), G.astype(np.float64).sum(0)) <= 1e-5
 
 
 def test_prepared_bwd_no_active_slots():

@@ -2,7 +2,11 @@
 implementations, so Dynamo traces SparseLinearFunction, the fused composed
 module and the fused transform without a graph break (the reference breaks the
 graph at its compiler-disabled factories, FT/kernel.py:301,315), and the
-compiled functions give outputs and grads bit-identical to eager."""
+compiled functions give outputs and grads bit-identical to eager -- under
+AOTAutograd alone and under Inductor, the reference's default compile backend
+(src/train/config.py:76, src/train/common.py:187-189), which generates the glue
+around the opaque ops (the sum of the two weight grads) -- also when the batch
+size changes between calls (dynamic shapes)."""
 
 import numpy as np
 import pytest
@@ -16,7 +20,9 @@ from src.model.transform_inputs import transform_inputs
 
 pytestmark = pytest.mark.gpu
 
-BACKEND = "aot_eager"  # Dynamo + AOTAutograd over fake tensors; the FT ops stay opaque
+# Dynamo + AOTAutograd over fake tensors, then eager kernels or Inductor's code;
+# the FT ops stay opaque in both
+BACKENDS = ["aot_eager", "inductor"]
 
 
 def _no_breaks(fn, *args):
@@ -26,8 +32,9 @@ def _no_breaks(fn, *args):
     assert ex.graph_count == 1
 
 
-def test_sparse_linear_compiles_without_graph_break():
-    announce("compile SparseLinearFunction")
+@pytest.mark.parametrize("backend", BACKENDS)
+def test_sparse_linear_compiles_without_graph_break(backend):
+    announce(f"compile SparseLinearFunction backend={backend}")
     g = np.random.default_rng(5)
     B, N, K, L = 3000, 4000, 32, 1048
     iw = dev(workloads.make_indices(g, B, N, K, 16, 32, sort=False))
@@ -51,7 +58,7 @@ def test_sparse_linear_compiles_without_graph_break():
         return ow.detach(), ob.detach(), W.grad, b.grad
 
     torch._dynamo.reset()
-    compiled = torch.compile(step, backend=BACKEND, fullgraph=True)
+    compiled = torch.compile(step, backend=backend, fullgraph=True)
     ref = run(step)
     for _ in range(2):  # the second call runs the cached graph
         got = run(compiled)
@@ -59,9 +66,49 @@ def test_sparse_linear_compiles_without_graph_break():
             assert torch.equal(a, r)
 
 
+@pytest.mark.parametrize("backend", BACKENDS)
+@pytest.mark.parametrize("dynamic", [True, None])
+def test_sparse_linear_compiles_with_varying_batch(backend, dynamic):
+    """Batch sizes 3000, 2999 and 40000 through one compiled step: with
+    dynamic=True every call runs one symbolic graph; with the default the
+    second size recompiles with a symbolic batch (a last partial batch, a
+    validation batch).  The prepared sort's buffer takes its size from the
+    library's layout either way (K = 32 >= L / 20 at L = 264; two position
+    chunks at B = 40000)."""
+    announce(f"compile SparseLinearFunction, varying batch, backend={backend} dynamic={dynamic}")
+    g = np.random.default_rng(8)
+    N, K, L = 3000, 32, 264
+    W0 = torch.from_numpy((g.standard_normal((N, L)) * 0.01).astype(np.float32)).to(DEV)
+    b0 = torch.from_numpy(g.uniform(-0.1, 0.1, L).astype(np.float32)).to(DEV)
+
+    def step(iw, ib, W, b):
+        return SparseLinearFunction.apply(iw, W, b), SparseLinearFunction.apply(ib, W, b)
+
+    def run(fn, iw, ib, gw, gb):
+        W = W0.clone().requires_grad_(True)
+        b = b0.clone().requires_grad_(True)
+        ow, ob = fn(iw, ib, W, b)
+        torch.autograd.backward([ow, ob], [gw, gb])
+        torch.cuda.synchronize()
+        return ow.detach(), ob.detach(), W.grad, b.grad
+
+    torch._dynamo.reset()
+    compiled = torch.compile(step, backend=backend, fullgraph=True, dynamic=dynamic)
+    for B in (3000, 2999, 40000):
+        iw = dev(workloads.make_indices(g, B, N, K, 16, 32, sort=False))
+        ib = dev(workloads.make_indices(g, B, N, K, 16, 32, sort=False))
+        gw = torch.randn(B, L, device=DEV)
+        gb = torch.randn(B, L, device=DEV)
+        ref = run(step, iw, ib, gw, gb)
+        got = run(compiled, iw, ib, gw, gb)
+        for a, r in zip(got, ref):
+            assert torch.equal(a, r), B
+
+
+@pytest.mark.parametrize("backend", BACKENDS)
 @pytest.mark.parametrize("name,B,L", [("HalfKAv2_hm^", 4096, 1048), ("Full_Threats+HalfKAv2_hm^", 1500, 520)])
-def test_composed_module_compiles_without_graph_break(name, B, L):
-    announce(f"compile composed module {name} B={B} L={L}")
+def test_composed_module_compiles_without_graph_break(name, B, L, backend):
+    announce(f"compile composed module {name} B={B} L={L} backend={backend}")
     torch.manual_seed(4)
     ft = get_feature_cls(name)(L).to(DEV)
     for f in ft.features:
@@ -85,15 +132,16 @@ def test_composed_module_compiles_without_graph_break(name, B, L):
         return [ow.detach(), ob.detach()] + [p.grad.clone() for p in ft.parameters()]
 
     torch._dynamo.reset()
-    compiled = torch.compile(ft, backend=BACKEND, fullgraph=True)
+    compiled = torch.compile(ft, backend=backend, fullgraph=True)
     ref = run(ft)
     got = run(compiled)
     for a, r in zip(got, ref):
         assert torch.equal(a, r)
 
 
-def test_fused_transform_compiles_without_graph_break():
-    announce("compile fused transform")
+@pytest.mark.parametrize("backend", BACKENDS)
+def test_fused_transform_compiles_without_graph_break(backend):
+    announce(f"compile fused transform backend={backend}")
     torch.manual_seed(6)
     L1, P, B = 1040, 8, 2048
     ft = get_feature_cls("HalfKAv2_hm^")(L1 + P).to(DEV)
@@ -125,7 +173,7 @@ def test_fused_transform_compiles_without_graph_break():
         return [l0.detach(), psqt.detach()] + [p.grad.clone() for p in ft.parameters()]
 
     torch._dynamo.reset()
-    compiled = torch.compile(step, backend=BACKEND, fullgraph=True)
+    compiled = torch.compile(step, backend=backend, fullgraph=True)
     ref = run(step)
     got = run(compiled)
     for a, r in zip(got, ref):
