@@ -428,6 +428,9 @@ constexpr int kRowLongBlocks = SFT_BWD_ROW_LONG_BLOCKS;  // long-segment workgro
 #endif
 constexpr int kBwdPosLds = SFT_BWD_POS_LDS;  // staged positions per workgroup
 
+#ifndef SFT_BWD_ROLL
+#define SFT_BWD_ROLL 1
+#endif
 // Sums one lane group's positions from `list` (LDS or global) into acc.  A
 // lane group has TCH lanes (one 16-byte chunk of the tile row each) and keeps
 // TCH row loads in flight.  Rows are 32-bit byte offsets from the grad tile's
@@ -444,6 +447,35 @@ __device__ __forceinline__ void bwd_tile_sum(const P *list, int n, int nmin, int
   };
   constexpr int U = TCH;  // one position per lane of the group when read from global memory
   int k = 0;
+  if (SFT_BWD_ROLL && FROM_LDS && nmin >= 2 * U) {
+    // A rolling window of U rows in flight over the rows every lane group of
+    // the wave has: each add frees the oldest row's registers, which take the
+    // row U places further at once, so the loads in flight do not drain to
+    // zero between steps.  Same adds, same order.  (Workload 1: 206.5 ->
+    // 204.2 us per launch, step 1.719 -> 1.712 ms; L = 136 and Full_Threats
+    // 0.5-1% per step.)
+    f32x4 w[U];
+    // Issued in the order the loop consumes them (no reordering across the
+    // barriers), so the loads in flight at the loop head are in the same
+    // order on both of its edges and each add waits for its own row only.
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      w[u] = row((int)list[u]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    for (k = U; k + U <= nmin; k += U) {
+      int b[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) b[u] = (int)list[k + u];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        acc += w[u];
+        w[u] = row(b[u]);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) acc += w[u];
+  }
   for (; k + U <= nmin; k += U) {
     int b[U];
     if (FROM_LDS) {
@@ -525,34 +557,49 @@ __host__ __device__ inline GatherLds gather_lds(int dst_mode) {
   return l;
 }
 
-template <bool NT, bool P16>
-__global__ __launch_bounds__(kBlock) void bwd_tiled_gather_kernel(const int32_t *__restrict__ seg,
-                                                                  const int32_t *__restrict__ sorted_pos,
-                                                                  const uint16_t *__restrict__ pos16, int chunk_base,
-                                                                  int64_t N,
-                                                                  const f32x4 *__restrict__ gt, int64_t B,
-                                                                  ColMap map, RowDst dst, f32x4 *__restrict__ tmp,
-                                                                  int src_mode, int dst_mode, int ntiles, int ngroups,
-                                                                  const int32_t *__restrict__ long_list,
-                                                                  const int *__restrict__ long_count, int nlong) {
+// The arguments of one tiled gather launch.
+struct TiledArgs {
+  const int32_t *seg, *sorted_pos;
+  const uint16_t *pos16;
+  int chunk_base;
+  int64_t N;
+  const f32x4 *gt;
+  int64_t B;
+  ColMap map;
+  RowDst dst;
+  f32x4 *tmp;
+  int src_mode, dst_mode, ntiles, ngroups;
+  const int32_t *long_list;
+  const int *long_count;
+  int nlong;
+};
+
+// Long-segment slot it.chunk of tile it.tile (whole workgroup).
+__device__ __forceinline__ void tiled_long_item(const TiledArgs &a, TileItem it, char *gsm) {
   constexpr int TCH = kBwdTileCh;
-  extern __shared__ __align__(16) char gsm[];
-  __shared__ int s_seg[kBwdFeat + 1], s_perm[kBwdFeat];
-  const int64_t nl_items = tile_sched_items_per_xcd(ntiles, nlong) * kXcds;
-  const bool long_item = (int64_t)blockIdx.x < nl_items;  // whole block: uniform
-  const TileItem it = long_item ? tile_sched_item(blockIdx.x, ntiles, nlong)
-                                : tile_sched_item(blockIdx.x - nl_items, ntiles, ngroups);
-  if (it.tile >= ntiles) return;  // whole block: uniform
-  if (long_item) {
-    const int cnt = *long_count;
-    for (int e = it.chunk; e < cnt; e += nlong) {
-      const int64_t f = long_list[e];
-      const int s0 = seg[f];
-      long_segment_sum_wg(sorted_pos, f, s0, seg[f + 1] - s0, it.tile, LongRows{gt, B * TCH, TCH}, map, dst, tmp,
-                          N, src_mode, dst_mode, reinterpret_cast<f32x4 *>(gsm));
-    }
-    return;
+  const int cnt = *a.long_count;
+  for (int e = it.chunk; e < cnt; e += a.nlong) {
+    const int64_t f = a.long_list[e];
+    const int s0 = a.seg[f];
+    long_segment_sum_wg(a.sorted_pos, f, s0, a.seg[f + 1] - s0, it.tile, LongRows{a.gt, a.B * TCH, TCH}, a.map,
+                        a.dst, a.tmp, a.N, a.src_mode, a.dst_mode, reinterpret_cast<f32x4 *>(gsm));
   }
+}
+
+// Feature block it.chunk of tile it.tile (whole workgroup; one barrier inside).
+template <bool NT, bool P16>
+__device__ __forceinline__ void tiled_feature_item(const TiledArgs &a, TileItem it, char *gsm, int *s_seg,
+                                                   int *s_perm) {
+  constexpr int TCH = kBwdTileCh;
+  const int32_t *__restrict__ seg = a.seg;
+  const int32_t *__restrict__ sorted_pos = a.sorted_pos;
+  const uint16_t *__restrict__ pos16 = a.pos16;
+  const int64_t N = a.N, B = a.B;
+  const ColMap &map = a.map;
+  const RowDst &dst = a.dst;
+  f32x4 *__restrict__ tmp = a.tmp;
+  const int src_mode = a.src_mode, dst_mode = a.dst_mode, chunk_base = a.chunk_base;
+  const f32x4 *__restrict__ gt = a.gt;
   const GatherLds lay = gather_lds(dst_mode);
   int *spos = reinterpret_cast<int *>(gsm);
   const int64_t cols4 = map.cols4;
@@ -672,7 +719,25 @@ __global__ __launch_bounds__(kBlock) void bwd_tiled_gather_kernel(const int32_t 
   }
 }
 
-// One position chunk's tiled weight-grad gather: one workgroup per item.
+// One item per workgroup: workgroup i serves item i / 8 of XCD i % 8 (the
+// long-segment slots first, then the feature blocks).
+template <bool NT, bool P16>
+__global__ __launch_bounds__(kBlock) void bwd_tiled_gather_kernel(TiledArgs a) {
+  extern __shared__ __align__(16) char gsm[];
+  __shared__ int s_seg[kBwdFeat + 1], s_perm[kBwdFeat];
+  const int64_t nl_items = tile_sched_items_per_xcd(a.ntiles, a.nlong) * kXcds;
+  const bool long_item = (int64_t)blockIdx.x < nl_items;  // whole block: uniform
+  const TileItem it = long_item ? tile_sched_item(blockIdx.x, a.ntiles, a.nlong)
+                                : tile_sched_item(blockIdx.x - nl_items, a.ntiles, a.ngroups);
+  if (it.tile >= a.ntiles) return;  // whole block: uniform
+  if (long_item)
+    tiled_long_item(a, it, gsm);
+  else
+    tiled_feature_item<NT, P16>(a, it, gsm, s_seg, s_perm);
+}
+
+
+// One position chunk's tiled weight-grad gather.
 // pos16: the slots' 16-bit chunk offsets (null when a chunk has more than
 // 65536 positions), chunk_base the first position of this launch's chunk.
 int launch_tiled_gather(bool nt, const int32_t *seg, const int32_t *pos, const uint16_t *pos16, int64_t chunk_base,
@@ -683,16 +748,13 @@ int launch_tiled_gather(bool nt, const int32_t *seg, const int32_t *pos, const u
   const size_t lds = (size_t)gather_lds(dst_mode).bytes;
   if ((uintptr_t)pos % 16 != 0 || (uintptr_t)pos16 % 16 != 0)  // 256-byte / 16-byte aligned workspace regions
     return fail(SFT_EINVAL, "tiled feature gather: sorted positions not 16-byte aligned");
+  const TiledArgs a{seg, pos, pos16, (int)chunk_base, N, gt, B, map, dst, tmp, src_mode, dst_mode, ntiles, ngroups,
+                    long_list, long_count, nlong};
+  const bool p16 = pos16 != nullptr;
   const dim3 grid((unsigned)(items * kXcds));
-  const int cb = (int)chunk_base;
-  if (pos16 != nullptr)
-    hipLaunchKernelGGL((nt ? bwd_tiled_gather_kernel<true, true> : bwd_tiled_gather_kernel<false, true>), grid,
-                       dim3(kBlock), lds, s, seg, pos, pos16, cb, N, gt, B, map, dst, tmp, src_mode, dst_mode, ntiles,
-                       ngroups, long_list, long_count, nlong);
-  else
-    hipLaunchKernelGGL((nt ? bwd_tiled_gather_kernel<true, false> : bwd_tiled_gather_kernel<false, false>), grid,
-                       dim3(kBlock), lds, s, seg, pos, pos16, cb, N, gt, B, map, dst, tmp, src_mode, dst_mode, ntiles,
-                       ngroups, long_list, long_count, nlong);
+  hipLaunchKernelGGL((nt ? (p16 ? bwd_tiled_gather_kernel<true, true> : bwd_tiled_gather_kernel<true, false>)
+                         : (p16 ? bwd_tiled_gather_kernel<false, true> : bwd_tiled_gather_kernel<false, false>)),
+                     grid, dim3(kBlock), lds, s, a);
   return check_launch("tiled feature gather");
 }
 
