@@ -36,6 +36,12 @@ int slot_sort(const int32_t *idx, int64_t M, int K, int64_t N, int chunk_rows, i
               unsigned **keys_sorted, int **pos_sorted, unsigned **digit_totals, int *digit_count, int *clear,
               int nclear, hipStream_t s);
 int *slot_sort_positions(int64_t M, int64_t N, int nchunks, void *ws);
+// The same sort with the segment pass folded in (a radix pass on the high key
+// bits, then one workgroup per bucket), for key spaces it covers.
+bool slot_sort_buckets_supported(int64_t N, int nchunks);
+int slot_sort_buckets(const int32_t *idx, int64_t M, int K, int64_t N, int chunk_rows, int nchunks, void *ws,
+                      int32_t *seg, int32_t *list, int *count, uint16_t *pos16, int long_period, int **pos_sorted,
+                      hipStream_t s);
 
 namespace {
 
@@ -1211,15 +1217,20 @@ int sort_and_segments(const int32_t *idx, int64_t B, int K, int64_t N, int nc, v
                       int32_t **pos, hipStream_t s) {
   const int64_t M = B * K;
   const SegBufs sb = seg_bufs(seg, nc, N);
+  const int64_t crow = nc > 1 ? half_rows(B) : B;
+  if (slot_sort_buckets_supported(N, nc)) {
+    ProfScope prof(kProfBwdSort, s);
+    return slot_sort_buckets(idx, M, K, N, (int)crow, nc, sort_ws, sb.seg, sb.list, sb.count,
+                             crow <= 65536 ? sb.pos16 : nullptr, kLongSeg, pos, s);
+  }
   unsigned *keys = nullptr, *totals = nullptr;
   int ntot = 0, rc;
   {
     ProfScope prof(kProfBwdSort, s);
-    if ((rc = slot_sort(idx, M, K, N, (int)(nc > 1 ? half_rows(B) : B), nc, sort_ws, &keys, pos, &totals, &ntot,
-                        sb.count, nc, s)) != SFT_OK)
+    if ((rc = slot_sort(idx, M, K, N, (int)crow, nc, sort_ws, &keys, pos, &totals, &ntot, sb.count, nc, s)) != SFT_OK)
       return rc;
   }
-  return launch_segments(keys, M, nc, N, totals, ntot, sb, *pos, nc > 1 ? half_rows(B) : B, s);
+  return launch_segments(keys, M, nc, N, totals, ntot, sb, *pos, crow, s);
 }
 
 }  // namespace
@@ -1443,13 +1454,19 @@ static int pair_sort_perspective(const int32_t *idx, int64_t B, int K, int64_t N
   unsigned *keys = nullptr, *totals = nullptr;
   int ntot = 0, rc;
   out.sb = seg_bufs(seg, nc, N);
+  const int64_t crow = nc > 1 ? half_rows(B) : B;
+  if (slot_sort_buckets_supported(N, nc)) {
+    ProfScope prof(kProfBwdSort, s);
+    return slot_sort_buckets(idx, M, K, N, (int)crow, nc, sort_ws, out.sb.seg, out.sb.list, out.sb.count,
+                             crow <= 65536 ? out.sb.pos16 : nullptr, kLongSeg, &out.pos, s);
+  }
   {
     ProfScope prof(kProfBwdSort, s);
-    if ((rc = slot_sort(idx, M, K, N, (int)(nc > 1 ? half_rows(B) : B), nc, sort_ws, &keys, &out.pos, &totals,
-                        &ntot, out.sb.count, nc, s)) != SFT_OK)
+    if ((rc = slot_sort(idx, M, K, N, (int)crow, nc, sort_ws, &keys, &out.pos, &totals, &ntot, out.sb.count, nc,
+                        s)) != SFT_OK)
       return rc;
   }
-  return launch_segments(keys, M, nc, N, totals, ntot, out.sb, out.pos, nc > 1 ? half_rows(B) : B, s);
+  return launch_segments(keys, M, nc, N, totals, ntot, out.sb, out.pos, crow, s);
 }
 
 // One perspective's position-chunk launches of the tiled gather, the sums

@@ -30,7 +30,10 @@ constexpr int kSortItems = 8;
 constexpr int kSortItemsBig = 16;
 constexpr int64_t kBigSort = 4 << 20;
 constexpr int kSortTile = kBlock * kSortItems;  // the smaller tile: sizes the count buffer
-constexpr int kMaxRadix = 512;
+constexpr int kMaxRadix = 1024;  // 10-bit digits (the bucket sort's first pass)
+#ifndef SFT_SORT_BUCKETS
+#define SFT_SORT_BUCKETS 1
+#endif
 
 // FastDiv (index_math.h): n / d by a divisor fixed at launch.
 
@@ -41,8 +44,10 @@ struct SlotKey {
   unsigned N;
   FastDiv divK, divChunk;
   unsigned sentinel;
-  __device__ __forceinline__ unsigned key(int64_t s) const {
-    const unsigned v = (unsigned)idx[s];
+  __device__ __forceinline__ unsigned key(int64_t s) const { return key_of(s, (unsigned)idx[s]); }
+  // The key of slot s from its loaded index value v (loads issued apart from
+  // the arithmetic, whose divisor checks are branches the loads do not cross).
+  __device__ __forceinline__ unsigned key_of(int64_t s, unsigned v) const {
     return v < N ? divChunk(divK((uint32_t)s)) * N + v : sentinel;
   }
   __device__ __forceinline__ int pos(int64_t s) const { return (int)divK((uint32_t)s); }
@@ -95,12 +100,21 @@ __global__ __launch_bounds__(kBlock) void radix_upsweep(SlotKey sk, const unsign
   const int64_t count = pass_count<R>(FIRST, M, prev_totals, red);
   __syncthreads();
   const int64_t base = (int64_t)blockIdx.x * (kBlock * IT);
+  if (count > 0) {  // block-uniform
+    // Every load first, from indices clamped into range (an out-of-range
+    // element loads a real one and is not counted): guarded loads compile to a
+    // branch and a full wait per load, a memory round trip per element.
+    unsigned k[IT];
 #pragma unroll
-  for (int i = 0; i < IT; ++i) {
-    const int64_t e = base + (int64_t)i * kBlock + tid;
-    if (e < count) {
-      const unsigned k = FIRST ? sk.key(e) : kin[e];
-      if (!FIRST || k < sk.sentinel) atomicAdd(&hw[wave][(k >> shift) & (R - 1)], 1u);
+    for (int i = 0; i < IT; ++i) {
+      const int64_t e = std::min<int64_t>(base + (int64_t)i * kBlock + tid, count - 1);
+      k[i] = FIRST ? (unsigned)sk.idx[e] : kin[e];
+    }
+#pragma unroll
+    for (int i = 0; i < IT; ++i) {
+      const int64_t e = base + (int64_t)i * kBlock + tid;
+      if (FIRST) k[i] = sk.key_of(std::min<int64_t>(e, count - 1), k[i]);
+      if (e < count && (!FIRST || k[i] < sk.sentinel)) atomicAdd(&hw[wave][(k[i] >> shift) & (R - 1)], 1u);
     }
   }
   __syncthreads();
@@ -202,17 +216,23 @@ __global__ __launch_bounds__(kBlock) void radix_downsweep(SlotKey sk, const unsi
   int val[IT];
   unsigned rank[IT];
   bool act[IT];
+  // loads from clamped indices, all issued before any is used (see the upsweep)
+  const int64_t last = n_in > 0 ? n_in - 1 : 0;
+#pragma unroll
+  for (int i = 0; i < IT; ++i) {
+    const int64_t ec = std::min<int64_t>(base + (int64_t)i * kWave + lane, last);
+    key[i] = FIRST ? (unsigned)sk.idx[ec] : kin[ec];
+    if (!FIRST) val[i] = vin[ec];
+  }
 #pragma unroll
   for (int i = 0; i < IT; ++i) {
     const int64_t e = base + (int64_t)i * kWave + lane;
-    key[i] = 0;
-    val[i] = 0;
-    act[i] = false;
-    if (e < n_in) {
-      key[i] = FIRST ? sk.key(e) : kin[e];
-      val[i] = FIRST ? sk.pos(e) : vin[e];
-      act[i] = !FIRST || key[i] < sk.sentinel;
+    const int64_t ec = std::min<int64_t>(e, last);
+    if (FIRST) {
+      key[i] = sk.key_of(ec, key[i]);
+      val[i] = sk.pos(ec);
     }
+    act[i] = e < n_in && (!FIRST || key[i] < sk.sentinel);
   }
   unsigned *my = wrun[wave];
 #pragma unroll
@@ -297,6 +317,179 @@ int run_passes(const SlotKey &sk, int64_t M, int passes, unsigned *kbuf[2], int 
   return SFT_OK;
 }
 
+// ---- bucket sort: one radix pass on the high key bits, then each bucket in one workgroup ----
+// Pass 1 (the radix kernels above, one pass, digit = key >> SB) leaves the
+// active slots grouped by bucket b = key >> SB, in slot order within a bucket.
+// Pass 2 sorts each bucket by its low SB bits with one workgroup: a digit
+// histogram gives the bucket's segment starts seg[key] = bucket start + the
+// count of smaller low digits (no neighbour comparisons), its long segments,
+// and then, tile by tile in slot order, stable ranks (per-wave match masks, as
+// the downsweep) place each slot's position and its 16-bit chunk offset.  The
+// order is the same as the LSD passes' (stable by key), so the backward that
+// reads it is bit-identical.  Buckets hold ~4-10 K slots at the FT's shapes.
+constexpr int kBucketBlock = 512;
+constexpr int kBucketWaves = kBucketBlock / kWave;
+constexpr int kBucketItems = 16;  // slots per thread per tile: tiles of 8192
+template <int SB>
+__global__ __launch_bounds__(kBucketBlock) void bucket_sort_kernel(
+    const unsigned *__restrict__ kin, const int *__restrict__ vin, const unsigned *__restrict__ totals, int ntot,
+    unsigned nkeys, FastDiv div_feat, unsigned nfeat, int *__restrict__ vout, uint16_t *__restrict__ pos16,
+    int chunk_rows, int32_t *__restrict__ seg, int32_t *__restrict__ long_list, int *__restrict__ long_count,
+    int long_period) {
+  constexpr int D = 1 << SB;
+  constexpr int TILE = kBucketBlock * kBucketItems;
+  constexpr int PER_WAVE = TILE / kBucketWaves;
+  __shared__ unsigned red[2][kBucketWaves];
+  __shared__ unsigned s_cnt[D], s_run[D], s_tile[D];
+  __shared__ unsigned wrun[kBucketWaves][D];
+  const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
+  const int b = blockIdx.x;
+  // bucket start (digit totals of the buckets before b) and the active total
+  unsigned before = 0, all = 0;
+  for (int i = tid; i < ntot; i += kBucketBlock) {
+    const unsigned v = totals[i];
+    all += v;
+    before += i < b ? v : 0u;
+  }
+#pragma unroll
+  for (int m = 1; m < kWave; m <<= 1) {
+    all += __shfl_xor(all, m);
+    before += __shfl_xor(before, m);
+  }
+  if (lane == 0) {
+    red[0][wave] = before;
+    red[1][wave] = all;
+  }
+  for (int d = tid; d < D; d += kBucketBlock) s_cnt[d] = 0;
+  __syncthreads();
+  unsigned bs = 0, total = 0;
+#pragma unroll
+  for (int w = 0; w < kBucketWaves; ++w) {
+    bs += red[0][w];
+    total += red[1][w];
+  }
+  const unsigned S = totals[b];
+  // A tile's slots: wave w owns the w-th contiguous eighth, walked in 64-slot
+  // rounds, so (wave, round, lane) is slot order.
+  unsigned key[kBucketItems], rank[kBucketItems];
+  int val[kBucketItems];
+  bool act[kBucketItems];
+  unsigned *my = wrun[wave];
+  // loads from clamped indices, all issued before any is used (see the
+  // upsweep); an empty bucket loads nothing
+  auto load_tile = [&](unsigned t0, bool vals) {
+#pragma unroll
+    for (int i = 0; i < kBucketItems; ++i) {
+      const unsigned e = t0 + (unsigned)(wave * PER_WAVE + i * kWave + lane);
+      act[i] = e < S;
+      const unsigned ec = bs + (e < S ? e : S - 1);
+      key[i] = S > 0 ? kin[ec] : 0u;
+      if (vals) val[i] = S > 0 ? vin[ec] : 0;
+    }
+  };
+  // Stable ranks of the tile in registers among its equal low digits, per
+  // wave (match masks), the wave's digit counts left in wrun[wave].
+  auto rank_tile = [&]() {
+#pragma unroll
+    for (int i = 0; i < kBucketItems; ++i) {
+      const unsigned d = key[i] & (D - 1);
+      const uint64_t peers = match_digit<SB>(d, act[i]);
+      if (act[i]) rank[i] = my[d] + (unsigned)popc_below(peers);
+      __builtin_amdgcn_wave_barrier();
+      if (act[i] && (int)(__ffsll((unsigned long long)peers) - 1) == lane) my[d] += (unsigned)__popcll(peers);
+      __builtin_amdgcn_wave_barrier();
+    }
+  };
+  // Per digit: wrun becomes the earlier waves' counts, s_tile the tile's count.
+  auto wave_bases = [&]() {
+    for (int d = tid; d < D; d += kBucketBlock) {
+      unsigned run = 0;
+#pragma unroll
+      for (int w = 0; w < kBucketWaves; ++w) {
+        const unsigned c = wrun[w][d];
+        wrun[w][d] = run;
+        run += c;
+      }
+      s_tile[d] = run;
+    }
+  };
+  auto place_tile = [&]() {
+#pragma unroll
+    for (int i = 0; i < kBucketItems; ++i) {
+      if (!act[i]) continue;
+      const unsigned d = key[i] & (D - 1);
+      const unsigned o = bs + s_run[d] + my[d] + rank[i];
+      vout[o] = val[i];
+      if (pos16 != nullptr) pos16[o] = (uint16_t)(val[i] - (int)div_feat(key[i]) * chunk_rows);
+    }
+  };
+  for (int d = tid; d < D; d += kBucketBlock)
+#pragma unroll
+    for (int w = 0; w < kBucketWaves; ++w) wrun[w][d] = 0;
+  // the digit counts of tiles after the first (buckets of more than one tile):
+  // their keys loaded whole, then counted
+  for (unsigned t0 = TILE; t0 < S; t0 += TILE) {  // block-uniform
+    load_tile(t0, false);
+#pragma unroll
+    for (int i = 0; i < kBucketItems; ++i)
+      if (act[i]) atomicAdd(&s_cnt[key[i] & (D - 1)], 1u);
+  }
+  // the first tile: ranked at once, its counts from the ranking
+  load_tile(0, true);
+  __syncthreads();
+  rank_tile();
+  __syncthreads();
+  wave_bases();
+  __syncthreads();
+  for (int d = tid; d < D; d += kBucketBlock) s_cnt[d] += s_tile[d];
+  __syncthreads();
+  if (wave == 0) wave_scan_digits<D>(s_cnt, s_run, lane);
+  __syncthreads();
+  // segment starts and long segments of the bucket's keys
+  for (int d = tid; d < D; d += kBucketBlock) {
+    const unsigned k = (unsigned)b * D + d;
+    if (k >= nkeys) continue;
+    const int64_t s0 = (int64_t)bs + s_run[d], s1 = s0 + s_cnt[d];
+    seg[k] = (int32_t)s0;
+    if (long_segment(s0, s1, long_period)) {
+      const unsigned c = div_feat(k);
+      const int at = atomicAdd(long_count + c, 1);
+      long_list[(int64_t)c * nfeat + at] = (int32_t)(k - c * nfeat);
+    }
+  }
+  if (b == 0 && tid == 0) seg[nkeys] = (int32_t)total;
+  place_tile();
+  // the other tiles, in order
+  for (unsigned t0 = TILE; t0 < S; t0 += TILE) {  // block-uniform
+    __syncthreads();
+    for (int d = tid; d < D; d += kBucketBlock) {
+      s_run[d] += s_tile[d];
+#pragma unroll
+      for (int w = 0; w < kBucketWaves; ++w) wrun[w][d] = 0;
+    }
+    load_tile(t0, true);
+    __syncthreads();
+    rank_tile();
+    __syncthreads();
+    wave_bases();
+    __syncthreads();
+    place_tile();
+  }
+}
+
+// One radix pass on bits [shift, shift + RB) of the keys built from the index
+// matrix (the first pass of run_passes).
+template <int RB, int IT>
+int run_high_pass(const SlotKey &sk, int64_t M, int shift, unsigned *kout, int *vout, unsigned *hist,
+                  unsigned *totals, int ntiles, int *clear, int nclear, hipStream_t s) {
+  hipLaunchKernelGGL((radix_upsweep<RB, true, IT>), dim3(ntiles), dim3(kBlock), 0, s, sk, nullptr, M, totals, ntiles,
+                     shift, hist);
+  hipLaunchKernelGGL(radix_scan_digits, dim3(1 << RB), dim3(kBlock), 0, s, hist, ntiles, totals, clear, nclear);
+  hipLaunchKernelGGL((radix_downsweep<RB, true, IT>), dim3(ntiles), dim3(kBlock), 0, s, sk, nullptr, nullptr, kout,
+                     vout, hist, totals, M, ntiles, shift);
+  return check_launch("slot bucket sort (first pass)");
+}
+
 }  // namespace
 
 // Workspace: two key/position buffer pairs (ping-pong), the histograms and
@@ -318,11 +511,13 @@ static void sort_passes(int64_t nkeys, int &rb, int &passes) {
   }
 }
 
-// Where slot_sort leaves the sorted positions in its workspace.
+bool slot_sort_buckets_supported(int64_t N, int nchunks);
+// Where slot_sort (or slot_sort_buckets) leaves the sorted positions in its workspace.
 int *slot_sort_positions(int64_t M, int64_t N, int nchunks, void *ws) {
-  int rb, passes;
-  sort_passes((int64_t)nchunks * N, rb, passes);
   const size_t a = align256((size_t)M * 4);
+  int rb, passes;
+  if (slot_sort_buckets_supported(N, nchunks)) passes = 2;  // the buckets' positions: the fourth buffer
+  else sort_passes((int64_t)nchunks * N, rb, passes);
   return reinterpret_cast<int *>(static_cast<char *>(ws) + (((passes - 1) & 1) ? 3 * a : a));
 }
 
@@ -354,6 +549,63 @@ int slot_sort(const int32_t *idx, int64_t M, int K, int64_t N, int chunk_rows, i
   *pos_sorted = vbuf[(passes - 1) & 1];
   *digit_totals = totals;
   *digit_count = 1 << rb;
+  return SFT_OK;
+}
+
+// Bucket-sort plan for keys below nkeys: low bits SB (7 or 8) sorted inside a
+// bucket, high bits RB (8-10) by the radix pass; false when the key space
+// needs more (then the LSD passes and the segment kernel run instead).
+static bool bucket_plan(int64_t nkeys, int &sb, int &rb) {
+  const int kb = (int)key_bits(nkeys - 1 > 0 ? nkeys - 1 : 1);
+  sb = kb >= 18 ? 8 : 7;
+  rb = std::max(8, kb - sb);
+  return rb <= 10;
+}
+bool slot_sort_buckets_supported(int64_t N, int nchunks) {
+  int sb, rb;
+  return SFT_SORT_BUCKETS && bucket_plan((int64_t)nchunks * N, sb, rb);
+}
+
+// The bucket sort with the segment pass folded in: sorted positions (returned),
+// their 16-bit chunk offsets (pos16, when not null), segment starts seg[0 ..
+// nchunks N], and per chunk the list of long segments (list + c N, count[c],
+// which the first pass zeroes).  Same results as slot_sort + the segment kernel.
+int slot_sort_buckets(const int32_t *idx, int64_t M, int K, int64_t N, int chunk_rows, int nchunks, void *ws,
+                      int32_t *seg, int32_t *list, int *count, uint16_t *pos16, int long_period, int **pos_sorted,
+                      hipStream_t s) {
+  char *w = static_cast<char *>(ws);
+  const size_t a = align256((size_t)M * 4);
+  unsigned *k1 = reinterpret_cast<unsigned *>(w);
+  int *v1 = reinterpret_cast<int *>(w + a);
+  int *v2 = reinterpret_cast<int *>(w + 3 * a);
+  const int max_tiles = (int)ceil_div(std::max<int64_t>(M, 1), kSortTile);
+  const bool big = M > kBigSort;
+  const int ntiles = (int)ceil_div(std::max<int64_t>(M, 1), (int64_t)kBlock * (big ? kSortItemsBig : kSortItems));
+  unsigned *hist = reinterpret_cast<unsigned *>(w + 4 * a);
+  unsigned *totals = reinterpret_cast<unsigned *>(w + 4 * a + align256((size_t)(kMaxRadix * max_tiles) * 4));
+  const unsigned nkeys = (unsigned)((int64_t)nchunks * N);
+  int sb, rb;
+  if (!bucket_plan(nkeys, sb, rb)) return fail(SFT_EINVAL, "slot bucket sort: key space too large");
+  const SlotKey sk{idx, (unsigned)N, FastDiv((uint32_t)K), FastDiv((uint32_t)chunk_rows), nkeys};
+  int rc;
+#define SFT_HIGH_PASS(RB)                                                                                          \
+  rc = big ? run_high_pass<RB, kSortItemsBig>(sk, M, sb, k1, v1, hist, totals, ntiles, count, nchunks, s)         \
+           : run_high_pass<RB, kSortItems>(sk, M, sb, k1, v1, hist, totals, ntiles, count, nchunks, s)
+  if (rb == 8) SFT_HIGH_PASS(8);
+  else if (rb == 9) SFT_HIGH_PASS(9);
+  else SFT_HIGH_PASS(10);
+#undef SFT_HIGH_PASS
+  if (rc != SFT_OK) return rc;
+  const int nb = (int)ceil_div(std::max<int64_t>(nkeys, 1), (int64_t)1 << sb);
+  const FastDiv div_feat((uint32_t)N);
+  if (sb == 8)
+    hipLaunchKernelGGL(bucket_sort_kernel<8>, dim3(nb), dim3(kBucketBlock), 0, s, k1, v1, totals, 1 << rb, nkeys,
+                       div_feat, (unsigned)N, v2, pos16, chunk_rows, seg, list, count, long_period);
+  else
+    hipLaunchKernelGGL(bucket_sort_kernel<7>, dim3(nb), dim3(kBucketBlock), 0, s, k1, v1, totals, 1 << rb, nkeys,
+                       div_feat, (unsigned)N, v2, pos16, chunk_rows, seg, list, count, long_period);
+  if ((rc = check_launch("slot bucket sort (buckets)")) != SFT_OK) return rc;
+  *pos_sorted = v2;
   return SFT_OK;
 }
 

@@ -263,7 +263,7 @@ def prep_buffer_bytes(B: int, K: int, N: int, L: int, flags: int, device: torch.
 # sizes (SymInt), which the C size query cannot take; CPU tests check that it
 # equals sft_ft_bwd_f32_prep_size over a sweep of shapes.
 _SORT_TILE = 2048              # kBlock * kSortItems (csrc/ft_sort.hip)
-_SORT_MAX_RADIX = 512          # kMaxRadix
+_SORT_MAX_RADIX = 1024         # kMaxRadix
 _BWD_MIN_TILES = 4             # SFT_BWD_MIN_TILES (csrc/common.h)
 _BWD_TILE_BYTES = 128          # one 32-column grad tile row
 _BWD_ONE_CHUNK_BYTES = 4 << 20  # SFT_BWD_ONE_CHUNK_BYTES
