@@ -593,6 +593,189 @@ __global__ __launch_bounds__(kBlock) void rank_lists_kernel(RankArgs a, int64_t 
   }
 }
 
+// Lists longer than the staged ones (K > 32, rows of 16-byte pieces): four
+// threads per position, each holding a quarter of the row in registers from
+// one batch of loads (nothing read twice), so a workgroup of 256 positions
+// runs 16 waves instead of 4 and each thread walks a quarter of the slots.
+// The quarters are combined across their four lanes with shuffles: the
+// running maximum of parts enters quarter q as the maximum over quarters
+// before it, and each pass's run takes the quarters' entries in quarter
+// order.  Same outputs as rank_lists_kernel (pos, count, list; with table
+// parts cut, roff and the packed runs).
+constexpr int kWideSubs = 4;
+constexpr int kWideBlock = kRankSortBlock * kWideSubs;  // 1024 threads
+constexpr int kWideWindow = 12288;                      // list entries staged in LDS at once (48 KB)
+template <int NL>  // 16-byte pieces per thread (quarters of up to 4 NL slots)
+__global__ __launch_bounds__(kWideBlock) void rank_lists_wide_kernel(RankArgs a, int64_t B, int64_t Bpad, int K,
+                                                                     int N, int kpad, int S) {
+  extern __shared__ int sm[];  // bins[K + 1] | offsets[K + 1] | (parts) run scans [kMaxParts][256] | window
+  unsigned *bin = reinterpret_cast<unsigned *>(sm), *off = bin + (K + 1);
+  int *scan = sm + round_up4(2 * (K + 1));  // 16-byte aligned: the window after it is read in 16-byte pieces
+  const RankLists &L = a.L[blockIdx.y];
+  const int32_t *__restrict__ idx = a.idx[blockIdx.y];
+  const int tid = threadIdx.x, j = tid % kWideSubs, lp = tid / kWideSubs;
+  const int64_t base = (int64_t)blockIdx.x * kRankSortBlock;
+  const int64_t b = base + lp;
+  const bool real = b < B;
+  const int32_t *row = idx + (real ? b : 0) * K;
+  for (int i = tid; i <= K; i += kWideBlock) bin[i] = 0u;
+  // quarter j = slots [j S, j S + S): every piece loaded first, from offsets
+  // clamped into the row; pieces past K or S, and padding positions, read as -1
+  i32x4 rv[NL];
+#pragma unroll
+  for (int u = 0; u < NL; ++u) {
+    const int k = j * S + 4 * u;
+    rv[u] = *reinterpret_cast<const i32x4 *>(row + (k < K - 4 ? k : K - 4));
+  }
+#pragma unroll
+  for (int u = 0; u < NL; ++u)
+    if (!real || 4 * u >= S || j * S + 4 * u >= K) rv[u] = i32x4{-1, -1, -1, -1};
+  const bool parts = a.nparts > 1;  // launch-uniform
+  auto part_of = [&](int v) { return parts ? (int)a.part_of((uint32_t)v) : 0; };
+  // the quarter's highest part; the running maximum entering it (quarters before)
+  int ml = 0;
+#pragma unroll
+  for (int u = 0; u < NL; ++u)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int v = rv[u][e];
+      ml = (unsigned)v < (unsigned)N ? max(ml, part_of(v)) : ml;
+    }
+  int incl = ml;
+#pragma unroll
+  for (int d = 1; d < kWideSubs; d <<= 1) {
+    const int o = __shfl_up(incl, d, kWideSubs);
+    if (j >= d) incl = max(incl, o);
+  }
+  int enter = __shfl_up(incl, 1, kWideSubs);
+  if (j == 0) enter = 0;
+  // the quarter's entries per pass (pass = running maximum of parts)
+  int cp[kMaxParts] = {0, 0, 0, 0};
+  {
+    int rm = enter;
+#pragma unroll
+    for (int u = 0; u < NL; ++u)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int v = rv[u][e];
+        const bool act = (unsigned)v < (unsigned)N;
+        rm = act ? max(rm, part_of(v)) : rm;
+#pragma unroll
+        for (int q = 0; q < kMaxParts; ++q) cp[q] += (act && rm == q) ? 1 : 0;
+      }
+  }
+  // per pass: entries of the quarters before this one, and the position's total
+  int pre[kMaxParts], tot[kMaxParts];
+#pragma unroll
+  for (int q = 0; q < kMaxParts; ++q) {
+    int s = cp[q];
+#pragma unroll
+    for (int d = 1; d < kWideSubs; d <<= 1) {
+      const int o = __shfl_up(s, d, kWideSubs);
+      if (j >= d) s += o;
+    }
+    pre[q] = s - cp[q];
+    tot[q] = __shfl(s, kWideSubs - 1, kWideSubs);
+  }
+  const int c = tot[0] + tot[1] + tot[2] + tot[3];
+  __syncthreads();  // bins cleared
+  unsigned mine = 0u;
+  if (j == 0 && real) mine = atomicAdd(&bin[c], 1u);
+  __syncthreads();
+  if (tid < kWave) {  // off[cc] = sum of bin[cc + 1 .. K], largest count first (as rank_lists_kernel)
+    unsigned carry = 0u;
+    for (int top = K; top >= 0; top -= kWave) {
+      const int cc = top - tid;
+      const unsigned v = cc >= 0 ? bin[cc] : 0u;
+      unsigned sc = v;
+#pragma unroll
+      for (int d = 1; d < kWave; d <<= 1) {
+        const unsigned o = __shfl_up(sc, d);
+        if (tid >= d) sc += o;
+      }
+      if (cc >= 0) off[cc] = carry + sc - v;
+      carry += __shfl(sc, kWave - 1);
+    }
+  }
+  __syncthreads();
+  mine = __shfl(mine, 0, kWideSubs);
+  const int rl = real ? (int)(off[c] + mine) : lp;  // positions past B are the block's last (padding) ranks
+  const int64_t r = base + rl;
+  if (j == 0 && r < Bpad) {
+    L.pos[r] = real ? (int32_t)b : -1;
+    L.count[r] = real ? c : 0;
+  }
+  if (parts) {  // packed runs (see "Table parts"): pass p's run of a rank is tot[p] long
+    if (j == 0) {
+#pragma unroll
+      for (int p = 0; p < kMaxParts; ++p) scan[p * kRankSortBlock + rl] = tot[p];
+    }
+    __syncthreads();
+    {  // inclusive scans of the run lengths in rank order, one per pass: thread = (pass, rank)
+      const int sp = tid / kRankSortBlock, si = tid % kRankSortBlock;
+      int *col = scan + sp * kRankSortBlock;
+      for (int d = 1; d < kRankSortBlock; d <<= 1) {
+        const int v = col[si] + (si >= d ? col[si - d] : 0);
+        __syncthreads();
+        col[si] = v;
+        __syncthreads();
+      }
+    }
+    int start[kMaxParts];
+    int64_t pbase = base * kpad;  // this block's region of the runs
+#pragma unroll
+    for (int p = 0; p < kMaxParts; ++p) {
+      start[p] = (int)(pbase + scan[p * kRankSortBlock + rl] - tot[p]);
+      pbase += scan[p * kRankSortBlock + kRankSortBlock - 1];
+    }
+    if (j == 0 && r < Bpad) {
+      L.cut[r] = i32x4{tot[0], tot[0] + tot[1], tot[0] + tot[1] + tot[2], a.nparts - 1};
+      L.roff[r] = i32x4{start[0], start[1], start[2], start[3]};
+    }
+    // The block's runs fill [base kpad, base kpad + total) of the list: they
+    // are placed in LDS a window at a time (each thread walks its quarter
+    // again from registers) and stored with coalesced 16-byte stores, instead
+    // of a 4-byte store per entry scattered over the block's region.
+    int *win = scan + kMaxParts * kRankSortBlock;
+    const int total = (int)(pbase - base * kpad);
+    int32_t *region = L.list + base * kpad;  // 16-byte aligned: kpad is a multiple of 4
+    for (int w0 = 0; w0 < total; w0 += kWideWindow) {  // block-uniform
+      int w[kMaxParts];
+#pragma unroll
+      for (int p = 0; p < kMaxParts; ++p) w[p] = start[p] - (int)(base * kpad) + pre[p] - w0;
+      int rm = enter;
+#pragma unroll
+      for (int u = 0; u < NL; ++u)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int v = rv[u][e];
+          if ((unsigned)v >= (unsigned)N) continue;
+          rm = max(rm, part_of(v));
+          const int at = rm == 0 ? w[0]++ : rm == 1 ? w[1]++ : rm == 2 ? w[2]++ : w[3]++;
+          if ((unsigned)at < (unsigned)kWideWindow) win[at] = v;
+        }
+      __syncthreads();
+      const int n = min(kWideWindow, total - w0);
+      i32x4 *dst4 = reinterpret_cast<i32x4 *>(region + w0);
+      const i32x4 *src4 = reinterpret_cast<const i32x4 *>(win);
+      for (int i = tid; i < n / 4; i += kWideBlock) dst4[i] = src4[i];
+      for (int i = (n & ~3) + tid; i < n; i += kWideBlock) region[w0 + i] = win[i];
+      __syncthreads();
+    }
+    return;
+  }
+  if (r < Bpad) {
+    int32_t *dst = L.list + r * kpad;
+    int at = pre[0];
+#pragma unroll
+    for (int u = 0; u < NL; ++u)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if ((unsigned)rv[u][e] < (unsigned)N) dst[at++] = rv[u][e];
+    for (int i = c + j; i < kpad; i += kWideSubs) dst[i] = N;
+  }
+}
+
 // Chunk c (of 32 ranks) of a tile pass -> rank chunk: the longest lists
 // first across all sort blocks -- chunk 0 of every block, then chunk 1 of
 // every block, and so on (the last block may hold fewer chunks) -- so a tile
@@ -1150,6 +1333,10 @@ static RankLists rank_lists_at(char *p, int64_t B, int K, int narrow) {
 
 // Table parts of a gather over N rows (see "Table parts"): as many as keep a
 // part's tile rows within SFT_FWD_PART_BYTES, at most kMaxParts.
+// Rank lists of K > 32 built by four threads per position (rank_lists_wide_kernel).
+#ifndef SFT_FWD_WIDE_RANKS
+#define SFT_FWD_WIDE_RANKS 1
+#endif
 #ifndef SFT_FWD_PART_BYTES
 #define SFT_FWD_PART_BYTES (7 << 19)
 #endif
@@ -1193,7 +1380,21 @@ static int build_rank_lists(const int32_t *idx0, const int32_t *idx1, int np, in
   const size_t lds = (size_t)(2 * (K + 1)) * 4 + std::max(rows_lds, scan_lds);
   const dim3 grid((unsigned)ceil_div(Bp, (int64_t)kRankSortBlock), (unsigned)np);
   ProfScope prof(kProfFwdRanks, s);
-  if (stage)
+  // longer lists: four threads per position, quarters of S slots (whole 16-byte pieces)
+  const int S = round_up4((K + kWideSubs - 1) / kWideSubs);
+  if (SFT_FWD_WIDE_RANKS && !stage && vec && S <= 48) {  // up to K = 192 (12 pieces a thread, no spills)
+    const size_t wlds =
+        (size_t)round_up4(2 * (K + 1)) * 4 + (nparts > 1 ? (size_t)(kMaxParts * kRankSortBlock + kWideWindow) * 4 : 0);
+#define SFT_WIDE_RANKS(NL)                                                                                        \
+  hipLaunchKernelGGL(rank_lists_wide_kernel<NL>, grid, dim3(kWideBlock), wlds, s, a, B, Bp, K, N, kpad, S)
+    const int nl = S / 4;
+    if (nl <= 4) SFT_WIDE_RANKS(4);
+    else if (nl <= 6) SFT_WIDE_RANKS(6);
+    else if (nl <= 8) SFT_WIDE_RANKS(8);
+    else if (nl <= 10) SFT_WIDE_RANKS(10);
+    else SFT_WIDE_RANKS(12);
+#undef SFT_WIDE_RANKS
+  } else if (stage)
     hipLaunchKernelGGL(rank_lists_kernel<true>, grid, dim3(kBlock), lds, s, a, B, Bp, K, N, kpad, vec);
   else
     hipLaunchKernelGGL(rank_lists_kernel<false>, grid, dim3(kBlock), lds, s, a, B, Bp, K, N, kpad, vec);

@@ -31,6 +31,12 @@ SHAPES = [
     (16, 400, 2500, 24, 228, 8, 24, True),    # 8 tiles, the last holding one chunk
     (17, 300, 1200, 32, 96, 0, 32, False),    # 3 tiles: row gather
     (18, 900, 3000, 32, 200, 8, 32, True),    # 7 tiles: leftover strands of two tiles per XCD
+    # lists of K > 32 built four threads a position (quarters of whole 16-byte pieces)
+    (19, 1000, 300, 36, 136, 0, 36, False),   # K = 36: quarters of 12 slots, the last piece of each padding
+    (20, 777, 85296, 100, 520, 0, 100, False),  # table parts, quarters of 28 slots, unsorted rows
+    (21, 513, 70000, 192, 264, 100, 192, False),  # the widest such lists: quarters of 48 slots
+    (22, 300, 85296, 196, 136, 150, 196, True),  # K = 196: one thread a position again
+    (23, 400, 60000, 64, 1048, 0, 64, True),  # table parts, sorted rows, many empty quarters
 ]
 
 
