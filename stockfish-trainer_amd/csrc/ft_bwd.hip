@@ -42,6 +42,11 @@ bool slot_sort_buckets_supported(int64_t N, int nchunks);
 int slot_sort_buckets(const int32_t *idx, int64_t M, int K, int64_t N, int chunk_rows, int nchunks, void *ws,
                       int32_t *seg, int32_t *list, int *count, uint16_t *pos16, int long_period, int **pos_sorted,
                       hipStream_t s);
+// Its two halves: the radix pass into ws, then the buckets from ws (only read).
+int slot_sort_buckets_high(const int32_t *idx, int64_t M, int K, int64_t N, int chunk_rows, int nchunks, void *ws,
+                           int *clear, int nclear, hipStream_t s);
+int slot_sort_buckets_low(const void *ws, int64_t M, int64_t N, int chunk_rows, int nchunks, int *vout,
+                          int32_t *seg, int32_t *list, int *count, uint16_t *pos16, int long_period, hipStream_t s);
 
 namespace {
 
@@ -1063,7 +1068,7 @@ void launch_gather(dim3 grid, hipStream_t s, const int32_t *seg_start, const int
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 struct BwdLayout {
-  size_t sort, seg, partial, gt, tmp, total;
+  size_t sort, seg, spos, partial, gt, tmp, total;
   int nparts;
 };
 
@@ -1100,18 +1105,25 @@ int64_t half_rows(int64_t B) { return ceil_div(B, kBwdHalves); }
 // SFT_BWD_PREPARED they live in the caller's prepared buffer instead
 // (make_prep_layout) and the workspace holds the rest.
 bool prep_pays(int64_t B, int K, int L, uint32_t flags);
+bool prep_split(int64_t B, int K, int64_t N, int L, uint32_t flags);
 int make_layout(int64_t B, int K, int64_t N, int L, uint32_t flags, BwdLayout &lay) {
   const int64_t M = B * K;
   lay.nparts = bias_parts(B);
   size_t off = 0;
   lay.partial = off;
   off = align256(off + (size_t)lay.nparts * (size_t)L * sizeof(float));
-  lay.sort = lay.seg = lay.gt = lay.tmp = off;
+  lay.sort = lay.seg = lay.spos = lay.gt = lay.tmp = off;
   if (!(flags & SFT_BWD_ATOMIC) && M > 0) {
     const int nc = sort_chunks(B, L, flags);
-    if (!((flags & SFT_BWD_PREPARED) && prep_pays(B, K, L, flags))) {
+    const bool prepared = (flags & SFT_BWD_PREPARED) && prep_pays(B, K, L, flags);
+    if (!prepared) {
       lay.sort = off;
       off = align256(off + slot_sort_workspace(M));
+      lay.seg = off;
+      off = align256(off + seg_region_bytes(nc, N, M));
+    } else if (prep_split(B, K, N, L, flags)) {  // the buckets' outputs: sorted positions and segments
+      lay.spos = off;
+      off = align256(off + (size_t)M * 4);
       lay.seg = off;
       off = align256(off + seg_region_bytes(nc, N, M));
     }
@@ -1199,6 +1211,17 @@ int launch_segments(const unsigned *keys, int64_t M, int nc, int64_t nfeat, cons
 bool prep_pays(int64_t B, int K, int L, uint32_t flags) {
   return !(flags & SFT_BWD_ATOMIC) && B * K > 0 && (int64_t)K * SFT_BWD_PREP_K_PER_L >= L;
 }
+// Split prepared sort: the forward runs only the bucket sort's radix pass,
+// the backward its buckets beside the bias pass, for shapes where the whole
+// sort outlasts the forward's gather it hides behind (rows narrow for their
+// slot count: K >= L / SFT_BWD_SPLIT_K_PER_L).
+#ifndef SFT_BWD_SPLIT_K_PER_L
+#define SFT_BWD_SPLIT_K_PER_L 5
+#endif
+bool prep_split(int64_t B, int K, int64_t N, int L, uint32_t flags) {
+  return prep_pays(B, K, L, flags) && (int64_t)K * SFT_BWD_SPLIT_K_PER_L >= L &&
+         slot_sort_buckets_supported(N, sort_chunks(B, L, flags));
+}
 struct PrepLayout {
   size_t sort, seg, total;
   int nc;
@@ -1252,6 +1275,11 @@ int bwd_prepare(const int32_t *idx, int64_t B, int K, int64_t N, int L, uint32_t
   if (prep == nullptr || prep_bytes < p.total || (uintptr_t)prep % 256 != 0)
     return fail(SFT_EWORKSPACE, "prepared buffer smaller than sft_ft_bwd_f32_prep_size() or not 256-byte aligned");
   char *w = static_cast<char *>(prep);
+  if (prep_split(B, K, N, L, flags)) {  // the radix pass only; the backward runs the buckets
+    ProfScope prof(kProfBwdSort, s);
+    return slot_sort_buckets_high(idx, B * K, K, N, (int)(p.nc > 1 ? half_rows(B) : B), p.nc, w + p.sort, nullptr, 0,
+                                  s);
+  }
   int32_t *pos = nullptr;
   return sort_and_segments(idx, B, K, N, p.nc, w + p.sort, reinterpret_cast<int32_t *>(w + p.seg), &pos, s);
 }
@@ -1303,8 +1331,26 @@ int bwd_f32(const int32_t *idx, int64_t B, int K, const float *grad, int64_t N, 
       return fail(SFT_EINVAL, "sft_ft_bwd_f32_prepared: weight_grad must be 16-byte aligned when the prepared sort "
                               "is in position chunks (batch above 32768 with the tiled gather)");
     char *pw = static_cast<char *>(prep);
-    seg = reinterpret_cast<int32_t *>(pw + pl.seg);
-    pos = slot_sort_positions(M, N, nc, pw + pl.sort);
+    if (prep_split(B, K, N, L, flags)) {
+      // the buckets on the side stream, beside the bias pass, from the radix
+      // pass the forward left in the prepared buffer, into the workspace
+      hipStream_t side;
+      if ((rc = fork_side(s, &side)) != SFT_OK) return rc;
+      side_join.emplace(s);
+      const SegBufs sbs = seg_bufs(seg, nc, N);
+      const int64_t crow = nc > 1 ? half_rows(B) : B;
+      pos = reinterpret_cast<int32_t *>(w + lay.spos);
+      ProfScope prof(kProfBwdSort, side);
+      hipLaunchKernelGGL(zero_kernel, dim3(1), dim3(kBlock), 0, side, reinterpret_cast<float *>(sbs.count),
+                         (int64_t)nc);  // the long-segment counts (the forward's radix pass left them alone)
+      if ((rc = check_launch("long-segment count clear")) != SFT_OK) return rc;
+      if ((rc = slot_sort_buckets_low(pw + pl.sort, M, N, (int)crow, nc, pos, sbs.seg, sbs.list, sbs.count,
+                                      crow <= 65536 ? sbs.pos16 : nullptr, kLongSeg, side)) != SFT_OK)
+        return rc;
+    } else {
+      seg = reinterpret_cast<int32_t *>(pw + pl.seg);
+      pos = slot_sort_positions(M, N, nc, pw + pl.sort);
+    }
   } else if (sorted) {
     hipStream_t side;
     if ((rc = fork_side(s, &side)) != SFT_OK) return rc;

@@ -340,8 +340,11 @@ __global__ __launch_bounds__(kBucketBlock) void bucket_sort_kernel(
   constexpr int TILE = kBucketBlock * kBucketItems;
   constexpr int PER_WAVE = TILE / kBucketWaves;
   __shared__ unsigned red[2][kBucketWaves];
-  __shared__ unsigned s_cnt[D], s_run[D], s_tile[D];
+  __shared__ unsigned s_cnt[D], s_run[D], s_tile[D], s_trun[D];
   __shared__ unsigned wrun[kBucketWaves][D];
+  __shared__ int s_val[TILE];  // a tile in sorted order: positions, digits, chunk offsets
+  __shared__ uint8_t s_dig[TILE];
+  __shared__ uint16_t s_p16[TILE];
   const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
   const int b = blockIdx.x;
   // bucket start (digit totals of the buckets before b) and the active total
@@ -413,14 +416,27 @@ __global__ __launch_bounds__(kBucketBlock) void bucket_sort_kernel(
       s_tile[d] = run;
     }
   };
-  auto place_tile = [&]() {
+  // The tile in sorted order in LDS (j = the digit's start in the tile + the
+  // earlier waves' count + the rank), then copied out: slot j of digit d goes
+  // to bs + s_run[d] + (j - s_trun[d]), so runs of one digit are stored by
+  // consecutive lanes (a one-tile bucket is one contiguous stretch) instead of
+  // each lane storing to a line of its own.
+  auto place_tile = [&](unsigned n) {
 #pragma unroll
     for (int i = 0; i < kBucketItems; ++i) {
       if (!act[i]) continue;
       const unsigned d = key[i] & (D - 1);
-      const unsigned o = bs + s_run[d] + my[d] + rank[i];
-      vout[o] = val[i];
-      if (pos16 != nullptr) pos16[o] = (uint16_t)(val[i] - (int)div_feat(key[i]) * chunk_rows);
+      const unsigned j = s_trun[d] + my[d] + rank[i];
+      s_val[j] = val[i];
+      s_dig[j] = (uint8_t)d;
+      if (pos16 != nullptr) s_p16[j] = (uint16_t)(val[i] - (int)div_feat(key[i]) * chunk_rows);
+    }
+    __syncthreads();
+    for (unsigned j = tid; j < n; j += kBucketBlock) {
+      const unsigned d = s_dig[j];
+      const unsigned o = bs + s_run[d] + (j - s_trun[d]);
+      vout[o] = s_val[j];
+      if (pos16 != nullptr) pos16[o] = s_p16[j];
     }
   };
   for (int d = tid; d < D; d += kBucketBlock)
@@ -444,6 +460,7 @@ __global__ __launch_bounds__(kBucketBlock) void bucket_sort_kernel(
   for (int d = tid; d < D; d += kBucketBlock) s_cnt[d] += s_tile[d];
   __syncthreads();
   if (wave == 0) wave_scan_digits<D>(s_cnt, s_run, lane);
+  if (wave == 1) wave_scan_digits<D>(s_tile, s_trun, lane);
   __syncthreads();
   // segment starts and long segments of the bucket's keys
   for (int d = tid; d < D; d += kBucketBlock) {
@@ -458,7 +475,7 @@ __global__ __launch_bounds__(kBucketBlock) void bucket_sort_kernel(
     }
   }
   if (b == 0 && tid == 0) seg[nkeys] = (int32_t)total;
-  place_tile();
+  place_tile(S < (unsigned)TILE ? S : (unsigned)TILE);
   // the other tiles, in order
   for (unsigned t0 = TILE; t0 < S; t0 += TILE) {  // block-uniform
     __syncthreads();
@@ -473,7 +490,9 @@ __global__ __launch_bounds__(kBucketBlock) void bucket_sort_kernel(
     __syncthreads();
     wave_bases();
     __syncthreads();
-    place_tile();
+    if (wave == 0) wave_scan_digits<D>(s_tile, s_trun, lane);
+    __syncthreads();
+    place_tile(S - t0 < (unsigned)TILE ? S - t0 : (unsigned)TILE);
   }
 }
 
@@ -566,46 +585,87 @@ bool slot_sort_buckets_supported(int64_t N, int nchunks) {
   return SFT_SORT_BUCKETS && bucket_plan((int64_t)nchunks * N, sb, rb);
 }
 
-// The bucket sort with the segment pass folded in: sorted positions (returned),
-// their 16-bit chunk offsets (pos16, when not null), segment starts seg[0 ..
-// nchunks N], and per chunk the list of long segments (list + c N, count[c],
-// which the first pass zeroes).  Same results as slot_sort + the segment kernel.
+// The bucket sort's buffers in a slot_sort workspace: the high pass's keys and
+// positions (k1, v1), its per-tile digit counts and digit totals, and the
+// buckets' sorted positions (v2, the fourth buffer).
+struct BucketBufs {
+  unsigned *k1;
+  int *v1, *v2;
+  unsigned *hist, *totals;
+  int ntiles, sb, rb;
+  bool big;
+};
+static int bucket_bufs(void *ws, int64_t M, int64_t N, int nchunks, BucketBufs &bb) {
+  char *w = static_cast<char *>(ws);
+  const size_t a = align256((size_t)M * 4);
+  const int max_tiles = (int)ceil_div(std::max<int64_t>(M, 1), kSortTile);
+  bb.k1 = reinterpret_cast<unsigned *>(w);
+  bb.v1 = reinterpret_cast<int *>(w + a);
+  bb.v2 = reinterpret_cast<int *>(w + 3 * a);
+  bb.hist = reinterpret_cast<unsigned *>(w + 4 * a);
+  bb.totals = reinterpret_cast<unsigned *>(w + 4 * a + align256((size_t)(kMaxRadix * max_tiles) * 4));
+  bb.big = M > kBigSort;
+  bb.ntiles = (int)ceil_div(std::max<int64_t>(M, 1), (int64_t)kBlock * (bb.big ? kSortItemsBig : kSortItems));
+  if (!bucket_plan((int64_t)nchunks * N, bb.sb, bb.rb)) return fail(SFT_EINVAL, "slot bucket sort: key space too large");
+  return SFT_OK;
+}
+
+// First half of the bucket sort: the radix pass on the high key bits, into
+// the workspace; zeroes clear[0 .. nclear) (stream-ordered).
+int slot_sort_buckets_high(const int32_t *idx, int64_t M, int K, int64_t N, int chunk_rows, int nchunks, void *ws,
+                           int *clear, int nclear, hipStream_t s) {
+  BucketBufs bb;
+  int rc = bucket_bufs(ws, M, N, nchunks, bb);
+  if (rc != SFT_OK) return rc;
+  const unsigned nkeys = (unsigned)((int64_t)nchunks * N);
+  const SlotKey sk{idx, (unsigned)N, FastDiv((uint32_t)K), FastDiv((uint32_t)chunk_rows), nkeys};
+#define SFT_HIGH_PASS(RB)                                                                                          \
+  rc = bb.big ? run_high_pass<RB, kSortItemsBig>(sk, M, bb.sb, bb.k1, bb.v1, bb.hist, bb.totals, bb.ntiles, clear, \
+                                                 nclear, s)                                                        \
+              : run_high_pass<RB, kSortItems>(sk, M, bb.sb, bb.k1, bb.v1, bb.hist, bb.totals, bb.ntiles, clear,    \
+                                              nclear, s)
+  if (bb.rb == 8) SFT_HIGH_PASS(8);
+  else if (bb.rb == 9) SFT_HIGH_PASS(9);
+  else SFT_HIGH_PASS(10);
+#undef SFT_HIGH_PASS
+  return rc;
+}
+
+// Second half: one workgroup per bucket over the high pass's output in ws
+// (only read), writing the sorted positions to vout, their 16-bit chunk
+// offsets (pos16, when not null), segment starts seg[0 .. nchunks N] and per
+// chunk the list of long segments (list + c N, count[c], which must be zero).
+int slot_sort_buckets_low(const void *ws, int64_t M, int64_t N, int chunk_rows, int nchunks, int *vout,
+                          int32_t *seg, int32_t *list, int *count, uint16_t *pos16, int long_period, hipStream_t s) {
+  BucketBufs bb;
+  int rc = bucket_bufs(const_cast<void *>(ws), M, N, nchunks, bb);
+  if (rc != SFT_OK) return rc;
+  const unsigned nkeys = (unsigned)((int64_t)nchunks * N);
+  const int nb = (int)ceil_div(std::max<int64_t>(nkeys, 1), (int64_t)1 << bb.sb);
+  const FastDiv div_feat((uint32_t)N);
+  if (bb.sb == 8)
+    hipLaunchKernelGGL(bucket_sort_kernel<8>, dim3(nb), dim3(kBucketBlock), 0, s, bb.k1, bb.v1, bb.totals, 1 << bb.rb,
+                       nkeys, div_feat, (unsigned)N, vout, pos16, chunk_rows, seg, list, count, long_period);
+  else
+    hipLaunchKernelGGL(bucket_sort_kernel<7>, dim3(nb), dim3(kBucketBlock), 0, s, bb.k1, bb.v1, bb.totals, 1 << bb.rb,
+                       nkeys, div_feat, (unsigned)N, vout, pos16, chunk_rows, seg, list, count, long_period);
+  return check_launch("slot bucket sort (buckets)");
+}
+
+// The bucket sort with the segment pass folded in: both halves, the sorted
+// positions in the workspace's fourth buffer (returned), the long-segment
+// counts zeroed by the first half.  Same results as slot_sort + the segment kernel.
 int slot_sort_buckets(const int32_t *idx, int64_t M, int K, int64_t N, int chunk_rows, int nchunks, void *ws,
                       int32_t *seg, int32_t *list, int *count, uint16_t *pos16, int long_period, int **pos_sorted,
                       hipStream_t s) {
-  char *w = static_cast<char *>(ws);
-  const size_t a = align256((size_t)M * 4);
-  unsigned *k1 = reinterpret_cast<unsigned *>(w);
-  int *v1 = reinterpret_cast<int *>(w + a);
-  int *v2 = reinterpret_cast<int *>(w + 3 * a);
-  const int max_tiles = (int)ceil_div(std::max<int64_t>(M, 1), kSortTile);
-  const bool big = M > kBigSort;
-  const int ntiles = (int)ceil_div(std::max<int64_t>(M, 1), (int64_t)kBlock * (big ? kSortItemsBig : kSortItems));
-  unsigned *hist = reinterpret_cast<unsigned *>(w + 4 * a);
-  unsigned *totals = reinterpret_cast<unsigned *>(w + 4 * a + align256((size_t)(kMaxRadix * max_tiles) * 4));
-  const unsigned nkeys = (unsigned)((int64_t)nchunks * N);
-  int sb, rb;
-  if (!bucket_plan(nkeys, sb, rb)) return fail(SFT_EINVAL, "slot bucket sort: key space too large");
-  const SlotKey sk{idx, (unsigned)N, FastDiv((uint32_t)K), FastDiv((uint32_t)chunk_rows), nkeys};
-  int rc;
-#define SFT_HIGH_PASS(RB)                                                                                          \
-  rc = big ? run_high_pass<RB, kSortItemsBig>(sk, M, sb, k1, v1, hist, totals, ntiles, count, nchunks, s)         \
-           : run_high_pass<RB, kSortItems>(sk, M, sb, k1, v1, hist, totals, ntiles, count, nchunks, s)
-  if (rb == 8) SFT_HIGH_PASS(8);
-  else if (rb == 9) SFT_HIGH_PASS(9);
-  else SFT_HIGH_PASS(10);
-#undef SFT_HIGH_PASS
+  BucketBufs bb;
+  int rc = bucket_bufs(ws, M, N, nchunks, bb);
   if (rc != SFT_OK) return rc;
-  const int nb = (int)ceil_div(std::max<int64_t>(nkeys, 1), (int64_t)1 << sb);
-  const FastDiv div_feat((uint32_t)N);
-  if (sb == 8)
-    hipLaunchKernelGGL(bucket_sort_kernel<8>, dim3(nb), dim3(kBucketBlock), 0, s, k1, v1, totals, 1 << rb, nkeys,
-                       div_feat, (unsigned)N, v2, pos16, chunk_rows, seg, list, count, long_period);
-  else
-    hipLaunchKernelGGL(bucket_sort_kernel<7>, dim3(nb), dim3(kBucketBlock), 0, s, k1, v1, totals, 1 << rb, nkeys,
-                       div_feat, (unsigned)N, v2, pos16, chunk_rows, seg, list, count, long_period);
-  if ((rc = check_launch("slot bucket sort (buckets)")) != SFT_OK) return rc;
-  *pos_sorted = v2;
+  if ((rc = slot_sort_buckets_high(idx, M, K, N, chunk_rows, nchunks, ws, count, nchunks, s)) != SFT_OK) return rc;
+  if ((rc = slot_sort_buckets_low(ws, M, N, chunk_rows, nchunks, bb.v2, seg, list, count, pos16, long_period, s)) !=
+      SFT_OK)
+    return rc;
+  *pos_sorted = bb.v2;
   return SFT_OK;
 }
 

@@ -257,13 +257,15 @@ def test_prepared_bwd_matches_the_backward(seed, B, N, K, L, lo, hi, sort):
     assert np.array_equal(db, db0)
 
 
-@pytest.mark.parametrize("B,L", [(40000, 256), (3000, 256)])
+@pytest.mark.parametrize("B,L", [(40000, 256), (3000, 256), (40000, 136), (3000, 136)])
 def test_prepared_bwd_reads_the_buffer_only(B, L):
     """Two backwards over one prepared buffer (autograd's retain_graph), the
     first with a grad that is only 4-byte aligned (the bias pass reads floats and
     still writes the grad tiles), the second aligned: both match the reference
     order, so the first left the buffer as the forward made it (K = 32 >= L / 20;
-    two position chunks at B = 40000, one at 3000)."""
+    two position chunks at B = 40000, one at 3000).  At L = 136 (K >= L / 5) the
+    buffer holds only the sort's radix pass and each backward sorts the buckets
+    into its own workspace."""
     announce(f"prepared bwd twice, unaligned then aligned grad B={B} L={L}")
     idx, W, b, G = case(31, B, 900, 32, L, 0, 32, True)
     assert _native.prep_buffer_bytes(B, 32, 900, L, _native.SFT_BWD_OVERWRITE, DEV) > 0
