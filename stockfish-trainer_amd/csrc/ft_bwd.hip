@@ -1031,8 +1031,19 @@ __global__ __launch_bounds__(kBlock) void bias_final_kernel(const T *__restrict_
   const int wave = uniform(threadIdx.x / kWave), lane = threadIdx.x % kWave;
   const int64_t c = (int64_t)blockIdx.x * kWavesPerBlock + wave;
   if (c >= cols) return;
+  // a lane's partials p = lane, lane + 64, ... in that order, 8 at a time, the
+  // 8 loaded first (from rows clamped into range) and then added (a pair of
+  // grads reduces 2 x 512 partials)
+  constexpr int kPer = 8;
   T s = T(0);
-  for (int p = lane; p < nparts; p += kWave) s += partial[(int64_t)p * cols + c];
+  for (int p0 = 0; p0 < nparts; p0 += kPer * kWave) {
+    T v[kPer];
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) v[i] = partial[(int64_t)min(p0 + lane + i * kWave, nparts - 1) * cols + c];
+#pragma unroll
+    for (int i = 0; i < kPer; ++i)
+      if (p0 + lane + i * kWave < nparts) s += v[i];
+  }
 #pragma unroll
   for (int m = 1; m < kWave; m <<= 1) s += shfl_xor_t(s, m);
   if (lane == 0) db[c] = overwrite ? s : db[c] + s;
