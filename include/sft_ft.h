@@ -136,6 +136,9 @@ int sft_ft_bwd_f32(const int32_t *idx, int64_t batch, int32_t max_active, const 
  * filled with the same indices, sizes and backward flags that the prepared
  * backward is called with; the backward only reads it, so it may be read by
  * more than one backward (a graph's backward run again with retain_graph).
+ * For rows narrow against their slot count (max_active >= output_size / 5)
+ * the forward runs only the sort's first (radix) pass into the buffer and the
+ * backward sorts the buckets beside its bias pass, into its workspace.
  * No reference counterpart: the reference sorts inside the backward
  * (FT/kernel.py:108-138), which this splits off its call
  * (FT/functions.py:12-48 forward, :50-72 backward).

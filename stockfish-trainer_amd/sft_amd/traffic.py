@@ -47,6 +47,7 @@ KINDS = [
     (r"\bfwd_i16_tiled_kernel\b", "fwd_i16_tiled_gather"),
     (r"\bfwd_i16_ranked_kernel\b", "fwd_i16_tiled_gather"),
     (r"\brank_lists_kernel\b", "fwd_rank_lists"),
+    (r"\brank_lists_wide_kernel<", "fwd_rank_lists"),
     (r"\bi16_relayout_kernel\b", "fwd_tile_relayout"),
     (r"\bfwd_i16_kernel<", "fwd_i16_gather"),
     (r"\bbwd_tiled_gather_kernel<", "bwd_tiled_gather"),
@@ -55,6 +56,8 @@ KINDS = [
     (r"\bbias_final_kernel<", "bwd_bias_final"),
     (r"\bseg_offsets_kernel\b", "bwd_segment_offsets"),
     (r"\bradix_", "bwd_feature_sort"),
+    (r"\bbucket_sort_kernel<", "bwd_feature_sort"),
+    (r"\bzero_kernel\b", "bwd_zero_fill"),
     (r"\bscatter_atomic_kernel<", "bwd_atomic_scatter"),
     (r"\bvirtual_reduce_kernel\b", "bwd_virtual_reduce"),
     (r"\bbwd_epilogue_kernel\b", "bwd_epilogue"),

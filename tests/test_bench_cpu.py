@@ -96,3 +96,27 @@ def test_step_bytes_against_a_brute_force_count(bench):
     assert bench.kernel_step_bytes("fwd_tile_relayout", w, pair) == 2 * 2 * 4 * N * L  # two calls, read + write
     assert bench.kernel_step_bytes("bwd_bias_partial", w, pair) == 2 * 4 * B * L  # the grad read per perspective
     assert bench.kernel_step_bytes("bwd_feature_sort", w, pair) is None  # no byte model: never priced
+
+
+def test_traffic_patterns_cover_the_traced_kernels():
+    """Every library kernel in the committed kernel traces of the five workloads
+    has a timing kind in sft_amd/traffic.py, so its counter bytes are attributed."""
+    import glob
+    import re
+    import sys
+
+    sys.path.insert(0, os.path.join(ROOT, "stockfish-trainer_amd"))
+    from sft_amd import traffic
+
+    names = set()
+    for w in ("halfka_b65536", "threats_b65536", "halfka_small_b65536", "halfka_b16384", "halfka_q16_b65536"):
+        for path in glob.glob(os.path.join(ROOT, "profiles", f"kernel_trace_{w}.md")):
+            for line in open(path):
+                m = re.match(r"\| `([^`]+)` \|", line)
+                if m:
+                    names.add(m.group(1))
+    assert names, "no traced kernels found"
+    library = [n for n in names if not n.startswith(("at::", "__amd", "l2_gather_probe"))]
+    assert library
+    missing = [n for n in library if traffic.kind_of(n) is None]
+    assert not missing, missing
