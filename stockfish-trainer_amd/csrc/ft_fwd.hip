@@ -940,6 +940,9 @@ __global__ __launch_bounds__(kBlock) void psqt_out_kernel(const f32x4 *__restric
 // 16-byte chunks and summed by the lanes that hold them (i16_relayout_kernel).
 // A tile is at most 64 MB, so row addresses are 32-bit offsets from the
 // tile's (wave-uniform) base.
+#ifndef SFT_I16_ROLL
+#define SFT_I16_ROLL 1
+#endif
 #ifndef SFT_I16_TILED_U
 #define SFT_I16_TILED_U 8
 #endif
@@ -987,6 +990,38 @@ __device__ __forceinline__ void i16_tile_rows(const int *mylist, int n, int nmin
     }
   };
   int k = 0;
+  if (SFT_I16_ROLL && !MIXED && nmin >= 2 * U) {
+    // A rolling window of U rows in flight over the rows every lane group of
+    // the wave has: each add frees the oldest row's registers, which take the
+    // row U places further at once.  The first U loads are issued in the order
+    // the loop consumes them, so each add waits for its own row only.  Same
+    // adds, same order (integer adds: any order gives the same sums anyway).
+    i16x8 w[U];
+#pragma unroll
+    for (int u = 0; u < U; u += 4) {
+      const i32x4 f4 = read4(mylist, u);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        w[u + e] = i16_row(tbase, lane_off, f4[e]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    for (k = U; k + U <= nmin; k += U) {
+      int fi[U];
+#pragma unroll
+      for (int u = 0; u < U; u += 4) {
+        const i32x4 f4 = read4(mylist, k + u);
+        fi[u] = f4[0], fi[u + 1] = f4[1], fi[u + 2] = f4[2], fi[u + 3] = f4[3];
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        add(w[u]);
+        w[u] = i16_row(tbase, lane_off, fi[u]);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) add(w[u]);
+  }
   for (; k + U <= nmin; k += U) {
     int fi[U];
 #pragma unroll
