@@ -851,6 +851,16 @@ __global__ __launch_bounds__(kBlock) void fwd_tiled_kernel(RankLists R0, RankLis
   int pos = rp[0];
 #pragma unroll
   for (int u = 1; u < PPW; ++u) pos = g == u ? rp[u] : pos;
+  f32x4 *__restrict__ raw = nullptr;
+  const int64_t pz = pos < 0 ? 0 : pos;
+  if (EPI) raw = (second ? epi.raw1 : epi.raw0) + (pz * ntiles + it.tile) * kTileCh + t;
+  else if (PARTS) raw = (second ? carry1 : carry0) + ((int64_t)it.tile * B + pz) * kTileCh + t;
+  // After the first pass, the sum earlier passes left, loaded first (every
+  // lane: padding ranks load position 0's) and used when a pass did store it
+  // (lo > 0 below).  Loaded before the run's bounds and entries instead of
+  // beside the first rows: a pass at Full_Threats 541 -> 526 us.
+  f32x4 carried = b4;
+  if (PARTS && part > 0) carried = EPI ? *raw : __builtin_nontemporal_load(raw);  // launch-uniform
   int nmax, lo = 0;
   bool work = true, final_pass = true;
   if (!PARTS) {  // whole lists
@@ -873,19 +883,28 @@ __global__ __launch_bounds__(kBlock) void fwd_tiled_kernel(RankLists R0, RankLis
     for (int off = kTileCh; off < kWave; off <<= 1) mx = max(mx, __shfl_xor(mx, off));
     nmax = uniform(mx);
     const i32x4 ro = R.roff[r];
-    const int32_t *__restrict__ src = R.list + (part == 0 ? ro[0] : (part == 1 ? ro[1] : (part == 2 ? ro[2] : ro[3])));
+    // The run, four entries per lane per round: the loads of a round issued
+    // first from indices clamped into the run (an empty run reads the list's
+    // first entry), then the pad row past its end.  (Guarded one-entry loads
+    // waited for each load in turn: a memory round trip per entry.)
+    const int32_t *__restrict__ src =
+        len > 0 ? R.list + (part == 0 ? ro[0] : (part == 1 ? ro[1] : (part == 2 ? ro[2] : ro[3]))) : R.list;
+    const int last = len > 0 ? len - 1 : 0;
     int *dst = list + g * kpad;
-    for (int j = t; j < round_up4(nmax); j += kTileCh) dst[j] = j < len ? src[j] : N;
+    const int n4 = round_up4(nmax);
+    for (int j0 = t; j0 < n4; j0 += 4 * kTileCh) {
+      int v[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) v[u] = src[min(j0 + u * kTileCh, last)];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int j = j0 + u * kTileCh;
+        if (j < n4) dst[j] = j < len ? v[u] : N;
+      }
+    }
   }
   wave_lds_barrier();
-  f32x4 start = b4;
-  f32x4 *__restrict__ raw = nullptr;
-  const int64_t pz = pos < 0 ? 0 : pos;
-  if (EPI) raw = (second ? epi.raw1 : epi.raw0) + (pz * ntiles + it.tile) * kTileCh + t;
-  else if (PARTS) raw = (second ? carry1 : carry0) + ((int64_t)it.tile * B + pz) * kTileCh + t;
-  if (PARTS && lo > 0 && pos >= 0 && work)  // the sum earlier passes left
-    start = EPI ? *raw : __builtin_nontemporal_load(raw);
-  f32x4 acc = f32_tile_rows(list + g * kpad, nmax, tbase, lane_off, start);
+  f32x4 acc = f32_tile_rows(list + g * kpad, nmax, tbase, lane_off, PARTS && lo > 0 && pos >= 0 && work ? carried : b4);
   if (!colok) acc = f32x4{0.f, 0.f, 0.f, 0.f};  // padding lanes read unwritten chunks; their raw rows stay 0
   if (pos < 0 || !work) return;                 // a padding rank, or nothing to do in this pass
   if (PARTS && !final_pass) {
