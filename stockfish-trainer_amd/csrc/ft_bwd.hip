@@ -449,9 +449,16 @@ constexpr int kBwdPosLds = SFT_BWD_POS_LDS;  // staged positions per workgroup
 // loads, padding lanes of the last tile included (a tile holds all TCH chunks
 // of each row; the caller does not store a padding lane's sum), so the loads
 // carry no execution masks.
-template <bool FROM_LDS, int TCH, typename P>
+//
+// The sum starts from *from when `use` (the sum an earlier position chunk
+// left), else from acc.  *from is loaded by every lane with the first rows,
+// in the same block of code (from must point at readable memory whatever
+// `use` is): a load whose value merges from a branch is waited for at the
+// merge, before the row loads are issued.
+template <bool FROM_LDS, int TCH, bool NT, typename P>
 __device__ __forceinline__ void bwd_tile_sum(const P *list, int n, int nmin, int nmax, int t,
-                                             const char *__restrict__ gtile, f32x4 &acc) {
+                                             const char *__restrict__ gtile, f32x4 &acc, const f32x4 *from,
+                                             bool use) {
   const uint32_t lane_off = (uint32_t)t * (uint32_t)sizeof(f32x4);
   auto row = [&](int b) {
     return *reinterpret_cast<const f32x4 *>(gtile + ((uint32_t)b * (uint32_t)(TCH * sizeof(f32x4)) + lane_off));
@@ -469,11 +476,18 @@ __device__ __forceinline__ void bwd_tile_sum(const P *list, int n, int nmin, int
     // Issued in the order the loop consumes them (no reordering across the
     // barriers), so the loads in flight at the loop head are in the same
     // order on both of its edges and each add waits for its own row only.
+    // (an opaque zero offset keeps this load here: the same load in both
+    // branches would be hoisted above them and waited for there)
+    int z = 0;
+    asm volatile("" : "+v"(z));
+    const f32x4 c = load_row<NT>(from + z);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       w[u] = row((int)list[u]);
       __builtin_amdgcn_sched_barrier(0);
     }
+    acc = use ? c : acc;
     for (k = U; k + U <= nmin; k += U) {
       int b[U];
 #pragma unroll
@@ -486,6 +500,9 @@ __device__ __forceinline__ void bwd_tile_sum(const P *list, int n, int nmin, int
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) acc += w[u];
+  } else {
+    const f32x4 c = load_row<NT>(from);
+    acc = use ? c : acc;
   }
   for (; k + U <= nmin; k += U) {
     int b[U];
@@ -706,18 +723,19 @@ __device__ __forceinline__ void tiled_feature_item(const TiledArgs &a, TileItem 
   const int colm = tile_col(map, it.tile, t);
   const bool colok = colm >= 0;
   const char *gtile = reinterpret_cast<const char *>(gt + (int64_t)it.tile * B * TCH);
-  // The sum the previous position chunk left: loaded by the lane itself here,
-  // just before its first row loads, so its latency overlaps theirs (staging
-  // it through LDS put it in front of the workgroup's barrier).  It is still
-  // the first operand of the adds.
+  // The sum the previous position chunk left, loaded by the lane itself with
+  // its first row loads so that its latency overlaps theirs (staging it
+  // through LDS put it in front of the workgroup's barrier); still the first
+  // operand of the adds.  Lanes without one load a grad line instead.
   f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
-  if (src_mode == kSrcTmp && live && !is_long && colok)
-    acc = load_row<NT>(tmp + tmp_row(it.tile, f, N) + t);  // stored with NT too
+  const bool cont = src_mode == kSrcTmp && live && !is_long && colok;
+  const f32x4 *from = src_mode == kSrcTmp ? tmp + tmp_row(it.tile, live ? f : fb, N) + t  // stored with NT too
+                                          : reinterpret_cast<const f32x4 *>(gtile) + t;
   if (staged)  // P16: offsets from the chunk's first grad row
-    bwd_tile_sum<true, TCH>(spos + (s0 - ra), n, nmin, nmax, t,
-                            P16 ? gtile + (size_t)chunk_base * (TCH * sizeof(f32x4)) : gtile, acc);
+    bwd_tile_sum<true, TCH, NT>(spos + (s0 - ra), n, nmin, nmax, t,
+                                P16 ? gtile + (size_t)chunk_base * (TCH * sizeof(f32x4)) : gtile, acc, from, cont);
   else
-    bwd_tile_sum<false, TCH>(sorted_pos + s0, n, nmin, nmax, t, gtile, acc);
+    bwd_tile_sum<false, TCH, NT>(sorted_pos + s0, n, nmin, nmax, t, gtile, acc, from, cont);
   if (!live || !colok || is_long) return;
   const int blk = block_of(f, dst.n, dst.start);
   f32x4 *d = pick(dst.p, blk) + (f - pick(dst.start, blk)) * cols4 + colm;
