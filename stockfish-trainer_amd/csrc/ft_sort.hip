@@ -153,6 +153,67 @@ __global__ __launch_bounds__(kBlock) void radix_scan_digits(unsigned *__restrict
   if (tid == kBlock - 1) totals[blockIdx.x] = part[tid];
 }
 
+// The same scan for up to kBlock * PER tiles: thread t holds the counts of
+// tiles t, t + 256, ... (coalesced, all loaded before any is used), a row of
+// 256 tiles is scanned with wave shuffles and one exchange of the wave totals,
+// and row j starts after the totals of rows 0 .. j-1.  (The loop above reads
+// each thread's run of counts one load after another and scans with 16
+// barriers: 16 us per call beside the bias pass at 1 024 tiles.)
+template <int PER>
+__global__ __launch_bounds__(kBlock) void radix_scan_digits_rows(unsigned *__restrict__ hist, int ntiles,
+                                                                 unsigned *__restrict__ totals,
+                                                                 int *__restrict__ clear, int nclear) {
+  __shared__ unsigned wsum[PER][kWavesPerBlock];
+  const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
+  if (blockIdx.x == 0)  // the caller's counters, zeroed here to save a launch
+    for (int i = tid; i < nclear; i += kBlock) clear[i] = 0;
+  unsigned *h = hist + (int64_t)blockIdx.x * ntiles;
+  unsigned v[PER], incl[PER];
+#pragma unroll
+  for (int j = 0; j < PER; ++j) v[j] = h[std::min(j * kBlock + tid, ntiles - 1)];
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    if (j * kBlock + tid >= ntiles) v[j] = 0u;
+    incl[j] = v[j];
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+      const unsigned o = __shfl_up(incl[j], off);
+      if (lane >= off) incl[j] += o;
+    }
+    if (lane == kWave - 1) wsum[j][wave] = incl[j];
+  }
+  __syncthreads();
+  unsigned rowbase = 0;
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    unsigned before = 0, row = 0;
+#pragma unroll
+    for (int w = 0; w < kWavesPerBlock; ++w) {
+      const unsigned x = wsum[j][w];
+      row += x;
+      before += w < wave ? x : 0u;
+    }
+    const int i = j * kBlock + tid;
+    if (i < ntiles) h[i] = rowbase + before + incl[j] - v[j];
+    rowbase += row;
+  }
+  if (tid == 0) totals[blockIdx.x] = rowbase;
+}
+
+// Exclusive scan of the per-tile counts of each of the nr digits, their totals.
+static void launch_scan_digits(int nr, unsigned *hist, int ntiles, unsigned *totals, int *clear, int nclear,
+                               hipStream_t s) {
+  const int per = (ntiles + kBlock - 1) / kBlock;
+#define SFT_SCAN_ROWS(P) \
+  hipLaunchKernelGGL(radix_scan_digits_rows<P>, dim3(nr), dim3(kBlock), 0, s, hist, ntiles, totals, clear, nclear)
+  if (per <= 2) SFT_SCAN_ROWS(2);
+  else if (per <= 4) SFT_SCAN_ROWS(4);
+  else if (per <= 8) SFT_SCAN_ROWS(8);
+  else if (per <= 16) SFT_SCAN_ROWS(16);
+  else hipLaunchKernelGGL(radix_scan_digits, dim3(nr), dim3(kBlock), 0, s, hist, ntiles, totals, clear, nclear);
+#undef SFT_SCAN_ROWS
+}
+
 // Exclusive scan of R per-digit values by one wave (R / 64 digits per lane).
 template <int R>
 __device__ __forceinline__ void wave_scan_digits(const unsigned *in, unsigned *out, int lane) {
@@ -303,8 +364,7 @@ int run_passes(const SlotKey &sk, int64_t M, int passes, unsigned *kbuf[2], int 
     else
       hipLaunchKernelGGL((radix_upsweep<RB, false, IT>), dim3(ntiles), dim3(kBlock), 0, s, sk, kin, M, totals, ntiles,
                          shift, hist);
-    hipLaunchKernelGGL(radix_scan_digits, dim3(1 << RB), dim3(kBlock), 0, s, hist, ntiles, totals, clear,
-                       p == 0 ? nclear : 0);
+    launch_scan_digits(1 << RB, hist, ntiles, totals, clear, p == 0 ? nclear : 0, s);
     if (p == 0)
       hipLaunchKernelGGL((radix_downsweep<RB, true, IT>), dim3(ntiles), dim3(kBlock), 0, s, sk, kin, vin, kout, vout,
                          hist, totals, M, ntiles, shift);
@@ -503,7 +563,7 @@ int run_high_pass(const SlotKey &sk, int64_t M, int shift, unsigned *kout, int *
                   unsigned *totals, int ntiles, int *clear, int nclear, hipStream_t s) {
   hipLaunchKernelGGL((radix_upsweep<RB, true, IT>), dim3(ntiles), dim3(kBlock), 0, s, sk, nullptr, M, totals, ntiles,
                      shift, hist);
-  hipLaunchKernelGGL(radix_scan_digits, dim3(1 << RB), dim3(kBlock), 0, s, hist, ntiles, totals, clear, nclear);
+  launch_scan_digits(1 << RB, hist, ntiles, totals, clear, nclear, s);
   hipLaunchKernelGGL((radix_downsweep<RB, true, IT>), dim3(ntiles), dim3(kBlock), 0, s, sk, nullptr, nullptr, kout,
                      vout, hist, totals, M, ntiles, shift);
   return check_launch("slot bucket sort (first pass)");
