@@ -585,6 +585,45 @@ __host__ __device__ inline GatherLds gather_lds(int dst_mode) {
   return l;
 }
 
+template <typename T>
+__device__ __forceinline__ T shfl_xor_t(T v, int m);
+template <>
+__device__ __forceinline__ float shfl_xor_t<float>(float v, int m) {
+  return __shfl_xor(v, m);
+}
+template <>
+__device__ __forceinline__ f32x4 shfl_xor_t<f32x4>(f32x4 v, int m) {
+  return f32x4{__shfl_xor(v.x, m), __shfl_xor(v.y, m), __shfl_xor(v.z, m), __shfl_xor(v.w, m)};
+}
+
+// db[c] (+)= sum over parts of partial[p, c].  One wave per column chunk: lane
+// l sums parts l, l+64, ..., then a fixed xor-shuffle tree.  Deterministic.
+template <typename T>
+__device__ __forceinline__ void bias_final_block(int64_t block, const T *__restrict__ partial, int nparts,
+                                                 int64_t cols, T *__restrict__ db, int overwrite) {
+  const int wave = uniform(threadIdx.x / kWave), lane = threadIdx.x % kWave;
+  const int64_t c = block * kWavesPerBlock + wave;
+  if (c >= cols) return;
+  // a lane's partials p = lane, lane + 64, ... in that order, 8 at a time, the
+  // 8 loaded first (from rows clamped into range) and then added (a pair of
+  // grads reduces 2 x 512 partials)
+  constexpr int kPer = 8;
+  T s = T(0);
+  for (int p0 = 0; p0 < nparts; p0 += kPer * kWave) {
+    T v[kPer];
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) v[i] = partial[(int64_t)min(p0 + lane + i * kWave, nparts - 1) * cols + c];
+#pragma unroll
+    for (int i = 0; i < kPer; ++i)
+      if (p0 + lane + i * kWave < nparts) s += v[i];
+  }
+#pragma unroll
+  for (int m = 1; m < kWave; m <<= 1) s += shfl_xor_t(s, m);
+  if (lane == 0) db[c] = overwrite ? s : db[c] + s;
+}
+// Workgroups of the bias reduction over cols columns (one wave per column).
+int64_t bias_final_blocks(int64_t cols) { return ceil_div(cols, (int64_t)kWavesPerBlock); }
+
 // The arguments of one tiled gather launch.
 struct TiledArgs {
   const int32_t *seg, *sorted_pos;
@@ -600,6 +639,13 @@ struct TiledArgs {
   const int32_t *long_list;
   const int *long_count;
   int nlong;
+  // workgroups from gblocks on reduce the bias partials instead (bias_final_block)
+  int64_t gblocks;
+  const f32x4 *bpart;
+  int bparts;
+  int64_t bcols;
+  f32x4 *db;
+  int boverwrite;
 };
 
 // Long-segment slot it.chunk of tile it.tile (whole workgroup).
@@ -749,11 +795,17 @@ __device__ __forceinline__ void tiled_feature_item(const TiledArgs &a, TileItem 
 }
 
 // One item per workgroup: workgroup i serves item i / 8 of XCD i % 8 (the
-// long-segment slots first, then the feature blocks).
+// long-segment slots first, then the feature blocks); workgroups after the
+// items, when the launch carries them, reduce the bias partials (the bias
+// pass's second step, which then needs no launch of its own).
 template <bool NT, bool P16>
 __global__ __launch_bounds__(kBlock) void bwd_tiled_gather_kernel(TiledArgs a) {
   extern __shared__ __align__(16) char gsm[];
   __shared__ int s_seg[kBwdFeat + 1], s_perm[kBwdFeat];
+  if ((int64_t)blockIdx.x >= a.gblocks) {  // whole block: uniform
+    bias_final_block<f32x4>((int64_t)blockIdx.x - a.gblocks, a.bpart, a.bparts, a.bcols, a.db, a.boverwrite);
+    return;
+  }
   const int64_t nl_items = tile_sched_items_per_xcd(a.ntiles, a.nlong) * kXcds;
   const bool long_item = (int64_t)blockIdx.x < nl_items;  // whole block: uniform
   const TileItem it = long_item ? tile_sched_item(blockIdx.x, a.ntiles, a.nlong)
@@ -769,18 +821,29 @@ __global__ __launch_bounds__(kBlock) void bwd_tiled_gather_kernel(TiledArgs a) {
 // One position chunk's tiled weight-grad gather.
 // pos16: the slots' 16-bit chunk offsets (null when a chunk has more than
 // 65536 positions), chunk_base the first position of this launch's chunk.
+// The bias reduction a tiled gather launch may carry: db (+)= the sum of
+// nparts partial rows of cols 16-byte chunks.
+struct BiasFinal {
+  const f32x4 *partial;
+  int nparts;
+  int64_t cols;
+  f32x4 *db;
+  int overwrite;
+};
 int launch_tiled_gather(bool nt, const int32_t *seg, const int32_t *pos, const uint16_t *pos16, int64_t chunk_base,
                         int64_t N, const f32x4 *gt, int64_t B, const ColMap &map, const RowDst &dst, f32x4 *tmp,
                         int src_mode, int dst_mode, int ntiles, int ngroups, const int32_t *long_list,
-                        const int *long_count, int nlong, hipStream_t s) {
+                        const int *long_count, int nlong, hipStream_t s, const BiasFinal *bias = nullptr) {
   const int64_t items = tile_sched_items_per_xcd(ntiles, nlong) + tile_sched_items_per_xcd(ntiles, ngroups);
   const size_t lds = (size_t)gather_lds(dst_mode).bytes;
   if ((uintptr_t)pos % 16 != 0 || (uintptr_t)pos16 % 16 != 0)  // 256-byte / 16-byte aligned workspace regions
     return fail(SFT_EINVAL, "tiled feature gather: sorted positions not 16-byte aligned");
+  const int64_t gblocks = items * kXcds;
   const TiledArgs a{seg, pos, pos16, (int)chunk_base, N, gt, B, map, dst, tmp, src_mode, dst_mode, ntiles, ngroups,
-                    long_list, long_count, nlong};
+                    long_list, long_count, nlong, gblocks, bias ? bias->partial : nullptr, bias ? bias->nparts : 0,
+                    bias ? bias->cols : 0, bias ? bias->db : nullptr, bias ? bias->overwrite : 0};
   const bool p16 = pos16 != nullptr;
-  const dim3 grid((unsigned)(items * kXcds));
+  const dim3 grid((unsigned)(gblocks + (bias ? bias_final_blocks(bias->cols) : 0)));
   hipLaunchKernelGGL((nt ? (p16 ? bwd_tiled_gather_kernel<true, true> : bwd_tiled_gather_kernel<true, false>)
                          : (p16 ? bwd_tiled_gather_kernel<false, true> : bwd_tiled_gather_kernel<false, false>)),
                      grid, dim3(kBlock), lds, s, a);
@@ -1031,40 +1094,9 @@ __global__ __launch_bounds__(kBlock) void bias_partial_kernel(const T *__restric
 }
 
 template <typename T>
-__device__ __forceinline__ T shfl_xor_t(T v, int m);
-template <>
-__device__ __forceinline__ float shfl_xor_t<float>(float v, int m) {
-  return __shfl_xor(v, m);
-}
-template <>
-__device__ __forceinline__ f32x4 shfl_xor_t<f32x4>(f32x4 v, int m) {
-  return f32x4{__shfl_xor(v.x, m), __shfl_xor(v.y, m), __shfl_xor(v.z, m), __shfl_xor(v.w, m)};
-}
-
-// db[c] (+)= sum over parts of partial[p, c].  One wave per column chunk: lane
-// l sums parts l, l+64, ..., then a fixed xor-shuffle tree.  Deterministic.
-template <typename T>
 __global__ __launch_bounds__(kBlock) void bias_final_kernel(const T *__restrict__ partial, int nparts, int64_t cols,
                                                             T *__restrict__ db, int overwrite) {
-  const int wave = uniform(threadIdx.x / kWave), lane = threadIdx.x % kWave;
-  const int64_t c = (int64_t)blockIdx.x * kWavesPerBlock + wave;
-  if (c >= cols) return;
-  // a lane's partials p = lane, lane + 64, ... in that order, 8 at a time, the
-  // 8 loaded first (from rows clamped into range) and then added (a pair of
-  // grads reduces 2 x 512 partials)
-  constexpr int kPer = 8;
-  T s = T(0);
-  for (int p0 = 0; p0 < nparts; p0 += kPer * kWave) {
-    T v[kPer];
-#pragma unroll
-    for (int i = 0; i < kPer; ++i) v[i] = partial[(int64_t)min(p0 + lane + i * kWave, nparts - 1) * cols + c];
-#pragma unroll
-    for (int i = 0; i < kPer; ++i)
-      if (p0 + lane + i * kWave < nparts) s += v[i];
-  }
-#pragma unroll
-  for (int m = 1; m < kWave; m <<= 1) s += shfl_xor_t(s, m);
-  if (lane == 0) db[c] = overwrite ? s : db[c] + s;
+  bias_final_block<T>(blockIdx.x, partial, nparts, cols, db, overwrite);
 }
 
 template <typename T, int G, int CPL>
@@ -1247,6 +1279,11 @@ bool prep_pays(int64_t B, int K, int L, uint32_t flags) {
 #ifndef SFT_BWD_SPLIT_K_PER_L
 #define SFT_BWD_SPLIT_K_PER_L 5
 #endif
+// The bias reduction in the first tiled gather launch instead of a launch of
+// its own.
+#ifndef SFT_BWD_FUSE_BIAS_FINAL
+#define SFT_BWD_FUSE_BIAS_FINAL 1
+#endif
 bool prep_split(int64_t B, int K, int64_t N, int L, uint32_t flags) {
   return prep_pays(B, K, L, flags) && (int64_t)K * SFT_BWD_SPLIT_K_PER_L >= L &&
          slot_sort_buckets_supported(N, sort_chunks(B, L, flags));
@@ -1389,12 +1426,15 @@ int bwd_f32(const int32_t *idx, int64_t B, int K, const float *grad, int64_t N, 
   const SegBufs sb = seg_bufs(seg, nc, N);
 
   // ---- bias grad ----
+  const bool fuse_bias_final = tiled && M > 0 && (L % 4 == 0) && ((uintptr_t)grad % 16 == 0) && ((uintptr_t)db % 16 == 0);
   {
     const bool vec = (L % 4 == 0) && ((uintptr_t)grad % 16 == 0) && ((uintptr_t)db % 16 == 0);
     if ((rc = launch_bias_partial(grad, B, L, lay.nparts, reinterpret_cast<float *>(w + lay.partial), gt, vec, s,
                                   kBwdTileCh)) != SFT_OK)
       return rc;
-    if ((rc = launch_bias_final(reinterpret_cast<const float *>(w + lay.partial), lay.nparts, L, db, overwrite, vec,
+    // with the tiled gather, its first launch reduces the partials too
+    if (!(fuse_bias_final && SFT_BWD_FUSE_BIAS_FINAL) &&
+        (rc = launch_bias_final(reinterpret_cast<const float *>(w + lay.partial), lay.nparts, L, db, overwrite, vec,
                                 s)) != SFT_OK)
       return rc;
   }
@@ -1452,13 +1492,16 @@ int bwd_f32(const int32_t *idx, int64_t B, int K, const float *grad, int64_t N, 
     dst.start[1] = N;
     dst.p[0] = reinterpret_cast<f32x4 *>(dW);
     f32x4 *tmp = reinterpret_cast<f32x4 *>(w + lay.tmp);
+    const BiasFinal bf{reinterpret_cast<const f32x4 *>(w + lay.partial), lay.nparts, cols4,
+                       reinterpret_cast<f32x4 *>(db), overwrite};
     for (int h = 0; h < nc; ++h) {
       ProfScope prof(kProfBwdTiled, s);
       const bool nt = (nc > 1 ? half_rows(B) : B) * kBwdTileCh * 16 >= kNtStoreTileBytes;
       const int64_t crow = nc > 1 ? half_rows(B) : B;
       rc = launch_tiled_gather(nt, seg + (int64_t)h * N, pos, crow <= 65536 ? sb.pos16 : nullptr, h * crow, N, gt, B,
                                map, dst, tmp, h == 0 ? kSrcZero : kSrcTmp, h == nc - 1 ? kDstOut : kDstTmp, ntiles,
-                               ngroups, sb.list + h * N, sb.count + h, kLongSlots, s);
+                               ngroups, sb.list + h * N, sb.count + h, kLongSlots, s,
+                               h == 0 && fuse_bias_final && SFT_BWD_FUSE_BIAS_FINAL ? &bf : nullptr);
       if (rc != SFT_OK) return rc;
     }
     return SFT_OK;
@@ -1548,7 +1591,8 @@ static int pair_sort_perspective(const int32_t *idx, int64_t B, int K, int64_t N
 // carried between chunks in tmp: perspective 0's last launch stores its sums to
 // dst, perspective 1's adds them to dst.
 static int pair_gather_perspective(int p, const SortedSlots &ss, int64_t B, int64_t N, const ColMap &map,
-                                   const f32x4 *gt, const RowDst &dst, f32x4 *tmp, int nc, hipStream_t s) {
+                                   const f32x4 *gt, const RowDst &dst, f32x4 *tmp, int nc, hipStream_t s,
+                                   const BiasFinal *bias = nullptr) {  // reduced by the first launch
   const int ntiles = map_tiles(map);
   const int ngroups = (int)ceil_div(N, bwd_feat_per_block());
   for (int h = 0; h < nc; ++h) {
@@ -1560,7 +1604,8 @@ static int pair_gather_perspective(int p, const SortedSlots &ss, int64_t B, int6
     const int64_t crow = nc > 1 ? half_rows(B) : B;
     const int rc = launch_tiled_gather(nt, ss.sb.seg + (int64_t)h * N, ss.pos, crow <= 65536 ? ss.sb.pos16 : nullptr,
                                        h * crow, N, gt, B, map, dst, tmp, src_mode,
-                                       dst_mode, ntiles, ngroups, ss.sb.list + h * N, ss.sb.count + h, kLongSlots, s);
+                                       dst_mode, ntiles, ngroups, ss.sb.list + h * N, ss.sb.count + h, kLongSlots, s,
+                                       h == 0 ? bias : nullptr);
     if (rc != SFT_OK) return rc;
   }
   return SFT_OK;
@@ -1623,16 +1668,22 @@ int bwd_pair_f32(const int32_t *idx0, const int32_t *idx1, int64_t B, int K, con
   // passes first, beside both sorts, took 133 against 107 us each (composed
   // HalfKAv2_hm^ step 1.752 -> 1.740 ms, Full_Threats+HalfKAv2_hm^ 6.988 ->
   // 6.951 ms).
+  // the bias reduction over both perspectives' partials rides in perspective
+  // 1's first gather launch
+  const BiasFinal bf{reinterpret_cast<const f32x4 *>(partial), 2 * lay.nparts, L / 4, reinterpret_cast<f32x4 *>(db), 1};
   for (int p = 0; p < 2; ++p) {
     const float *grad = p == 0 ? grad0 : grad1;
     if ((rc = launch_bias_partial(grad, B, L, lay.nparts, partial + (size_t)p * lay.nparts * L, gt, true, s)) !=
         SFT_OK)
       return rc;
     if ((rc = wait_side(s, p)) != SFT_OK) return rc;
-    if ((rc = pair_gather_perspective(p, ss[p], B, N, map, gt, dst, tmp, lay.nc, s)) != SFT_OK) return rc;
+    if ((rc = pair_gather_perspective(p, ss[p], B, N, map, gt, dst, tmp, lay.nc, s,
+                                      p == 1 && SFT_BWD_FUSE_BIAS_FINAL ? &bf : nullptr)) != SFT_OK)
+      return rc;
   }
   side_join.release();
-  if ((rc = launch_bias_final(partial, 2 * lay.nparts, L, db, 1, true, s)) != SFT_OK) return rc;
+  if (!SFT_BWD_FUSE_BIAS_FINAL && (rc = launch_bias_final(partial, 2 * lay.nparts, L, db, 1, true, s)) != SFT_OK)
+    return rc;
   return virtual_reduce(vgrad_src, vgrad, vperiod, vreps, nvirt, L / 4, s);
 }
 
@@ -1710,13 +1761,18 @@ int bwd_transform_f32(const int32_t *idx0, const int32_t *idx1, int64_t B, int K
                        map_tiles(map));
     if ((rc = check_launch("epilogue backward")) != SFT_OK) return rc;
   }
-  if ((rc = launch_bias_final(reinterpret_cast<const float *>(w + lay.partial), lay.nparts, L, db, 1, true, s)) !=
-      SFT_OK)
+  // the bias reduction rides in perspective 0's first gather launch
+  const BiasFinal bf{reinterpret_cast<const f32x4 *>(w + lay.partial), lay.nparts, L / 4,
+                     reinterpret_cast<f32x4 *>(db), 1};
+  if (!SFT_BWD_FUSE_BIAS_FINAL &&
+      (rc = launch_bias_final(reinterpret_cast<const float *>(w + lay.partial), lay.nparts, L, db, 1, true, s)) !=
+          SFT_OK)
     return rc;
   f32x4 *tmp = reinterpret_cast<f32x4 *>(w + lay.tmp);
   for (int p = 0; p < 2; ++p) {
     if ((rc = wait_side(s, p)) != SFT_OK) return rc;
-    if ((rc = pair_gather_perspective(p, ss[p], B, N, map, p == 0 ? gt0 : gt1, dst, tmp, lay.nc, s)) != SFT_OK)
+    if ((rc = pair_gather_perspective(p, ss[p], B, N, map, p == 0 ? gt0 : gt1, dst, tmp, lay.nc, s,
+                                      p == 0 && SFT_BWD_FUSE_BIAS_FINAL ? &bf : nullptr)) != SFT_OK)
       return rc;
   }
   side_join.release();
