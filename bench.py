@@ -1018,11 +1018,27 @@ def main() -> int:
             log(f"[bench] {w.name} Zipf alpha {alpha}: {entry['ms_per_step']:.3f} ms/step")
             torch.cuda.empty_cache()
         result["skewed"] = skewed
+        # The headline batch and width with index rows the GPU encoder makes
+        # from random positions (HalfKAv2_hm: one king bucket's rows per
+        # perspective, fewer active features than the uniform U[16, 32] rows)
+        # over the encoder's 24 576-row table.
+        entry, sd = run_fp32(args, w, dev, encoded=True, graph=args.graph)
+        del sd
+        result["encoded"] = {"indices": "HalfKAv2_hm rows of the GPU encoder over random positions "
+                                        "(sft_amd.positions.random_positions, seed 1)",
+                             "num_inputs": entry["num_inputs"],
+                             "active_mean": entry["active_mean"], "ms_per_step": entry["ms_per_step"],
+                             "positions_per_s": entry["positions_per_s"],
+                             "fwd_f32_tiled_gather_avg_ms":
+                                 entry["kernels"].get("fwd_f32_tiled_gather", {}).get("avg_ms"),
+                             "bwd_tiled_gather_avg_ms": entry["kernels"].get("bwd_tiled_gather", {}).get("avg_ms")}
+        log(f"[bench] {w.name} encoder rows ({entry['active_mean']:.1f} active): {entry['ms_per_step']:.3f} ms/step")
+        torch.cuda.empty_cache()
     print(json.dumps(result), flush=True)
     return 0
 
 
-def run_fp32(args, w, dev, zipf=None, traffic=None, l2_attainable=None, graph=True, hashes=False):
+def run_fp32(args, w, dev, zipf=None, traffic=None, l2_attainable=None, graph=True, hashes=False, encoded=False):
     """Times the fp32 step of one workload (both perspectives through
     SparseLinearFunction, fwd + bwd); returns its measurements and the inputs."""
     import torch
@@ -1031,6 +1047,12 @@ def run_fp32(args, w, dev, zipf=None, traffic=None, l2_attainable=None, graph=Tr
     from src.model.modules.feature_transformer import SparseLinearFunction
     from src.model.modules.feature_transformer import kernel as ftk
 
+    if encoded:  # the encoder's HalfKAv2_hm rows index a table of HalfKav2Hm.NUM_INPUTS rows
+        import dataclasses
+
+        from src.model.modules.features.halfka_v2_hm import HalfKav2Hm
+
+        w = dataclasses.replace(w, name=w.name + "_encoded", feature_set="HalfKAv2_hm", N=HalfKav2Hm.NUM_INPUTS)
     log(f"[bench] generating {w.name}: B={w.B} N={w.N} K={w.K} active U[{w.lo},{w.hi}] L={w.L}")
     d = workloads.make_fp32_inputs(w)
     if zipf is not None:
@@ -1039,6 +1061,15 @@ def run_fp32(args, w, dev, zipf=None, traffic=None, l2_attainable=None, graph=Tr
                                                  zipf)
         d["idx_b"] = workloads.make_zipf_indices(workloads.rng(w.wid, workloads.S_BLACK), w.B, w.N, w.K, w.lo, w.hi,
                                                  zipf)
+    if encoded:
+        from sft_amd import encode, positions
+
+        log(f"[bench] index rows from the GPU encoder over {w.B} random positions")
+        boards, stm = positions.random_positions(w.B, seed=1)
+        enc = encode.encode_batch(torch.from_numpy(boards).to(dev), torch.from_numpy(stm).to(dev), "HalfKAv2_hm")
+        d["idx_w"] = enc["white"].cpu().numpy()
+        d["idx_b"] = enc["black"].cpu().numpy()
+        del enc
     iw = torch.from_numpy(d["idx_w"]).to(dev)
     ib = torch.from_numpy(d["idx_b"]).to(dev)
     W = torch.from_numpy(d["W"]).to(dev).requires_grad_(True)
@@ -1138,6 +1169,7 @@ def run_fp32(args, w, dev, zipf=None, traffic=None, l2_attainable=None, graph=Tr
         out["traffic_source"] = traffic["source"]
     if hashes:
         out["input_sha256"] = {k: workloads.sha256(v) for k, v in d.items()}
+    out["active_mean"] = float(((d["idx_w"] >= 0).sum() + (d["idx_b"] >= 0).sum()) / (2 * w.B))
     return out, d
 
 

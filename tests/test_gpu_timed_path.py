@@ -9,7 +9,8 @@ the summed weight grad bit-exact with the two reference-order weight grads
 binary64 (FT/kernel.py:269).  Then the fused ComposedFeatureTransformer
 (FEAT/composed.py:49-54) at B = 65 536 for both feature sets against the
 composed oracle: outputs and block weight grads bit-exact, virtual and bias
-grads within 1e-5 of binary64."""
+grads within 1e-5 of binary64.  And the headline step over the index rows the
+GPU encoder makes from random positions (bench.py's encoder-rows leg)."""
 
 import numpy as np
 import pytest
@@ -45,6 +46,44 @@ def test_sparse_linear_step_full_workload(wid):
     rb, _ = ft_oracle.bwd_f32(d["idx_b"], d["g_b"], w.N)
     assert np.array_equal(host(W.grad), rw + rb)  # autograd adds the two dense grads in binary32
     db64 = d["g_w"].astype(np.float64).sum(0) + d["g_b"].astype(np.float64).sum(0)
+    assert rel_err(host(b.grad), db64) <= 1e-5
+
+
+def test_sparse_linear_step_encoder_rows():
+    """bench.py's encoder-rows leg: the headline batch and width (B = 65 536,
+    L = 1048) with the HalfKAv2_hm rows the GPU encoder makes from random
+    positions (one king bucket's rows per perspective, 2-32 active, -1 after
+    them) over the encoder's 24 576-row table, through the same step."""
+    import dataclasses
+
+    from sft_amd import encode, positions
+    from src.model.modules.features.halfka_v2_hm import HalfKav2Hm
+
+    w = dataclasses.replace(workloads.WORKLOADS[1], N=HalfKav2Hm.NUM_INPUTS)
+    announce(f"timed step {w.name} with encoder rows B={w.B} N={w.N} L={w.L}")
+    boards, stm = positions.random_positions(w.B, seed=1)
+    enc = encode.encode_batch(torch.from_numpy(boards).to(DEV), torch.from_numpy(stm).to(DEV), "HalfKAv2_hm")
+    iw, ib = enc["white"], enc["black"]
+    niw, nib = host(iw), host(ib)
+    assert niw.shape == (w.B, 32) and niw.max() < w.N and (niw >= 0).sum(1).min() >= 2
+    g = np.random.default_rng(7)
+    Wn = (g.standard_normal((w.N, w.L), dtype=np.float32) * 0.01).astype(np.float32)
+    bn = g.standard_normal(w.L, dtype=np.float32)
+    gw = g.standard_normal((w.B, w.L), dtype=np.float32)
+    gb = g.standard_normal((w.B, w.L), dtype=np.float32)
+    W = dev(Wn).requires_grad_(True)
+    b = dev(bn).requires_grad_(True)
+    ow = SparseLinearFunction.apply(iw, W, b)
+    ob = SparseLinearFunction.apply(ib, W, b)
+    torch.autograd.backward([ow, ob], [dev(gw), dev(gb)])
+    torch.cuda.synchronize()
+    assert np.array_equal(host(ow), ft_oracle.fwd_f32(niw, Wn, bn))
+    assert np.array_equal(host(ob), ft_oracle.fwd_f32(nib, Wn, bn))
+    del ow, ob
+    rw, _ = ft_oracle.bwd_f32(niw, gw, w.N)
+    rb, _ = ft_oracle.bwd_f32(nib, gb, w.N)
+    assert np.array_equal(host(W.grad), rw + rb)
+    db64 = gw.astype(np.float64).sum(0) + gb.astype(np.float64).sum(0)
     assert rel_err(host(b.grad), db64) <= 1e-5
 
 
