@@ -49,25 +49,35 @@ def test_sparse_linear_step_full_workload(wid):
     assert rel_err(host(b.grad), db64) <= 1e-5
 
 
-def test_sparse_linear_step_encoder_rows():
-    """bench.py's encoder-rows leg: the headline batch and width (B = 65 536,
-    L = 1048) with the HalfKAv2_hm rows the GPU encoder makes from random
-    positions (one king bucket's rows per perspective, 2-32 active, -1 after
-    them) over the encoder's 24 576-row table, through the same step."""
+@pytest.mark.parametrize("feature_set", ["HalfKAv2_hm", "Full_Threats+HalfKAv2_hm"])
+def test_sparse_linear_step_encoder_rows(feature_set):
+    """The step over the index rows the GPU encoder makes from random positions
+    at B = 65 536, L = 1048: for HalfKAv2_hm bench.py's encoder-rows leg (one
+    king bucket's rows per perspective, 2-32 active, -1 after them, over the
+    encoder's 24 576-row table); for Full_Threats+HalfKAv2_hm the table-part
+    forward and the sort under the forward over rows whose threats come by
+    colour and piece, not by index (a fifth of them go back to an earlier
+    table part)."""
     import dataclasses
 
     from sft_amd import encode, positions
+    from src.model.modules.features.full_threats import FullThreats
     from src.model.modules.features.halfka_v2_hm import HalfKav2Hm
 
-    w = dataclasses.replace(workloads.WORKLOADS[1], N=HalfKav2Hm.NUM_INPUTS)
-    announce(f"timed step {w.name} with encoder rows B={w.B} N={w.N} L={w.L}")
+    threats = feature_set.startswith("Full_Threats")
+    N = HalfKav2Hm.NUM_INPUTS + (FullThreats.NUM_INPUTS if threats else 0)
+    w = dataclasses.replace(workloads.WORKLOADS[2 if threats else 1], N=N)
     boards, stm = positions.random_positions(w.B, seed=1)
-    enc = encode.encode_batch(torch.from_numpy(boards).to(DEV), torch.from_numpy(stm).to(DEV), "HalfKAv2_hm")
+    enc = encode.encode_batch(torch.from_numpy(boards).to(DEV), torch.from_numpy(stm).to(DEV), feature_set)
     iw, ib = enc["white"], enc["black"]
     niw, nib = host(iw), host(ib)
-    assert niw.shape == (w.B, 32) and niw.max() < w.N and (niw >= 0).sum(1).min() >= 2
+    K = niw.shape[1]
+    prepared = _native.prep_buffer_bytes(w.B, K, N, w.L, _native.SFT_BWD_OVERWRITE, DEV) > 0
+    announce(f"timed step {feature_set} encoder rows B={w.B} N={N} K={K} L={w.L} sort under the forward={prepared}")
+    assert niw.max() < N and (niw >= 0).sum(1).min() >= 2
+    assert prepared == threats
     g = np.random.default_rng(7)
-    Wn = (g.standard_normal((w.N, w.L), dtype=np.float32) * 0.01).astype(np.float32)
+    Wn = (g.standard_normal((N, w.L), dtype=np.float32) * 0.01).astype(np.float32)
     bn = g.standard_normal(w.L, dtype=np.float32)
     gw = g.standard_normal((w.B, w.L), dtype=np.float32)
     gb = g.standard_normal((w.B, w.L), dtype=np.float32)
@@ -80,8 +90,8 @@ def test_sparse_linear_step_encoder_rows():
     assert np.array_equal(host(ow), ft_oracle.fwd_f32(niw, Wn, bn))
     assert np.array_equal(host(ob), ft_oracle.fwd_f32(nib, Wn, bn))
     del ow, ob
-    rw, _ = ft_oracle.bwd_f32(niw, gw, w.N)
-    rb, _ = ft_oracle.bwd_f32(nib, gb, w.N)
+    rw, _ = ft_oracle.bwd_f32(niw, gw, N)
+    rb, _ = ft_oracle.bwd_f32(nib, gb, N)
     assert np.array_equal(host(W.grad), rw + rb)
     db64 = gw.astype(np.float64).sum(0) + gb.astype(np.float64).sum(0)
     assert rel_err(host(b.grad), db64) <= 1e-5
