@@ -1018,6 +1018,23 @@ def main() -> int:
             log(f"[bench] {w.name} Zipf alpha {alpha}: {entry['ms_per_step']:.3f} ms/step")
             torch.cuda.empty_cache()
         result["skewed"] = skewed
+        # The headline with the reference's own HalfKAv2_hm^ table height
+        # (24 576 rows, FEAT/halfka_v2_hm.py:50) instead of 23 232, uniform rows.
+        import dataclasses
+
+        from src.model.modules.features.halfka_v2_hm import HalfKav2Hm
+
+        wn = dataclasses.replace(w, name=w.name + "_n24576", N=HalfKav2Hm.NUM_INPUTS)
+        entry, sd = run_fp32(args, wn, dev, graph=args.graph)
+        del sd
+        result["sensitivity"] = [{"num_inputs": wn.N, "ms_per_step": entry["ms_per_step"],
+                                  "positions_per_s": entry["positions_per_s"],
+                                  "fwd_f32_tiled_gather_avg_ms":
+                                      entry["kernels"].get("fwd_f32_tiled_gather", {}).get("avg_ms"),
+                                  "bwd_tiled_gather_avg_ms":
+                                      entry["kernels"].get("bwd_tiled_gather", {}).get("avg_ms")}]
+        log(f"[bench] {wn.name}: {entry['ms_per_step']:.3f} ms/step")
+        torch.cuda.empty_cache()
         # The headline batch and width with index rows the GPU encoder makes
         # from random positions (HalfKAv2_hm: one king bucket's rows per
         # perspective, fewer active features than the uniform U[16, 32] rows)
