@@ -143,3 +143,28 @@ def test_device_quantizer_matches_oracle():
     x = (g.standard_normal((1000, 1040)) * 0.02).astype(np.float32)
     for scale in (127.0, 255.0):
         assert np.array_equal(host(quantize_weight_i16(dev(x), scale)), ft_oracle.quantize_i16(x, scale))
+
+
+def test_q16_module_encoder_rows():
+    """The int16 forward of both perspectives through QuantizedFeatureTransformer
+    (the packed table) over the HalfKAv2_hm rows the GPU encoder makes from
+    random positions (one king bucket's rows per perspective, 2-32 active, -1
+    after them), at B = 65 536 over the encoder's 24 576-row table: bit-exact
+    with the oracle."""
+    from sft_amd import encode, positions
+    from src.model.modules.features.halfka_v2_hm import HalfKav2Hm
+
+    B, N, L, P = 65536, HalfKav2Hm.NUM_INPUTS, 1040, 8
+    announce(f"q16 module, encoder rows B={B} N={N} L={L} P={P}")
+    boards, stm = positions.random_positions(B, seed=3)
+    enc = encode.encode_batch(torch.from_numpy(boards).to(DEV), torch.from_numpy(stm).to(DEV), "HalfKAv2_hm")
+    g = np.random.default_rng(13)
+    Wq = g.integers(-3000, 3000, size=(N, L)).astype(np.int16)
+    bq = g.integers(-3000, 3000, size=L).astype(np.int16)
+    ps = g.integers(-10**6, 10**6, size=(N, P)).astype(np.int32)
+    qft = QuantizedFeatureTransformer(dev(Wq), dev(bq), dev(ps), 0, 127)
+    (ow, pw), (ob, pb) = qft(enc["white"], enc["black"])
+    for o, p, i in ((ow, pw, enc["white"]), (ob, pb, enc["black"])):
+        ro, rp = ft_oracle.fwd_i16(host(i), Wq, bq, ps, 0, 127, False)
+        assert np.array_equal(host(o), ro)
+        assert np.array_equal(host(p), rp)
