@@ -97,10 +97,14 @@ def test_sparse_linear_step_encoder_rows(feature_set):
     assert rel_err(host(b.grad), db64) <= 1e-5
 
 
+@pytest.mark.parametrize("rows", ["uniform", "encoder"])
 @pytest.mark.parametrize("name", ["HalfKAv2_hm^", "Full_Threats+HalfKAv2_hm^"])
-def test_fused_module_full_batch_matches_composed_oracle(name):
+def test_fused_module_full_batch_matches_composed_oracle(name, rows):
+    """rows="encoder": the index rows the GPU encoder makes from random positions
+    (for the composed set: threats by colour and piece, then HalfKAv2_hm offset
+    by 60 720), the layout the module sees in training."""
     B, L = 65536, 1048
-    announce(f"fused module {name} B={B} L={L} vs composed oracle")
+    announce(f"fused module {name} B={B} L={L} {rows} rows vs composed oracle")
     torch.manual_seed(5)
     ft = get_feature_cls(name)(L).to(DEV)
     assert ft.fused
@@ -111,8 +115,17 @@ def test_fused_module_full_batch_matches_composed_oracle(name):
     g = np.random.default_rng(65536 + len(name))
     K = ft.MAX_ACTIVE_FEATURES
     lo = 16 if K == 32 else 32
-    iw = workloads.make_indices(g, B, ft.NUM_INPUTS, K, lo, K, sort=False)
-    ib = workloads.make_indices(g, B, ft.NUM_INPUTS, K, lo, K, sort=True)
+    if rows == "encoder":
+        from sft_amd import encode, positions
+
+        boards, stm = positions.random_positions(B, seed=5)
+        enc = encode.encode_batch(torch.from_numpy(boards).to(DEV), torch.from_numpy(stm).to(DEV), name)
+        iw, ib = host(enc["white"]), host(enc["black"])
+        assert iw.shape == (B, K) and iw.max() < ft.NUM_INPUTS
+        del enc
+    else:
+        iw = workloads.make_indices(g, B, ft.NUM_INPUTS, K, lo, K, sort=False)
+        ib = workloads.make_indices(g, B, ft.NUM_INPUTS, K, lo, K, sort=True)
     gw = g.standard_normal((B, L), dtype=np.float32)
     gb = g.standard_normal((B, L), dtype=np.float32)
     ow, ob = ft(dev(iw), dev(ib))
