@@ -134,3 +134,60 @@ def test_fused_transform_equals_reference_ops(name, B):
             assert err <= 1e-5, (n, err)
         else:
             assert torch.equal(fg[n], rg[n]), n
+
+
+@pytest.mark.parametrize("name", ["HalfKAv2_hm^", "Full_Threats+HalfKAv2_hm^"])
+def test_transform_encoder_batch_matches_oracles(name):
+    """The trainer's data flow end to end: the GPU encoder makes the index rows,
+    side to move and PSQT bucket of random positions, and the fused epilogue op
+    runs on them over the module's tables (B = 16 384, L1 = 1040, 8 PSQT
+    buckets).  l0 and psqt bit-exact, table grads bit-exact, virtual and bias
+    grads within 1e-5 of binary64, against the composed and epilogue oracles."""
+    from sft_amd import encode, positions
+
+    B, L1, P = 16384, 1040, 8
+    L = L1 + P
+    announce(f"transform over encoder rows {name} B={B}")
+    boards, stm = positions.random_positions(B, seed=9)
+    enc = encode.encode_batch(torch.from_numpy(boards).to(DEV), torch.from_numpy(stm).to(DEV), name)
+    idx0, idx1 = host(enc["white"]), host(enc["black"])
+    us = host(enc["us"]).reshape(-1).astype(np.float32)
+    k = host(enc["psqt_indices"]).astype(np.int64)
+    assert set(np.unique(us)) <= {0.0, 1.0} and k.min() >= 0 and k.max() < P
+    torch.manual_seed(9)
+    ft = get_feature_cls(name)(L).to(DEV)
+    g = np.random.default_rng(9)
+    blocks = []
+    for f in ft.features:
+        w = (g.standard_normal(tuple(f.weight.shape)) * 0.1).astype(np.float32)
+        v = (g.standard_normal(tuple(f.virtual_weight.shape)) * 0.05).astype(np.float32) \
+            if hasattr(f, "virtual_weight") else None
+        blocks.append((w, v))
+    bias = g.uniform(0.0, 0.6, L).astype(np.float32)
+    g_l0 = g.standard_normal((B, L1)).astype(np.float32)
+    g_psqt = g.standard_normal(B).astype(np.float32)
+
+    tw = [dev(w) for w, _ in blocks]
+    tv = [None if v is None else dev(v) for _, v in blocks]
+    l0 = torch.full((B, L1), float("nan"), device=DEV)
+    psqt = torch.full((B,), float("nan"), device=DEV)
+    saved = _native.ft_fwd_transform_f32(enc["white"], enc["black"], tw, tv, dev(bias), dev(us), enc["psqt_indices"],
+                                         L1, l0, psqt)
+    dw = [torch.full_like(t, float("nan")) for t in tw]
+    dv = [None if t is None else torch.full_like(t, float("nan")) for t in tv]
+    db = torch.full((L,), float("nan"), device=DEV)
+    _native.ft_bwd_transform_f32(enc["white"], enc["black"], dev(g_l0), dev(g_psqt), dev(us), enc["psqt_indices"],
+                                 saved, L1, dw, dv, db)
+    torch.cuda.synchronize()
+
+    xw, xb = composed_oracle.composed_fwd(idx0, idx1, blocks, bias)
+    rl0, rpsqt = epilogue_oracle.fwd(xw, xb, us, k, L1)
+    assert np.array_equal(_bits(host(l0)), _bits(rl0))
+    assert np.array_equal(_bits(host(psqt)), _bits(rpsqt.reshape(-1)))
+    dxw, dxb = epilogue_oracle.bwd(xw, xb, us, k, L1, g_l0, g_psqt)
+    rw, rv, rdb = composed_oracle.composed_bwd(idx0, idx1, dxw, dxb, blocks)
+    for s in range(len(blocks)):
+        assert np.array_equal(host(dw[s]), rw[s]), s
+        if rv[s] is not None:
+            assert dw_rel_err(host(dv[s]), rv[s]) <= 1e-5, s
+    assert rel_err(host(db), rdb) <= 1e-5
