@@ -381,15 +381,15 @@ constexpr int kMaxParts = 4;
 // lists are assembled in LDS (row stride kpad + 1, free of bank conflicts)
 // and stored with coalesced 16-byte stores; else each thread stores its own.
 template <bool STAGE>
-__global__ __launch_bounds__(kBlock) void rank_lists_kernel(RankArgs a, int64_t B, int64_t Bpad, int K, int N,
-                                                            int kpad, int vec) {
+__device__ __forceinline__ void rank_lists_block(const RankArgs &a, int bx, int by, int64_t B, int64_t Bpad, int K,
+                                                 int N, int kpad, int vec) {
   extern __shared__ int sm[];  // bins[K + 1] | offsets[K + 1] | (STAGE) 256 rows of kpad + 1 | (parts) run scans
   unsigned *bin = reinterpret_cast<unsigned *>(sm), *off = bin + (K + 1);
   int *rows = sm + 2 * (K + 1);
-  const RankLists &L = a.L[blockIdx.y];
-  const int32_t *__restrict__ idx = a.idx[blockIdx.y];
+  const RankLists &L = a.L[by];
+  const int32_t *__restrict__ idx = a.idx[by];
   const int tid = threadIdx.x;
-  const int64_t base = (int64_t)blockIdx.x * kRankSortBlock;
+  const int64_t base = (int64_t)bx * kRankSortBlock;
   const int64_t b = base + tid;
   const bool real = b < B;
   const int32_t *row = idx + (real ? b : 0) * K;
@@ -591,6 +591,12 @@ __global__ __launch_bounds__(kBlock) void rank_lists_kernel(RankArgs a, int64_t 
       out[i] = i32x4{src[0], src[1], src[2], src[3]};
     }
   }
+}
+
+template <bool STAGE>
+__global__ __launch_bounds__(kBlock) void rank_lists_kernel(RankArgs a, int64_t B, int64_t Bpad, int K, int N,
+                                                            int kpad, int vec) {
+  rank_lists_block<STAGE>(a, (int)blockIdx.x, (int)blockIdx.y, B, Bpad, K, N, kpad, vec);
 }
 
 // Lists longer than the staged ones (K > 32, rows of 16-byte pieces): four
@@ -1281,11 +1287,12 @@ void launch_fwd_i16(dim3 grid, size_t lds, hipStream_t s, const int32_t *idx, in
 // Wt[(t * (N + 1) + r) * 8 + q] = W[r, 4 * (8 t + q) .. +3], and row N of
 // every tile = -0.0 (the pad row); the table's padding chunks of the last
 // tile are not written.
-static __global__ __launch_bounds__(kBlock) void tile_relayout_kernel(const f32x4 *__restrict__ W, int64_t N, int64_t cols4,
-                                                               f32x4 *__restrict__ Wt) {
+// Workgroup b of g re-lays chunks b * kBlock + tid, + g * kBlock, ... out.
+__device__ __forceinline__ void tile_relayout_part(int64_t b, int64_t g, const f32x4 *__restrict__ W, int64_t N,
+                                                   int64_t cols4, f32x4 *__restrict__ Wt) {
   const int64_t body = N * cols4, total = body + ceil_div(cols4, (int64_t)8) * 8;
   const int64_t rows = tile_rows(N);
-  for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < total; i += (int64_t)gridDim.x * kBlock) {
+  for (int64_t i = b * kBlock + threadIdx.x; i < total; i += g * kBlock) {
     if (i < body) {
       const int64_t r = i / cols4, c = i % cols4;
       const int64_t t = c / 8, q = c % 8;
@@ -1295,6 +1302,29 @@ static __global__ __launch_bounds__(kBlock) void tile_relayout_kernel(const f32x
       Wt[(t * rows + N) * 8 + q] = f32x4{-0.f, -0.f, -0.f, -0.f};
     }
   }
+}
+static __global__ __launch_bounds__(kBlock) void tile_relayout_kernel(const f32x4 *__restrict__ W, int64_t N, int64_t cols4,
+                                                               f32x4 *__restrict__ Wt) {
+  tile_relayout_part(blockIdx.x, gridDim.x, W, N, cols4, Wt);
+}
+
+// The staged rank lists and the table re-layout in one launch: workgroups
+// 0 .. nrank-1 build the rank lists (rank_lists_block, nrx per perspective),
+// the others re-lay the table out.  Both only read the indices and the table,
+// so they need no order between them, and the gather after them then waits for
+// one launch instead of two back to back.
+#ifndef SFT_FWD_FUSE_RANKS
+#define SFT_FWD_FUSE_RANKS 1
+#endif
+static __global__ __launch_bounds__(kBlock) void relayout_rank_kernel(RankArgs a, int64_t B, int64_t Bpad, int K,
+                                                                      int N, int kpad, int vec, int nrx, int nrank,
+                                                                      const f32x4 *__restrict__ W, int64_t cols4,
+                                                                      f32x4 *__restrict__ Wt) {
+  if ((int)blockIdx.x < nrank) {  // whole block: uniform
+    rank_lists_block<true>(a, (int)blockIdx.x % nrx, (int)blockIdx.x / nrx, B, Bpad, K, N, kpad, vec);
+    return;
+  }
+  tile_relayout_part((int64_t)blockIdx.x - nrank, (int64_t)gridDim.x - nrank, W, N, cols4, Wt);
 }
 
 void launch_tile_relayout(const f32x4 *src, int64_t rows, int64_t cols4, f32x4 *dst, hipStream_t s) {
@@ -1411,8 +1441,11 @@ static int lists_narrow(int K, int64_t N, int nparts) {
 }
 
 // Rank lists of np perspectives (idx[p] -> R[p]) in one launch.
+// With relay_W, the table re-layout into relay_Wt too: in the same launch as
+// the staged rank lists when SFT_FWD_FUSE_RANKS, else launched first.
 static int build_rank_lists(const int32_t *idx0, const int32_t *idx1, int np, int64_t B, int K, int N,
-                            const RankLists &R0, const RankLists &R1, int nparts, hipStream_t s, const char *who) {
+                            const RankLists &R0, const RankLists &R1, int nparts, hipStream_t s, const char *who,
+                            const f32x4 *relay_W = nullptr, int64_t relay_cols4 = 0, f32x4 *relay_Wt = nullptr) {
   RankArgs a;
   a.idx[0] = idx0;
   a.idx[1] = idx1;
@@ -1433,6 +1466,23 @@ static int build_rank_lists(const int32_t *idx0, const int32_t *idx1, int np, in
   const size_t scan_lds = nparts > 1 ? (size_t)kMaxParts * kRankSortBlock * 4 : 0;  // run scans, over the rows
   const size_t lds = (size_t)(2 * (K + 1)) * 4 + std::max(rows_lds, scan_lds);
   const dim3 grid((unsigned)ceil_div(Bp, (int64_t)kRankSortBlock), (unsigned)np);
+  if (relay_W != nullptr && SFT_FWD_FUSE_RANKS && stage && lds <= kMaxIndexLds) {
+    ProfScope prof(kProfFwdRelayout, s);
+    const int64_t total = (int64_t)N * relay_cols4 + ceil_div(relay_cols4, (int64_t)8) * 8;
+    const int nrank = (int)(grid.x * grid.y);
+    const int64_t nrel = std::min<int64_t>(ceil_div(total, kBlock), 1 << 16);
+    hipLaunchKernelGGL(relayout_rank_kernel, dim3((unsigned)(nrank + nrel)), dim3(kBlock), lds, s, a, B, Bp, K, N,
+                       kpad, vec, (int)grid.x, nrank, relay_W, relay_cols4, relay_Wt);
+    return check_launch((std::string(who) + " (re-layout and rank lists)").c_str());
+  }
+  if (relay_W != nullptr) {
+    {
+      ProfScope prof(kProfFwdRelayout, s);
+      launch_tile_relayout(relay_W, N, relay_cols4, relay_Wt, s);
+    }
+    const int rc = check_launch((std::string(who) + " (relayout)").c_str());
+    if (rc != SFT_OK) return rc;
+  }
   ProfScope prof(kProfFwdRanks, s);
   // longer lists: four threads per position, quarters of S slots (whole 16-byte pieces)
   const int S = round_up4((K + kWideSubs - 1) / kWideSubs);
@@ -1495,13 +1545,9 @@ int fwd_f32_tiled(const int32_t *idx, int64_t B, int K, const float *W, int64_t 
   char *lists = static_cast<char *>(ws) + align256((size_t)(ntiles * tile_rows(N) * kTileF) * 4);
   const RankLists R = rank_lists_at(lists, B, K, lists_narrow(K, N, nparts));
   f32x4 *carry = nparts > 1 ? reinterpret_cast<f32x4 *>(lists + rank_lists_bytes(B, K)) : nullptr;
-  {
-    ProfScope prof(kProfFwdRelayout, s);
-    launch_tile_relayout(reinterpret_cast<const f32x4 *>(W), N, cols4, wt, s);
-  }
-  int rc = check_launch("sft_ft_fwd_f32_ex (relayout)");
+  int rc = build_rank_lists(idx, idx, 1, B, K, (int)N, R, R, nparts, s, who, reinterpret_cast<const f32x4 *>(W), cols4,
+                            wt);
   if (rc != SFT_OK) return rc;
-  if ((rc = build_rank_lists(idx, idx, 1, B, K, (int)N, R, R, nparts, s, who)) != SFT_OK) return rc;
   const int nchunks = (int)(rank_pad(B) / kRanksPerBlock);
   const int64_t blocks = tile_sched_items_per_xcd(ntiles, nchunks) * kXcds;
   for (int part = 0; part < nparts; ++part) {

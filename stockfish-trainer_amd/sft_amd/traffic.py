@@ -43,6 +43,7 @@ KINDS = [
     (r"\bfwd_tiled_kernel<", "fwd_f32_tiled_gather"),
     (r"\bfwd_f32_kernel<", "fwd_f32_gather"),
     (r"\btile_relayout_kernel\b", "fwd_tile_relayout"),
+    (r"\brelayout_rank_kernel\b", "fwd_tile_relayout"),  # the re-layout with the staged rank lists
     (r"\bfold_relayout_kernel\b", "fwd_fold_relayout"),
     (r"\bfwd_i16_tiled_kernel\b", "fwd_i16_tiled_gather"),
     (r"\bfwd_i16_ranked_kernel\b", "fwd_i16_tiled_gather"),
