@@ -46,7 +46,10 @@ int slot_sort_buckets(const int32_t *idx, int64_t M, int K, int64_t N, int chunk
 int slot_sort_buckets_high(const int32_t *idx, int64_t M, int K, int64_t N, int chunk_rows, int nchunks, void *ws,
                            int *clear, int nclear, hipStream_t s);
 int slot_sort_buckets_low(const void *ws, int64_t M, int64_t N, int chunk_rows, int nchunks, int *vout,
-                          int32_t *seg, int32_t *list, int *count, uint16_t *pos16, int long_period, hipStream_t s);
+                          int32_t *seg, int32_t *list, int *count, uint16_t *pos16, int long_period, hipStream_t s,
+                          int bfirst = 0, int bend = -1);
+// Buckets that complete position chunk 0 (0: no such split).
+int slot_sort_buckets_chunk0(int64_t N, int nchunks);
 
 namespace {
 
@@ -1284,6 +1287,17 @@ bool prep_pays(int64_t B, int K, int L, uint32_t flags) {
 #ifndef SFT_BWD_FUSE_BIAS_FINAL
 #define SFT_BWD_FUSE_BIAS_FINAL 1
 #endif
+// With the split prepared sort and the gather in position chunks, the
+// backward's buckets in two launches: those that complete chunk 0 first, so
+// that chunk 0's gather waits for them only and the rest run beside it
+// (L = 136: 0.3805-0.3816 -> 0.3778-0.3802 ms per step, A/B builds on two boxes).  The whole sort in the
+// backward (radix pass and buckets beside the bias pass) split the same way
+// was slower (workload 1: 1.7072-1.7089 -> 1.7099-1.7118 ms): there the
+// buckets are a smaller part of the sort the bias pass hides.
+#ifndef SFT_BWD_SPLIT_BUCKETS
+#define SFT_BWD_SPLIT_BUCKETS 1
+#endif
+constexpr int kChunk0Mark = 1;  // side-stream mark after chunk 0's buckets
 bool prep_split(int64_t B, int K, int64_t N, int L, uint32_t flags) {
   return prep_pays(B, K, L, flags) && (int64_t)K * SFT_BWD_SPLIT_K_PER_L >= L &&
          slot_sort_buckets_supported(N, sort_chunks(B, L, flags));
@@ -1384,6 +1398,10 @@ int bwd_f32(const int32_t *idx, int64_t B, int K, const float *grad, int64_t N, 
   int32_t *seg = reinterpret_cast<int32_t *>(w + lay.seg);
   int32_t *pos = nullptr;
   std::optional<SideJoinGuard> side_join;  // joins the side stream on every early return
+  // chunk 0's gather waits for the buckets of chunk 0 only (kChunk0Mark)
+  const bool chunk0_split = SFT_BWD_SPLIT_BUCKETS && sorted && prepared && tiled && nc > 1 &&
+                            prep_split(B, K, N, L, flags) && slot_sort_buckets_chunk0(N, nc) > 0;
+  bool chunk0_marked = false;
   if (sorted && prepared) {
     PrepLayout pl;
     make_prep_layout(B, K, N, L, flags, pl);
@@ -1410,9 +1428,18 @@ int bwd_f32(const int32_t *idx, int64_t B, int K, const float *grad, int64_t N, 
       hipLaunchKernelGGL(zero_kernel, dim3(1), dim3(kBlock), 0, side, reinterpret_cast<float *>(sbs.count),
                          (int64_t)nc);  // the long-segment counts (the forward's radix pass left them alone)
       if ((rc = check_launch("long-segment count clear")) != SFT_OK) return rc;
+      const int nb0 = chunk0_split ? slot_sort_buckets_chunk0(N, nc) : 0;
       if ((rc = slot_sort_buckets_low(pw + pl.sort, M, N, (int)crow, nc, pos, sbs.seg, sbs.list, sbs.count,
-                                      crow <= 65536 ? sbs.pos16 : nullptr, kLongSeg, side)) != SFT_OK)
+                                      crow <= 65536 ? sbs.pos16 : nullptr, kLongSeg, side, 0,
+                                      nb0 > 0 ? nb0 : -1)) != SFT_OK)
         return rc;
+      if (nb0 > 0) {
+        if ((rc = mark_side(kChunk0Mark)) != SFT_OK) return rc;
+        chunk0_marked = true;
+        if ((rc = slot_sort_buckets_low(pw + pl.sort, M, N, (int)crow, nc, pos, sbs.seg, sbs.list, sbs.count,
+                                        crow <= 65536 ? sbs.pos16 : nullptr, kLongSeg, side, nb0, -1)) != SFT_OK)
+          return rc;
+      }
     } else {
       seg = reinterpret_cast<int32_t *>(pw + pl.seg);
       pos = slot_sort_positions(M, N, nc, pw + pl.sort);
@@ -1438,7 +1465,10 @@ int bwd_f32(const int32_t *idx, int64_t B, int K, const float *grad, int64_t N, 
                                 s)) != SFT_OK)
       return rc;
   }
-  if (side_join) {
+  if (chunk0_marked) {
+    // the rest of the buckets still run: joined before chunk 1's gather
+    if ((rc = wait_side(s, kChunk0Mark)) != SFT_OK) return rc;
+  } else if (side_join) {
     if ((rc = join_side(s)) != SFT_OK) return rc;
     side_join->release();
   }
@@ -1495,6 +1525,10 @@ int bwd_f32(const int32_t *idx, int64_t B, int K, const float *grad, int64_t N, 
     const BiasFinal bf{reinterpret_cast<const f32x4 *>(w + lay.partial), lay.nparts, cols4,
                        reinterpret_cast<f32x4 *>(db), overwrite};
     for (int h = 0; h < nc; ++h) {
+      if (h == 1 && chunk0_marked) {
+        if ((rc = join_side(s)) != SFT_OK) return rc;
+        side_join->release();
+      }
       ProfScope prof(kProfBwdTiled, s);
       const bool nt = (nc > 1 ? half_rows(B) : B) * kBwdTileCh * 16 >= kNtStoreTileBytes;
       const int64_t crow = nc > 1 ? half_rows(B) : B;

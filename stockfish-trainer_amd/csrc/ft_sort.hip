@@ -395,7 +395,7 @@ __global__ __launch_bounds__(kBucketBlock) void bucket_sort_kernel(
     const unsigned *__restrict__ kin, const int *__restrict__ vin, const unsigned *__restrict__ totals, int ntot,
     unsigned nkeys, FastDiv div_feat, unsigned nfeat, int *__restrict__ vout, uint16_t *__restrict__ pos16,
     int chunk_rows, int32_t *__restrict__ seg, int32_t *__restrict__ long_list, int *__restrict__ long_count,
-    int long_period) {
+    int long_period, int b0) {
   constexpr int D = 1 << SB;
   constexpr int TILE = kBucketBlock * kBucketItems;
   constexpr int PER_WAVE = TILE / kBucketWaves;
@@ -406,7 +406,7 @@ __global__ __launch_bounds__(kBucketBlock) void bucket_sort_kernel(
   __shared__ uint8_t s_dig[TILE];
   __shared__ uint16_t s_p16[TILE];
   const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
-  const int b = blockIdx.x;
+  const int b = (int)blockIdx.x + b0;  // bucket
   // bucket start (digit totals of the buckets before b) and the active total
   unsigned before = 0, all = 0;
   for (int i = tid; i < ntot; i += kBucketBlock) {
@@ -695,21 +695,40 @@ int slot_sort_buckets_high(const int32_t *idx, int64_t M, int K, int64_t N, int 
 // (only read), writing the sorted positions to vout, their 16-bit chunk
 // offsets (pos16, when not null), segment starts seg[0 .. nchunks N] and per
 // chunk the list of long segments (list + c N, count[c], which must be zero).
+// Buckets [bfirst, bend) only (bend < 0: to the last); split launches must
+// together cover every bucket once, bucket 0 (which also stores seg[nchunks N])
+// included.
 int slot_sort_buckets_low(const void *ws, int64_t M, int64_t N, int chunk_rows, int nchunks, int *vout,
-                          int32_t *seg, int32_t *list, int *count, uint16_t *pos16, int long_period, hipStream_t s) {
+                          int32_t *seg, int32_t *list, int *count, uint16_t *pos16, int long_period, hipStream_t s,
+                          int bfirst, int bend) {
   BucketBufs bb;
   int rc = bucket_bufs(const_cast<void *>(ws), M, N, nchunks, bb);
   if (rc != SFT_OK) return rc;
   const unsigned nkeys = (unsigned)((int64_t)nchunks * N);
   const int nb = (int)ceil_div(std::max<int64_t>(nkeys, 1), (int64_t)1 << bb.sb);
+  if (bend < 0 || bend > nb) bend = nb;
+  if (bfirst < 0 || bfirst > bend) return fail(SFT_EINVAL, "slot bucket sort: bucket range out of order");
+  if (bfirst == bend) return SFT_OK;
   const FastDiv div_feat((uint32_t)N);
+  const dim3 grid((unsigned)(bend - bfirst));
   if (bb.sb == 8)
-    hipLaunchKernelGGL(bucket_sort_kernel<8>, dim3(nb), dim3(kBucketBlock), 0, s, bb.k1, bb.v1, bb.totals, 1 << bb.rb,
-                       nkeys, div_feat, (unsigned)N, vout, pos16, chunk_rows, seg, list, count, long_period);
+    hipLaunchKernelGGL(bucket_sort_kernel<8>, grid, dim3(kBucketBlock), 0, s, bb.k1, bb.v1, bb.totals, 1 << bb.rb,
+                       nkeys, div_feat, (unsigned)N, vout, pos16, chunk_rows, seg, list, count, long_period, bfirst);
   else
-    hipLaunchKernelGGL(bucket_sort_kernel<7>, dim3(nb), dim3(kBucketBlock), 0, s, bb.k1, bb.v1, bb.totals, 1 << bb.rb,
-                       nkeys, div_feat, (unsigned)N, vout, pos16, chunk_rows, seg, list, count, long_period);
+    hipLaunchKernelGGL(bucket_sort_kernel<7>, grid, dim3(kBucketBlock), 0, s, bb.k1, bb.v1, bb.totals, 1 << bb.rb,
+                       nkeys, div_feat, (unsigned)N, vout, pos16, chunk_rows, seg, list, count, long_period, bfirst);
   return check_launch("slot bucket sort (buckets)");
+}
+
+// Buckets [0, n) hold every key of position chunk 0 and the first key of
+// chunk 1 (key N: its segment start ends chunk 0's last segment), so after
+// them chunk 0's positions, segment starts and long-segment list are final;
+// 0 when there is one chunk or no bucket plan.
+int slot_sort_buckets_chunk0(int64_t N, int nchunks) {
+  int sb, rb;
+  if (nchunks < 2 || N <= 0 || !bucket_plan((int64_t)nchunks * N, sb, rb)) return 0;
+  const int64_t nb = ceil_div((int64_t)nchunks * N, (int64_t)1 << sb);
+  return (int)std::min<int64_t>(nb, (N >> sb) + 1);
 }
 
 // The bucket sort with the segment pass folded in: both halves, the sorted
@@ -722,8 +741,8 @@ int slot_sort_buckets(const int32_t *idx, int64_t M, int K, int64_t N, int chunk
   int rc = bucket_bufs(ws, M, N, nchunks, bb);
   if (rc != SFT_OK) return rc;
   if ((rc = slot_sort_buckets_high(idx, M, K, N, chunk_rows, nchunks, ws, count, nchunks, s)) != SFT_OK) return rc;
-  if ((rc = slot_sort_buckets_low(ws, M, N, chunk_rows, nchunks, bb.v2, seg, list, count, pos16, long_period, s)) !=
-      SFT_OK)
+  if ((rc = slot_sort_buckets_low(ws, M, N, chunk_rows, nchunks, bb.v2, seg, list, count, pos16, long_period, s, 0,
+                                  -1)) != SFT_OK)
     return rc;
   *pos_sorted = bb.v2;
   return SFT_OK;
