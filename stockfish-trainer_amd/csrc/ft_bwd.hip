@@ -1136,8 +1136,21 @@ struct BwdLayout {
   int nparts;
 };
 
-int bias_parts(int64_t B) {
-  return (int)std::max<int64_t>(1, std::min<int64_t>(kBiasMaxParts, ceil_div(B, kBiasRowsPerBlock)));
+// Beside the whole sort (radix pass and buckets on the side stream, which
+// outlasts the bias pass at B = 65536), the pass takes 7/8 of the row blocks:
+// 448 instead of 512 at B = 65536, L = 1048, step 1.706-1.712 -> 1.670-1.678 ms
+// (A/B builds on three boxes; 384: 1.680, 320: 1.693, 256: 1.693 ms); the
+// composed pair op, whose two sorts run beside both bias passes, 1.700 ->
+// 1.693 ms (Full_Threats+HalfKAv2_hm^ 6.634 -> 6.620 ms).  At B = 16384 (256 ->
+// 224 blocks) fewer blocks were even; with the prepared sort (nothing or only
+// the buckets beside the pass) the pass keeps them all (L = 136, 384 blocks:
+// 0.377 -> 0.383 ms).
+#ifndef SFT_BIAS_BESIDE_SORT_EIGHTHS
+#define SFT_BIAS_BESIDE_SORT_EIGHTHS 7
+#endif
+int bias_parts(int64_t B, bool beside_sort) {
+  const int64_t p = std::max<int64_t>(1, std::min<int64_t>(kBiasMaxParts, ceil_div(B, kBiasRowsPerBlock)));
+  return (int)(beside_sort ? std::max<int64_t>(1, p * SFT_BIAS_BESIDE_SORT_EIGHTHS / 8) : p);
 }
 
 bool tiled_shape(int64_t B, int L, uint32_t flags) {
@@ -1172,7 +1185,8 @@ bool prep_pays(int64_t B, int K, int L, uint32_t flags);
 bool prep_split(int64_t B, int K, int64_t N, int L, uint32_t flags);
 int make_layout(int64_t B, int K, int64_t N, int L, uint32_t flags, BwdLayout &lay) {
   const int64_t M = B * K;
-  lay.nparts = bias_parts(B);
+  lay.nparts = bias_parts(B, !(flags & SFT_BWD_ATOMIC) && M > 0 &&
+                                 !((flags & SFT_BWD_PREPARED) && prep_pays(B, K, L, flags)));
   size_t off = 0;
   lay.partial = off;
   off = align256(off + (size_t)lay.nparts * (size_t)L * sizeof(float));
@@ -1569,7 +1583,7 @@ struct PairLayout {
 
 void make_pair_layout(int64_t B, int K, int64_t N, int L, PairLayout &lay) {
   const int64_t M = B * K;
-  lay.nparts = bias_parts(B);
+  lay.nparts = bias_parts(B, M > 0);  // both sorts run on the side stream
   lay.nc = sort_chunks(B, L, SFT_BWD_OVERWRITE);
   size_t off = 0;
   lay.partial = off;

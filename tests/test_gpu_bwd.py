@@ -246,15 +246,19 @@ def _prepared(idx, G, N, W=None, grad_offset=0):
 @pytest.mark.parametrize("seed,B,N,K,L,lo,hi,sort", SHAPES)
 def test_prepared_bwd_matches_the_backward(seed, B, N, K, L, lo, hi, sort):
     """Sorting under the forward changes nothing: the forward and the prepared
-    backward are bit-identical to the ordinary calls (tiled and row gathers, one
-    and two position chunks, long segments)."""
+    backward's weight grad are bit-identical to the ordinary calls (tiled and
+    row gathers, one and two position chunks, long segments).  The bias grad's
+    row blocks differ between the two (the ordinary call's bias pass runs
+    beside the whole sort and takes fewer), so both are held to the bias-grad
+    bound, 1e-5 of binary64."""
     announce(f"prepared bwd seed={seed} B={B} N={N} K={K} L={L}")
     idx, W, b, G = case(seed, B, N, K, L, lo, hi, sort)
     out, dW, db = _prepared(idx, G, N, W)
     assert np.array_equal(out, ft_oracle.fwd_f32(idx, W, np.zeros(L, np.float32)))
     dW0, db0 = run_bwd(idx, G, N, _native.SFT_BWD_OVERWRITE)
     assert np.array_equal(dW, dW0)
-    assert np.array_equal(db, db0)
+    db64 = G.astype(np.float64).sum(0)
+    assert rel_err(db, db64) <= 1e-5 and rel_err(db0, db64) <= 1e-5
 
 
 @pytest.mark.parametrize("B,L", [(40000, 256), (3000, 256), (40000, 136), (3000, 136)])
