@@ -282,6 +282,23 @@ def test_prepared_bwd_reads_the_buffer_only(B, L):
         assert rel_err(db, db64) <= 1e-5
 
 
+@pytest.mark.parametrize("N", [1023, 1024, 1025, 1152])
+def test_prepared_bwd_chunk0_buckets_edge(N):
+    """The split prepared sort's buckets run in two launches, those holding
+    every key of position chunk 0 and the first key of chunk 1 (key N, whose
+    segment start ends chunk 0's last segment) first.  Feature counts at and
+    around a multiple of the 128-key bucket (N = 1024, 1152: key N opens a
+    bucket of its own) keep the weight grad bit-exact (B = 40000: two position
+    chunks; L = 136: K >= L / 5)."""
+    announce(f"prepared bwd, chunk-0 buckets N={N}")
+    B, K, L = 40000, 32, 136
+    idx, W, b, G = case(40 + N % 7, B, N, K, L, 0, 32, True)
+    _, i, prep = _prepare(idx, N, L)
+    dW, db = _prepared_bwd(i, G, N, prep)
+    assert np.array_equal(dW, ft_oracle.bwd_f32(idx, G, N)[0])
+    assert rel_err(db, G.astype(np.float64).sum(0)) <= 1e-5
+
+
 def test_prepared_bwd_unaligned_weight_grad():
     """A weight grad that is only 4-byte aligned needs the row gather, which
     sorts in one position chunk: refused (before any launch) when the prepared
