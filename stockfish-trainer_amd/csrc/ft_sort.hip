@@ -25,10 +25,17 @@ namespace {
 
 // Slots per thread of a sort tile: 8 (2048-slot tiles) for up to kBigSort
 // slots, 16 above, where fewer tiles shrink the per-tile digit counts the
-// scans walk (10.5 M slots: 278 -> 226 us per sort; 2.1 M slots: 65 vs 72 us).
+// scans walk (10.5 M slots: 278 -> 226 us per sort).  Alone, a 2.1 M-slot sort
+// was faster with 8 (65 vs 72 us), but beside the kernels it shares the GPU
+// with the steps are faster with 16 at every batch: B = 65536, L = 1048 1.671
+// -> 1.666 ms, L = 136 0.378 -> 0.376 ms, B = 16384 0.575 -> 0.574 ms (A/B
+// builds, same box), so the threshold is 0.
 constexpr int kSortItems = 8;
 constexpr int kSortItemsBig = 16;
-constexpr int64_t kBigSort = 4 << 20;
+#ifndef SFT_SORT_BIG_SLOTS
+#define SFT_SORT_BIG_SLOTS 0
+#endif
+constexpr int64_t kBigSort = SFT_SORT_BIG_SLOTS;
 constexpr int kSortTile = kBlock * kSortItems;  // the smaller tile: sizes the count buffer
 constexpr int kMaxRadix = 1024;  // 10-bit digits (the bucket sort's first pass)
 #ifndef SFT_SORT_BUCKETS
