@@ -396,7 +396,12 @@ int run_passes(const SlotKey &sk, int64_t M, int passes, unsigned *kbuf[2], int 
 // reads it is bit-identical.  Buckets hold ~4-10 K slots at the FT's shapes.
 constexpr int kBucketBlock = 512;
 constexpr int kBucketWaves = kBucketBlock / kWave;
-constexpr int kBucketItems = 16;  // slots per thread per tile: tiles of 8192
+// (8 per thread, tiles of 4096 and half the LDS: steps 1.665 -> 1.670 ms at
+// L = 1048 and 0.375 -> 0.379 ms at L = 136, B = 65536; even at B = 16384.)
+#ifndef SFT_BUCKET_ITEMS
+#define SFT_BUCKET_ITEMS 16
+#endif
+constexpr int kBucketItems = SFT_BUCKET_ITEMS;  // slots per thread per tile: tiles of 8192
 template <int SB>
 __global__ __launch_bounds__(kBucketBlock) void bucket_sort_kernel(
     const unsigned *__restrict__ kin, const int *__restrict__ vin, const unsigned *__restrict__ totals, int ntot,
