@@ -745,8 +745,7 @@ int slot_sort_buckets_low(const void *ws, int64_t M, int64_t N, int chunk_rows, 
 int slot_sort_buckets_chunk0(int64_t N, int nchunks) {
   int sb, rb;
   if (nchunks < 2 || N <= 0 || !bucket_plan((int64_t)nchunks * N, sb, rb)) return 0;
-  const int64_t nb = ceil_div((int64_t)nchunks * N, (int64_t)1 << sb);
-  return (int)std::min<int64_t>(nb, (N >> sb) + 1);
+  return buckets_through_chunk0(N, nchunks, sb);
 }
 
 // The bucket sort with the segment pass folded in: both halves, the sorted

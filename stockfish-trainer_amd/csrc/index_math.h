@@ -19,6 +19,17 @@ namespace sft {
 SFT_HD inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 SFT_HD inline int round_up4(int v) { return (v + 3) & ~3; }
 
+// ---- bucket sort over (position chunk, feature) keys: key = chunk * N + f ----
+// Buckets hold 2^sb consecutive keys.  The first n buckets hold every key of
+// chunk 0 and key N, the first of chunk 1, whose segment start ends chunk 0's
+// last segment; n is the fewest that do (0 with one chunk or no features).
+SFT_HD inline int buckets_through_chunk0(int64_t N, int nchunks, int sb) {
+  if (nchunks < 2 || N <= 0) return 0;
+  const int64_t nb = ceil_div((int64_t)nchunks * N, (int64_t)1 << sb);
+  const int64_t n = (N >> sb) + 1;
+  return (int)(n < nb ? n : nb);
+}
+
 // ---- n / d for 32-bit n by a divisor fixed at launch ----
 // Multiply-high by a magic number (Granlund & Montgomery 1994, round-up
 // variant): with l = ceil(log2 d) and m = floor(2^32 (2^l - d) / d) + 1,

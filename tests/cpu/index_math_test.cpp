@@ -180,6 +180,21 @@ static void check_long_rule(std::mt19937_64 &rng, int period) {
   }
 }
 
+// The buckets that complete position chunk 0 (keys 0 .. N - 1 and key N):
+// none of those keys lies in a later bucket, the count is the fewest that
+// holds them, and it never exceeds the buckets of the key space.
+static void check_chunk0_buckets(int64_t N, int nchunks, int sb) {
+  const int n = buckets_through_chunk0(N, nchunks, sb);
+  const int64_t nb = ceil_div((int64_t)nchunks * N, (int64_t)1 << sb);
+  CHECK(n >= 1 && n <= nb, "N=%lld nchunks=%d sb=%d: %d of %lld buckets", (long long)N, nchunks, sb, n,
+        (long long)nb);
+  for (int64_t key = 0; key <= N; ++key)
+    CHECK((key >> sb) < n, "N=%lld sb=%d: key %lld in bucket %lld of %d", (long long)N, sb, (long long)key,
+          (long long)(key >> sb), n);
+  CHECK((N >> sb) == n - 1, "N=%lld sb=%d: %d buckets, key N in bucket %lld", (long long)N, sb, n,
+        (long long)(N >> sb));
+}
+
 int main() {
   // the sort divides slot numbers by max_active (K) and positions by the
   // position-chunk rows (ceil(B / 2) or B); cover every K the ABI allows up to
@@ -197,6 +212,12 @@ int main() {
     for (int tch : {4, 8, 16}) check_map(plain_map(cols4, tch));
   for (int half4 = 1; half4 <= 300; ++half4)
     for (int psqt4 : {0, 1, 2, 3, 8, 9, 17}) check_map(paired_map(2 * half4 + psqt4, half4));
+
+  for (int sb : {7, 8})
+    for (int64_t N = 1; N <= 2100; ++N)
+      for (int nchunks : {2, 3}) check_chunk0_buckets(N, nchunks, sb);
+  for (int64_t N : {22528, 23232, 24576, 60720, 85296, 85297}) check_chunk0_buckets(N, 2, N >= 65536 ? 8 : 7);
+  CHECK(buckets_through_chunk0(1000, 1, 7) == 0, "one chunk has no chunk-0 split");
 
   std::mt19937_64 rng(12345);
   for (int period : {1, 2, 3, 8, 128, 256}) check_long_rule(rng, period);
