@@ -904,7 +904,13 @@ struct BwdEpilogue {
   f32x4 *partial;            // [gridDim.x][cols4]
   int P;
 };
-constexpr int kEpiRows = 64;  // positions per workgroup
+// 80 rows: 820 workgroups at B = 65536, leaving the two sorts beside the pass
+// more of the CUs' slots (epilogue op 1.955 -> 1.915 ms per step, Full_Threats
+// 7.091 -> 7.048 ms against 64 rows; 96 rows: 1.918 / 7.049 ms).
+#ifndef SFT_EPI_ROWS
+#define SFT_EPI_ROWS 80
+#endif
+constexpr int kEpiRows = SFT_EPI_ROWS;  // positions per workgroup
 #ifndef SFT_EPI_IT
 #define SFT_EPI_IT 3
 #endif
