@@ -1150,13 +1150,13 @@ struct BwdLayout {
 // 1.693 ms (Full_Threats+HalfKAv2_hm^ 6.634 -> 6.620 ms).  At B = 16384 (256 ->
 // 224 blocks) fewer blocks were even; with the prepared sort (nothing or only
 // the buckets beside the pass) the pass keeps them all (L = 136, 384 blocks:
-// 0.377 -> 0.383 ms).
-#ifndef SFT_BIAS_BESIDE_SORT_EIGHTHS
-#define SFT_BIAS_BESIDE_SORT_EIGHTHS 7
+// 0.377 -> 0.383 ms).  13/16 and 15/16 of the blocks were even or slower.
+#ifndef SFT_BIAS_BESIDE_SORT_16THS
+#define SFT_BIAS_BESIDE_SORT_16THS 14
 #endif
 int bias_parts(int64_t B, bool beside_sort) {
   const int64_t p = std::max<int64_t>(1, std::min<int64_t>(kBiasMaxParts, ceil_div(B, kBiasRowsPerBlock)));
-  return (int)(beside_sort ? std::max<int64_t>(1, p * SFT_BIAS_BESIDE_SORT_EIGHTHS / 8) : p);
+  return (int)(beside_sort ? std::max<int64_t>(1, p * SFT_BIAS_BESIDE_SORT_16THS / 16) : p);
 }
 
 bool tiled_shape(int64_t B, int L, uint32_t flags) {
